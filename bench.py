@@ -1,0 +1,185 @@
+#!/usr/bin/env python3
+"""Benchmark of the Continuum Attention operator on one MI355X.
+
+Workload: the isolated CA operator at
+[B,H,T,D] = [2,16,2048,64] fp32, forward + backward, causal full context,
+Q,K,V ~ N(0,1) with the op's own 1/sqrt(64) scale, log_gain = 0 (tau = 1),
+upstream grad ~ N(0,1), seed 0.  One "step" is one forward + backward of the
+operator with inputs already resident in HBM.
+
+Prints ONE JSON line (rank 0).  `value` is the median fwd+bwd milliseconds
+(lower is better).  `roofline` is for the dominant kernel, from HIP events
+recorded around each kernel launch on the launch stream during the timed
+steps; `cpu_baseline` times the CPU port of the reference's PyTorch CPU path
+(oracle/ca_cpu_port.py) on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_FP32_MFMA_TFLOPS = 157.3
+SHAPE = (2, 16, 2048, 64)
+
+
+def pairs(B, H, T):
+    return B * H * T * (T + 1) // 2
+
+
+# algorithmic flops per causal (query, key) pair, per kernel (D = head dim)
+def kernel_flops_per_pair(D):
+    return {"ca_fwd": 4 * D,        # S = QK^T, O = WV
+            "ca_bwd_dkdv": 8 * D,   # S recompute, dP = dY V^T, dV = W^T dY, dK = dS^T Q
+            "ca_bwd_dq": 2 * D}     # dQ = dS K
+
+
+def cpu_baseline(sample_heads=4, reps=3):
+    import torch
+    from oracle import ca_cpu_port as P
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    B, H, T, D = SHAPE
+    g = torch.Generator().manual_seed(0)
+    q, k, v, dy = (torch.randn(1, sample_heads, T, D, generator=g) for _ in range(4))
+    rho = torch.zeros(sample_heads)
+    P.port_forward(q, k, v, rho, 128)  # warm-up
+    fw, bw = [], []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        P.port_forward(q, k, v, rho, 128)
+        t1 = time.perf_counter()
+        P.port_backward(q, k, v, rho, dy, 128)
+        t2 = time.perf_counter()
+        fw.append(t1 - t0)
+        bw.append(t2 - t1)
+    scale = (B * H) / sample_heads
+    total_ms = (statistics.median(fw) + statistics.median(bw)) * 1e3 * scale
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(total_ms, 1), "unit": "ms per fwd+bwd (extrapolated)",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": (f"[1,{sample_heads},{T},{D}] fp32 fwd+bwd, query_tile=128, median of {reps} "
+                       f"after 1 warm-up, x{scale:g} for the [2,16,2048,64] workload"),
+            "fwd_ms": round(statistics.median(fw) * 1e3 * scale, 1),
+            "bwd_ms": round(statistics.median(bw) * 1e3 * scale, 1),
+            "cpu_model": model, "os_cpu_count": os.cpu_count(), "affinity": threads}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
+              "the CA operator shards trivially over (batch, head) slices -- see DESIGN.md",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    ca = importlib.import_module("continuum-attention_amd")
+    ca.native.load()
+    dev = torch.device("cuda:0")
+    torch.backends.cuda.matmul.allow_tf32 = False
+
+    B, H, T, D = SHAPE
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(SHAPE, generator=g).to(dev).requires_grad_(True) for _ in range(3))
+    rho = torch.zeros(H, device=dev, requires_grad=True)
+    dy = torch.randn(SHAPE, generator=g).to(dev)
+
+    def step():
+        y = ca.continuum_attention(q, k, v, rho, 128)
+        torch.autograd.grad(y, (q, k, v, rho), dy)
+        return y
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    fwd, bwd, tot = [], [], []
+    ca.native.timing_enable(True)
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for _ in range(args.steps):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        ev[0].record()
+        y = ca.continuum_attention(q, k, v, rho, 128)
+        ev[1].record()
+        torch.autograd.grad(y, (q, k, v, rho), dy)
+        ev[2].record()
+        fwd.append(ev)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    kt = ca.native.timing_read()
+    ca.native.timing_enable(False)
+    for ev in fwd:
+        tot.append(ev[0].elapsed_time(ev[2]))
+        bwd.append(ev[1].elapsed_time(ev[2]))
+    fwd = [ev[0].elapsed_time(ev[1]) for ev in fwd]
+
+    P = pairs(B, H, T)
+    flops_total = 14 * D * P
+    ms = statistics.median(tot)
+    per_kernel = {n: {"avg_ms": round(t / c, 4), "launches": c}
+                  for n, (t, c) in kt.items() if c}
+    fpp = kernel_flops_per_pair(D)
+    dom = max((n for n in per_kernel if n in fpp), key=lambda n: per_kernel[n]["avg_ms"])
+    dom_ms = kt[dom][0] / kt[dom][1]
+    achieved = fpp[dom] * P / (dom_ms * 1e-3) / 1e12
+    op_tflops = flops_total / (ms * 1e-3) / 1e12
+    for n in per_kernel:
+        if n in fpp:
+            per_kernel[n]["tflops"] = round(fpp[n] * P / (kt[n][0] / kt[n][1] * 1e-3) / 1e12, 2)
+
+    out = {
+        "metric": "CA fwd+bwd ms @[2,16,2048,64] fp32; % of fp32-MFMA roofline; CA-S tokens/s",
+        "value": round(ms, 4),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic N(0,1) q,k,v,dY, seed 0",
+        "config": {"workload": "CA operator fwd+bwd [B,H,T,D]=[2,16,2048,64] fp32, causal, "
+                               "log_gain=0 (BASELINE config 2)",
+                   "B": B, "H": H, "T": T, "D": D, "query_tile": 128},
+        "fwd_ms": round(statistics.median(fwd), 4),
+        "bwd_ms": round(statistics.median(bwd), 4),
+        "op_tflops": round(op_tflops, 2),
+        "op_roofline_frac": round(op_tflops / PEAK_FP32_MFMA_TFLOPS, 4),
+        "algorithmic_gflop": round(flops_total / 1e9, 3),
+        "wall_s_timed_region": round(wall, 3),
+        "kernels": per_kernel,
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2),
+                     "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": None},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

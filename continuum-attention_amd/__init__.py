@@ -1,0 +1,17 @@
+"""MI355X-native Continuum Attention (CA) operator.
+
+Public API (mirrors akhadangi/continuum-attention, cuda/continuum_attention.py:650-783):
+    continuum_attention(q, k, v, log_gain, query_tile=64)
+    _CAExactTiled  (torch.autograd.Function)
+
+The arithmetic runs in hand-written HIP kernels (csrc/, built into
+libca_hip.so by build.py) behind the C ABI in include/continuum_attention_amd.h.
+The package directory name contains a hyphen; import it with
+``importlib.import_module("continuum-attention_amd")``.
+"""
+from . import _native as native
+from .ops import (SUPPORTED_HEAD_DIMS, _CAExactTiled, ca_backward, ca_forward,
+                  continuum_attention)
+
+__all__ = ["continuum_attention", "_CAExactTiled", "ca_forward", "ca_backward", "native",
+           "SUPPORTED_HEAD_DIMS"]

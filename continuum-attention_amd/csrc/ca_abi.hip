@@ -1,0 +1,225 @@
+// C ABI of libca_hip.so: plain pointers, sizes and a HIP stream handle.
+// Declarations and the reference interfaces they replace: include/continuum_attention_amd.h.
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <vector>
+
+#include "../../include/continuum_attention_amd.h"
+#include "ca_kernels.h"
+
+namespace ca {
+template <int D>
+hipError_t set_bwd_attrs();
+}
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+constexpr int kSplitTiles = 16;  // forward split length in 32-key tiles
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+int check_shape(int B, int H, int T, int D) {
+  if (B <= 0 || H <= 0 || T <= 0)
+    return fail(CA_ERR_INVALID, "invalid shape B=%d H=%d T=%d (all must be positive)", B, H, T);
+  if (D != 8 && D != 16 && D != 32 && D != 64)
+    return fail(CA_ERR_UNSUPPORTED, "head dim D=%d not supported (HIP kernels cover D in {8,16,32,64})", D);
+  if ((long long)B * H * T * D > (1ll << 31) - 1)
+    return fail(CA_ERR_UNSUPPORTED, "tensor of %lld elements exceeds the 2^31 element limit",
+                (long long)B * H * T * D);
+  if (T > 65536) return fail(CA_ERR_UNSUPPORTED, "T=%d exceeds the supported 65536", T);
+  return CA_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+struct BwdLayout {
+  size_t ds, dvec, gain, total;
+};
+BwdLayout bwd_layout(int B, int H, int T) {
+  const int BH = B * H;
+  BwdLayout L;
+  L.ds = 0;
+  L.dvec = align256(ca::bwd_ds_floats(BH, T) * sizeof(float));
+  L.gain = L.dvec + align256((size_t)BH * T * sizeof(float));
+  L.total = L.gain + align256((size_t)BH * ca::bwd_num_key_blocks(T) * sizeof(float));
+  return L;
+}
+
+bool g_attrs_done = false;
+int ensure_attrs() {
+  if (g_attrs_done) return CA_OK;
+  hipError_t e = ca::set_bwd_attrs<8>();
+  if (e == hipSuccess) e = ca::set_bwd_attrs<16>();
+  if (e == hipSuccess) e = ca::set_bwd_attrs<32>();
+  if (e == hipSuccess) e = ca::set_bwd_attrs<64>();
+  if (e != hipSuccess) return fail(CA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+  g_attrs_done = true;
+  return CA_OK;
+}
+
+// ---- per-kernel event timing ------------------------------------------------
+struct TimedLaunch {
+  int id;
+  hipEvent_t start, stop;
+};
+bool g_timing = false;
+std::vector<TimedLaunch> g_launches;  // recorded, not yet read
+std::vector<hipEvent_t> g_event_pool;
+int g_open_id = -1;
+hipEvent_t g_open_start = nullptr;
+
+hipEvent_t pool_event() {
+  if (!g_event_pool.empty()) {
+    hipEvent_t e = g_event_pool.back();
+    g_event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+}  // namespace
+
+namespace ca {
+void timer_begin(int id, hipStream_t s) {
+  if (!g_timing) return;
+  g_open_start = pool_event();
+  g_open_id = id;
+  if (g_open_start) (void)hipEventRecord(g_open_start, s);
+}
+void timer_end(int id, hipStream_t s) {
+  if (!g_timing || g_open_id != id || !g_open_start) return;
+  hipEvent_t stop = pool_event();
+  if (!stop) return;
+  (void)hipEventRecord(stop, s);
+  g_launches.push_back({id, g_open_start, stop});
+  g_open_start = nullptr;
+  g_open_id = -1;
+}
+}  // namespace ca
+
+extern "C" {
+
+int ca_timing_enable(int on) {
+  g_timing = on != 0;
+  for (auto& l : g_launches) {
+    g_event_pool.push_back(l.start);
+    g_event_pool.push_back(l.stop);
+  }
+  g_launches.clear();
+  return CA_OK;
+}
+
+int ca_timing_read(double* total_ms, int* launches, int n) {
+  if (!total_ms || !launches || n <= 0) return fail(CA_ERR_INVALID, "ca_timing_read: bad buffers");
+  for (int i = 0; i < n; ++i) {
+    total_ms[i] = 0.0;
+    launches[i] = 0;
+  }
+  for (auto& l : g_launches) {
+    hipError_t e = hipEventSynchronize(l.stop);
+    float ms = 0.f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, l.start, l.stop);
+    if (e != hipSuccess) return fail(CA_ERR_HIP, "ca_timing_read: %s", hipGetErrorString(e));
+    if (l.id < n) {
+      total_ms[l.id] += ms;
+      launches[l.id] += 1;
+    }
+    g_event_pool.push_back(l.start);
+    g_event_pool.push_back(l.stop);
+  }
+  g_launches.clear();
+  return CA_OK;
+}
+
+
+int ca_abi_version(void) { return CA_ABI_VERSION; }
+
+const char* ca_last_error(void) { return g_err; }
+
+size_t ca_fwd_workspace_bytes(int B, int H, int T, int D) {
+  if (B <= 0 || H <= 0 || T <= 0) return 0;
+  (void)D;
+  return ca::fwd_part_floats(B * H, T, kSplitTiles) * sizeof(float);
+}
+
+int ca_fwd_f32(const float* q, const float* k, const float* v, const float* log_gain, float* out,
+               float* stats, void* workspace, size_t workspace_bytes, int B, int H, int T, int D,
+               void* stream) {
+  int rc = check_shape(B, H, T, D);
+  if (rc) return rc;
+  if (!q || !k || !v || !log_gain || !out || !stats)
+    return fail(CA_ERR_INVALID, "null tensor pointer");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+    return fail(CA_ERR_INVALID, "q, k, v and out must be 16-byte aligned");
+  const size_t need = ca_fwd_workspace_bytes(B, H, T, D);
+  if (workspace_bytes < need || (need && !workspace))
+    return fail(CA_ERR_WORKSPACE, "forward workspace of %zu bytes required, %zu given", need,
+                workspace_bytes);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e;
+  float* part = static_cast<float*>(workspace);
+  switch (D) {
+    case 8: e = ca::launch_fwd<8>(q, k, v, log_gain, out, stats, part, B, H, T, kSplitTiles, s); break;
+    case 16: e = ca::launch_fwd<16>(q, k, v, log_gain, out, stats, part, B, H, T, kSplitTiles, s); break;
+    case 32: e = ca::launch_fwd<32>(q, k, v, log_gain, out, stats, part, B, H, T, kSplitTiles, s); break;
+    default: e = ca::launch_fwd<64>(q, k, v, log_gain, out, stats, part, B, H, T, kSplitTiles, s); break;
+  }
+  if (e != hipSuccess) return fail(CA_ERR_HIP, "forward launch: %s", hipGetErrorString(e));
+  return CA_OK;
+}
+
+size_t ca_bwd_workspace_bytes(int B, int H, int T, int D) {
+  if (B <= 0 || H <= 0 || T <= 0) return 0;
+  (void)D;
+  return bwd_layout(B, H, T).total;
+}
+
+int ca_bwd_f32(const float* q, const float* k, const float* v, const float* log_gain,
+               const float* out, const float* stats, const float* dout, float* dq, float* dk,
+               float* dv, float* dlog_gain, void* workspace, size_t workspace_bytes, int B, int H,
+               int T, int D, void* stream) {
+  int rc = check_shape(B, H, T, D);
+  if (rc) return rc;
+  if (!q || !k || !v || !log_gain || !out || !stats || !dout || !dq || !dk || !dv || !dlog_gain)
+    return fail(CA_ERR_INVALID, "null tensor pointer");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dout) || !aligned16(dk) ||
+      !aligned16(dv))
+    return fail(CA_ERR_INVALID, "q, k, v, dout, dk and dv must be 16-byte aligned");
+  const BwdLayout L = bwd_layout(B, H, T);
+  if (!workspace || workspace_bytes < L.total)
+    return fail(CA_ERR_WORKSPACE, "backward workspace of %zu bytes required, %zu given", L.total,
+                workspace_bytes);
+  if ((rc = ensure_attrs())) return rc;
+  char* ws = static_cast<char*>(workspace);
+  float* dsbuf = reinterpret_cast<float*>(ws + L.ds);
+  float* dvec = reinterpret_cast<float*>(ws + L.dvec);
+  float* gain = reinterpret_cast<float*>(ws + L.gain);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e;
+  switch (D) {
+    case 8: e = ca::launch_bwd<8>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, dsbuf, dvec, gain, B, H, T, s); break;
+    case 16: e = ca::launch_bwd<16>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, dsbuf, dvec, gain, B, H, T, s); break;
+    case 32: e = ca::launch_bwd<32>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, dsbuf, dvec, gain, B, H, T, s); break;
+    default: e = ca::launch_bwd<64>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, dsbuf, dvec, gain, B, H, T, s); break;
+  }
+  if (e != hipSuccess) return fail(CA_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
+  return CA_OK;
+}
+
+}  // extern "C"

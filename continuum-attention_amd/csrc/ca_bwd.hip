@@ -1,0 +1,492 @@
+// Continuum Attention backward (gfx950, fp32 MFMA), analytic first-order VJP.
+//
+// Replaces the per-query-tile loop of _CAExactTiled.backward
+// (cuda/continuum_attention.py:697-766): the QK^T and dY.V^T recomputation,
+// the fused score-VJP kernels (ca_backward_fused_kernel /
+// ca_backward_half_kernel, cuda/continuum_attention.py:230-293,337-405) and
+// the dV/dQ/dK/dRho contractions.
+//
+// Kernels (all deterministic, no atomics):
+//   ca_bwd_rowdot   Dl_i = dY_i . y_i   (equals sum_j W_ij dW_ij; the reference
+//                   forms the same row mean at cuda/continuum_attention.py:268-269)
+//   ca_bwd_dkdv     one work group per (slice, 62-key block); 4 waves take
+//                   interleaved 32-query tiles.  Per tile: S^T = K Q^T and
+//                   dP^T = V dY^T by MFMA, W and dS in registers, then
+//                   dV^T += dY^T W and dK^T += Q^T dS by MFMA after an LDS
+//                   transpose.  dS is also written to a packed lower-triangular
+//                   buffer for the dQ pass; per-block gain partials sum dS*s.
+//   ca_bwd_dq       dQ = c dS K, one work group per (slice, 32-query tile).
+//   ca_bwd_gain     dRho_h = sum over batch and key blocks of the partials.
+//
+// Key-block layout: the work group owns weight keys [w0, w0+62); its 64 MFMA
+// key slots are keys w0-1 .. w0+62 (slot s = key w0-1+s), so both neighbours
+// of every owned key are inside the tile.  Lane half h, register n holds slot
+// 32h+n of query q.
+#include "ca_common.h"
+#include "ca_kernels.h"
+
+namespace ca {
+
+template <int D>
+struct Bwd {
+  static constexpr int DH = D / 2;
+  static constexpr int NMB = (D + 31) / 32;
+  static constexpr int C4 = D / 4;
+  static constexpr int CH = DH / 4;
+  static constexpr int LDQ = D + 4;   // padded row stride (floats) of the Q / dY tiles
+  static constexpr int LDW = 64 + 4;  // padded row stride of the W / dS tiles
+  static constexpr int WAVE_FLOATS = 2 * 32 * LDQ + 2 * 32 * LDW;
+  static constexpr int LDS_FLOATS = 4 * WAVE_FLOATS + 64 * D;  // + shared V slots
+};
+
+// XOR swizzle of the V-slot float4 chunks: the A-operand rows read together
+// (slots 16b+{0..3} and 32+16b+{0..3}, ...) land in distinct bank groups.
+__device__ __forceinline__ int vswz(int row, int chunks_per_half) {
+  return ((row & 3) | ((row >> 3) & 4)) & (chunks_per_half - 1);
+}
+
+__global__ __launch_bounds__(256) void ca_bwd_rowdot_kernel(const float* __restrict__ dout,
+                                                            const float* __restrict__ out,
+                                                            float* __restrict__ dvec, int rows,
+                                                            int D) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  float x = (lane < D) ? dout[(size_t)row * D + lane] * out[(size_t)row * D + lane] : 0.f;
+  x = wave_sum(x);
+  if (lane == 0) dvec[row] = x;
+}
+
+__device__ __forceinline__ size_t tri_block(int qt, int kt) {
+  return (size_t)qt * (qt + 1) / 2 + kt;
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    const float* __restrict__ dO, const float* __restrict__ stats, const float* __restrict__ dvec,
+    const float* __restrict__ log_gain, float* __restrict__ dK, float* __restrict__ dV,
+    float* __restrict__ dsbuf, float* __restrict__ gain_part, int BH, int H, int T) {
+  using P = Bwd<D>;
+  extern __shared__ float lds[];
+
+  const int nkb = bwd_num_key_blocks(T);
+  const int nqt = num_q_tiles(T);
+  const size_t nblk = (size_t)nqt * (nqt + 1) / 2;
+  const int bh = blockIdx.x % BH;
+  const int kb = blockIdx.x / BH;  // ascending: heaviest key blocks first
+  const int w0 = kBwdKeys * kb;
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6;
+  const int lane = tid & 63;
+  const int q = lane & 31;
+  const int h = lane >> 5;
+
+  float* Qt = lds + w * P::WAVE_FLOATS;
+  float* dOt = Qt + 32 * P::LDQ;
+  float* Wt = dOt + 32 * P::LDQ;
+  float* dSt = Wt + 32 * P::LDW;
+
+  const size_t slice = (size_t)bh * T * D;
+  const int head = bh % H;
+  const float cl2 = head_scale_log2(log_gain, head, D);
+
+  // A operands of S^T = K Q^T (registers) and dP^T = V dY^T (work-group
+  // shared LDS, XOR-swizzled float4 chunks): rows of this block's 64 slots.
+  f32x4* vsl = reinterpret_cast<f32x4*>(lds + 4 * P::WAVE_FLOATS);
+  for (int e = tid; e < 64 * P::C4; e += 256) {
+    const int row = e / P::C4, c = e % P::C4;
+    const int key = w0 - 1 + row;
+    f32x4 vv = {0.f, 0.f, 0.f, 0.f};
+    if (key >= 0 && key < T) vv = reinterpret_cast<const f32x4*>(V + slice + (size_t)key * D)[c];
+    const int half = c / P::CH, cc = c % P::CH;
+    vsl[row * P::C4 + half * P::CH + (cc ^ vswz(row, P::CH))] = vv;
+  }
+  float ka[2][P::DH];
+  int vrow[2];
+  {
+    const int i = lane & 31;
+    const int rsub = ((i >> 3) << 2) | (i & 3);
+    const int hh = (i >> 2) & 1;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      vrow[b] = 32 * hh + 16 * b + rsub;
+      const int key = w0 - 1 + vrow[b];
+      const bool ok = key >= 0 && key < T;
+      const f32x4* kp = reinterpret_cast<const f32x4*>(K + slice + (size_t)(ok ? key : 0) * D + h * P::DH);
+#pragma unroll
+      for (int c = 0; c < P::CH; ++c) {
+        f32x4 kv = ok ? kp[c] : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ka[b][4 * c + e] = kv[e];
+      }
+    }
+  }
+  __syncthreads();
+
+  f32x16 accv[P::NMB][2], acck[P::NMB][2];
+#pragma unroll
+  for (int mb = 0; mb < P::NMB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        accv[mb][nb][r] = 0.f;
+        acck[mb][nb][r] = 0.f;
+      }
+  float gacc = 0.f;
+
+  const int qt0 = w0 / 32;
+  for (int qt = qt0 + w; qt < nqt; qt += 4) {
+    const int i0 = 32 * qt;
+    // ---- stage this wave's Q (pre-scaled) and dY tiles ----
+    for (int e = lane; e < 32 * P::C4; e += 64) {
+      const int row = e / P::C4, c = e % P::C4;
+      const int qi = i0 + row;
+      f32x4 qv = {0.f, 0.f, 0.f, 0.f}, ov = {0.f, 0.f, 0.f, 0.f};
+      if (qi < T) {
+        qv = reinterpret_cast<const f32x4*>(Q + slice + (size_t)qi * D)[c];
+        ov = reinterpret_cast<const f32x4*>(dO + slice + (size_t)qi * D)[c];
+      }
+      qv *= cl2;
+      *reinterpret_cast<f32x4*>(Qt + row * P::LDQ + 4 * c) = qv;
+      *reinterpret_cast<f32x4*>(dOt + row * P::LDQ + 4 * c) = ov;
+    }
+    const int i = i0 + q;
+    const bool qvalid = i < T;
+    float m2 = 0.f, invz = 0.f, dz = 0.f;
+    if (qvalid) {
+      m2 = stats[((size_t)bh * T + i) * 2 + 0];
+      invz = stats[((size_t)bh * T + i) * 2 + 1];
+      dz = dvec[(size_t)bh * T + i] * invz;
+    }
+    wave_lds_sync();
+
+    // ---- S^T and dP^T ----
+    f32x16 sacc[2], pacc[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        sacc[b][r] = 0.f;
+        pacc[b][r] = 0.f;
+      }
+    {
+      const float* qrow = Qt + q * P::LDQ + h * P::DH;
+      const float* orow = dOt + q * P::LDQ + h * P::DH;
+#pragma unroll
+      for (int c = 0; c < P::CH; ++c) {
+        const f32x4 qv = *reinterpret_cast<const f32x4*>(qrow + 4 * c);
+        const f32x4 ov = *reinterpret_cast<const f32x4*>(orow + 4 * c);
+        f32x4 vv[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          vv[b] = vsl[vrow[b] * P::C4 + h * P::CH + (c ^ vswz(vrow[b], P::CH))];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+#pragma unroll
+          for (int b = 0; b < 2; ++b) {
+            sacc[b] = mfma32(ka[b][4 * c + e], qv[e], sacc[b]);
+            pacc[b] = mfma32(vv[b][e], ov[e], pacc[b]);
+          }
+        }
+      }
+    }
+
+    // ---- weights and score gradients of this lane's 32 slots ----
+    // Streams over the slots; W overwrites sacc and dS overwrites pacc in place.
+    const int kbase = w0 - 1 + 32 * h;  // key of register 0
+    const bool need_mask = (w0 == 0) || (w0 + 62 > i0);
+    auto slot_vis = [&](int n) {
+      const int key = kbase + n;
+      return !need_mask || (key >= 0 && key <= i);
+    };
+    // half 1's first segment starts at half 0's last slot
+    float sl, pl, gl;
+    {
+      const bool v31 = slot_vis(31);
+      const float s31 = v31 ? sacc[1][15] : m2;
+      const float g31 = v31 ? fmaf(pacc[1][15], invz, -dz) : 0.f;
+      sl = xhalf(s31);
+      pl = fast_exp2(sl - m2);
+      gl = xhalf(g31);
+    }
+    float r_prev = 0.f, dr_prev = 0.f, xl0 = 0.f, xdl0 = 0.f;
+    // finalises slot n from its own (s,p,g), incoming right share and outgoing left share
+    auto finish = [&](int n, float sv, float pv, float gv, float wv, float dv) {
+      const int key = kbase + n;
+      if (slot_vis(n) && (key == 0 || key == i)) {
+        // half-token caps (first key, last visible key); both when i == 0
+        const float cap = (key == 0 && key == i) ? pv : 0.5f * pv;
+        wv += cap;
+        dv = fmaf(cap, gv, dv);
+      }
+      const int slot = 32 * h + n;
+      const bool owned = slot >= 1 && slot <= 62;
+      dv = owned ? dv : 0.f;
+      gacc = fmaf(dv, sv, gacc);
+      sacc[n >> 4][n & 15] = owned ? wv * invz : 0.f;
+      pacc[n >> 4][n & 15] = dv;
+    };
+#pragma unroll
+    for (int n = 0; n < 32; ++n) {
+      const bool vis = slot_vis(n);
+      const float sr = vis ? sacc[n >> 4][n & 15] : m2;
+      const float gr = vis ? fmaf(pacc[n >> 4][n & 15], invz, -dz) : 0.f;
+      const float pr = fast_exp2(sr - m2);
+      float Lv, Rv, dLv, dRv;
+      seg_shares_grad(sl, sr, pl, pr, gl, gr, Lv, Rv, dLv, dRv);
+      const int key = kbase + n;  // right key of this segment
+      bool ok = (n > 0) || (h == 1);
+      if (need_mask) ok = ok && key >= 1 && key <= i;
+      if (!ok) {
+        Lv = 0.f; Rv = 0.f; dLv = 0.f; dRv = 0.f;
+      }
+      if (n == 0) {
+        xl0 = xhalf(Lv);  // half 1's first left share belongs to half 0's last slot
+        xdl0 = xhalf(dLv);
+      } else {
+        finish(n - 1, sl, pl, gl, r_prev + Lv, dr_prev + dLv);
+      }
+      r_prev = Rv;
+      dr_prev = dRv;
+      sl = sr;
+      pl = pr;
+      gl = gr;
+    }
+    finish(31, sl, pl, gl, r_prev + (h ? 0.f : xl0), dr_prev + (h ? 0.f : xdl0));
+
+    // ---- transpose through LDS ----
+    {
+      float* wrow = Wt + q * P::LDW + 32 * h;
+      float* drow = dSt + q * P::LDW + 32 * h;
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          *reinterpret_cast<f32x4*>(wrow + 16 * b + 4 * c) =
+              f32x4{sacc[b][4 * c], sacc[b][4 * c + 1], sacc[b][4 * c + 2], sacc[b][4 * c + 3]};
+          *reinterpret_cast<f32x4*>(drow + 16 * b + 4 * c) =
+              f32x4{pacc[b][4 * c], pacc[b][4 * c + 1], pacc[b][4 * c + 2], pacc[b][4 * c + 3]};
+        }
+    }
+    wave_lds_sync();
+
+    // ---- dV^T += dY^T W,  dK^T += Q^T dS,  spill dS ----
+#pragma unroll 4
+    for (int r = 0; r < 16; ++r) {
+      const int qr = 16 * h + r;  // query row of the contraction
+      float ado[P::NMB], aq[P::NMB], bw[2], bd[2];
+#pragma unroll
+      for (int mb = 0; mb < P::NMB; ++mb) {
+        const bool dok = 32 * mb + q < D;
+        const int col = dok ? 32 * mb + q : 0;
+        ado[mb] = dok ? dOt[qr * P::LDQ + col] : 0.f;
+        aq[mb] = dok ? Qt[qr * P::LDQ + col] : 0.f;
+      }
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        bw[nb] = Wt[qr * P::LDW + 32 * nb + q];
+        bd[nb] = dSt[qr * P::LDW + 32 * nb + q];
+      }
+#pragma unroll
+      for (int mb = 0; mb < P::NMB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+          accv[mb][nb] = mfma32(ado[mb], bw[nb], accv[mb][nb]);
+          acck[mb][nb] = mfma32(aq[mb], bd[nb], acck[mb][nb]);
+        }
+      const int qi = i0 + qr;
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const int slot = 32 * nb + q;
+        const int key = w0 - 1 + slot;
+        if (slot >= 1 && slot <= 62 && key < T && qi < T && key <= qi) {
+          const size_t off = (((size_t)bh * nblk + tri_block(qi >> 5, key >> 5)) << 10) +
+                             ((qi & 31) << 5) + (key & 31);
+          dsbuf[off] = bd[nb];
+        }
+      }
+    }
+  }
+
+  // ---- reduce the 4 waves' partial dV^T / dK^T through LDS ----
+  __syncthreads();
+  constexpr int NE = P::NMB * 2 * 16;  // accumulator elements per lane per matrix
+  float* redv = lds;
+  float* redk = lds + 4 * NE * 64;
+#pragma unroll
+  for (int mb = 0; mb < P::NMB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int e = (mb * 2 + nb) * 16 + r;
+        redv[(w * NE + e) * 64 + lane] = accv[mb][nb][r];
+        redk[(w * NE + e) * 64 + lane] = acck[mb][nb][r];
+      }
+  const float gw_sum = wave_sum(gacc);
+  __syncthreads();
+  // groups of 4 consecutive d (one float4 store) are split across the waves
+  constexpr int NG = P::NMB * 2 * 4;
+  for (int gi = w; gi < NG; gi += 4) {
+    const int mb = gi / 8, nb = (gi / 4) % 2, r4 = gi % 4;
+    const int slot = 32 * nb + q;
+    const int key = w0 - 1 + slot;
+    const int d0 = 32 * mb + 8 * r4 + 4 * h;
+    f32x4 sv = {0.f, 0.f, 0.f, 0.f}, sk = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww)
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        const int e = (mb * 2 + nb) * 16 + 4 * r4 + e4;
+        sv[e4] += redv[(ww * NE + e) * 64 + lane];
+        sk[e4] += redk[(ww * NE + e) * 64 + lane];
+      }
+    if (slot >= 1 && slot <= 62 && key < T && d0 < D) {
+      *reinterpret_cast<f32x4*>(dV + slice + (size_t)key * D + d0) = sv;
+      *reinterpret_cast<f32x4*>(dK + slice + (size_t)key * D + d0) = sk * kLn2;
+    }
+  }
+  __syncthreads();
+  if (lane == 0) lds[w] = gw_sum;
+  __syncthreads();
+  if (tid == 0) gain_part[(size_t)bh * nkb + kb] = (lds[0] + lds[1] + lds[2] + lds[3]) * kLn2;
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict__ dsbuf,
+                                                        const float* __restrict__ K,
+                                                        const float* __restrict__ log_gain,
+                                                        float* __restrict__ dQ, int BH, int H,
+                                                        int T) {
+  using P = Bwd<D>;
+  __shared__ float red[4 * P::NMB * 16 * 64];
+  const int nqt = num_q_tiles(T);
+  const size_t nblk = (size_t)nqt * (nqt + 1) / 2;
+  const int bh = blockIdx.x % BH;
+  const int qt = nqt - 1 - blockIdx.x / BH;  // heaviest (longest rows) first
+  const int i0 = 32 * qt;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, q = lane & 31, h = lane >> 5;
+  const size_t slice = (size_t)bh * T * D;
+  const float c = head_scale_log2(log_gain, bh % H, D) * kLn2;
+
+  f32x16 acc[P::NMB];
+#pragma unroll
+  for (int nb = 0; nb < P::NMB; ++nb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[nb][r] = 0.f;
+
+  const int i = i0 + q;
+  for (int kt = w; kt <= qt; kt += 4) {
+    const float* blk = dsbuf + (((size_t)bh * nblk + tri_block(qt, kt)) << 10);
+    const f32x4* arow = reinterpret_cast<const f32x4*>(blk + (q << 5) + 16 * h);
+    float a[16];
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) {
+      const f32x4 v4 = arow[c4];
+      a[4 * c4 + 0] = v4[0]; a[4 * c4 + 1] = v4[1]; a[4 * c4 + 2] = v4[2]; a[4 * c4 + 3] = v4[3];
+    }
+    const int kbase = 32 * kt + 16 * h;
+    if (kt == qt || i >= T) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) a[r] = (kbase + r <= i && i < T) ? a[r] : 0.f;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = kbase + r;
+#pragma unroll
+      for (int nb = 0; nb < P::NMB; ++nb) {
+        const bool ok = key < T && (32 * nb + q) < D;
+        const float b = ok ? K[slice + (size_t)key * D + 32 * nb + q] : 0.f;
+        acc[nb] = mfma32(a[r], b, acc[nb]);
+      }
+    }
+  }
+#pragma unroll
+  for (int nb = 0; nb < P::NMB; ++nb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[((w * P::NMB + nb) * 16 + r) * 64 + lane] = acc[nb][r];
+  __syncthreads();
+  // wave w finalises registers r with r % 4 == w
+  for (int nb = 0; nb < P::NMB; ++nb)
+    for (int r = w; r < 16; r += 4) {
+      float sum = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < 4; ++ww) sum += red[((ww * P::NMB + nb) * 16 + r) * 64 + lane];
+      const int row = i0 + 8 * (r >> 2) + 4 * h + (r & 3);
+      const int d = 32 * nb + q;
+      if (row < T && d < D) dQ[slice + (size_t)row * D + d] = sum * c;
+    }
+}
+
+__global__ void ca_bwd_gain_kernel(const float* __restrict__ gain_part,
+                                   float* __restrict__ dlog_gain, int B, int H, int nkb) {
+  const int h = blockIdx.x * blockDim.x + threadIdx.x;
+  if (h >= H) return;
+  float s = 0.f;
+  for (int b = 0; b < B; ++b)
+    for (int k = 0; k < nkb; ++k) s += gain_part[((size_t)b * H + h) * nkb + k];
+  dlog_gain[h] = s;
+}
+
+template <int D>
+hipError_t launch_bwd(const float* q, const float* k, const float* v, const float* log_gain,
+                      const float* o, const float* stats, const float* dout, float* dq, float* dk,
+                      float* dv, float* dlog_gain, float* dsbuf, float* dvec, float* gain_part,
+                      int B, int H, int T, hipStream_t stream) {
+  using P = Bwd<D>;
+  const int BH = B * H;
+  const int rows = BH * T;
+  timer_begin(kBwdRowdot, stream);
+  hipLaunchKernelGGL(ca_bwd_rowdot_kernel, dim3((rows + 3) / 4), dim3(256), 0, stream, dout, o,
+                     dvec, rows, D);
+  timer_end(kBwdRowdot, stream);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const size_t lds_bytes = sizeof(float) * P::LDS_FLOATS;
+  const int nkb = bwd_num_key_blocks(T);
+  timer_begin(kBwdDkdv, stream);
+  hipLaunchKernelGGL(ca_bwd_dkdv_kernel<D>, dim3(nkb * BH), dim3(256), lds_bytes, stream, q, k,
+                     v, dout, stats, dvec, log_gain, dk, dv, dsbuf, gain_part, BH, H, T);
+  timer_end(kBwdDkdv, stream);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  timer_begin(kBwdDq, stream);
+  hipLaunchKernelGGL(ca_bwd_dq_kernel<D>, dim3(num_q_tiles(T) * BH), dim3(256), 0, stream, dsbuf,
+                     k, log_gain, dq, BH, H, T);
+  timer_end(kBwdDq, stream);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  timer_begin(kBwdGain, stream);
+  hipLaunchKernelGGL(ca_bwd_gain_kernel, dim3((H + 63) / 64), dim3(64), 0, stream, gain_part,
+                     dlog_gain, B, H, nkb);
+  timer_end(kBwdGain, stream);
+  return hipGetLastError();
+}
+
+template <int D>
+hipError_t set_bwd_attrs() {
+  using P = Bwd<D>;
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(&ca_bwd_dkdv_kernel<D>),
+                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)(sizeof(float) * P::LDS_FLOATS));
+}
+
+template hipError_t set_bwd_attrs<8>();
+template hipError_t set_bwd_attrs<16>();
+template hipError_t set_bwd_attrs<32>();
+template hipError_t set_bwd_attrs<64>();
+
+#define CA_INST_BWD(DD)                                                                        \
+  template hipError_t launch_bwd<DD>(const float*, const float*, const float*, const float*,   \
+                                     const float*, const float*, const float*, float*, float*, \
+                                     float*, float*, float*, float*, float*, int, int, int,    \
+                                     hipStream_t);
+CA_INST_BWD(8)
+CA_INST_BWD(16)
+CA_INST_BWD(32)
+CA_INST_BWD(64)
+
+}  // namespace ca

@@ -1,0 +1,413 @@
+// Continuum Attention forward (gfx950, fp32 MFMA).
+//
+// Replaces, for the forward pass, the per-query-tile loop of
+// _CAExactTiled.forward (cuda/continuum_attention.py:650-694): the QK^T bmm,
+// the weight kernel (ca_weights_kernel / ca_forward_half_kernel,
+// cuda/continuum_attention.py:136-163,300-328) and the W.V bmm, fused so that
+// neither scores nor weights leave registers.
+//
+// Work item: one 128-query group (4 waves x 32 queries) of one (b,h) slice and
+// one contiguous range ("split") of 32-key weight tiles.  The 4 waves share
+// double-buffered K/V tiles in LDS.  Items are launched heaviest-first; groups
+// whose key range spans several splits write un-normalised partials that
+// ca_fwd_combine merges (log-sum-exp style; deterministic order).
+//
+// Per wave, the S^T = K Q^T tile (32 keys x 32 queries) is computed with
+// v_mfma_f32_32x32x2_f32 with keys permuted so that lane (q, h) holds 16
+// consecutive keys of query q.  Segment neighbours are then in the same
+// lane; only the segment crossing the two lane halves needs permlane32_swap.
+//
+// Weight tile t covers weight keys [32t, 32t+32); its score tile covers keys
+// [32t+1, 32t+33).  Lane half h, register n: score key 32t+1+16h+n, weight
+// key 32t+16h+n.  The segment ending at score key k gives its left share to
+// weight key k-1 (same register) and its right share to weight key k (next
+// register; carried across halves / tiles).
+#include "ca_common.h"
+#include "ca_kernels.h"
+
+namespace ca {
+
+template <int D>
+struct Fwd {
+  static constexpr int DH = D / 2;            // d values per lane half in the S^T operand
+  static constexpr int NMB = (D + 31) / 32;   // 32-row d blocks of O^T
+  static constexpr int C4 = D / 4;            // float4 chunks per row
+  static constexpr int CH = DH / 4;           // float4 chunks per lane half
+  static constexpr int TILE_F4 = 32 * C4;     // float4 per 32-row tile
+  static constexpr int LD_PER_THREAD = (TILE_F4 + 255) / 256;
+};
+
+// XOR swizzle of the K tile's float4 chunks (conflict-free A-operand reads
+// for the permuted key order; see key_of_arow).
+__device__ __forceinline__ int kswz(int row, int chunks_per_half) {
+  return ((row & 3) | ((row >> 2) & 4)) & (chunks_per_half - 1);
+}
+
+// Item decoding: items are (group g, split s) in descending g, then s.
+__device__ __forceinline__ void fwd_decode_item(int item, int G, int T, int C, int& g, int& s,
+                                                int& nsplit) {
+  const int ntiles_all = (T + 31) / 32;
+  for (int gg = G - 1; gg >= 0; --gg) {
+    int nt = min(4 * gg + 4, ntiles_all);
+    int ns = (nt + C - 1) / C;
+    if (item < ns) {
+      g = gg;
+      s = item;
+      nsplit = ns;
+      return;
+    }
+    item -= ns;
+  }
+  g = -1; s = 0; nsplit = 0;
+}
+
+template <int D>
+__device__ __forceinline__ float halo_dot(const float* qreg, const float* __restrict__ krow) {
+  constexpr int DH = D / 2;
+  const int h = (threadIdx.x >> 5) & 1;
+  const f32x4* kp = reinterpret_cast<const f32x4*>(krow + h * DH);
+  float acc = 0.0f;
+#pragma unroll
+  for (int c = 0; c < DH / 4; ++c) {
+    f32x4 kv = kp[c];
+    acc = fmaf(qreg[4 * c + 0], kv[0], acc);
+    acc = fmaf(qreg[4 * c + 1], kv[1], acc);
+    acc = fmaf(qreg[4 * c + 2], kv[2], acc);
+    acc = fmaf(qreg[4 * c + 3], kv[3], acc);
+  }
+  return acc + xhalf(acc);
+}
+
+template <int D>
+__global__ __launch_bounds__(256, 2) void ca_fwd_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    const float* __restrict__ log_gain, float* __restrict__ O, float* __restrict__ stats,
+    float* __restrict__ part, int BH, int H, int T, int C, int G, int smax) {
+  using P = Fwd<D>;
+  __shared__ f32x4 lds_k[2][P::TILE_F4];
+  __shared__ float lds_v[2][32 * D];
+
+  const int bh = blockIdx.x % BH;
+  const int item = blockIdx.x / BH;
+  int g, split, nsplit;
+  fwd_decode_item(item, G, T, C, g, split, nsplit);
+  if (g < 0) return;
+
+  const int ntiles_all = (T + 31) / 32;
+  const int nt = min(4 * g + 4, ntiles_all);
+  const int t_b = split * C;
+  const int t_e = min(nt, t_b + C);
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6;
+  const int lane = tid & 63;
+  const int q = lane & 31;
+  const int h = lane >> 5;
+  const int i = 128 * g + 32 * w + q;  // this lane's query
+  const bool qvalid = i < T;
+  const int wave_tmax = 4 * g + w;      // diagonal tile of this wave
+  const bool wave_active = (128 * g + 32 * w < T) && (t_b <= wave_tmax);
+
+  const size_t slice = (size_t)bh * T * D;
+  const float* Qs = Q + slice;
+  const float* Ks = K + slice;
+  const float* Vs = V + slice;
+  const int head = bh % H;
+  const float cl2 = head_scale_log2(log_gain, head, D);
+
+  // B operand of S^T: lane (q,h) holds Q[i][h*DH + k] * c*log2e
+  float qreg[P::DH];
+  {
+    const f32x4* qp = reinterpret_cast<const f32x4*>(Qs + (size_t)(qvalid ? i : 0) * D + h * P::DH);
+#pragma unroll
+    for (int c = 0; c < P::CH; ++c) {
+      f32x4 v4 = qvalid ? qp[c] : f32x4{0.f, 0.f, 0.f, 0.f};
+      qreg[4 * c + 0] = v4[0] * cl2;
+      qreg[4 * c + 1] = v4[1] * cl2;
+      qreg[4 * c + 2] = v4[2] * cl2;
+      qreg[4 * c + 3] = v4[3] * cl2;
+    }
+  }
+
+  // ---- split-start state -------------------------------------------------
+  float m_ref = 0.f, s_carry = 0.f, r_carry = 0.f, zsum = 0.f;
+  if (wave_active) {
+    if (t_b == 0) {
+      s_carry = halo_dot<D>(qreg, Ks);
+      m_ref = s_carry;
+    } else {
+      const int k0 = 32 * t_b;  // <= first query of this wave, so both halo keys are visible
+      s_carry = halo_dot<D>(qreg, Ks + (size_t)k0 * D);
+      const float s_prev = halo_dot<D>(qreg, Ks + (size_t)(k0 - 1) * D);
+      m_ref = fmaxf(s_carry, s_prev);
+      float l_unused;
+      seg_shares(s_prev, s_carry, fast_exp2(s_prev - m_ref), fast_exp2(s_carry - m_ref), l_unused,
+                 r_carry);
+    }
+  }
+
+  f32x16 acc_o[P::NMB];
+#pragma unroll
+  for (int mb = 0; mb < P::NMB; ++mb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc_o[mb][r] = 0.f;
+
+  // ---- cooperative tile loads ------------------------------------------
+  f32x4 pre_k[P::LD_PER_THREAD], pre_v[P::LD_PER_THREAD];
+  auto load_tile = [&](int t) {
+#pragma unroll
+    for (int j = 0; j < P::LD_PER_THREAD; ++j) {
+      const int e = tid + 256 * j;
+      f32x4 kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
+      if (e < P::TILE_F4) {
+        const int row = e / P::C4, c = e % P::C4;
+        const int kk = 32 * t + 1 + row;  // score key
+        const int vk = 32 * t + row;      // weight key
+        if (kk < T) kv = reinterpret_cast<const f32x4*>(Ks + (size_t)kk * D)[c];
+        if (vk < T) vv = reinterpret_cast<const f32x4*>(Vs + (size_t)vk * D)[c];
+      }
+      pre_k[j] = kv;
+      pre_v[j] = vv;
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < P::LD_PER_THREAD; ++j) {
+      const int e = tid + 256 * j;
+      if (e < P::TILE_F4) {
+        const int row = e / P::C4, c = e % P::C4;
+        const int half = c / P::CH, cc = c % P::CH;
+        lds_k[buf][row * P::C4 + half * P::CH + (cc ^ kswz(row, P::CH))] = pre_k[j];
+        reinterpret_cast<f32x4*>(&lds_v[buf][0])[e] = pre_v[j];
+      }
+    }
+  };
+
+  load_tile(t_b);
+  store_tile(0);
+  __syncthreads();
+
+  const int arow = key_of_arow(lane);  // K-tile row this lane feeds to the A operand
+
+  for (int t = t_b; t < t_e; ++t) {
+    const int buf = (t - t_b) & 1;
+    if (t + 1 < t_e) load_tile(t + 1);
+
+    if (wave_active && t <= wave_tmax) {
+      const bool diag = (t == wave_tmax);
+      // ---- S^T = K Q^T (log2 units) ----
+      f32x16 sacc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
+      {
+        const f32x4* krow = &lds_k[buf][arow * P::C4 + h * P::CH];
+#pragma unroll
+        for (int c = 0; c < P::CH; ++c) {
+          f32x4 kv = krow[c ^ kswz(arow, P::CH)];
+          sacc = mfma32(kv[0], qreg[4 * c + 0], sacc);
+          sacc = mfma32(kv[1], qreg[4 * c + 1], sacc);
+          sacc = mfma32(kv[2], qreg[4 * c + 2], sacc);
+          sacc = mfma32(kv[3], qreg[4 * c + 3], sacc);
+        }
+      }
+      const int kbase = 32 * t + 1 + 16 * h;  // score key of register 0
+      // ---- row max of the tile (visible keys only) ----
+      float mt = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const bool vis = !diag || (kbase + r <= i);
+        mt = fmaxf(mt, vis ? sacc[r] : -INFINITY);
+      }
+      mt = fmaxf(mt, xhalf(mt));
+      // Lazy rescale, decided per query: a lane whose own max did not grow
+      // keeps its shift and multiplies by exactly 1, so no query's rounding
+      // depends on other (possibly later) queries of the wave.
+      const bool grow = mt > m_ref + kLazyRescale;
+      if (wave_any(grow)) {
+        const float m_new = grow ? mt : m_ref;
+        const float alpha = grow ? fast_exp2(m_ref - m_new) : 1.0f;
+#pragma unroll
+        for (int mb = 0; mb < P::NMB; ++mb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc_o[mb][r] *= alpha;
+        zsum *= alpha;
+        r_carry *= alpha;
+        m_ref = m_new;
+      }
+      if (diag) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[r] = (kbase + r <= i) ? sacc[r] : m_ref;
+      }
+      // ---- left neighbour of register 0, and carries ----
+      const float xs15 = xhalf(sacc[15]);
+      float sl = h ? xs15 : s_carry;
+      s_carry = xs15;  // next tile, half 0: score key 32t+32
+      float pl = fast_exp2(sl - m_ref);
+
+      // ---- stream over segments; weights overwrite sacc in place ----
+      // weight register r (weight key kbase-1+r) = left share of segment r
+      // + right share of segment r-1 (+ caps); register 0's incoming right
+      // share is added after the loop.
+      float r_prev = 0.f, zt = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float sr = sacc[r];
+        const float pr = fast_exp2(sr - m_ref);
+        float Lv, Rv;
+        seg_shares(sl, sr, pl, pr, Lv, Rv);
+        if (diag && (kbase + r > i)) {
+          Lv = 0.f;
+          Rv = 0.f;
+        }
+        float x = Lv + r_prev;
+        const int wk = kbase - 1 + r;  // weight key, its score is sl
+        if (diag && wk == i) x = fmaf(0.5f, pl, x);  // last half-token cap
+        if (wk == 0) x = fmaf(0.5f, pl, x);           // first half-token cap
+        sacc[r] = x;
+        zt += x;
+        r_prev = Rv;
+        sl = sr;
+        pl = pr;
+      }
+      const float xr15 = xhalf(r_prev);
+      const float r_in = h ? xr15 : r_carry;
+      r_carry = xr15;
+      sacc[0] += r_in;
+      zsum += zt + r_in;
+
+      // ---- O^T += V^T W^T ----
+      const bool dok = q < D;  // only D < 32 pads the d block
+      const float* vcol = &lds_v[buf][(16 * h) * D + (dok ? q : 0)];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+#pragma unroll
+        for (int mb = 0; mb < P::NMB; ++mb) {
+          const float a = dok ? vcol[r * D + 32 * mb] : 0.f;
+          acc_o[mb] = mfma32(a, sacc[r], acc_o[mb]);
+        }
+      }
+    }
+
+    if (t + 1 < t_e) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue ----
+  if (128 * g + 32 * w >= T) return;
+  const float ztot = zsum + xhalf(zsum);
+  const bool single = (nsplit == 1);
+  float* dst;
+  float scl;
+  if (single) {
+    dst = O + slice + (size_t)i * D;
+    scl = 1.0f / ztot;
+  } else {
+    // part layout: [BH][smax][T][D] outputs then [BH][smax][T][2] (m, Z)
+    dst = part + (((size_t)bh * smax + split) * T + i) * D;
+    scl = 1.0f;
+  }
+  if (!wave_active) {
+    // this wave's queries see none of this split's keys: empty partial
+    if (qvalid) {
+      for (int d = h; d < D; d += 2) dst[d] = 0.f;
+      if (h == 0) {
+        float* mz = part + (size_t)BH * smax * T * D + (((size_t)bh * smax + split) * T + i) * 2;
+        mz[0] = -1e30f;
+        mz[1] = 0.f;
+      }
+    }
+    return;
+  }
+  if (!qvalid) return;
+#pragma unroll
+  for (int mb = 0; mb < P::NMB; ++mb) {
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int d0 = 32 * mb + 8 * r4 + 4 * h;
+      if (d0 < D) {
+        f32x4 v4 = {acc_o[mb][4 * r4 + 0] * scl, acc_o[mb][4 * r4 + 1] * scl,
+                    acc_o[mb][4 * r4 + 2] * scl, acc_o[mb][4 * r4 + 3] * scl};
+        *reinterpret_cast<f32x4*>(dst + d0) = v4;
+      }
+    }
+  }
+  if (h == 0) {
+    if (single) {
+      stats[((size_t)bh * T + i) * 2 + 0] = m_ref;
+      stats[((size_t)bh * T + i) * 2 + 1] = scl;
+    } else {
+      float* mz = part + (size_t)BH * smax * T * D + (((size_t)bh * smax + split) * T + i) * 2;
+      mz[0] = m_ref;
+      mz[1] = ztot;
+    }
+  }
+}
+
+// Merges split partials of rows whose group spans more than one split.
+template <int D>
+__global__ __launch_bounds__(256) void ca_fwd_combine_kernel(const float* __restrict__ part,
+                                                             float* __restrict__ O,
+                                                             float* __restrict__ stats, int BH,
+                                                             int T, int C, int smax) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);  // one wave per row
+  const int lane = threadIdx.x & 63;
+  if (row >= BH * T) return;
+  const int bh = row / T, i = row % T;
+  const int g = i / 128;
+  const int ntiles_all = (T + 31) / 32;
+  const int nt = min(4 * g + 4, ntiles_all);
+  const int ns = (nt + C - 1) / C;
+  if (ns <= 1) return;
+  const float* mz = part + (size_t)BH * smax * T * D;
+  float M = -INFINITY;
+  for (int s = 0; s < ns; ++s) M = fmaxf(M, mz[(((size_t)bh * smax + s) * T + i) * 2]);
+  float Z = 0.f, acc = 0.f;
+  for (int s = 0; s < ns; ++s) {
+    const size_t base = ((size_t)bh * smax + s) * T + i;
+    const float f = fast_exp2(mz[base * 2] - M);
+    Z = fmaf(mz[base * 2 + 1], f, Z);
+    if (lane < D) acc = fmaf(part[base * D + lane], f, acc);
+  }
+  const float invz = 1.0f / Z;
+  if (lane < D) O[(size_t)row * D + lane] = acc * invz;
+  if (lane == 0) {
+    stats[(size_t)row * 2 + 0] = M;
+    stats[(size_t)row * 2 + 1] = invz;
+  }
+}
+
+template <int D>
+hipError_t launch_fwd(const float* q, const float* k, const float* v, const float* log_gain,
+                      float* o, float* stats, float* part, int B, int H, int T, int C,
+                      hipStream_t stream) {
+  const int BH = B * H;
+  const int G = (T + 127) / 128;
+  const int smax = fwd_max_splits(T, C);
+  const int items = fwd_num_items(T, C);
+  timer_begin(kFwd, stream);
+  hipLaunchKernelGGL(ca_fwd_kernel<D>, dim3(items * BH), dim3(256), 0, stream, q, k, v, log_gain,
+                     o, stats, part, BH, H, T, C, G, smax);
+  timer_end(kFwd, stream);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (smax > 1) {
+    const int rows = BH * T;
+    timer_begin(kFwdCombine, stream);
+    hipLaunchKernelGGL(ca_fwd_combine_kernel<D>, dim3((rows + 3) / 4), dim3(256), 0, stream, part,
+                       o, stats, BH, T, C, smax);
+    timer_end(kFwdCombine, stream);
+    e = hipGetLastError();
+  }
+  return e;
+}
+
+template hipError_t launch_fwd<8>(const float*, const float*, const float*, const float*, float*,
+                                  float*, float*, int, int, int, int, hipStream_t);
+template hipError_t launch_fwd<16>(const float*, const float*, const float*, const float*, float*,
+                                   float*, float*, int, int, int, int, hipStream_t);
+template hipError_t launch_fwd<32>(const float*, const float*, const float*, const float*, float*,
+                                   float*, float*, int, int, int, int, hipStream_t);
+template hipError_t launch_fwd<64>(const float*, const float*, const float*, const float*, float*,
+                                   float*, float*, int, int, int, int, hipStream_t);
+
+}  // namespace ca

@@ -1,0 +1,55 @@
+// Internal launch interface between the C ABI (ca_abi.hip) and the kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+
+namespace ca {
+
+// Forward work decomposition: 128-query groups, 32-key weight tiles, splits of
+// at most C tiles per work item.
+inline int fwd_group_tiles(int g, int T) {
+  const int all = (T + 31) / 32;
+  return (4 * g + 4 < all) ? 4 * g + 4 : all;
+}
+inline int fwd_max_splits(int T, int C) {
+  const int G = (T + 127) / 128;
+  return (fwd_group_tiles(G - 1, T) + C - 1) / C;
+}
+inline int fwd_num_items(int T, int C) {
+  const int G = (T + 127) / 128;
+  int n = 0;
+  for (int g = 0; g < G; ++g) n += (fwd_group_tiles(g, T) + C - 1) / C;
+  return n;
+}
+inline size_t fwd_part_floats(int BH, int T, int C) {
+  const int smax = fwd_max_splits(T, C);
+  if (smax <= 1) return 0;
+  return (size_t)BH * smax * T * 66;  // D <= 64 outputs + (m, Z); sized for the largest D
+}
+
+// Backward: key blocks owned by one dK/dV work group.
+constexpr int kBwdKeys = 62;
+__host__ __device__ inline int bwd_num_key_blocks(int T) { return (T + kBwdKeys - 1) / kBwdKeys; }
+__host__ __device__ inline int num_q_tiles(int T) { return (T + 31) / 32; }
+inline size_t bwd_ds_floats(int BH, int T) {
+  const size_t n = num_q_tiles(T);
+  return (size_t)BH * (n * (n + 1) / 2) * 1024;
+}
+
+// Per-kernel HIP-event timing (diagnostics; off unless ca_timing_enable(1)).
+enum KernelId { kFwd = 0, kFwdCombine, kBwdRowdot, kBwdDkdv, kBwdDq, kBwdGain, kNumKernels };
+void timer_begin(int id, hipStream_t s);
+void timer_end(int id, hipStream_t s);
+
+template <int D>
+hipError_t launch_fwd(const float* q, const float* k, const float* v, const float* log_gain,
+                      float* o, float* stats, float* part, int B, int H, int T, int C,
+                      hipStream_t stream);
+
+template <int D>
+hipError_t launch_bwd(const float* q, const float* k, const float* v, const float* log_gain,
+                      const float* o, const float* stats, const float* dout, float* dq, float* dk,
+                      float* dv, float* dlog_gain, float* dsbuf, float* dvec, float* gain_part,
+                      int B, int H, int T, hipStream_t stream);
+
+}  // namespace ca

@@ -1,0 +1,87 @@
+/* C ABI of the MI355X-native Continuum Attention operator (libca_hip.so).
+ *
+ * Plain pointers, sizes and an opaque HIP stream handle; no torch or HIP types
+ * in the signatures.  All tensors are float32, contiguous, device-resident,
+ * laid out [B, H, T, D] (row-major, D fastest).  The caller allocates every
+ * output and workspace; the library allocates nothing.  Every call is
+ * asynchronous on `stream` (NULL = the default stream) and returns CA_OK or an
+ * error code whose text ca_last_error() returns (thread-local).
+ *
+ * This library replaces the native half of the reference operator
+ * (akhadangi/continuum-attention):
+ *   - the pybind extension built by _ca_cuda_extension
+ *     (cuda/continuum_attention.py:35-63, 608-620), and
+ *   - the per-query-tile bmm + kernel loops of _CAExactTiled.forward/backward
+ *     (cuda/continuum_attention.py:650-766),
+ * behind the same Python entry point continuum_attention(q,k,v,log_gain,
+ * query_tile) (cuda/continuum_attention.py:768-783).
+ */
+#ifndef CONTINUUM_ATTENTION_AMD_H
+#define CONTINUUM_ATTENTION_AMD_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CA_ABI_VERSION 1
+
+enum {
+  CA_OK = 0,
+  CA_ERR_INVALID = 1,     /* bad pointer, alignment or shape */
+  CA_ERR_UNSUPPORTED = 2, /* head dim or size outside the kernels' range */
+  CA_ERR_WORKSPACE = 3,   /* workspace missing or too small */
+  CA_ERR_HIP = 4          /* a HIP launch or runtime call failed */
+};
+
+/* Version of this ABI (CA_ABI_VERSION). */
+int ca_abi_version(void);
+
+/* Text of the last error raised on the calling thread ("" if none). */
+const char* ca_last_error(void);
+
+/* Bytes of device workspace ca_fwd_f32 needs for this shape (may be 0). */
+size_t ca_fwd_workspace_bytes(int B, int H, int T, int D);
+
+/* Forward: out = W(S) v with S = exp(log_gain[h]) / sqrt(D) * q k^T, exact CA
+ * weights W (segment moments, half-token caps, causal).  Also writes per-row
+ * statistics stats[B*H*T][2] = (row shift in log2 units, 1/Z) that
+ * ca_bwd_f32 consumes.  log_gain has H entries.  D in {8, 16, 32, 64}.
+ * Replaces: _CAExactTiled.forward (cuda/continuum_attention.py:651-694) with
+ * ext.forward / ext.forward_half / ext.direct_output
+ * (cuda/continuum_attention.py:460-471, 556-590). */
+int ca_fwd_f32(const float* q, const float* k, const float* v, const float* log_gain, float* out,
+               float* stats, void* workspace, size_t workspace_bytes, int B, int H, int T, int D,
+               void* stream);
+
+/* Bytes of device workspace ca_bwd_f32 needs for this shape. */
+size_t ca_bwd_workspace_bytes(int B, int H, int T, int D);
+
+/* Backward (first order): given dout = dL/dout, writes dq, dk, dv ([B,H,T,D])
+ * and dlog_gain[H] = sum dS * S.  out and stats must come from ca_fwd_f32 on
+ * the same inputs.
+ * Replaces: _CAExactTiled.backward (cuda/continuum_attention.py:697-766) with
+ * ext.backward_fused / ext.backward_half(_gw16) / ext.backward
+ * (cuda/continuum_attention.py:487-554, 592-605). */
+int ca_bwd_f32(const float* q, const float* k, const float* v, const float* log_gain,
+               const float* out, const float* stats, const float* dout, float* dq, float* dk,
+               float* dv, float* dlog_gain, void* workspace, size_t workspace_bytes, int B, int H,
+               int T, int D, void* stream);
+
+/* ---- Diagnostics (no counterpart in the reference; used by bench.py) -------
+ * Per-kernel timing with HIP events recorded on the launch stream around each
+ * kernel launch of the calls above.  Kernel ids: 0 forward, 1 forward split
+ * combine, 2 backward row dot, 3 backward dK/dV, 4 backward dQ, 5 backward
+ * gain reduction.  ca_timing_enable(on) turns recording on/off and discards
+ * unread records; ca_timing_read waits for the recorded events and returns the
+ * summed milliseconds and launch counts per id (n entries), then clears them.
+ * Not thread-safe; meant for single-threaded benchmarking. */
+int ca_timing_enable(int on);
+int ca_timing_read(double* total_ms, int* launches, int n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CONTINUUM_ATTENTION_AMD_H */

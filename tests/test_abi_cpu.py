@@ -1,0 +1,100 @@
+"""CPU-only checks of the drop-in boundary: the C-ABI library loads, exports
+every symbol its header declares, validates arguments before touching the GPU,
+and the Python operator keeps the reference's error contract.
+
+No test here launches a kernel (this container has no GPU).
+"""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "continuum_attention_amd.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ca_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_expected_entry_points():
+    names = header_functions()
+    for n in ("ca_fwd_f32", "ca_bwd_f32", "ca_fwd_workspace_bytes", "ca_bwd_workspace_bytes",
+              "ca_last_error", "ca_abi_version"):
+        assert n in names
+
+
+def test_library_exports_every_header_symbol(ca):
+    lib = ca.native.load()
+    for name in header_functions():
+        assert hasattr(lib, name), name
+        assert name in ca.native.SIGNATURES, name
+    assert lib.ca_abi_version() == ca.native.ABI_VERSION
+
+
+def test_workspace_sizes(ca):
+    lib = ca.native.load()
+    # one 128-query group fits one forward split: no partials needed
+    assert lib.ca_fwd_workspace_bytes(2, 16, 512, 64) == 0
+    assert lib.ca_fwd_workspace_bytes(2, 16, 2048, 64) > 0
+    nqt = 2048 // 32
+    ds_bytes = 2 * 16 * (nqt * (nqt + 1) // 2) * 1024 * 4
+    assert lib.ca_bwd_workspace_bytes(2, 16, 2048, 64) >= ds_bytes + 2 * 16 * 2048 * 4
+    assert lib.ca_bwd_workspace_bytes(0, 1, 1, 64) == 0
+
+
+@pytest.mark.parametrize("shape,code", [((0, 1, 8, 64), 1), ((1, 1, 0, 64), 1),
+                                        ((1, 1, 8, 128), 2), ((1, 1, 8, 24), 2)])
+def test_argument_errors_before_any_launch(ca, shape, code):
+    lib = ca.native.load()
+    p = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    rc = lib.ca_fwd_f32(p, p, p, p, p, p, None, 0, *shape, None)
+    assert rc == code
+    assert lib.ca_last_error().decode()
+    rc = lib.ca_bwd_f32(p, p, p, p, p, p, p, p, p, p, p, None, 0, *shape, None)
+    assert rc == code
+
+
+def test_null_misaligned_and_workspace_errors(ca):
+    lib = ca.native.load()
+    p = ctypes.c_void_p(4096)
+    assert lib.ca_fwd_f32(None, p, p, p, p, p, None, 0, 1, 1, 8, 64, None) == 1
+    assert b"null" in lib.ca_last_error()
+    odd = ctypes.c_void_p(4100)
+    assert lib.ca_fwd_f32(odd, p, p, p, p, p, None, 0, 1, 1, 8, 64, None) == 1
+    assert b"aligned" in lib.ca_last_error()
+    need = lib.ca_fwd_workspace_bytes(1, 1, 4096, 64)
+    assert need > 0
+    assert lib.ca_fwd_f32(p, p, p, p, p, p, p, need - 1, 1, 1, 4096, 64, None) == 3
+    assert b"workspace" in lib.ca_last_error()
+    assert lib.ca_bwd_f32(p, p, p, p, p, p, p, p, p, p, p, p, 16, 1, 1, 64, 64, None) == 3
+
+
+def test_python_errors_follow_reference_contract(ca, monkeypatch):
+    q = torch.zeros(1, 1, 4, 16)
+    with pytest.raises(ValueError, match="must share dtype"):
+        ca.continuum_attention(q, q.double(), q, torch.zeros(1))
+    monkeypatch.setenv("CA_CUDA_MODE", "bogus")
+    with pytest.raises(ValueError, match="CA_CUDA_MODE"):
+        ca.continuum_attention(q, q, q, torch.zeros(1))
+    monkeypatch.setenv("CA_CUDA_MODE", "prefix_v6")
+    # no CPU path: CPU tensors are rejected loudly instead of falling back
+    with pytest.raises(RuntimeError, match="ROCm GPU tensors only"):
+        ca.continuum_attention(q, q, q, torch.zeros(1))
+    with pytest.raises(ValueError, match="query_tile"):
+        ca.continuum_attention(q, q, q, torch.zeros(1), 0)
+
+
+def test_package_does_not_import_the_oracle():
+    pkg = os.path.join(ROOT, "continuum-attention_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".h", ".cpp")):
+                src = open(os.path.join(dirpath, f)).read()
+                src = re.sub(r'""".*?"""', "", src, flags=re.S)
+                src = re.sub(r"#.*|//.*", "", src)
+                assert "oracle" not in src, f

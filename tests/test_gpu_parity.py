@@ -1,0 +1,212 @@
+"""GPU parity of the HIP operator against the float64 oracle (oracle/ca_oracle.py).
+
+Bar: max relative error max|x-ref|/max|ref| <= 1e-4
+on outputs and <= 1e-3 on gradients (dq, dk, dv, dlog_gain); exact causality
+(outputs bitwise unchanged, future gradients exactly 0).  Every call goes
+through the C ABI (libca_hip.so via ctypes) behind continuum_attention().
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ca_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+OUT_TOL = 1e-4
+GRAD_TOL = 1e-3
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def rel(a, b):
+    a = np.asarray(a, np.float64); b = np.asarray(b, np.float64)
+    den = np.abs(b).max()
+    return float(np.abs(a - b).max() / (den if den > 0 else 1.0))
+
+
+def make_inputs(shape, seed, mag=1.0, gains=None, dev="cuda"):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(shape, generator=g) * mag
+    k = torch.randn(shape, generator=g) * mag
+    v = torch.randn(shape, generator=g)
+    dy = torch.randn(shape, generator=g)
+    H = shape[1]
+    rho = torch.zeros(H) if gains is None else torch.tensor(gains, dtype=torch.float32)
+    return q, k, v, rho, dy
+
+
+def run_hip(ca, q, k, v, rho, dy, tile=64):
+    qd, kd, vd, rd = (x.cuda().requires_grad_(True) for x in (q, k, v, rho))
+    y = ca.continuum_attention(qd, kd, vd, rd, tile)
+    grads = torch.autograd.grad((y * dy.cuda()).sum(), (qd, kd, vd, rd))
+    torch.cuda.synchronize()
+    return y.detach().cpu().numpy(), [g.cpu().numpy() for g in grads]
+
+
+def check_case(ca, shape, seed, mag=1.0, gains=None, label=""):
+    say(f"[case] {label} shape={shape} seed={seed} mag={mag} gains={gains}")
+    q, k, v, rho, dy = make_inputs(shape, seed, mag, gains)
+    y, grads = run_hip(ca, q, k, v, rho, dy)
+    yo = O.ca_forward(q.numpy(), k.numpy(), v.numpy(), rho.numpy())[0]
+    go = O.ca_backward(q.numpy(), k.numpy(), v.numpy(), rho.numpy(), dy.numpy())
+    ey = rel(y, yo)
+    eg = [rel(a, b) for a, b in zip(grads, go)]
+    say(f"   out {ey:.2e}  dq {eg[0]:.2e} dk {eg[1]:.2e} dv {eg[2]:.2e} drho {eg[3]:.2e}")
+    assert np.all(np.isfinite(y)) and all(np.all(np.isfinite(g)) for g in grads)
+    assert ey <= OUT_TOL
+    for name, e in zip(("dq", "dk", "dv", "drho"), eg):
+        assert e <= GRAD_TOL, name
+    return ey, eg
+
+
+def test_config1_cpu_operator_shape(gpu_ca):
+    """[1,2,64,16] fp32, seed 0 (torch.manual_seed order q,k,v,dy), tau=1."""
+    say("[case] config1 [1,2,64,16] seed 0")
+    torch.manual_seed(0)
+    q, k, v = (torch.randn(1, 2, 64, 16) for _ in range(3))
+    dy = torch.randn(1, 2, 64, 16)
+    rho = torch.zeros(2)
+    y, grads = run_hip(gpu_ca, q, k, v, rho, dy)
+    yo = O.ca_forward(q.numpy(), k.numpy(), v.numpy(), rho.numpy())[0]
+    go = O.ca_backward(q.numpy(), k.numpy(), v.numpy(), rho.numpy(), dy.numpy())
+    assert rel(y, yo) <= OUT_TOL
+    for a, b in zip(grads, go):
+        assert rel(a, b) <= GRAD_TOL
+
+
+def test_reference_ca_check_shape(gpu_ca):
+    """cuda/continuum_attention.py:1363-1401: [1,2,9,8], seed 1234, fwd <= 2e-5 abs, grads <= 3e-4 abs."""
+    say("[case] ca_check [1,2,9,8]")
+    torch.manual_seed(1234)
+    q, k, v = (torch.randn(1, 2, 9, 8) for _ in range(3))
+    rho = torch.zeros(2)
+    g = torch.randn(1, 2, 9, 8)
+    y, grads = run_hip(gpu_ca, q, k, v, rho, g, tile=4)
+    yo = O.ca_forward(q.numpy(), k.numpy(), v.numpy(), rho.numpy())[0]
+    go = O.ca_backward(q.numpy(), k.numpy(), v.numpy(), rho.numpy(), g.numpy())
+    assert np.abs(y - yo).max() <= 2e-5
+    for a, b in zip(grads, go):
+        assert np.abs(a - b).max() <= 3e-4
+
+
+@pytest.mark.parametrize("T", [1, 2, 3, 31, 32, 33, 62, 63, 64, 65, 124, 125, 127, 128, 129, 192, 257])
+def test_ragged_lengths(gpu_ca, T):
+    check_case(gpu_ca, (1, 2, T, 64), 100 + T, 1.0, [0.0, 0.3], f"ragged T={T}")
+
+
+@pytest.mark.parametrize("D", [8, 16, 32, 64])
+def test_head_dims(gpu_ca, D):
+    check_case(gpu_ca, (2, 2, 129, D), 7 + D, 1.0, [0.0, math.log(1 / 0.3)], f"D={D}")
+
+
+@pytest.mark.parametrize("mag", [0.0, 0.01, 2.5, 4.0])
+def test_score_magnitudes(gpu_ca, mag):
+    """Equal scores (mag 0: delta exactly 0, uniform limit), tiny and large deltas."""
+    check_case(gpu_ca, (1, 2, 200, 64), 31, mag, [0.0, 0.2], f"mag={mag}")
+
+
+def test_forward_splits_and_combine(gpu_ca):
+    """T=1000 and 1537 span several forward splits (combine kernel) and many
+    backward key blocks."""
+    check_case(gpu_ca, (1, 2, 1000, 64), 5, 1.0, [0.1, -0.2], "splits T=1000")
+    check_case(gpu_ca, (1, 1, 1537, 32), 6, 1.5, [0.0], "splits T=1537")
+
+
+def test_repeated_keys_taylor_branch(gpu_ca):
+    """Adjacent equal keys make delta exactly 0 (verify_backward_mps.py:49-51)
+    and near-duplicate keys keep |delta| ~ 1e-4 (config 5 heads 0-7)."""
+    say("[case] repeated / near-duplicate keys")
+    torch.manual_seed(77)
+    T = 300
+    q = torch.randn(1, 2, T, 64)
+    k = torch.randn(1, 2, T, 64)
+    k[:, 0, 1::2] = k[:, 0, 0::2][:, :T // 2]               # exact repeats
+    k[:, 1] = torch.cumsum(torch.randn(T, 64) * 1e-4, 0) + torch.randn(1, 64)
+    v = torch.randn(1, 2, T, 64)
+    dy = torch.randn(1, 2, T, 64)
+    rho = torch.tensor([0.0, 0.5])
+    y, grads = run_hip(gpu_ca, q, k, v, rho, dy)
+    yo = O.ca_forward(q.numpy(), k.numpy(), v.numpy(), rho.numpy())[0]
+    go = O.ca_backward(q.numpy(), k.numpy(), v.numpy(), rho.numpy(), dy.numpy())
+    assert rel(y, yo) <= OUT_TOL
+    for a, b in zip(grads, go):
+        assert rel(a, b) <= GRAD_TOL
+
+
+def test_uniform_limit_exact(gpu_ca):
+    """q = 0 gives equal scores: CA reduces to uniform causal averaging
+    (test_acma.py:71-76)."""
+    say("[case] uniform limit")
+    T = 333
+    v = torch.randn(1, 3, T, 32)
+    q = torch.zeros(1, 3, T, 32)
+    k = torch.randn(1, 3, T, 32)
+    y = gpu_ca.continuum_attention(q.cuda(), k.cuda(), v.cuda(), torch.zeros(3).cuda()).cpu()
+    ref = torch.cumsum(v.double(), 2) / torch.arange(1, T + 1, dtype=torch.float64).view(1, 1, T, 1)
+    assert (y.double() - ref).abs().max().item() <= 2e-5
+
+
+def test_causality_exact_T2048(gpu_ca):
+    """cuda/benchmark.py:54-81: future edits leave earlier outputs bitwise
+    unchanged; a prefix loss gives exactly zero gradient to future q, k, v."""
+    say("[case] causality T=2048")
+    torch.manual_seed(1649)
+    T = 2048
+    q, k, v = (torch.randn(1, 2, T, 64, device="cuda") for _ in range(3))
+    rho = torch.tensor([0.0, 0.2], device="cuda")
+    with torch.no_grad():
+        y0 = gpu_ca.continuum_attention(q, k, v, rho, 128)
+        for cut in (0, 127, 128, 1023, 1024, 2046):
+            qp, kp, vp = q.clone(), k.clone(), v.clone()
+            qp[:, :, cut + 1:] = torch.randn_like(qp[:, :, cut + 1:]) * 2.5
+            kp[:, :, cut + 1:] = torch.randn_like(kp[:, :, cut + 1:]) * 2.5
+            vp[:, :, cut + 1:] = torch.randn_like(vp[:, :, cut + 1:]) * 2.5
+            y1 = gpu_ca.continuum_attention(qp, kp, vp, rho, 128)
+            assert torch.equal(y0[:, :, :cut + 1], y1[:, :, :cut + 1]), cut
+    for cut in (0, 127, 128, 1023, 1024, 2046):
+        qt, kt, vt = (x.clone().requires_grad_(True) for x in (q, k, v))
+        y = gpu_ca.continuum_attention(qt, kt, vt, rho, 128)
+        gq, gk, gv = torch.autograd.grad(y[:, :, :cut + 1].sum(), (qt, kt, vt))
+        for g in (gq, gk, gv):
+            fut = g[:, :, cut + 1:]
+            assert fut.numel() == 0 or fut.abs().max().item() == 0.0, cut
+
+
+def test_config2_full_size(gpu_ca):
+    """[2,16,2048,64] fp32, seed 0, rho=0.  Full outputs and
+    gradients vs the oracle for two heads (both batches); size-independent
+    invariants for every head: sum_j dV_j = sum_i dY_i, sum_j dK_j = 0,
+    sum_i q_i.dQ_i = sum_j k_j.dK_j = dRho_h."""
+    say("[case] config2 [2,16,2048,64]")
+    torch.manual_seed(0)
+    shape = (2, 16, 2048, 64)
+    q, k, v = (torch.randn(shape) for _ in range(3))
+    dy = torch.randn(shape)
+    rho = torch.zeros(16)
+    y, (dq, dk, dv, dr) = run_hip(gpu_ca, q, k, v, rho, dy)
+    for h in (0, 9):
+        sl = (slice(None), slice(h, h + 1))
+        yo, _, _ = O.ca_forward(q[sl].numpy(), k[sl].numpy(), v[sl].numpy(), rho[h:h + 1].numpy())
+        go = O.ca_backward(q[sl].numpy(), k[sl].numpy(), v[sl].numpy(), rho[h:h + 1].numpy(),
+                           dy[sl].numpy())
+        say(f"   head {h}: out {rel(y[sl], yo):.2e} dq {rel(dq[sl], go[0]):.2e} "
+            f"dk {rel(dk[sl], go[1]):.2e} dv {rel(dv[sl], go[2]):.2e} drho {rel(dr[h:h+1], go[3]):.2e}")
+        assert rel(y[sl], yo) <= OUT_TOL
+        assert rel(dq[sl], go[0]) <= GRAD_TOL
+        assert rel(dk[sl], go[1]) <= GRAD_TOL
+        assert rel(dv[sl], go[2]) <= GRAD_TOL
+        assert rel(dr[h:h + 1], go[3]) <= GRAD_TOL
+    dvs = dv.astype(np.float64).sum(2)
+    np.testing.assert_allclose(dvs, dy.double().sum(2).numpy(), rtol=0, atol=2e-3)
+    assert np.abs(dk.astype(np.float64).sum(2)).max() <= 2e-3
+    qdq = (q.double().numpy() * dq).sum(axis=(0, 2, 3))
+    kdk = (k.double().numpy() * dk).sum(axis=(0, 2, 3))
+    np.testing.assert_allclose(qdq, dr, rtol=1e-3, atol=1e-2)
+    np.testing.assert_allclose(kdk, dr, rtol=1e-3, atol=1e-2)
