@@ -85,6 +85,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 256 MiB device copy (to scale rocprof FETCH/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -93,6 +95,16 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.copy_calibration:
+        n = 64 * 1024 * 1024  # 256 MiB of fp32 read + 256 MiB written per copy
+        src = torch.randn(n, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_read": 4 * n, "copy_calibration_bytes_written": 4 * n,
+                          "launches": 5}), flush=True)
+        return
     ca = importlib.import_module("continuum-attention_amd")
     ca.native.load()
     dev = torch.device("cuda:0")

@@ -355,6 +355,13 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
   if (tid == 0) gain_part[(size_t)bh * nkb + kb] = (lds[0] + lds[1] + lds[2] + lds[3]) * kLn2;
 }
 
+// dQ = c dS K as a tiled GEMM over the packed lower-triangular dS blocks.
+// Work group: 64 queries (two 32-query tiles) of one slice.  Wave w takes
+// query tile w&1 and the key blocks of parity w>>1; each iteration stages the
+// next 64 K rows (two 32-key blocks) in LDS (double-buffered), so every K block
+// is read from L2 once per work group and shared by two waves.  The dS
+// operand of the next block is prefetched into registers.  The two parities
+// are summed through LDS at the end (fixed order).
 template <int D>
 __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict__ dsbuf,
                                                         const float* __restrict__ K,
@@ -362,15 +369,24 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
                                                         float* __restrict__ dQ, int BH, int H,
                                                         int T) {
   using P = Bwd<D>;
-  __shared__ float red[4 * P::NMB * 16 * 64];
+  constexpr int KF4 = 64 * P::C4;                     // float4 per 64-row K stage
+  constexpr int KLD = (KF4 + 255) / 256;              // float4 loads per thread
+  __shared__ f32x4 kst[2][KF4];
+  __shared__ float red[2 * P::NMB * 16 * 64];
   const int nqt = num_q_tiles(T);
+  const int nqg = (nqt + 1) / 2;
   const size_t nblk = (size_t)nqt * (nqt + 1) / 2;
   const int bh = blockIdx.x % BH;
-  const int qt = nqt - 1 - blockIdx.x / BH;  // heaviest (longest rows) first
-  const int i0 = 32 * qt;
+  const int qg = nqg - 1 - blockIdx.x / BH;  // heaviest (longest rows) first
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, q = lane & 31, h = lane >> 5;
+  const int qsub = w & 1, par = w >> 1;
+  const int qt = 2 * qg + qsub;
+  const bool wave_on = qt < nqt;
+  const int i = 32 * qt + q;
   const size_t slice = (size_t)bh * T * D;
   const float c = head_scale_log2(log_gain, bh % H, D) * kLn2;
+  const int nkb = min(2 * qg + 2, nqt);
+  const int iters = (nkb + 1) / 2;
 
   f32x16 acc[P::NMB];
 #pragma unroll
@@ -378,47 +394,87 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[nb][r] = 0.f;
 
-  const int i = i0 + q;
-  for (int kt = w; kt <= qt; kt += 4) {
+  f32x4 pre[KLD];
+  auto load_k = [&](int it) {
+#pragma unroll
+    for (int j = 0; j < KLD; ++j) {
+      const int e = tid + 256 * j;
+      f32x4 v = {0.f, 0.f, 0.f, 0.f};
+      if (e < KF4) {
+        const int key = 64 * it + e / P::C4;
+        if (key < T) v = reinterpret_cast<const f32x4*>(K + slice + (size_t)key * D)[e % P::C4];
+      }
+      pre[j] = v;
+    }
+  };
+  auto store_k = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < KLD; ++j) {
+      const int e = tid + 256 * j;
+      if (e < KF4) kst[buf][e] = pre[j];
+    }
+  };
+  auto load_a = [&](int kt, float* a) {
     const float* blk = dsbuf + (((size_t)bh * nblk + tri_block(qt, kt)) << 10);
     const f32x4* arow = reinterpret_cast<const f32x4*>(blk + (q << 5) + 16 * h);
-    float a[16];
 #pragma unroll
     for (int c4 = 0; c4 < 4; ++c4) {
       const f32x4 v4 = arow[c4];
       a[4 * c4 + 0] = v4[0]; a[4 * c4 + 1] = v4[1]; a[4 * c4 + 2] = v4[2]; a[4 * c4 + 3] = v4[3];
     }
-    const int kbase = 32 * kt + 16 * h;
-    if (kt == qt || i >= T) {
+  };
+
+  float a_next[16];
+  if (wave_on && par <= qt) load_a(par, a_next);
+  load_k(0);
+  store_k(0);
+  __syncthreads();
+  const int dcol = (q < D) ? q : 0;
+  for (int it = 0; it < iters; ++it) {
+    const int buf = it & 1;
+    const int kt = 2 * it + par;
+    if (it + 1 < iters) load_k(it + 1);
+    if (wave_on && kt <= qt) {
+      float a[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) a[r] = (kbase + r <= i && i < T) ? a[r] : 0.f;
-    }
+      for (int r = 0; r < 16; ++r) a[r] = a_next[r];
+      if (kt + 2 <= qt) load_a(kt + 2, a_next);
+      const int kbase = 32 * kt + 16 * h;
+      if (kt == qt || i >= T) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = kbase + r;
+        for (int r = 0; r < 16; ++r) a[r] = (kbase + r <= i && i < T) ? a[r] : 0.f;
+      }
+      const float* kb = reinterpret_cast<const float*>(&kst[buf][0]) + (32 * par + 16 * h) * D + dcol;
 #pragma unroll
-      for (int nb = 0; nb < P::NMB; ++nb) {
-        const bool ok = key < T && (32 * nb + q) < D;
-        const float b = ok ? K[slice + (size_t)key * D + 32 * nb + q] : 0.f;
-        acc[nb] = mfma32(a[r], b, acc[nb]);
+      for (int r = 0; r < 16; ++r) {
+#pragma unroll
+        for (int nb = 0; nb < P::NMB; ++nb) {
+          const float b = (32 * nb + q < D) ? kb[r * D + 32 * nb] : 0.f;
+          acc[nb] = mfma32(a[r], b, acc[nb]);
+        }
       }
     }
+    if (it + 1 < iters) store_k(buf ^ 1);
+    __syncthreads();
   }
+  if (par == 1) {
 #pragma unroll
-  for (int nb = 0; nb < P::NMB; ++nb)
+    for (int nb = 0; nb < P::NMB; ++nb)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) red[((w * P::NMB + nb) * 16 + r) * 64 + lane] = acc[nb][r];
+      for (int r = 0; r < 16; ++r) red[((qsub * P::NMB + nb) * 16 + r) * 64 + lane] = acc[nb][r];
+  }
   __syncthreads();
-  // wave w finalises registers r with r % 4 == w
-  for (int nb = 0; nb < P::NMB; ++nb)
-    for (int r = w; r < 16; r += 4) {
-      float sum = 0.f;
+  if (par == 0 && wave_on) {
 #pragma unroll
-      for (int ww = 0; ww < 4; ++ww) sum += red[((ww * P::NMB + nb) * 16 + r) * 64 + lane];
-      const int row = i0 + 8 * (r >> 2) + 4 * h + (r & 3);
-      const int d = 32 * nb + q;
-      if (row < T && d < D) dQ[slice + (size_t)row * D + d] = sum * c;
-    }
+    for (int nb = 0; nb < P::NMB; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float sum = acc[nb][r] + red[((qsub * P::NMB + nb) * 16 + r) * 64 + lane];
+        const int row = 32 * qt + 8 * (r >> 2) + 4 * h + (r & 3);
+        const int d = 32 * nb + q;
+        if (row < T && d < D) dQ[slice + (size_t)row * D + d] = sum * c;
+      }
+  }
 }
 
 __global__ void ca_bwd_gain_kernel(const float* __restrict__ gain_part,
@@ -454,8 +510,8 @@ hipError_t launch_bwd(const float* q, const float* k, const float* v, const floa
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   timer_begin(kBwdDq, stream);
-  hipLaunchKernelGGL(ca_bwd_dq_kernel<D>, dim3(num_q_tiles(T) * BH), dim3(256), 0, stream, dsbuf,
-                     k, log_gain, dq, BH, H, T);
+  hipLaunchKernelGGL(ca_bwd_dq_kernel<D>, dim3((num_q_tiles(T) + 1) / 2 * BH), dim3(256), 0,
+                     stream, dsbuf, k, log_gain, dq, BH, H, T);
   timer_end(kBwdDq, stream);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
