@@ -188,6 +188,16 @@ def main():
                      "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": None},
         "cpu_baseline": None,
     }
+    traffic_file = os.path.join(ROOT, "profiles", "ca_op_2x16x2048x64_hbm_traffic.json")
+    if os.path.exists(traffic_file):
+        # HBM bytes per launch of the dominant kernel, from the committed
+        # rocprofv3 FETCH_SIZE / WRITE_SIZE passes (copy-calibrated)
+        tr = json.load(open(traffic_file))
+        for name, rec in tr.get("kernels", {}).items():
+            if name.startswith(dom + "_kernel") or name.startswith(dom + "<"):
+                out["roofline"]["traffic"] = rec["total_bytes"]
+                out["roofline"]["traffic_source"] = (
+                    f"profiles/ca_op_2x16x2048x64_hbm_traffic.md (commit {tr.get('commit')})")
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)
