@@ -22,6 +22,8 @@ HIPCC_FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-ffp-contract=fast",
+    # no NaN or infinity is ever produced or tested; lets fmax/fmin skip canonicalisation
+    "-fno-honor-nans", "-fno-honor-infinities",
     # packed fp32 VALU forms are disabled on this target
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",

@@ -22,6 +22,8 @@
 // key slots are keys w0-1 .. w0+62 (slot s = key w0-1+s), so both neighbours
 // of every owned key are inside the tile.  Lane half h, register n holds slot
 // 32h+n of query q.
+#include <type_traits>
+
 #include "ca_common.h"
 #include "ca_kernels.h"
 
@@ -45,16 +47,23 @@ __device__ __forceinline__ int vswz(int row, int chunks_per_half) {
   return ((row & 3) | ((row >> 3) & 4)) & (chunks_per_half - 1);
 }
 
+// Dl_i = dY_i . y_i: one float4 chunk per thread, D/4 lanes per row.
+template <int D>
 __global__ __launch_bounds__(256) void ca_bwd_rowdot_kernel(const float* __restrict__ dout,
                                                             const float* __restrict__ out,
-                                                            float* __restrict__ dvec, int rows,
-                                                            int D) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= rows) return;
-  float x = (lane < D) ? dout[(size_t)row * D + lane] * out[(size_t)row * D + lane] : 0.f;
-  x = wave_sum(x);
-  if (lane == 0) dvec[row] = x;
+                                                            float* __restrict__ dvec, int rows) {
+  constexpr int C4 = D / 4;
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  const int row = t / C4, c = t % C4;
+  float x = 0.f;
+  if (row < rows) {
+    const f32x4 a = reinterpret_cast<const f32x4*>(dout + (size_t)row * D)[c];
+    const f32x4 b = reinterpret_cast<const f32x4*>(out + (size_t)row * D)[c];
+    x = a[0] * b[0] + a[1] * b[1] + a[2] * b[2] + a[3] * b[3];
+  }
+#pragma unroll
+  for (int o = C4 / 2; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+  if (row < rows && c == 0) dvec[row] = x;
 }
 
 __device__ __forceinline__ size_t tri_block(int qt, int kt) {
@@ -138,29 +147,50 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
   float gacc = 0.f;
 
   const int qt0 = w0 / 32;
-  for (int qt = qt0 + w; qt < nqt; qt += 4) {
+  // Next query tile of this wave, prefetched into registers while the current
+  // tile's dV/dK MFMAs run (32 rows x D floats of Q and of dY, plus row stats).
+  constexpr int PF = (32 * P::C4 + 63) / 64;  // float4 per lane per matrix
+  f32x4 pf_q[PF], pf_o[PF];
+  float pf_m2 = 0.f, pf_invz = 0.f, pf_d = 0.f;
+  auto prefetch = [&](int qt) {
     const int i0 = 32 * qt;
-    // ---- stage this wave's Q (pre-scaled) and dY tiles ----
-    for (int e = lane; e < 32 * P::C4; e += 64) {
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+      const int e = lane + 64 * j;
       const int row = e / P::C4, c = e % P::C4;
       const int qi = i0 + row;
       f32x4 qv = {0.f, 0.f, 0.f, 0.f}, ov = {0.f, 0.f, 0.f, 0.f};
-      if (qi < T) {
+      if (e < 32 * P::C4 && qi < T) {
         qv = reinterpret_cast<const f32x4*>(Q + slice + (size_t)qi * D)[c];
         ov = reinterpret_cast<const f32x4*>(dO + slice + (size_t)qi * D)[c];
       }
-      qv *= cl2;
-      *reinterpret_cast<f32x4*>(Qt + row * P::LDQ + 4 * c) = qv;
-      *reinterpret_cast<f32x4*>(dOt + row * P::LDQ + 4 * c) = ov;
+      pf_q[j] = qv;
+      pf_o[j] = ov;
     }
     const int i = i0 + q;
-    const bool qvalid = i < T;
-    float m2 = 0.f, invz = 0.f, dz = 0.f;
-    if (qvalid) {
-      m2 = stats[((size_t)bh * T + i) * 2 + 0];
-      invz = stats[((size_t)bh * T + i) * 2 + 1];
-      dz = dvec[(size_t)bh * T + i] * invz;
+    pf_m2 = 0.f; pf_invz = 0.f; pf_d = 0.f;
+    if (i < T) {
+      pf_m2 = stats[((size_t)bh * T + i) * 2 + 0];
+      pf_invz = stats[((size_t)bh * T + i) * 2 + 1];
+      pf_d = dvec[(size_t)bh * T + i];
     }
+  };
+  if (qt0 + w < nqt) prefetch(qt0 + w);
+
+  for (int qt = qt0 + w; qt < nqt; qt += 4) {
+    const int i0 = 32 * qt;
+    // ---- stage this wave's Q (pre-scaled) and dY tiles from the prefetch ----
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+      const int e = lane + 64 * j;
+      if (e < 32 * P::C4) {
+        const int row = e / P::C4, c = e % P::C4;
+        *reinterpret_cast<f32x4*>(Qt + row * P::LDQ + 4 * c) = pf_q[j] * cl2;
+        *reinterpret_cast<f32x4*>(dOt + row * P::LDQ + 4 * c) = pf_o[j];
+      }
+    }
+    const int i = i0 + q;
+    const float m2 = pf_m2, invz = pf_invz, dz = pf_d * pf_invz;
     wave_lds_sync();
 
     // ---- S^T and dP^T ----
@@ -196,66 +226,77 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
 
     // ---- weights and score gradients of this lane's 32 slots ----
     // Streams over the slots; W overwrites sacc and dS overwrites pacc in place.
+    // Tiles that may hold invisible keys (or key 0 / the caps) take the general
+    // path; all others need no masks.
     const int kbase = w0 - 1 + 32 * h;  // key of register 0
     const bool need_mask = (w0 == 0) || (w0 + 62 > i0);
-    auto slot_vis = [&](int n) {
-      const int key = kbase + n;
-      return !need_mask || (key >= 0 && key <= i);
-    };
-    // half 1's first segment starts at half 0's last slot
-    float sl, pl, gl;
-    {
-      const bool v31 = slot_vis(31);
-      const float s31 = v31 ? sacc[1][15] : m2;
-      const float g31 = v31 ? fmaf(pacc[1][15], invz, -dz) : 0.f;
-      sl = xhalf(s31);
-      pl = fast_exp2(sl - m2);
-      gl = xhalf(g31);
-    }
-    float r_prev = 0.f, dr_prev = 0.f, xl0 = 0.f, xdl0 = 0.f;
-    // finalises slot n from its own (s,p,g), incoming right share and outgoing left share
-    auto finish = [&](int n, float sv, float pv, float gv, float wv, float dv) {
-      const int key = kbase + n;
-      if (slot_vis(n) && (key == 0 || key == i)) {
-        // half-token caps (first key, last visible key); both when i == 0
-        const float cap = (key == 0 && key == i) ? pv : 0.5f * pv;
-        wv += cap;
-        dv = fmaf(cap, gv, dv);
+    auto segments = [&](auto general_tag) {
+      constexpr bool kGeneral = decltype(general_tag)::value;
+      auto slot_vis = [&](int n) {
+        const int key = kbase + n;
+        return !kGeneral || (key >= 0 && key <= i);
+      };
+      // half 1's first segment starts at half 0's last slot
+      float sl, pl, gl;
+      {
+        const bool v31 = slot_vis(31);
+        const float s31 = v31 ? sacc[1][15] : m2;
+        const float g31 = v31 ? fmaf(pacc[1][15], invz, -dz) : 0.f;
+        sl = xhalf(s31);
+        pl = fast_exp2(sl - m2);
+        gl = xhalf(g31);
       }
-      const int slot = 32 * h + n;
-      const bool owned = slot >= 1 && slot <= 62;
-      dv = owned ? dv : 0.f;
-      gacc = fmaf(dv, sv, gacc);
-      sacc[n >> 4][n & 15] = owned ? wv * invz : 0.f;
-      pacc[n >> 4][n & 15] = dv;
-    };
+      float r_prev = 0.f, dr_prev = 0.f, xl0 = 0.f, xdl0 = 0.f;
+      // finalises slot n from its own (s,p,g), incoming right and outgoing left shares
+      auto finish = [&](int n, float sv, float pv, float gv, float wv, float dv) {
+        if (kGeneral) {
+          // half-token caps on the first key and the last visible key (both when i == 0)
+          const int key = kbase + n;
+          const bool vis = slot_vis(n);
+          const float cap = (vis && key == 0 ? 0.5f * pv : 0.f) + (vis && key == i ? 0.5f * pv : 0.f);
+          wv += cap;
+          dv = fmaf(cap, gv, dv);
+        }
+        const int slot = 32 * h + n;
+        const bool owned = slot >= 1 && slot <= 62;
+        dv = owned ? dv : 0.f;
+        gacc = fmaf(dv, sv, gacc);
+        sacc[n >> 4][n & 15] = owned ? wv * invz : 0.f;
+        pacc[n >> 4][n & 15] = dv;
+      };
 #pragma unroll
-    for (int n = 0; n < 32; ++n) {
-      const bool vis = slot_vis(n);
-      const float sr = vis ? sacc[n >> 4][n & 15] : m2;
-      const float gr = vis ? fmaf(pacc[n >> 4][n & 15], invz, -dz) : 0.f;
-      const float pr = fast_exp2(sr - m2);
-      float Lv, Rv, dLv, dRv;
-      seg_shares_grad(sl, sr, pl, pr, gl, gr, Lv, Rv, dLv, dRv);
-      const int key = kbase + n;  // right key of this segment
-      bool ok = (n > 0) || (h == 1);
-      if (need_mask) ok = ok && key >= 1 && key <= i;
-      if (!ok) {
-        Lv = 0.f; Rv = 0.f; dLv = 0.f; dRv = 0.f;
+      for (int n = 0; n < 32; ++n) {
+        const bool vis = slot_vis(n);
+        const float sr = vis ? sacc[n >> 4][n & 15] : m2;
+        const float gr = vis ? fmaf(pacc[n >> 4][n & 15], invz, -dz) : 0.f;
+        const float pr = fast_exp2(sr - m2);
+        float Lv, Rv, dLv, dRv;
+        seg_shares_grad(sl, sr, pl, pr, gl, gr, Lv, Rv, dLv, dRv);
+        const int key = kbase + n;  // right key of this segment
+        bool ok = (n > 0) || (h == 1);
+        if (kGeneral) ok = ok && key >= 1 && key <= i;
+        Lv = ok ? Lv : 0.f;
+        Rv = ok ? Rv : 0.f;
+        dLv = ok ? dLv : 0.f;
+        dRv = ok ? dRv : 0.f;
+        if (n == 0) {
+          xl0 = xhalf(Lv);  // half 1's first left share belongs to half 0's last slot
+          xdl0 = xhalf(dLv);
+        } else {
+          finish(n - 1, sl, pl, gl, r_prev + Lv, dr_prev + dLv);
+        }
+        r_prev = Rv;
+        dr_prev = dRv;
+        sl = sr;
+        pl = pr;
+        gl = gr;
       }
-      if (n == 0) {
-        xl0 = xhalf(Lv);  // half 1's first left share belongs to half 0's last slot
-        xdl0 = xhalf(dLv);
-      } else {
-        finish(n - 1, sl, pl, gl, r_prev + Lv, dr_prev + dLv);
-      }
-      r_prev = Rv;
-      dr_prev = dRv;
-      sl = sr;
-      pl = pr;
-      gl = gr;
-    }
-    finish(31, sl, pl, gl, r_prev + (h ? 0.f : xl0), dr_prev + (h ? 0.f : xdl0));
+      finish(31, sl, pl, gl, r_prev + (h ? 0.f : xl0), dr_prev + (h ? 0.f : xdl0));
+    };
+    if (need_mask)
+      segments(std::true_type{});
+    else
+      segments(std::false_type{});
 
     // ---- transpose through LDS ----
     {
@@ -272,9 +313,10 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
         }
     }
     wave_lds_sync();
+    if (qt + 4 < nqt) prefetch(qt + 4);
 
     // ---- dV^T += dY^T W,  dK^T += Q^T dS,  spill dS ----
-#pragma unroll 4
+#pragma unroll 2
     for (int r = 0; r < 16; ++r) {
       const int qr = 16 * h + r;  // query row of the contraction
       float ado[P::NMB], aq[P::NMB], bw[2], bd[2];
@@ -477,14 +519,18 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   }
 }
 
-__global__ void ca_bwd_gain_kernel(const float* __restrict__ gain_part,
-                                   float* __restrict__ dlog_gain, int B, int H, int nkb) {
-  const int h = blockIdx.x * blockDim.x + threadIdx.x;
-  if (h >= H) return;
-  float s = 0.f;
+// dRho_h = sum over batch and key blocks of the per-block partials; one wave
+// per head, fixed summation order.
+__global__ __launch_bounds__(64) void ca_bwd_gain_kernel(const float* __restrict__ gain_part,
+                                                         float* __restrict__ dlog_gain, int B,
+                                                         int H, int nkb) {
+  const int h = blockIdx.x;
+  const int lane = threadIdx.x;
+  float acc = 0.f;
   for (int b = 0; b < B; ++b)
-    for (int k = 0; k < nkb; ++k) s += gain_part[((size_t)b * H + h) * nkb + k];
-  dlog_gain[h] = s;
+    for (int k = lane; k < nkb; k += 64) acc += gain_part[((size_t)b * H + h) * nkb + k];
+  acc = wave_sum(acc);
+  if (lane == 0) dlog_gain[h] = acc;
 }
 
 template <int D>
@@ -496,8 +542,8 @@ hipError_t launch_bwd(const float* q, const float* k, const float* v, const floa
   const int BH = B * H;
   const int rows = BH * T;
   timer_begin(kBwdRowdot, stream);
-  hipLaunchKernelGGL(ca_bwd_rowdot_kernel, dim3((rows + 3) / 4), dim3(256), 0, stream, dout, o,
-                     dvec, rows, D);
+  hipLaunchKernelGGL(ca_bwd_rowdot_kernel<D>, dim3((rows * (D / 4) + 255) / 256), dim3(256), 0,
+                     stream, dout, o, dvec, rows);
   timer_end(kBwdRowdot, stream);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -516,8 +562,8 @@ hipError_t launch_bwd(const float* q, const float* k, const float* v, const floa
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   timer_begin(kBwdGain, stream);
-  hipLaunchKernelGGL(ca_bwd_gain_kernel, dim3((H + 63) / 64), dim3(64), 0, stream, gain_part,
-                     dlog_gain, B, H, nkb);
+  hipLaunchKernelGGL(ca_bwd_gain_kernel, dim3(H), dim3(64), 0, stream, gain_part, dlog_gain, B,
+                     H, nkb);
   timer_end(kBwdGain, stream);
   return hipGetLastError();
 }

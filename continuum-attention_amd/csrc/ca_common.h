@@ -21,8 +21,8 @@
 // e^{-max(d,0)}(J0-J1)(d) = m1(-d) (pinned in tests/test_oracle.py), so one
 // set of decaying integrals serves both signs of the difference and nothing
 // subtracts nearly equal closed-form terms below the series threshold.
-// For t < 0.5 the integrals use their Taylor series (degree 7/7/8); the
-// closed forms are used above, where their cancellation costs < 5 bits.
+// For t < 0.75 the integrals use fitted degree-5 polynomials; the closed
+// forms are used above, where their cancellation costs < 4 bits.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -34,7 +34,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLn2 = 0.69314718055994531f;
 constexpr float kLog2e = 1.44269504088896341f;
-constexpr float kSeriesT = 0.5f;     // series below, closed form at/above
+constexpr float kSeriesT = 0.75f;    // fitted polynomials below, closed form at/above
+constexpr float kNegBig = -1.0e30f;  // finite "minus infinity" sentinel
 constexpr float kLazyRescale = 8.0f;  // forward keeps p <= 2^8 between rescales
 
 __device__ __forceinline__ f32x16 mfma32(float a, float b, f32x16 c) {
@@ -73,39 +74,35 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-// --- decaying integrals, Taylor series (t < 0.5) ---------------------------
-// K1(t) = sum (-t)^k / (k! (k+2)),  K0-K1 = sum (-t)^k / (k+2)!,
-// K2(t) = sum (-t)^k / (k! (k+3)).
+// --- decaying integrals below the switch point (t < 0.75) -----------------
+// Degree-5 polynomials fitted (weighted least squares with Lawson
+// reweighting toward minimax relative error) to K1 = int u e^{-tu},
+// K0-K1 = int (1-u) e^{-tu} and K2 = int u^2 e^{-tu} on [0, 0.75]: max
+// relative error 2.8e-8 / 3.6e-9 / 3.8e-8 in exact arithmetic, ~1.6e-7 with
+// float32 Horner evaluation.  tests/test_device_math.py re-checks these
+// constants (parsed from this file) against the float64 oracle.
+__device__ __forceinline__ float poly5(float t, float c0, float c1, float c2, float c3, float c4,
+                                       float c5) {
+  float r = fmaf(c5, t, c4);
+  r = fmaf(r, t, c3);
+  r = fmaf(r, t, c2);
+  r = fmaf(r, t, c1);
+  return fmaf(r, t, c0);
+}
+// CA_SERIES_K1
 __device__ __forceinline__ float series_K1(float t) {
-  float r = -1.0f / 45360.0f;
-  r = fmaf(r, t, 1.0f / 5760.0f);
-  r = fmaf(r, t, -1.0f / 840.0f);
-  r = fmaf(r, t, 1.0f / 144.0f);
-  r = fmaf(r, t, -1.0f / 30.0f);
-  r = fmaf(r, t, 1.0f / 8.0f);
-  r = fmaf(r, t, -1.0f / 3.0f);
-  return fmaf(r, t, 0.5f);
+  return poly5(t, 4.999999862e-01f, -3.333320860e-01f, 1.249812735e-01f, -3.322858567e-02f,
+               6.674105707e-03f, -8.569940316e-04f);
 }
+// CA_SERIES_K0MK1
 __device__ __forceinline__ float series_K0mK1(float t) {
-  float r = -1.0f / 362880.0f;
-  r = fmaf(r, t, 1.0f / 40320.0f);
-  r = fmaf(r, t, -1.0f / 5040.0f);
-  r = fmaf(r, t, 1.0f / 720.0f);
-  r = fmaf(r, t, -1.0f / 120.0f);
-  r = fmaf(r, t, 1.0f / 24.0f);
-  r = fmaf(r, t, -1.0f / 6.0f);
-  return fmaf(r, t, 0.5f);
+  return poly5(t, 4.999999982e-01f, -1.666664961e-01f, 4.166404157e-02f, -8.318396947e-03f,
+               1.349916558e-03f, -1.501583445e-04f);
 }
+// CA_SERIES_K2
 __device__ __forceinline__ float series_K2(float t) {
-  float r = 1.0f / 443520.0f;
-  r = fmaf(r, t, -1.0f / 50400.0f);
-  r = fmaf(r, t, 1.0f / 6480.0f);
-  r = fmaf(r, t, -1.0f / 960.0f);
-  r = fmaf(r, t, 1.0f / 168.0f);
-  r = fmaf(r, t, -1.0f / 36.0f);
-  r = fmaf(r, t, 1.0f / 10.0f);
-  r = fmaf(r, t, -1.0f / 4.0f);
-  return fmaf(r, t, 1.0f / 3.0f);
+  return poly5(t, 3.333333207e-01f, -2.499988710e-01f, 9.998316696e-02f, -2.768409257e-02f,
+               5.711472720e-03f, -7.451890149e-04f);
 }
 
 // Forward shares of one segment: L -> left key, R -> right key.
@@ -119,9 +116,12 @@ __device__ __forceinline__ void seg_shares(float sl, float sr, float pl, float p
   const float dl = pmax - pmin;
   const float ea_c = fmaf(-t, pmin, dl) * inv_t2;
   const float eb_c = fmaf(t, pmax, -dl) * inv_t2;
+  // both branches are evaluated and selected (no divergent control flow)
+  const float ea_s = pmax * series_K1(t);
+  const float eb_s = pmax * series_K0mK1(t);
   const bool small = t < kSeriesT;
-  const float ea = small ? pmax * series_K1(t) : ea_c;
-  const float eb = small ? pmax * series_K0mK1(t) : eb_c;
+  const float ea = small ? ea_s : ea_c;
+  const float eb = small ? eb_s : eb_c;
   const bool up = d2 >= 0.0f;
   R = up ? eb : ea;
   L = up ? ea : eb;
@@ -140,10 +140,13 @@ __device__ __forceinline__ void seg_shares_grad(float sl, float sr, float pl, fl
   const float ea_c = fmaf(-t, pmin, dl) * inv_t2;
   const float eb_c = fmaf(t, pmax, -dl) * inv_t2;
   const float ek_c = fmaf(2.0f, ea_c, -pmin) * (t * inv_t2);
+  const float ea_s = pmax * series_K1(t);
+  const float eb_s = pmax * series_K0mK1(t);
+  const float ek_s = pmax * series_K2(t);
   const bool small = t < kSeriesT;
-  const float ea = small ? pmax * series_K1(t) : ea_c;
-  const float eb = small ? pmax * series_K0mK1(t) : eb_c;
-  const float ek = small ? pmax * series_K2(t) : ek_c;
+  const float ea = small ? ea_s : ea_c;
+  const float eb = small ? eb_s : eb_c;
+  const float ek = small ? ek_s : ek_c;
   const bool up = d2 >= 0.0f;
   const float ghi = up ? gr : gl;
   const float glo = up ? gl : gr;

@@ -22,6 +22,8 @@
 // key 32t+16h+n.  The segment ending at score key k gives its left share to
 // weight key k-1 (same register) and its right share to weight key k (next
 // register; carried across halves / tiles).
+#include <type_traits>
+
 #include "ca_common.h"
 #include "ca_kernels.h"
 
@@ -133,8 +135,8 @@ __global__ __launch_bounds__(256, 2) void ca_fwd_kernel(
   float m_ref = 0.f, s_carry = 0.f, r_carry = 0.f, zsum = 0.f;
   if (wave_active) {
     if (t_b == 0) {
-      s_carry = halo_dot<D>(qreg, Ks);
-      m_ref = s_carry;
+      m_ref = halo_dot<D>(qreg, Ks);
+      s_carry = 0.0f;  // score of key 0 relative to m_ref
     } else {
       const int k0 = 32 * t_b;  // <= first query of this wave, so both halo keys are visible
       s_carry = halo_dot<D>(qreg, Ks + (size_t)k0 * D);
@@ -143,6 +145,7 @@ __global__ __launch_bounds__(256, 2) void ca_fwd_kernel(
       float l_unused;
       seg_shares(s_prev, s_carry, fast_exp2(s_prev - m_ref), fast_exp2(s_carry - m_ref), l_unused,
                  r_carry);
+      s_carry -= m_ref;  // carried scores are kept relative to m_ref
     }
   }
 
@@ -193,12 +196,16 @@ __global__ __launch_bounds__(256, 2) void ca_fwd_kernel(
     const int buf = (t - t_b) & 1;
     if (t + 1 < t_e) load_tile(t + 1);
 
-    if (wave_active && t <= wave_tmax) {
-      const bool diag = (t == wave_tmax);
-      // ---- S^T = K Q^T (log2 units) ----
+    // The first tile (first half-token cap) and the diagonal tile (causal mask,
+    // last cap) take the general path; every other tile needs neither.
+    auto tile = [&](auto general_tag) {
+      constexpr bool kGeneral = decltype(general_tag)::value;
+      const bool diag = kGeneral && (t == wave_tmax);
+      // ---- S^T = K Q^T - m_ref (log2 units; the row shift rides in the
+      //      accumulator so the MFMA returns s - m directly) ----
       f32x16 sacc;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
+      for (int r = 0; r < 16; ++r) sacc[r] = -m_ref;
       {
         const f32x4* krow = &lds_k[buf][arow * P::C4 + h * P::CH];
 #pragma unroll
@@ -211,38 +218,41 @@ __global__ __launch_bounds__(256, 2) void ca_fwd_kernel(
         }
       }
       const int kbase = 32 * t + 1 + 16 * h;  // score key of register 0
-      // ---- row max of the tile (visible keys only) ----
-      float mt = -INFINITY;
+      // ---- row max of the tile (visible keys only), relative to m_ref ----
+      float mt = kNegBig;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const bool vis = !diag || (kbase + r <= i);
-        mt = fmaxf(mt, vis ? sacc[r] : -INFINITY);
+        mt = fmaxf(mt, vis ? sacc[r] : kNegBig);
       }
       mt = fmaxf(mt, xhalf(mt));
       // Lazy rescale, decided per query: a lane whose own max did not grow
-      // keeps its shift and multiplies by exactly 1, so no query's rounding
+      // shifts by exactly 0 and scales by exactly 1, so no query's rounding
       // depends on other (possibly later) queries of the wave.
-      const bool grow = mt > m_ref + kLazyRescale;
+      const bool grow = mt > kLazyRescale;
       if (wave_any(grow)) {
-        const float m_new = grow ? mt : m_ref;
-        const float alpha = grow ? fast_exp2(m_ref - m_new) : 1.0f;
+        const float shift = grow ? mt : 0.0f;
+        const float alpha = grow ? fast_exp2(-shift) : 1.0f;
 #pragma unroll
         for (int mb = 0; mb < P::NMB; ++mb)
 #pragma unroll
           for (int r = 0; r < 16; ++r) acc_o[mb][r] *= alpha;
         zsum *= alpha;
         r_carry *= alpha;
-        m_ref = m_new;
+        m_ref += shift;
+        s_carry -= shift;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[r] -= shift;
       }
       if (diag) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[r] = (kbase + r <= i) ? sacc[r] : m_ref;
+        for (int r = 0; r < 16; ++r) sacc[r] = (kbase + r <= i) ? sacc[r] : 0.0f;
       }
-      // ---- left neighbour of register 0, and carries ----
+      // ---- left neighbour of register 0, and carries (all relative to m_ref) ----
       const float xs15 = xhalf(sacc[15]);
       float sl = h ? xs15 : s_carry;
       s_carry = xs15;  // next tile, half 0: score key 32t+32
-      float pl = fast_exp2(sl - m_ref);
+      float pl = fast_exp2(sl);
 
       // ---- stream over segments; weights overwrite sacc in place ----
       // weight register r (weight key kbase-1+r) = left share of segment r
@@ -252,17 +262,17 @@ __global__ __launch_bounds__(256, 2) void ca_fwd_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float sr = sacc[r];
-        const float pr = fast_exp2(sr - m_ref);
+        const float pr = fast_exp2(sr);
         float Lv, Rv;
         seg_shares(sl, sr, pl, pr, Lv, Rv);
-        if (diag && (kbase + r > i)) {
-          Lv = 0.f;
-          Rv = 0.f;
-        }
+        const bool seg_ok = !diag || (kbase + r <= i);
+        Lv = seg_ok ? Lv : 0.0f;
+        Rv = seg_ok ? Rv : 0.0f;
         float x = Lv + r_prev;
         const int wk = kbase - 1 + r;  // weight key, its score is sl
-        if (diag && wk == i) x = fmaf(0.5f, pl, x);  // last half-token cap
-        if (wk == 0) x = fmaf(0.5f, pl, x);           // first half-token cap
+        const float cap_last = (diag && wk == i) ? 0.5f * pl : 0.0f;   // last half-token cap
+        const float cap_first = (kGeneral && wk == 0) ? 0.5f * pl : 0.0f;          // first half-token cap
+        x += cap_last + cap_first;
         sacc[r] = x;
         zt += x;
         r_prev = Rv;
@@ -286,6 +296,12 @@ __global__ __launch_bounds__(256, 2) void ca_fwd_kernel(
           acc_o[mb] = mfma32(a, sacc[r], acc_o[mb]);
         }
       }
+    };
+    if (wave_active && t <= wave_tmax) {
+      if (t == 0 || t == wave_tmax)
+        tile(std::true_type{});
+      else
+        tile(std::false_type{});
     }
 
     if (t + 1 < t_e) store_tile(buf ^ 1);
@@ -343,14 +359,16 @@ __global__ __launch_bounds__(256, 2) void ca_fwd_kernel(
   }
 }
 
-// Merges split partials of rows whose group spans more than one split.
+// Merges split partials of rows whose group spans more than one split: one
+// float4 chunk of one row per thread, splits summed in index order.
 template <int D>
 __global__ __launch_bounds__(256) void ca_fwd_combine_kernel(const float* __restrict__ part,
                                                              float* __restrict__ O,
                                                              float* __restrict__ stats, int BH,
                                                              int T, int C, int smax) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);  // one wave per row
-  const int lane = threadIdx.x & 63;
+  constexpr int C4 = D / 4;
+  const int tix = blockIdx.x * 256 + threadIdx.x;
+  const int row = tix / C4, c = tix % C4;
   if (row >= BH * T) return;
   const int bh = row / T, i = row % T;
   const int g = i / 128;
@@ -359,18 +377,19 @@ __global__ __launch_bounds__(256) void ca_fwd_combine_kernel(const float* __rest
   const int ns = (nt + C - 1) / C;
   if (ns <= 1) return;
   const float* mz = part + (size_t)BH * smax * T * D;
-  float M = -INFINITY;
+  float M = kNegBig;
   for (int s = 0; s < ns; ++s) M = fmaxf(M, mz[(((size_t)bh * smax + s) * T + i) * 2]);
-  float Z = 0.f, acc = 0.f;
+  float Z = 0.f;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int s = 0; s < ns; ++s) {
     const size_t base = ((size_t)bh * smax + s) * T + i;
     const float f = fast_exp2(mz[base * 2] - M);
     Z = fmaf(mz[base * 2 + 1], f, Z);
-    if (lane < D) acc = fmaf(part[base * D + lane], f, acc);
+    acc += reinterpret_cast<const f32x4*>(part + base * D)[c] * f;
   }
   const float invz = 1.0f / Z;
-  if (lane < D) O[(size_t)row * D + lane] = acc * invz;
-  if (lane == 0) {
+  reinterpret_cast<f32x4*>(O + (size_t)row * D)[c] = acc * invz;
+  if (c == 0) {
     stats[(size_t)row * 2 + 0] = M;
     stats[(size_t)row * 2 + 1] = invz;
   }
@@ -393,8 +412,8 @@ hipError_t launch_fwd(const float* q, const float* k, const float* v, const floa
   if (smax > 1) {
     const int rows = BH * T;
     timer_begin(kFwdCombine, stream);
-    hipLaunchKernelGGL(ca_fwd_combine_kernel<D>, dim3((rows + 3) / 4), dim3(256), 0, stream, part,
-                       o, stats, BH, T, C, smax);
+    hipLaunchKernelGGL(ca_fwd_combine_kernel<D>, dim3((rows * (D / 4) + 255) / 256), dim3(256), 0,
+                       stream, part, o, stats, BH, T, C, smax);
     timer_end(kFwdCombine, stream);
     e = hipGetLastError();
   }
