@@ -146,6 +146,7 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
       }
   float gacc = 0.f;
 
+  float* st_dummy = dsbuf + (((size_t)BH * nblk) << 10) + tid;  // 256 spare words
   const int qt0 = w0 / 32;
   // Next query tile of this wave, prefetched into registers while the current
   // tile's dV/dK MFMAs run (32 rows x D floats of Q and of dY, plus row stats).
@@ -193,34 +194,41 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
     const float m2 = pf_m2, invz = pf_invz, dz = pf_d * pf_invz;
     wave_lds_sync();
 
-    // ---- S^T and dP^T ----
+    // ---- S^T (minus the row shift, folded into the accumulator) and dP^T ----
+    // Operands of chunk c+1 are read from LDS before the MFMAs of chunk c issue.
     f32x16 sacc[2], pacc[2];
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        sacc[b][r] = 0.f;
+        sacc[b][r] = -m2;
         pacc[b][r] = 0.f;
       }
     {
-      const float* qrow = Qt + q * P::LDQ + h * P::DH;
-      const float* orow = dOt + q * P::LDQ + h * P::DH;
-#pragma unroll
-      for (int c = 0; c < P::CH; ++c) {
-        const f32x4 qv = *reinterpret_cast<const f32x4*>(qrow + 4 * c);
-        const f32x4 ov = *reinterpret_cast<const f32x4*>(orow + 4 * c);
-        f32x4 vv[2];
+      const f32x4* qrow = reinterpret_cast<const f32x4*>(Qt + q * P::LDQ + h * P::DH);
+      const f32x4* orow = reinterpret_cast<const f32x4*>(dOt + q * P::LDQ + h * P::DH);
+      f32x4 qv_n, ov_n, vv_n[2];
+      auto fetch = [&](int c) {
+        qv_n = qrow[c];
+        ov_n = orow[c];
 #pragma unroll
         for (int b = 0; b < 2; ++b)
-          vv[b] = vsl[vrow[b] * P::C4 + h * P::CH + (c ^ vswz(vrow[b], P::CH))];
+          vv_n[b] = vsl[vrow[b] * P::C4 + h * P::CH + (c ^ vswz(vrow[b], P::CH))];
+      };
+      fetch(0);
+#pragma unroll
+      for (int c = 0; c < P::CH; ++c) {
+        const f32x4 qv = qv_n, ov = ov_n, vv0 = vv_n[0], vv1 = vv_n[1];
+        if (c + 1 < P::CH) fetch(c + 1);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-#pragma unroll
-          for (int b = 0; b < 2; ++b) {
-            sacc[b] = mfma32(ka[b][4 * c + e], qv[e], sacc[b]);
-            pacc[b] = mfma32(vv[b][e], ov[e], pacc[b]);
-          }
+          sacc[0] = mfma32(ka[0][4 * c + e], qv[e], sacc[0]);
+          pacc[0] = mfma32(vv0[e], ov[e], pacc[0]);
+          sacc[1] = mfma32(ka[1][4 * c + e], qv[e], sacc[1]);
+          pacc[1] = mfma32(vv1[e], ov[e], pacc[1]);
         }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
 
@@ -229,7 +237,8 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
     // Tiles that may hold invisible keys (or key 0 / the caps) take the general
     // path; all others need no masks.
     const int kbase = w0 - 1 + 32 * h;  // key of register 0
-    const bool need_mask = (w0 == 0) || (w0 + 62 > i0);
+    const bool need_mask = (w0 == 0) || (w0 + 62 > i0) || (i0 + 32 > T);
+    float dsum = 0.f;
     auto segments = [&](auto general_tag) {
       constexpr bool kGeneral = decltype(general_tag)::value;
       auto slot_vis = [&](int n) {
@@ -240,10 +249,10 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
       float sl, pl, gl;
       {
         const bool v31 = slot_vis(31);
-        const float s31 = v31 ? sacc[1][15] : m2;
+        const float s31 = v31 ? sacc[1][15] : 0.f;
         const float g31 = v31 ? fmaf(pacc[1][15], invz, -dz) : 0.f;
         sl = xhalf(s31);
-        pl = fast_exp2(sl - m2);
+        pl = fast_exp2(sl);
         gl = xhalf(g31);
       }
       float r_prev = 0.f, dr_prev = 0.f, xl0 = 0.f, xdl0 = 0.f;
@@ -260,16 +269,17 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
         const int slot = 32 * h + n;
         const bool owned = slot >= 1 && slot <= 62;
         dv = owned ? dv : 0.f;
-        gacc = fmaf(dv, sv, gacc);
+        gacc = fmaf(dv, sv, gacc);  // sv is s - m2; the m2 * sum(dS) part is added per tile
+        dsum += dv;
         sacc[n >> 4][n & 15] = owned ? wv * invz : 0.f;
         pacc[n >> 4][n & 15] = dv;
       };
 #pragma unroll
       for (int n = 0; n < 32; ++n) {
         const bool vis = slot_vis(n);
-        const float sr = vis ? sacc[n >> 4][n & 15] : m2;
+        const float sr = vis ? sacc[n >> 4][n & 15] : 0.f;  // s - m2
         const float gr = vis ? fmaf(pacc[n >> 4][n & 15], invz, -dz) : 0.f;
-        const float pr = fast_exp2(sr - m2);
+        const float pr = fast_exp2(sr);
         float Lv, Rv, dLv, dRv;
         seg_shares_grad(sl, sr, pl, pr, gl, gr, Lv, Rv, dLv, dRv);
         const int key = kbase + n;  // right key of this segment
@@ -297,6 +307,7 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
       segments(std::true_type{});
     else
       segments(std::false_type{});
+    gacc = fmaf(m2, dsum, gacc);
 
     // ---- transpose through LDS ----
     {
@@ -316,39 +327,73 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
     if (qt + 4 < nqt) prefetch(qt + 4);
 
     // ---- dV^T += dY^T W,  dK^T += Q^T dS,  spill dS ----
-#pragma unroll 2
-    for (int r = 0; r < 16; ++r) {
-      const int qr = 16 * h + r;  // query row of the contraction
-      float ado[P::NMB], aq[P::NMB], bw[2], bd[2];
-#pragma unroll
-      for (int mb = 0; mb < P::NMB; ++mb) {
-        const bool dok = 32 * mb + q < D;
-        const int col = dok ? 32 * mb + q : 0;
-        ado[mb] = dok ? dOt[qr * P::LDQ + col] : 0.f;
-        aq[mb] = dok ? Qt[qr * P::LDQ + col] : 0.f;
-      }
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        bw[nb] = Wt[qr * P::LDW + 32 * nb + q];
-        bd[nb] = dSt[qr * P::LDW + 32 * nb + q];
-      }
-#pragma unroll
-      for (int mb = 0; mb < P::NMB; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-          accv[mb][nb] = mfma32(ado[mb], bw[nb], accv[mb][nb]);
-          acck[mb][nb] = mfma32(aq[mb], bd[nb], acck[mb][nb]);
-        }
-      const int qi = i0 + qr;
+    // Operands of query row r+1 are read from LDS before the MFMAs of row r.
+    // dS goes to the packed lower-triangular 32x32 blocks of row tile qt:
+    // lane (q, h) writes key w0-1+32nb+q of query rows i0+16h+r.
+    float* st_ptr[2];
+    bool st_ok[2];
+    {
+      float* rowblk = dsbuf + (((size_t)bh * nblk + tri_block(qt, 0)) << 10);
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
         const int slot = 32 * nb + q;
         const int key = w0 - 1 + slot;
-        if (slot >= 1 && slot <= 62 && key < T && qi < T && key <= qi) {
-          const size_t off = (((size_t)bh * nblk + tri_block(qi >> 5, key >> 5)) << 10) +
-                             ((qi & 31) << 5) + (key & 31);
-          dsbuf[off] = bd[nb];
+        st_ok[nb] = slot >= 1 && slot <= 62 && key < T && (key >> 5) <= qt;
+        const int kk = st_ok[nb] ? key : 0;
+        st_ptr[nb] = rowblk + ((kk >> 5) << 10) + ((16 * h) << 5) + (kk & 31);
+      }
+    }
+    {
+      const int col0 = q < D ? q : 0;
+      float ado_n[P::NMB], aq_n[P::NMB], bw_n[2], bd_n[2];
+      auto fetch = [&](int r) {
+        const int qr = 16 * h + r;
+#pragma unroll
+        for (int mb = 0; mb < P::NMB; ++mb) {
+          const bool dok = 32 * mb + q < D;
+          ado_n[mb] = dok ? dOt[qr * P::LDQ + 32 * mb + col0] : 0.f;
+          aq_n[mb] = dok ? Qt[qr * P::LDQ + 32 * mb + col0] : 0.f;
         }
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+          bw_n[nb] = Wt[qr * P::LDW + 32 * nb + q];
+          bd_n[nb] = dSt[qr * P::LDW + 32 * nb + q];
+        }
+      };
+      fetch(0);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float ado[P::NMB], aq[P::NMB], bw[2], bd[2];
+#pragma unroll
+        for (int mb = 0; mb < P::NMB; ++mb) {
+          ado[mb] = ado_n[mb];
+          aq[mb] = aq_n[mb];
+        }
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+          bw[nb] = bw_n[nb];
+          bd[nb] = bd_n[nb];
+        }
+        if (r + 1 < 16) fetch(r + 1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int mb = 0; mb < P::NMB; ++mb)
+#pragma unroll
+          for (int nb = 0; nb < 2; ++nb) {
+            accv[mb][nb] = mfma32(ado[mb], bw[nb], accv[mb][nb]);
+            acck[mb][nb] = mfma32(aq[mb], bd[nb], acck[mb][nb]);
+          }
+        // spill dS (branch-free: masked lanes write a per-lane dummy word)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+          bool ok = st_ok[nb];
+          if (need_mask) {
+            const int qi = i0 + 16 * h + r;
+            ok = ok && (w0 - 1 + 32 * nb + q <= qi) && qi < T;
+          }
+          *(ok ? st_ptr[nb] + 32 * r : st_dummy) = bd[nb];
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   }

@@ -2,27 +2,35 @@
 //
 // Segment math
 // ------------
-// A segment joins two adjacent keys (left l, right r) of one query row.  With
-// scores in log2 units (the kernels pre-scale q by c_h*log2(e)) the natural
-// score difference is t = |s_r - s_l| * ln2, and with the row shift m the
-// endpoint weights are p = 2^(s - m).  Writing hi/lo for the endpoint with the
-// larger/smaller score, Pmax = p_hi, Pmin = p_lo = Pmax e^-t, and the decaying
-// integrals K_n(t) = int_0^1 u^n e^{-t u} du, the reference's segment terms
-// (architecture.py:32-62,91-96; analytic_reference.py:12-75) become
+// A segment joins two adjacent keys (left l, right r) of one query row.  The
+// kernels keep scores in log2 units relative to the row shift m (q is
+// pre-scaled by c_h*log2(e) and -m rides in the MFMA accumulator), so the
+// endpoint weights are p = 2^s and the signed natural difference is
+// x = (s_r - s_l) * ln2.  With J_n(x) = int_0^1 u^n e^{x u} du the
+// reference's segment terms (architecture.py:32-62,91-96;
+// analytic_reference.py:12-75, there written with shifted moments of |x|) are
 //
-//   share to hi endpoint   E*B  = Pmax (K0 - K1) = (t Pmax - (Pmax - Pmin)) / t^2
-//   share to lo endpoint   E*A  = Pmax  K1       = ((Pmax - Pmin) - t Pmin) / t^2
-//   second moment          E*K2 = Pmax  K2       = (2 E*A - Pmin) / t
+//   right share   R = p_l J1(x)          left share  L = p_l (J0 - J1)(x)
+//   p_l J2(x)     (second moment, backward only)
 //
-// and the score-gradient contributions of the segment are
-//   dS_hi += g_hi (EB - EA + EK2) + g_lo (EA - EK2)
-//   dS_lo += g_hi (EA - EK2)      + g_lo EK2.
-// This is the reference's J0/J1/J2 form rewritten with the mirror identity
-// e^{-max(d,0)}(J0-J1)(d) = m1(-d) (pinned in tests/test_oracle.py), so one
-// set of decaying integrals serves both signs of the difference and nothing
-// subtracts nearly equal closed-form terms below the series threshold.
-// For t < 0.75 the integrals use fitted degree-5 polynomials; the closed
-// forms are used above, where their cancellation costs < 4 bits.
+// and the score-gradient contributions, with centred, 1/Z-scaled weight
+// gradients g_l, g_r, are
+//
+//   dS_r += g_l (R - p_l J2) + g_r p_l J2
+//   dS_l += g_l (L - R + p_l J2) + g_r (R - p_l J2).
+//
+// For |x| >= 0.75 the closed forms, using p_l e^x = p_r and dp = p_r - p_l,
+//   p_l J0 = dp / x,   R = (p_r - dp/x) / x,   L = dp/x - R,
+//   p_l J2 = (p_r - 2R) / x
+// need a single reciprocal and no ordering of the endpoints.  For |x| < 0.75
+// they cancel, and R = p_l J1(x), L = p_r J1(-x) (mirror identity
+// e^{x}J1(-x) = (J0-J1)(x), pinned in tests/test_oracle.py), with J1 and J2
+// split into even and odd parts J(x) = E(x^2) + x O(x^2) so one evaluation
+// serves both shares.  The polynomial coefficients are fitted (weighted least
+// squares with Lawson reweighting toward minimax relative error) on
+// [-0.75, 0.75]: max relative error 3.8e-9 (J1) and 5.2e-9 (J2) in exact
+// arithmetic, ~2e-7 in float32.  tests/test_device_math.py re-checks these
+// constants and formulas in float32 against the float64 oracle.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -34,7 +42,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLn2 = 0.69314718055994531f;
 constexpr float kLog2e = 1.44269504088896341f;
-constexpr float kSeriesT = 0.75f;    // fitted polynomials below, closed form at/above
+constexpr float kSeriesT = 0.75f;    // |x| below: fitted polynomials; at/above: closed form
 constexpr float kNegBig = -1.0e30f;  // finite "minus infinity" sentinel
 constexpr float kLazyRescale = 8.0f;  // forward keeps p <= 2^8 between rescales
 
@@ -74,57 +82,44 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-// --- decaying integrals below the switch point (t < 0.75) -----------------
-// Degree-5 polynomials fitted (weighted least squares with Lawson
-// reweighting toward minimax relative error) to K1 = int u e^{-tu},
-// K0-K1 = int (1-u) e^{-tu} and K2 = int u^2 e^{-tu} on [0, 0.75]: max
-// relative error 2.8e-8 / 3.6e-9 / 3.8e-8 in exact arithmetic, ~1.6e-7 with
-// float32 Horner evaluation.  tests/test_device_math.py re-checks these
-// constants (parsed from this file) against the float64 oracle.
-__device__ __forceinline__ float poly5(float t, float c0, float c1, float c2, float c3, float c4,
-                                       float c5) {
-  float r = fmaf(c5, t, c4);
-  r = fmaf(r, t, c3);
-  r = fmaf(r, t, c2);
-  r = fmaf(r, t, c1);
-  return fmaf(r, t, c0);
+__device__ __forceinline__ float poly3(float y, float c0, float c1, float c2, float c3) {
+  return fmaf(fmaf(fmaf(c3, y, c2), y, c1), y, c0);
 }
-// CA_SERIES_K1
-__device__ __forceinline__ float series_K1(float t) {
-  return poly5(t, 4.999999862e-01f, -3.333320860e-01f, 1.249812735e-01f, -3.322858567e-02f,
-               6.674105707e-03f, -8.569940316e-04f);
+// CA_J1_EVEN
+__device__ __forceinline__ float j1_even(float y) {
+  return poly3(y, 4.999999983e-01f, 1.250001046e-01f, 6.943487325e-03f, 1.763820432e-04f);
 }
-// CA_SERIES_K0MK1
-__device__ __forceinline__ float series_K0mK1(float t) {
-  return poly5(t, 4.999999982e-01f, -1.666664961e-01f, 4.166404157e-02f, -8.318396947e-03f,
-               1.349916558e-03f, -1.501583445e-04f);
+// CA_J1_ODD
+__device__ __forceinline__ float j1_odd(float y) {
+  return poly3(y, 3.333333406e-01f, 3.333323677e-02f, 1.190763457e-03f, 2.193350522e-05f);
 }
-// CA_SERIES_K2
-__device__ __forceinline__ float series_K2(float t) {
-  return poly5(t, 3.333333207e-01f, -2.499988710e-01f, 9.998316696e-02f, -2.768409257e-02f,
-               5.711472720e-03f, -7.451890149e-04f);
+// CA_J2_EVEN
+__device__ __forceinline__ float j2_even(float y) {
+  return poly3(y, 3.333333318e-01f, 1.000000935e-01f, 5.951518136e-03f, 1.568314444e-04f);
+}
+// CA_J2_ODD
+__device__ __forceinline__ float j2_odd(float y) {
+  return poly3(y, 2.500000075e-01f, 2.777767623e-02f, 1.041977470e-03f, 1.968927945e-05f);
 }
 
 // Forward shares of one segment: L -> left key, R -> right key.
-// sl/sr are log2-unit scores, pl/pr their weights 2^(s-m).
+// sl/sr are log2-unit scores relative to the row shift, pl/pr = 2^sl, 2^sr.
+// Both branches are evaluated and selected (no divergent control flow).
 __device__ __forceinline__ void seg_shares(float sl, float sr, float pl, float pr, float& L,
                                            float& R) {
-  const float d2 = sr - sl;
-  const float t = fabsf(d2) * kLn2;
-  const float pmax = fmaxf(pl, pr), pmin = fminf(pl, pr);
-  const float inv_t2 = fast_rcp(t * t);
-  const float dl = pmax - pmin;
-  const float ea_c = fmaf(-t, pmin, dl) * inv_t2;
-  const float eb_c = fmaf(t, pmax, -dl) * inv_t2;
-  // both branches are evaluated and selected (no divergent control flow)
-  const float ea_s = pmax * series_K1(t);
-  const float eb_s = pmax * series_K0mK1(t);
-  const bool small = t < kSeriesT;
-  const float ea = small ? ea_s : ea_c;
-  const float eb = small ? eb_s : eb_c;
-  const bool up = d2 >= 0.0f;
-  R = up ? eb : ea;
-  L = up ? ea : eb;
+  const float x = (sr - sl) * kLn2;
+  const float dp = pr - pl;
+  const float inv_x = fast_rcp(x);
+  const float a = dp * inv_x;           // p_l J0
+  const float rc = (pr - a) * inv_x;    // p_l J1
+  const float lc = a - rc;              // p_l (J0 - J1)
+  const float y = x * x;
+  const float e1 = j1_even(y), o1 = j1_odd(y);
+  const float rs = pl * fmaf(x, o1, e1);   // p_l J1(x)
+  const float ls = pr * fmaf(-x, o1, e1);  // p_r J1(-x)
+  const bool small = fabsf(x) < kSeriesT;
+  R = small ? rs : rc;
+  L = small ? ls : lc;
 }
 
 // Forward shares and score-gradient contributions of one segment.
@@ -132,31 +127,25 @@ __device__ __forceinline__ void seg_shares(float sl, float sr, float pl, float p
 __device__ __forceinline__ void seg_shares_grad(float sl, float sr, float pl, float pr, float gl,
                                                 float gr, float& L, float& R, float& dL,
                                                 float& dR) {
-  const float d2 = sr - sl;
-  const float t = fabsf(d2) * kLn2;
-  const float pmax = fmaxf(pl, pr), pmin = fminf(pl, pr);
-  const float inv_t2 = fast_rcp(t * t);
-  const float dl = pmax - pmin;
-  const float ea_c = fmaf(-t, pmin, dl) * inv_t2;
-  const float eb_c = fmaf(t, pmax, -dl) * inv_t2;
-  const float ek_c = fmaf(2.0f, ea_c, -pmin) * (t * inv_t2);
-  const float ea_s = pmax * series_K1(t);
-  const float eb_s = pmax * series_K0mK1(t);
-  const float ek_s = pmax * series_K2(t);
-  const bool small = t < kSeriesT;
-  const float ea = small ? ea_s : ea_c;
-  const float eb = small ? eb_s : eb_c;
-  const float ek = small ? ek_s : ek_c;
-  const bool up = d2 >= 0.0f;
-  const float ghi = up ? gr : gl;
-  const float glo = up ? gl : gr;
-  const float ex = ea - ek;
-  const float dhi = fmaf(ghi, eb - ea + ek, glo * ex);
-  const float dlo = fmaf(ghi, ex, glo * ek);
-  R = up ? eb : ea;
-  L = up ? ea : eb;
-  dR = up ? dhi : dlo;
-  dL = up ? dlo : dhi;
+  const float x = (sr - sl) * kLn2;
+  const float dp = pr - pl;
+  const float inv_x = fast_rcp(x);
+  const float a = dp * inv_x;
+  const float rc = (pr - a) * inv_x;
+  const float lc = a - rc;
+  const float j2c = fmaf(-2.0f, rc, pr) * inv_x;  // p_l J2
+  const float y = x * x;
+  const float e1 = j1_even(y), o1 = j1_odd(y);
+  const float rs = pl * fmaf(x, o1, e1);
+  const float ls = pr * fmaf(-x, o1, e1);
+  const float j2s = pl * fmaf(x, j2_odd(y), j2_even(y));
+  const bool small = fabsf(x) < kSeriesT;
+  R = small ? rs : rc;
+  L = small ? ls : lc;
+  const float j2 = small ? j2s : j2c;
+  const float xm = R - j2;  // p_l (J1 - J2)
+  dR = fmaf(gl, xm, gr * j2);
+  dL = fmaf(gl, L - xm, gr * xm);
 }
 
 // 32x32x2 MFMA output layout: register r of lane l holds row

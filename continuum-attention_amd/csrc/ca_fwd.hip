@@ -206,6 +206,18 @@ __global__ __launch_bounds__(256, 2) void ca_fwd_kernel(
       f32x16 sacc;
 #pragma unroll
       for (int r = 0; r < 16; ++r) sacc[r] = -m_ref;
+      // V^T operands of this tile's PV product, read now so their LDS latency
+      // hides behind the S^T MFMAs and the segment math
+      const bool dok = q < D;  // only D < 32 pads the d block
+      float va[P::NMB][16];
+      {
+        const float* vcol = &lds_v[buf][(16 * h) * D + (dok ? q : 0)];
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+#pragma unroll
+          for (int mb = 0; mb < P::NMB; ++mb) va[mb][r] = dok ? vcol[r * D + 32 * mb] : 0.f;
+      }
+      __builtin_amdgcn_sched_barrier(0);
       {
         const f32x4* krow = &lds_k[buf][arow * P::C4 + h * P::CH];
 #pragma unroll
@@ -286,15 +298,10 @@ __global__ __launch_bounds__(256, 2) void ca_fwd_kernel(
       zsum += zt + r_in;
 
       // ---- O^T += V^T W^T ----
-      const bool dok = q < D;  // only D < 32 pads the d block
-      const float* vcol = &lds_v[buf][(16 * h) * D + (dok ? q : 0)];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
 #pragma unroll
-        for (int mb = 0; mb < P::NMB; ++mb) {
-          const float a = dok ? vcol[r * D + 32 * mb] : 0.f;
-          acc_o[mb] = mfma32(a, sacc[r], acc_o[mb]);
-        }
+        for (int mb = 0; mb < P::NMB; ++mb) acc_o[mb] = mfma32(va[mb][r], sacc[r], acc_o[mb]);
       }
     };
     if (wave_active && t <= wave_tmax) {

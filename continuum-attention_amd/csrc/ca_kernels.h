@@ -33,7 +33,7 @@ __host__ __device__ inline int bwd_num_key_blocks(int T) { return (T + kBwdKeys 
 __host__ __device__ inline int num_q_tiles(int T) { return (T + 31) / 32; }
 inline size_t bwd_ds_floats(int BH, int T) {
   const size_t n = num_q_tiles(T);
-  return (size_t)BH * (n * (n + 1) / 2) * 1024;
+  return (size_t)BH * (n * (n + 1) / 2) * 1024 + 256;  // + per-thread dummy words
 }
 
 // Per-kernel HIP-event timing (diagnostics; off unless ca_timing_enable(1)).
