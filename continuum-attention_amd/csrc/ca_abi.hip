@@ -55,7 +55,7 @@ BwdLayout bwd_layout(int B, int H, int T) {
   L.ds = 0;
   L.dvec = align256(ca::bwd_ds_floats(BH, T) * sizeof(float));
   L.gain = L.dvec + align256((size_t)BH * T * sizeof(float));
-  L.total = L.gain + align256((size_t)BH * ca::bwd_num_key_blocks(T) * sizeof(float));
+  L.total = L.gain + align256((size_t)BH * ca::dq_num_groups(T) * sizeof(float));
   return L;
 }
 

@@ -14,9 +14,11 @@
 //                   dP^T = V dY^T by MFMA, W and dS in registers, then
 //                   dV^T += dY^T W and dK^T += Q^T dS by MFMA after an LDS
 //                   transpose.  dS is also written to a packed lower-triangular
-//                   buffer for the dQ pass; per-block gain partials sum dS*s.
-//   ca_bwd_dq       dQ = c dS K, one work group per (slice, 32-query tile).
-//   ca_bwd_gain     dRho_h = sum over batch and key blocks of the partials.
+//                   buffer for the dQ pass.
+//   ca_bwd_dq       dQ = c dS K, one work group per (slice, 64 queries); its
+//                   epilogue also forms the gain partial sum_i q_i . dQ_i
+//                   (= sum_ij dS_ij s_ij, since s_ij = c q_i . k_j).
+//   ca_bwd_gain     dRho_h = sum over batch and query groups of the partials.
 //
 // Key-block layout: the work group owns weight keys [w0, w0+62); its 64 MFMA
 // key slots are keys w0-1 .. w0+62 (slot s = key w0-1+s), so both neighbours
@@ -75,11 +77,10 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, const float* __restrict__ stats, const float* __restrict__ dvec,
     const float* __restrict__ log_gain, float* __restrict__ dK, float* __restrict__ dV,
-    float* __restrict__ dsbuf, float* __restrict__ gain_part, int BH, int H, int T) {
+    float* __restrict__ dsbuf, int BH, int H, int T) {
   using P = Bwd<D>;
   extern __shared__ float lds[];
 
-  const int nkb = bwd_num_key_blocks(T);
   const int nqt = num_q_tiles(T);
   const size_t nblk = (size_t)nqt * (nqt + 1) / 2;
   const int bh = blockIdx.x % BH;
@@ -144,8 +145,6 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
         accv[mb][nb][r] = 0.f;
         acck[mb][nb][r] = 0.f;
       }
-  float gacc = 0.f;
-
   float* st_dummy = dsbuf + (((size_t)BH * nblk) << 10) + tid;  // 256 spare words
   const int qt0 = w0 / 32;
   // Next query tile of this wave, prefetched into registers while the current
@@ -238,7 +237,6 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
     // path; all others need no masks.
     const int kbase = w0 - 1 + 32 * h;  // key of register 0
     const bool need_mask = (w0 == 0) || (w0 + 62 > i0) || (i0 + 32 > T);
-    float dsum = 0.f;
     auto segments = [&](auto general_tag) {
       constexpr bool kGeneral = decltype(general_tag)::value;
       auto slot_vis = [&](int n) {
@@ -269,8 +267,6 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
         const int slot = 32 * h + n;
         const bool owned = slot >= 1 && slot <= 62;
         dv = owned ? dv : 0.f;
-        gacc = fmaf(dv, sv, gacc);  // sv is s - m2; the m2 * sum(dS) part is added per tile
-        dsum += dv;
         sacc[n >> 4][n & 15] = owned ? wv * invz : 0.f;
         pacc[n >> 4][n & 15] = dv;
       };
@@ -307,7 +303,6 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
       segments(std::true_type{});
     else
       segments(std::false_type{});
-    gacc = fmaf(m2, dsum, gacc);
 
     // ---- transpose through LDS ----
     {
@@ -413,7 +408,6 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
         redv[(w * NE + e) * 64 + lane] = accv[mb][nb][r];
         redk[(w * NE + e) * 64 + lane] = acck[mb][nb][r];
       }
-  const float gw_sum = wave_sum(gacc);
   __syncthreads();
   // groups of 4 consecutive d (one float4 store) are split across the waves
   constexpr int NG = P::NMB * 2 * 4;
@@ -436,10 +430,6 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
       *reinterpret_cast<f32x4*>(dK + slice + (size_t)key * D + d0) = sk * kLn2;
     }
   }
-  __syncthreads();
-  if (lane == 0) lds[w] = gw_sum;
-  __syncthreads();
-  if (tid == 0) gain_part[(size_t)bh * nkb + kb] = (lds[0] + lds[1] + lds[2] + lds[3]) * kLn2;
 }
 
 // dQ = c dS K as a tiled GEMM over the packed lower-triangular dS blocks.
@@ -448,18 +438,22 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
 // next 64 K rows (two 32-key blocks) in LDS (double-buffered), so every K block
 // is read from L2 once per work group and shared by two waves.  The dS
 // operand of the next block is prefetched into registers.  The two parities
-// are summed through LDS at the end (fixed order).
+// are summed through LDS at the end (fixed order).  The epilogue writes the
+// work group's gain partial sum_i q_i . dQ_i (fixed order).
 template <int D>
 __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict__ dsbuf,
+                                                        const float* __restrict__ Q,
                                                         const float* __restrict__ K,
                                                         const float* __restrict__ log_gain,
-                                                        float* __restrict__ dQ, int BH, int H,
-                                                        int T) {
+                                                        float* __restrict__ dQ,
+                                                        float* __restrict__ gain_part, int BH,
+                                                        int H, int T) {
   using P = Bwd<D>;
   constexpr int KF4 = 64 * P::C4;                     // float4 per 64-row K stage
   constexpr int KLD = (KF4 + 255) / 256;              // float4 loads per thread
   __shared__ f32x4 kst[2][KF4];
   __shared__ float red[2 * P::NMB * 16 * 64];
+  __shared__ float gred[2];
   const int nqt = num_q_tiles(T);
   const int nqg = (nqt + 1) / 2;
   const size_t nblk = (size_t)nqt * (nqt + 1) / 2;
@@ -544,6 +538,18 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
     if (it + 1 < iters) store_k(buf ^ 1);
     __syncthreads();
   }
+  // Q rows for the gain partial, loaded as one batch before the reduction
+  float qv[P::NMB][16];
+  if (par == 0 && wave_on) {
+#pragma unroll
+    for (int nb = 0; nb < P::NMB; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = 32 * qt + 8 * (r >> 2) + 4 * h + (r & 3);
+        const int d = 32 * nb + q;
+        qv[nb][r] = (row < T && d < D) ? Q[slice + (size_t)row * D + d] : 0.f;
+      }
+  }
   if (par == 1) {
 #pragma unroll
     for (int nb = 0; nb < P::NMB; ++nb)
@@ -551,29 +557,38 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
       for (int r = 0; r < 16; ++r) red[((qsub * P::NMB + nb) * 16 + r) * 64 + lane] = acc[nb][r];
   }
   __syncthreads();
-  if (par == 0 && wave_on) {
+  if (par == 0) {
+    float g = 0.f;
+    if (wave_on) {
 #pragma unroll
-    for (int nb = 0; nb < P::NMB; ++nb)
+      for (int nb = 0; nb < P::NMB; ++nb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float sum = acc[nb][r] + red[((qsub * P::NMB + nb) * 16 + r) * 64 + lane];
-        const int row = 32 * qt + 8 * (r >> 2) + 4 * h + (r & 3);
-        const int d = 32 * nb + q;
-        if (row < T && d < D) dQ[slice + (size_t)row * D + d] = sum * c;
-      }
+        for (int r = 0; r < 16; ++r) {
+          const float sum = acc[nb][r] + red[((qsub * P::NMB + nb) * 16 + r) * 64 + lane];
+          const int row = 32 * qt + 8 * (r >> 2) + 4 * h + (r & 3);
+          const int d = 32 * nb + q;
+          const float val = sum * c;
+          g = fmaf(qv[nb][r], val, g);
+          if (row < T && d < D) dQ[slice + (size_t)row * D + d] = val;
+        }
+    }
+    g = wave_sum(g);
+    if (lane == 0) gred[qsub] = g;
   }
+  __syncthreads();
+  if (tid == 0) gain_part[(size_t)bh * nqg + qg] = gred[0] + gred[1];
 }
 
-// dRho_h = sum over batch and key blocks of the per-block partials; one wave
-// per head, fixed summation order.
+// dRho_h = sum over batch and query groups of the per-group partials; one
+// wave per head, fixed summation order.
 __global__ __launch_bounds__(64) void ca_bwd_gain_kernel(const float* __restrict__ gain_part,
                                                          float* __restrict__ dlog_gain, int B,
-                                                         int H, int nkb) {
+                                                         int H, int ngroups) {
   const int h = blockIdx.x;
   const int lane = threadIdx.x;
   float acc = 0.f;
   for (int b = 0; b < B; ++b)
-    for (int k = lane; k < nkb; k += 64) acc += gain_part[((size_t)b * H + h) * nkb + k];
+    for (int k = lane; k < ngroups; k += 64) acc += gain_part[((size_t)b * H + h) * ngroups + k];
   acc = wave_sum(acc);
   if (lane == 0) dlog_gain[h] = acc;
 }
@@ -596,19 +611,20 @@ hipError_t launch_bwd(const float* q, const float* k, const float* v, const floa
   const int nkb = bwd_num_key_blocks(T);
   timer_begin(kBwdDkdv, stream);
   hipLaunchKernelGGL(ca_bwd_dkdv_kernel<D>, dim3(nkb * BH), dim3(256), lds_bytes, stream, q, k,
-                     v, dout, stats, dvec, log_gain, dk, dv, dsbuf, gain_part, BH, H, T);
+                     v, dout, stats, dvec, log_gain, dk, dv, dsbuf, BH, H, T);
   timer_end(kBwdDkdv, stream);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   timer_begin(kBwdDq, stream);
-  hipLaunchKernelGGL(ca_bwd_dq_kernel<D>, dim3((num_q_tiles(T) + 1) / 2 * BH), dim3(256), 0,
-                     stream, dsbuf, k, log_gain, dq, BH, H, T);
+  const int nqg = dq_num_groups(T);
+  hipLaunchKernelGGL(ca_bwd_dq_kernel<D>, dim3(nqg * BH), dim3(256), 0, stream, dsbuf, q, k,
+                     log_gain, dq, gain_part, BH, H, T);
   timer_end(kBwdDq, stream);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   timer_begin(kBwdGain, stream);
   hipLaunchKernelGGL(ca_bwd_gain_kernel, dim3(H), dim3(64), 0, stream, gain_part, dlog_gain, B,
-                     H, nkb);
+                     H, nqg);
   timer_end(kBwdGain, stream);
   return hipGetLastError();
 }

@@ -19,17 +19,17 @@
 //   dS_r += g_l (R - p_l J2) + g_r p_l J2
 //   dS_l += g_l (L - R + p_l J2) + g_r (R - p_l J2).
 //
-// For |x| >= 0.75 the closed forms, using p_l e^x = p_r and dp = p_r - p_l,
+// For |x| >= 0.5 the closed forms, using p_l e^x = p_r and dp = p_r - p_l,
 //   p_l J0 = dp / x,   R = (p_r - dp/x) / x,   L = dp/x - R,
 //   p_l J2 = (p_r - 2R) / x
-// need a single reciprocal and no ordering of the endpoints.  For |x| < 0.75
+// need a single reciprocal and no ordering of the endpoints.  For |x| < 0.5
 // they cancel, and R = p_l J1(x), L = p_r J1(-x) (mirror identity
 // e^{x}J1(-x) = (J0-J1)(x), pinned in tests/test_oracle.py), with J1 and J2
 // split into even and odd parts J(x) = E(x^2) + x O(x^2) so one evaluation
 // serves both shares.  The polynomial coefficients are fitted (weighted least
 // squares with Lawson reweighting toward minimax relative error) on
-// [-0.75, 0.75]: max relative error 3.8e-9 (J1) and 5.2e-9 (J2) in exact
-// arithmetic, ~2e-7 in float32.  tests/test_device_math.py re-checks these
+// [-0.5, 0.5] with quadratic E and O: max relative error 1.7e-7 (J1) and
+// 2.2e-7 (J2) in exact arithmetic, about float32 resolution.  tests/test_device_math.py re-checks these
 // constants and formulas in float32 against the float64 oracle.
 #pragma once
 #include <hip/hip_runtime.h>
@@ -42,7 +42,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLn2 = 0.69314718055994531f;
 constexpr float kLog2e = 1.44269504088896341f;
-constexpr float kSeriesT = 0.75f;    // |x| below: fitted polynomials; at/above: closed form
+constexpr float kSeriesT = 0.5f;     // |x| below: fitted polynomials; at/above: closed form
 constexpr float kNegBig = -1.0e30f;  // finite "minus infinity" sentinel
 constexpr float kLazyRescale = 8.0f;  // forward keeps p <= 2^8 between rescales
 
@@ -82,24 +82,24 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-__device__ __forceinline__ float poly3(float y, float c0, float c1, float c2, float c3) {
-  return fmaf(fmaf(fmaf(c3, y, c2), y, c1), y, c0);
+__device__ __forceinline__ float poly2(float y, float c0, float c1, float c2) {
+  return fmaf(fmaf(c2, y, c1), y, c0);
 }
 // CA_J1_EVEN
 __device__ __forceinline__ float j1_even(float y) {
-  return poly3(y, 4.999999983e-01f, 1.250001046e-01f, 6.943487325e-03f, 1.763820432e-04f);
+  return poly2(y, 5.000000812e-01f, 1.249939939e-01f, 7.009293473e-03f);
 }
 // CA_J1_ODD
 __device__ __forceinline__ float j1_odd(float y) {
-  return poly3(y, 3.333333406e-01f, 3.333323677e-02f, 1.190763457e-03f, 2.193350522e-05f);
+  return poly2(y, 3.333331177e-01f, 3.333620685e-02f, 1.187037119e-03f);
 }
 // CA_J2_EVEN
 __device__ __forceinline__ float j2_even(float y) {
-  return poly3(y, 3.333333318e-01f, 1.000000935e-01f, 5.951518136e-03f, 1.568314444e-04f);
+  return poly2(y, 3.333334046e-01f, 9.999468968e-02f, 6.009913146e-03f);
 }
 // CA_J2_ODD
 __device__ __forceinline__ float j2_odd(float y) {
-  return poly3(y, 2.500000075e-01f, 2.777767623e-02f, 1.041977470e-03f, 1.968927945e-05f);
+  return poly2(y, 2.499997786e-01f, 2.778081007e-02f, 1.037130167e-03f);
 }
 
 // Forward shares of one segment: L -> left key, R -> right key.

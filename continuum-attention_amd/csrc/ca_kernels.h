@@ -31,6 +31,8 @@ inline size_t fwd_part_floats(int BH, int T, int C) {
 constexpr int kBwdKeys = 62;
 __host__ __device__ inline int bwd_num_key_blocks(int T) { return (T + kBwdKeys - 1) / kBwdKeys; }
 __host__ __device__ inline int num_q_tiles(int T) { return (T + 31) / 32; }
+// dQ work groups (64 queries each) per slice; also the gain partials per slice.
+__host__ __device__ inline int dq_num_groups(int T) { return (num_q_tiles(T) + 1) / 2; }
 inline size_t bwd_ds_floats(int BH, int T) {
   const size_t n = num_q_tiles(T);
   return (size_t)BH * (n * (n + 1) / 2) * 1024 + 256;  // + per-thread dummy words
