@@ -26,6 +26,9 @@ HIPCC_FLAGS = [
     "-fno-honor-nans", "-fno-honor-infinities",
     # packed fp32 VALU forms are disabled on this target
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # keep MFMA accumulators in VGPRs: the dK/dV kernel otherwise shuffles
+    # loop-carried tiles between AGPRs every iteration (~100 moves per tile)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall",
     "-Wno-unused-function",
 ]

@@ -13,8 +13,8 @@
 //                   interleaved 32-query tiles.  Per tile: S^T = K Q^T and
 //                   dP^T = V dY^T by MFMA, W and dS in registers, then
 //                   dV^T += dY^T W and dK^T += Q^T dS by MFMA after an LDS
-//                   transpose.  dS is also written to a packed lower-triangular
-//                   buffer for the dQ pass.
+//                   transpose.  dS is also written, straight from registers,
+//                   as 32x64 row blocks for the dQ pass.
 //   ca_bwd_dq       dQ = c dS K, one work group per (slice, 64 queries); its
 //                   epilogue also forms the gain partial sum_i q_i . dQ_i
 //                   (= sum_ij dS_ij s_ij, since s_ij = c q_i . k_j).
@@ -68,10 +68,6 @@ __global__ __launch_bounds__(256) void ca_bwd_rowdot_kernel(const float* __restr
   if (row < rows && c == 0) dvec[row] = x;
 }
 
-__device__ __forceinline__ size_t tri_block(int qt, int kt) {
-  return (size_t)qt * (qt + 1) / 2 + kt;
-}
-
 template <int D>
 __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
@@ -82,7 +78,6 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
   extern __shared__ float lds[];
 
   const int nqt = num_q_tiles(T);
-  const size_t nblk = (size_t)nqt * (nqt + 1) / 2;
   const int bh = blockIdx.x % BH;
   const int kb = blockIdx.x / BH;  // ascending: heaviest key blocks first
   const int w0 = kBwdKeys * kb;
@@ -145,8 +140,9 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
         accv[mb][nb][r] = 0.f;
         acck[mb][nb][r] = 0.f;
       }
-  float* st_dummy = dsbuf + (((size_t)BH * nblk) << 10) + tid;  // 256 spare words
   const int qt0 = w0 / 32;
+  // dS block index of (this wave's current query tile, kb)
+  long long ds_blk = (long long)bh * ds_blocks_before(nqt) + ds_blocks_before(qt0 + w) + kb;
   // Next query tile of this wave, prefetched into registers while the current
   // tile's dV/dK MFMAs run (32 rows x D floats of Q and of dY, plus row stats).
   constexpr int PF = (32 * P::C4 + 63) / 64;  // float4 per lane per matrix
@@ -304,6 +300,18 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
     else
       segments(std::false_type{});
 
+    // ---- dS row block for the dQ pass: row q, slots 32h..32h+31 ----
+    {
+      float* dst = dsbuf + ((size_t)ds_blk << 11) + q * 64 + 32 * h;
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          *reinterpret_cast<f32x4*>(dst + 16 * b + 4 * c) =
+              f32x4{pacc[b][4 * c], pacc[b][4 * c + 1], pacc[b][4 * c + 2], pacc[b][4 * c + 3]};
+      ds_blk += ds_kb_count(qt) + ds_kb_count(qt + 1) + ds_kb_count(qt + 2) + ds_kb_count(qt + 3);
+    }
+
     // ---- transpose through LDS ----
     {
       float* wrow = Wt + q * P::LDW + 32 * h;
@@ -321,23 +329,8 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
     wave_lds_sync();
     if (qt + 4 < nqt) prefetch(qt + 4);
 
-    // ---- dV^T += dY^T W,  dK^T += Q^T dS,  spill dS ----
+    // ---- dV^T += dY^T W,  dK^T += Q^T dS ----
     // Operands of query row r+1 are read from LDS before the MFMAs of row r.
-    // dS goes to the packed lower-triangular 32x32 blocks of row tile qt:
-    // lane (q, h) writes key w0-1+32nb+q of query rows i0+16h+r.
-    float* st_ptr[2];
-    bool st_ok[2];
-    {
-      float* rowblk = dsbuf + (((size_t)bh * nblk + tri_block(qt, 0)) << 10);
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        const int slot = 32 * nb + q;
-        const int key = w0 - 1 + slot;
-        st_ok[nb] = slot >= 1 && slot <= 62 && key < T && (key >> 5) <= qt;
-        const int kk = st_ok[nb] ? key : 0;
-        st_ptr[nb] = rowblk + ((kk >> 5) << 10) + ((16 * h) << 5) + (kk & 31);
-      }
-    }
     {
       const int col0 = q < D ? q : 0;
       float ado_n[P::NMB], aq_n[P::NMB], bw_n[2], bd_n[2];
@@ -378,16 +371,6 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
             accv[mb][nb] = mfma32(ado[mb], bw[nb], accv[mb][nb]);
             acck[mb][nb] = mfma32(aq[mb], bd[nb], acck[mb][nb]);
           }
-        // spill dS (branch-free: masked lanes write a per-lane dummy word)
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-          bool ok = st_ok[nb];
-          if (need_mask) {
-            const int qi = i0 + 16 * h + r;
-            ok = ok && (w0 - 1 + 32 * nb + q <= qi) && qi < T;
-          }
-          *(ok ? st_ptr[nb] + 32 * r : st_dummy) = bd[nb];
-        }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -432,14 +415,16 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
   }
 }
 
-// dQ = c dS K as a tiled GEMM over the packed lower-triangular dS blocks.
-// Work group: 64 queries (two 32-query tiles) of one slice.  Wave w takes
-// query tile w&1 and the key blocks of parity w>>1; each iteration stages the
-// next 64 K rows (two 32-key blocks) in LDS (double-buffered), so every K block
-// is read from L2 once per work group and shared by two waves.  The dS
-// operand of the next block is prefetched into registers.  The two parities
-// are summed through LDS at the end (fixed order).  The epilogue writes the
-// work group's gain partial sum_i q_i . dQ_i (fixed order).
+// dQ = c dS K as a tiled GEMM over the dS row blocks written by ca_bwd_dkdv.
+// Work group: 64 queries (two 32-query tiles) of one slice.  Per key block kb
+// the 64 K rows of its slots (keys 62kb-1 .. 62kb+62) are staged in LDS
+// (double-buffered) and shared by all four waves: wave w takes query tile
+// w&1 and the slot half w>>1 of the MFMA k-range (lane half h supplies slots
+// 32h + s at k-step s).  Halo slots and invisible keys carry dS = 0, so no
+// masks are needed.  The dS operand of the next block is prefetched into
+// registers.  The two halves are summed through LDS at the end (fixed
+// order), and the epilogue writes the work group's gain partial
+// sum_i q_i . dQ_i (fixed order).
 template <int D>
 __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict__ dsbuf,
                                                         const float* __restrict__ Q,
@@ -455,19 +440,22 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   __shared__ float red[2 * P::NMB * 16 * 64];
   __shared__ float gred[2];
   const int nqt = num_q_tiles(T);
-  const int nqg = (nqt + 1) / 2;
-  const size_t nblk = (size_t)nqt * (nqt + 1) / 2;
+  const int nqg = dq_num_groups(T);
+  const int nkb = bwd_num_key_blocks(T);
   const int bh = blockIdx.x % BH;
   const int qg = nqg - 1 - blockIdx.x / BH;  // heaviest (longest rows) first
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, q = lane & 31, h = lane >> 5;
   const int qsub = w & 1, par = w >> 1;
   const int qt = 2 * qg + qsub;
   const bool wave_on = qt < nqt;
-  const int i = 32 * qt + q;
   const size_t slice = (size_t)bh * T * D;
   const float c = head_scale_log2(log_gain, bh % H, D) * kLn2;
-  const int nkb = min(2 * qg + 2, nqt);
-  const int iters = (nkb + 1) / 2;
+  // key blocks met by this wave's tile and by the work group's last tile
+  const int my_kb = wave_on ? min(ds_kb_count(qt), nkb) : 0;
+  const int iters = min(ds_kb_count(min(2 * qg + 1, nqt - 1)), nkb);
+  const float* arow = dsbuf +
+                      (((size_t)bh * ds_blocks_before(nqt) + ds_blocks_before(wave_on ? qt : 0)) << 11) +
+                      q * 64 + 32 * h + 16 * par;
 
   f32x16 acc[P::NMB];
 #pragma unroll
@@ -476,14 +464,15 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
     for (int r = 0; r < 16; ++r) acc[nb][r] = 0.f;
 
   f32x4 pre[KLD];
-  auto load_k = [&](int it) {
+  auto load_k = [&](int kb) {
 #pragma unroll
     for (int j = 0; j < KLD; ++j) {
       const int e = tid + 256 * j;
       f32x4 v = {0.f, 0.f, 0.f, 0.f};
       if (e < KF4) {
-        const int key = 64 * it + e / P::C4;
-        if (key < T) v = reinterpret_cast<const f32x4*>(K + slice + (size_t)key * D)[e % P::C4];
+        const int key = kBwdKeys * kb - 1 + e / P::C4;
+        if (key >= 0 && key < T)
+          v = reinterpret_cast<const f32x4*>(K + slice + (size_t)key * D)[e % P::C4];
       }
       pre[j] = v;
     }
@@ -495,37 +484,30 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
       if (e < KF4) kst[buf][e] = pre[j];
     }
   };
-  auto load_a = [&](int kt, float* a) {
-    const float* blk = dsbuf + (((size_t)bh * nblk + tri_block(qt, kt)) << 10);
-    const f32x4* arow = reinterpret_cast<const f32x4*>(blk + (q << 5) + 16 * h);
+  auto load_a = [&](int kb, float* a) {
+    const f32x4* src = reinterpret_cast<const f32x4*>(arow + ((size_t)kb << 11));
 #pragma unroll
     for (int c4 = 0; c4 < 4; ++c4) {
-      const f32x4 v4 = arow[c4];
+      const f32x4 v4 = src[c4];
       a[4 * c4 + 0] = v4[0]; a[4 * c4 + 1] = v4[1]; a[4 * c4 + 2] = v4[2]; a[4 * c4 + 3] = v4[3];
     }
   };
 
   float a_next[16];
-  if (wave_on && par <= qt) load_a(par, a_next);
+  if (my_kb > 0) load_a(0, a_next);
   load_k(0);
   store_k(0);
   __syncthreads();
   const int dcol = (q < D) ? q : 0;
   for (int it = 0; it < iters; ++it) {
     const int buf = it & 1;
-    const int kt = 2 * it + par;
     if (it + 1 < iters) load_k(it + 1);
-    if (wave_on && kt <= qt) {
+    if (it < my_kb) {
       float a[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) a[r] = a_next[r];
-      if (kt + 2 <= qt) load_a(kt + 2, a_next);
-      const int kbase = 32 * kt + 16 * h;
-      if (kt == qt || i >= T) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) a[r] = (kbase + r <= i && i < T) ? a[r] : 0.f;
-      }
-      const float* kb = reinterpret_cast<const float*>(&kst[buf][0]) + (32 * par + 16 * h) * D + dcol;
+      if (it + 1 < my_kb) load_a(it + 1, a_next);
+      const float* kb = reinterpret_cast<const float*>(&kst[buf][0]) + (32 * h + 16 * par) * D + dcol;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
 #pragma unroll

@@ -33,9 +33,41 @@ __host__ __device__ inline int bwd_num_key_blocks(int T) { return (T + kBwdKeys 
 __host__ __device__ inline int num_q_tiles(int T) { return (T + 31) / 32; }
 // dQ work groups (64 queries each) per slice; also the gain partials per slice.
 __host__ __device__ inline int dq_num_groups(int T) { return (num_q_tiles(T) + 1) / 2; }
+
+// sum_{i=0}^{n-1} floor((a*i + b) / m) for n, m >= 1 and a, b >= 0 (Euclid-like
+// reduction, O(log m) steps).
+__host__ __device__ inline long long floor_sum(long long n, long long m, long long a, long long b) {
+  long long ans = 0;
+  while (true) {
+    if (a >= m) {
+      ans += (n - 1) * n / 2 * (a / m);
+      a %= m;
+    }
+    if (b >= m) {
+      ans += n * (b / m);
+      b %= m;
+    }
+    const long long y_max = a * n + b;
+    if (y_max < m) break;
+    n = y_max / m;
+    b = y_max % m;
+    const long long t = m;
+    m = a;
+    a = t;
+  }
+  return ans;
+}
+
+// dS blocks for the dQ pass: one 32-query x 64-slot block (row-major, slot s
+// of key block kb is key 62*kb - 1 + s) for every query tile qt and key block
+// kb that meets it (62*kb <= 32*qt + 31).  Blocks are stored qt-major, kb
+// ascending, so a dQ work group reads its rows contiguously.
+__host__ __device__ inline int ds_kb_count(int qt) { return (32 * qt + 31) / kBwdKeys + 1; }
+__host__ __device__ inline long long ds_blocks_before(int qt) {
+  return qt <= 0 ? 0 : qt + floor_sum(qt, kBwdKeys, 32, 31);
+}
 inline size_t bwd_ds_floats(int BH, int T) {
-  const size_t n = num_q_tiles(T);
-  return (size_t)BH * (n * (n + 1) / 2) * 1024 + 256;  // + per-thread dummy words
+  return (size_t)BH * (size_t)ds_blocks_before(num_q_tiles(T)) * 2048;
 }
 
 // Per-kernel HIP-event timing (diagnostics; off unless ca_timing_enable(1)).
