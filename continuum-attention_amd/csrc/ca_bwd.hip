@@ -463,6 +463,19 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[nb][r] = 0.f;
 
+  // Every row of dS sums to zero (the weights are invariant to a common score
+  // shift), so dQ_i = c sum_j dS_ij (k_j - k_ref) for any k_ref.  The staged
+  // keys are taken relative to the key at the group's first query: when
+  // neighbouring keys nearly coincide the products stay small instead of
+  // cancelling in fp32 (|k| ~ 1 against |k_j - k_ref| ~ 1e-2 in the
+  // near-duplicate-key case), and the gain partial sum_i q_i . dQ_i inherits
+  // the same accuracy.
+  f32x4 kref[KLD];
+  {
+    const f32x4* kr = reinterpret_cast<const f32x4*>(K + slice + (size_t)(64 * qg) * D);
+#pragma unroll
+    for (int j = 0; j < KLD; ++j) kref[j] = kr[(tid + 256 * j) % P::C4];
+  }
   f32x4 pre[KLD];
   auto load_k = [&](int kb) {
 #pragma unroll
@@ -472,7 +485,7 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
       if (e < KF4) {
         const int key = kBwdKeys * kb - 1 + e / P::C4;
         if (key >= 0 && key < T)
-          v = reinterpret_cast<const f32x4*>(K + slice + (size_t)key * D)[e % P::C4];
+          v = reinterpret_cast<const f32x4*>(K + slice + (size_t)key * D)[e % P::C4] - kref[j];
       }
       pre[j] = v;
     }

@@ -252,3 +252,30 @@ def ca_forward_rows(q, k, v, log_gain, b, h, rows):
     s = (q[b, h, rows] @ k[b, h, :T].T) * c
     W = ca_weights(s, rows)[0]
     return W @ v[b, h, :T]
+
+
+def ca_backward_rows(q, k, v, log_gain, dy, b, h, rows):
+    """Backward restricted to selected query rows of one (b, h) slice.
+
+    Returns ``(dq_rows, dk_part, dv_part, drho_part)``: ``dq_rows`` are the
+    complete dQ of those rows (row i of dS depends only on row i of S), and
+    ``dk_part``/``dv_part`` (``[T, D]``) and ``drho_part`` are the rows'
+    contributions to dK, dV and dRho (cuda/continuum_attention.py:754-764).
+    For the suffix ``rows = [T-n, T)`` the parts are the complete dK and dV
+    of keys ``j >= T-n`` (only queries ``i >= j`` see key j), which lets a
+    long-T test check exact gradients without the ``[T, T]`` problem.
+    """
+    q = np.asarray(q, np.float64); k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64); dy = np.asarray(dy, np.float64)
+    T, D = q.shape[-2:]
+    c = head_scale(log_gain, D)[h]
+    rows = np.asarray(rows)
+    n = int(rows.max()) + 1
+    s = (q[b, h, rows] @ k[b, h, :n].T) * c
+    W = ca_weights(s, rows)[0]
+    gw = dy[b, h, rows] @ v[b, h, :n].T
+    ds = ca_weights_vjp(s, gw, W, rows)
+    dk = np.zeros((T, D)); dv = np.zeros((T, D))
+    dv[:n] = W.T @ dy[b, h, rows]
+    dk[:n] = c * (ds.T @ q[b, h, rows])
+    return c * (ds @ k[b, h, :n]), dk, dv, float((ds * s).sum())

@@ -244,6 +244,36 @@ def test_operator_gradients_vs_finite_differences():
     _fd_check((2, 1, 6, 3), 12, [-0.4])
 
 
+def test_backward_rows_decomposition():
+    """The row-restricted backward used by the long-T GPU test: its dQ rows
+    equal the full backward's, the row sets' dK/dV/dRho parts sum to the full
+    gradients, and a suffix of rows alone gives the complete dK/dV of the
+    suffix keys.  The full backward is pinned by autograd and finite
+    differences above, so a wrong slice or transposition here fails."""
+    rng = np.random.default_rng(21)
+    shape = (2, 2, 45, 8)
+    q, k, v, dy = (rng.standard_normal(shape) * 1.5 for _ in range(4))
+    rho = np.array([0.2, -0.5])
+    dq, dk, dv, drho = O.ca_backward(q, k, v, rho, dy)
+    b, h, T = 1, 1, shape[2]
+    parts = [np.arange(0, 7), np.array([7, 8, 20, 33]), np.setdiff1d(np.arange(9, T), [20, 33])]
+    acc_k = np.zeros((T, 8)); acc_v = np.zeros((T, 8)); acc_r = 0.0
+    for rows in parts:
+        dq_r, dk_p, dv_p, dr_p = O.ca_backward_rows(q, k, v, rho, dy, b, h, rows)
+        np.testing.assert_allclose(dq_r, dq[b, h, rows], atol=1e-13)
+        acc_k += dk_p; acc_v += dv_p; acc_r += dr_p
+    np.testing.assert_allclose(acc_k, dk[b, h], atol=1e-13)
+    np.testing.assert_allclose(acc_v, dv[b, h], atol=1e-13)
+    # drho sums over batches: batch 0 of head 1 adds the rest
+    full0 = O.ca_backward_rows(q, k, v, rho, dy, 0, h, np.arange(T))[3]
+    assert acc_r + full0 == pytest.approx(drho[h], abs=1e-12)
+    suffix = np.arange(30, T)
+    _, dk_s, dv_s, _ = O.ca_backward_rows(q, k, v, rho, dy, b, h, suffix)
+    np.testing.assert_allclose(dk_s[30:], dk[b, h, 30:], atol=1e-13)
+    np.testing.assert_allclose(dv_s[30:], dv[b, h, 30:], atol=1e-13)
+    assert np.abs(dk_s[:30] - dk[b, h, :30]).max() > 1e-3  # earlier keys are incomplete
+
+
 def test_reference_ca_check_case():
     """cuda/continuum_attention.py:1363-1401 (ca_check): [1,2,9,8], tile 4,
     seed 1234: the fp32 CPU port agrees with the fp64 oracle (fwd <= 2e-5,
