@@ -35,12 +35,14 @@ SIGNATURES = {
     "ca_bwd_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "ca_bwd_f32": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
                         _i, _i, _i, _i, _vp]),
+    "ca_weights_f32": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "ca_weights_bwd_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "ca_timing_enable": (_i, [_i]),
     "ca_timing_read": (_i, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i), _i]),
 }
 
 KERNEL_NAMES = ("ca_fwd", "ca_fwd_combine", "ca_bwd_rowdot", "ca_bwd_dkdv", "ca_bwd_dq",
-                "ca_bwd_gain")
+                "ca_bwd_gain", "ca_weights", "ca_weights_bwd")
 
 _lib = None
 

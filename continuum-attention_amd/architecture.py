@@ -1,0 +1,189 @@
+"""Small-variant caller of the CA operator: ``CausalAttention`` and ``TinyLM``.
+
+Counterpart of the reference's architecture.py:108-245 (the TinyStories
+backbone: variants A/B/F/G are ordinary causal softmax, P/R/S/H exact
+continuous memory).  Module names, parameter shapes, initialisation and
+state-dict keys are the reference's, so its checkpoints load unchanged and the
+parameter budgets agree (5,008,640 / 5,008,664 at seq_len 192, test_acma.py:
+21-26; 5,090,560 / 5,090,584 at 512, test_hp_only.py:13-23).
+
+Backends for the continuous variants (all run the HIP kernels, none has a CPU
+path):
+
+* ``'hip'``: the fused operator ``continuum_attention`` (no ``[T, T]`` tensor);
+  the variant's q scaling (``1/tau`` or ``exp(log_qk_gain)``) is applied to q
+  before the call and the operator gets ``log_gain = 0``, so its own scale is
+  the reference's ``1/sqrt(D)`` (architecture.py:134-146).
+* ``'hip_weights'``: materialised logits -> ``continuous_attention_weights``
+  (HIP row kernels) -> ``W @ v``, the reference backend's structure
+  (architecture.py:146-177).
+* The reference's own backend names are accepted for drop-in use:
+  ``'reference'`` and ``'mixed'``, and the Metal ones ``'metal_weights'``,
+  ``'metal_analytic'`` and ``'metal_long'``, map to ``'hip_weights'``
+  (identical weights); ``'metal_direct'`` maps to ``'hip'``.
+
+The softmax variants use torch's softmax / SDPA exactly as the reference does
+(architecture.py:157-161); they are not part of the CA operator.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+from torch import nn
+from torch.nn import functional as F
+
+from .ops import continuum_attention
+from .weights import continuous_attention_weights
+
+VARIANTS = ("A", "B", "F", "G", "P", "R", "S", "H")
+_BACKEND_MAP = {"hip": "hip", "hip_weights": "hip_weights", "reference": "hip_weights",
+                "mixed": "hip_weights", "metal_weights": "hip_weights",
+                "metal_analytic": "hip_weights", "metal_long": "hip_weights",
+                "metal_direct": "hip"}
+
+
+class RMSNorm(nn.Module):
+    """x / rms(x) * weight, eps 1e-5 (architecture.py:21-29)."""
+
+    def __init__(self, width, eps=1e-5):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(width))
+        self.eps = eps
+
+    def forward(self, x):
+        return x * torch.rsqrt(x.square().mean(dim=-1, keepdim=True) + self.eps) * self.weight
+
+
+class CausalAttention(nn.Module):
+    """Multi-head causal attention with the reference's eight variants
+    (architecture.py:108-177)."""
+
+    def __init__(self, width, heads, seq_len, variant="B", backend="hip", fixed_tau=0.30):
+        super().__init__()
+        if variant not in VARIANTS:
+            raise ValueError("variant must be A, B, F, G, P, R, S or H")
+        if backend not in _BACKEND_MAP:
+            raise ValueError("backend must be one of " + ", ".join(_BACKEND_MAP))
+        if width % heads:
+            raise ValueError("width must be divisible by heads")
+        if fixed_tau <= 0:
+            raise ValueError("fixed_tau must be > 0")
+        self.variant = variant
+        self.backend = backend
+        self.path = _BACKEND_MAP[backend]
+        self.heads = heads
+        self.width = width
+        self.head_dim = width // heads
+        self.fixed_tau = float(fixed_tau)
+        self.continuous = variant in ("P", "R", "S", "H")
+        if variant in ("F", "G", "S", "H"):
+            g0 = -math.log(0.30) if variant in ("G", "H") else 0.0
+            self.log_qk_gain = nn.Parameter(torch.full((heads,), g0))
+        self.qkv = nn.Linear(width, 3 * width, bias=False)
+        self.out = nn.Linear(width, width, bias=False)
+        self.register_buffer("causal_mask", torch.ones(seq_len, seq_len, dtype=torch.bool).tril(),
+                             persistent=False)
+
+    def _qkv(self, x):
+        Bsz, T, _ = x.shape
+        q, k, v = (t.view(Bsz, T, self.heads, self.head_dim).transpose(1, 2)
+                   for t in self.qkv(x).chunk(3, dim=-1))
+        if self.variant in ("B", "P"):
+            q = q * (1.0 / self.fixed_tau)
+        elif self.variant in ("F", "G", "S", "H"):
+            q = q * self.log_qk_gain.exp().view(1, -1, 1, 1)
+        return q, k, v
+
+    def _logits(self, q, k):
+        return (q @ k.transpose(-2, -1).contiguous()) * (self.head_dim ** -0.5)
+
+    def _weights(self, q, k, v=None):
+        logits = self._logits(q, k)
+        if self.continuous:
+            return continuous_attention_weights(logits)
+        T = q.size(-2)
+        return F.softmax(logits.masked_fill(~self.causal_mask[:T, :T], -torch.inf), dim=-1)
+
+    def attention_weights(self, x):
+        q, k, v = self._qkv(x)
+        return self._weights(q, k, v)
+
+    def forward(self, x):
+        Bsz, T, _ = x.shape
+        q, k, v = self._qkv(x)
+        if self.continuous and self.path == "hip":
+            zero = torch.zeros(self.heads, device=q.device, dtype=torch.float32)
+            y = continuum_attention(q, k, v, zero)
+        elif not self.continuous and self.backend != "reference":
+            y = F.scaled_dot_product_attention(q, k, v, is_causal=True, dropout_p=0.0)
+        else:
+            y = self._weights(q, k, v) @ v
+        return self.out(y.transpose(1, 2).reshape(Bsz, T, self.width))
+
+
+class SwiGLU(nn.Module):
+    def __init__(self, width, hidden):
+        super().__init__()
+        self.gate_up = nn.Linear(width, 2 * hidden, bias=False)
+        self.down = nn.Linear(hidden, width, bias=False)
+
+    def forward(self, x):
+        gate, value = self.gate_up(x).chunk(2, dim=-1)
+        return self.down(F.silu(gate) * value)
+
+
+class Block(nn.Module):
+    def __init__(self, width, hidden, heads, seq_len, variant, backend, fixed_tau):
+        super().__init__()
+        self.norm_attn = RMSNorm(width)
+        self.attn = CausalAttention(width, heads, seq_len, variant, backend, fixed_tau)
+        self.norm_mlp = RMSNorm(width)
+        self.mlp = SwiGLU(width, hidden)
+
+    def forward(self, x):
+        x = x + self.attn(self.norm_attn(x))
+        return x + self.mlp(self.norm_mlp(x))
+
+
+class TinyLM(nn.Module):
+    """Pre-norm byte LM with learned positions and a tied head
+    (architecture.py:180-241).  ``layers`` defaults to the reference's six
+    blocks ``b0 .. b5``; BASELINE's CA-P configuration uses four."""
+
+    def __init__(self, variant="B", backend="hip", seq_len=192, width=256, hidden=720, heads=4,
+                 fixed_tau=0.30, layers=6):
+        super().__init__()
+        if layers < 1:
+            raise ValueError("layers must be >= 1")
+        self.seq_len = seq_len
+        self.variant = variant
+        self.layers = layers
+        self.tok_embed = nn.Embedding(256, width)
+        self.pos_embed = nn.Embedding(seq_len, width)
+        for i in range(layers):
+            self.add_module(f"b{i}", Block(width, hidden, heads, seq_len, variant, backend, fixed_tau))
+        self.final_norm = RMSNorm(width)
+        self.lm_head = nn.Linear(width, 256, bias=False)
+        self.lm_head.weight = self.tok_embed.weight
+        self.apply(self._init_weights)
+
+    @staticmethod
+    def _init_weights(module):
+        if isinstance(module, (nn.Linear, nn.Embedding)):
+            nn.init.normal_(module.weight, mean=0.0, std=0.02)
+
+    def forward(self, tokens):
+        _, length = tokens.shape
+        if length > self.seq_len:
+            raise ValueError("Sequence exceeds model seq_len")
+        pos = torch.arange(length, device=tokens.device)
+        x = self.tok_embed(tokens) + self.pos_embed(pos)[None, :, :]
+        for i in range(self.layers):
+            x = getattr(self, f"b{i}")(x)
+        return self.lm_head(self.final_norm(x))
+
+
+def parameters(model):
+    """Trainable parameter count (architecture.py:244-245)."""
+    return sum(p.numel() for p in model.parameters() if p.requires_grad)

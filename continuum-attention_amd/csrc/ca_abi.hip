@@ -222,4 +222,45 @@ int ca_bwd_f32(const float* q, const float* k, const float* v, const float* log_
   return CA_OK;
 }
 
+static int check_rows(const char* fn, int BH, int Q, int K, int start) {
+  if (BH <= 0 || Q <= 0 || K <= 0 || start < 0)
+    return fail(CA_ERR_INVALID, "%s: invalid shape BH=%d Q=%d K=%d start=%d", fn, BH, Q, K, start);
+  if ((long long)start + Q > K)
+    return fail(CA_ERR_INVALID,
+                "%s: queries start..start+Q-1 = %d..%lld need their keys, but K=%d < start+Q", fn,
+                start, (long long)start + Q - 1, K);
+  if ((long long)BH * Q > (1ll << 31) - 1)
+    return fail(CA_ERR_UNSUPPORTED, "%s: BH*Q=%lld rows exceed 2^31-1", fn, (long long)BH * Q);
+  return CA_OK;
+}
+
+int ca_weights_f32(const float* scores, float* weights, float* stats, int BH, int Q, int K,
+                   int start, void* stream) {
+  int rc = check_rows("ca_weights_f32", BH, Q, K, start);
+  if (rc) return rc;
+  if (!scores || !weights || !stats) return fail(CA_ERR_INVALID, "ca_weights_f32: null pointer");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  ca::timer_begin(ca::kWeights, s);
+  hipError_t e = ca::launch_weights(scores, weights, stats, BH, Q, K, start, s);
+  ca::timer_end(ca::kWeights, s);
+  if (e != hipSuccess) return fail(CA_ERR_HIP, "ca_weights_f32 launch: %s", hipGetErrorString(e));
+  return CA_OK;
+}
+
+int ca_weights_bwd_f32(const float* scores, const float* grad_weights, float* weights,
+                       float* grad_scores, int BH, int Q, int K, int start, void* stream) {
+  int rc = check_rows("ca_weights_bwd_f32", BH, Q, K, start);
+  if (rc) return rc;
+  if (!scores || !grad_weights || !grad_scores)
+    return fail(CA_ERR_INVALID, "ca_weights_bwd_f32: null pointer");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  ca::timer_begin(ca::kWeightsBwd, s);
+  hipError_t e = ca::launch_weights_bwd(scores, grad_weights, weights, grad_scores, BH, Q, K,
+                                        start, s);
+  ca::timer_end(ca::kWeightsBwd, s);
+  if (e != hipSuccess)
+    return fail(CA_ERR_HIP, "ca_weights_bwd_f32 launch: %s", hipGetErrorString(e));
+  return CA_OK;
+}
+
 }  // extern "C"

@@ -103,11 +103,11 @@ __device__ __forceinline__ float j2_odd(float y) {
 }
 
 // Forward shares of one segment: L -> left key, R -> right key.
-// sl/sr are log2-unit scores relative to the row shift, pl/pr = 2^sl, 2^sr.
+// x is the signed natural score difference s_r - s_l; pl/pr are the endpoint
+// weights relative to the row shift.  seg_shares takes log2-unit scores sl/sr
+// (pl/pr = 2^sl, 2^sr) instead of x.
 // Both branches are evaluated and selected (no divergent control flow).
-__device__ __forceinline__ void seg_shares(float sl, float sr, float pl, float pr, float& L,
-                                           float& R) {
-  const float x = (sr - sl) * kLn2;
+__device__ __forceinline__ void seg_shares_x(float x, float pl, float pr, float& L, float& R) {
   const float dp = pr - pl;
   const float inv_x = fast_rcp(x);
   const float a = dp * inv_x;           // p_l J0
@@ -121,13 +121,15 @@ __device__ __forceinline__ void seg_shares(float sl, float sr, float pl, float p
   R = small ? rs : rc;
   L = small ? ls : lc;
 }
+__device__ __forceinline__ void seg_shares(float sl, float sr, float pl, float pr, float& L,
+                                           float& R) {
+  seg_shares_x((sr - sl) * kLn2, pl, pr, L, R);
+}
 
 // Forward shares and score-gradient contributions of one segment.
 // gl/gr are the centred, 1/Z-scaled weight gradients g = (dY.v - Dl) / Z.
-__device__ __forceinline__ void seg_shares_grad(float sl, float sr, float pl, float pr, float gl,
-                                                float gr, float& L, float& R, float& dL,
-                                                float& dR) {
-  const float x = (sr - sl) * kLn2;
+__device__ __forceinline__ void seg_shares_grad_x(float x, float pl, float pr, float gl, float gr,
+                                                  float& L, float& R, float& dL, float& dR) {
   const float dp = pr - pl;
   const float inv_x = fast_rcp(x);
   const float a = dp * inv_x;
@@ -146,6 +148,16 @@ __device__ __forceinline__ void seg_shares_grad(float sl, float sr, float pl, fl
   const float xm = R - j2;  // p_l (J1 - J2)
   dR = fmaf(gl, xm, gr * j2);
   dL = fmaf(gl, L - xm, gr * xm);
+}
+__device__ __forceinline__ void seg_shares_grad(float sl, float sr, float pl, float pr, float gl,
+                                                float gr, float& L, float& R, float& dL,
+                                                float& dR) {
+  seg_shares_grad_x((sr - sl) * kLn2, pl, pr, gl, gr, L, R, dL, dR);
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
 }
 
 // 32x32x2 MFMA output layout: register r of lane l holds row

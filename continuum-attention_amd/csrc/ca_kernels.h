@@ -71,9 +71,18 @@ inline size_t bwd_ds_floats(int BH, int T) {
 }
 
 // Per-kernel HIP-event timing (diagnostics; off unless ca_timing_enable(1)).
-enum KernelId { kFwd = 0, kFwdCombine, kBwdRowdot, kBwdDkdv, kBwdDq, kBwdGain, kNumKernels };
+enum KernelId {
+  kFwd = 0, kFwdCombine, kBwdRowdot, kBwdDkdv, kBwdDq, kBwdGain, kWeights, kWeightsBwd, kNumKernels
+};
 void timer_begin(int id, hipStream_t s);
 void timer_end(int id, hipStream_t s);
+
+// Weight-materialising row kernels (ca_weights.hip).
+hipError_t launch_weights(const float* scores, float* weights, float* stats, int BH, int Q, int K,
+                          int start, hipStream_t stream);
+hipError_t launch_weights_bwd(const float* scores, const float* grad_weights, float* weights,
+                              float* grad_scores, int BH, int Q, int K, int start,
+                              hipStream_t stream);
 
 template <int D>
 hipError_t launch_fwd(const float* q, const float* k, const float* v, const float* log_gain,

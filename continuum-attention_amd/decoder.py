@@ -1,0 +1,237 @@
+"""CA-S byte decoder: the reference's main caller of the CA operator.
+
+Counterpart of ``ContinuumDecoderConfig`` / ``ContinuumDecoderLM``
+(cuda/continuum_attention.py:784-923): a pre-norm decoder with RMSNorm
+(eps 1e-6), interleaved RoPE (theta 1e4), exact Continuum Attention with a
+learned per-head score gain ``log_qk_gain`` (init 0, tau = 1), tanh-GELU MLP
+and an untied byte head.  Module names, parameter shapes, initialisation
+(std .02, residual projections .02/sqrt(2L)) and state-dict keys are the
+reference's, so its checkpoints load unchanged; the default configuration has
+101,205,120 parameters (cuda/test_cpu.py:25-27).
+
+Only the attention operator is this package's: ``continuum_attention`` runs
+the HIP kernels with float32 scores whatever the autocast dtype, and returns
+``v.dtype``.  ``train_step`` is one optimisation step as the reference's
+training loop takes it (cuda/continuum_attention.py:1195-1230): autocast
+forward + cross-entropy, backward, gradient clipping, AdamW.
+"""
+from __future__ import annotations
+
+import contextlib
+import math
+from dataclasses import dataclass
+
+import torch
+from torch import nn
+from torch.nn import functional as F
+
+from .ops import continuum_attention
+
+
+@dataclass
+class ContinuumDecoderConfig:
+    """Decoder hyper-parameters (cuda/continuum_attention.py:784-814)."""
+    vocab_size: int = 256
+    block_size: int = 2048
+    d_model: int = 1024
+    n_heads: int = 16
+    n_layers: int = 8
+    mlp_ratio: float = 4.0
+    dropout: float = 0.0
+    eps: float = 1e-6
+    rope_theta: float = 10000.0
+    grad_checkpointing: bool = False
+    ca_query_tile: int = 64
+
+    def __post_init__(self):
+        if self.d_model % self.n_heads:
+            raise ValueError("d_model must be divisible by n_heads")
+        if (self.d_model // self.n_heads) % 2:
+            raise ValueError("RoPE needs even head dimension")
+        if self.n_layers <= 0 or self.block_size < 2 or self.ca_query_tile <= 0:
+            raise ValueError("Invalid layer, context or CA query tile count")
+        if self.dropout != 0:
+            raise ValueError("The CA operator has no attention dropout; use --dropout 0.0")
+
+
+class RMSNorm(nn.Module):
+    """weight * x / rms(x) (cuda/continuum_attention.py:817-823)."""
+
+    def __init__(self, dim, eps=1e-6):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(dim))
+        self.eps = eps
+
+    def forward(self, x):
+        return self.weight * x * torch.rsqrt(x.square().mean(-1, keepdim=True) + self.eps)
+
+
+_ROPE_CACHE: dict = {}
+
+
+def _rope_tables(T, D, theta, device, dtype):
+    """cos/sin of position x frequency, each frequency repeated for its pair,
+    in ``dtype`` (cuda/continuum_attention.py:826-831); cached per shape."""
+    key = (T, D, float(theta), device, dtype)
+    tab = _ROPE_CACHE.get(key)
+    if tab is None:
+        freq = 1.0 / (theta ** (torch.arange(0, D, 2, device=device, dtype=torch.float32) / D))
+        phase = torch.outer(torch.arange(T, device=device, dtype=torch.float32), freq)
+        cos = phase.cos().repeat_interleave(2, -1).to(dtype)[None, None]
+        sin = phase.sin().repeat_interleave(2, -1).to(dtype)[None, None]
+        tab = (cos, sin)
+        if len(_ROPE_CACHE) > 64:
+            _ROPE_CACHE.clear()
+        _ROPE_CACHE[key] = tab
+    return tab
+
+
+def _rotate_pairs(t):
+    """(x0, x1) -> (-x1, x0) for each interleaved pair of the last axis."""
+    pairs = t.unflatten(-1, (-1, 2))
+    return torch.stack((-pairs[..., 1], pairs[..., 0]), -1).flatten(-2)
+
+
+def apply_rope(q, k, theta):
+    """Interleaved rotary embedding at each position, computed in q's dtype
+    (cuda/continuum_attention.py:826-835)."""
+    cos, sin = _rope_tables(q.shape[-2], q.shape[-1], theta, q.device, q.dtype)
+    return q * cos + _rotate_pairs(q) * sin, k * cos + _rotate_pairs(k) * sin
+
+
+class ContinuumSelfAttention(nn.Module):
+    """qkv projection -> RoPE -> CA operator -> output projection
+    (cuda/continuum_attention.py:838-854)."""
+
+    def __init__(self, dim, heads, rope_theta, ca_query_tile):
+        super().__init__()
+        self.heads = heads
+        self.head_dim = dim // heads
+        self.rope_theta = rope_theta
+        self.ca_query_tile = ca_query_tile
+        self.qkv = nn.Linear(dim, 3 * dim, bias=False)
+        self.out = nn.Linear(dim, dim, bias=False)
+        self.out._residual_proj = True
+        # positive per-head score gain exp(log_qk_gain), starting at 1
+        self.log_qk_gain = nn.Parameter(torch.zeros(heads))
+
+    def forward(self, x):
+        Bsz, T, C = x.shape
+        q, k, v = self.qkv(x).view(Bsz, T, 3, self.heads, self.head_dim).permute(2, 0, 3, 1, 4).unbind(0)
+        q, k = apply_rope(q, k, self.rope_theta)
+        y = continuum_attention(q, k, v, self.log_qk_gain, self.ca_query_tile)
+        return self.out(y.transpose(1, 2).reshape(Bsz, T, C))
+
+
+class GELUMLP(nn.Module):
+    """fc1 -> tanh-GELU -> fc2 (cuda/continuum_attention.py:857-866)."""
+
+    def __init__(self, dim, ratio, dropout):
+        super().__init__()
+        hidden = int(dim * ratio)
+        self.fc1 = nn.Linear(dim, hidden, bias=False)
+        self.fc2 = nn.Linear(hidden, dim, bias=False)
+        self.fc2._residual_proj = True
+        self.dropout = nn.Dropout(dropout)
+
+    def forward(self, x):
+        return self.fc2(self.dropout(F.gelu(self.fc1(x), approximate="tanh")))
+
+
+class CADecoderBlock(nn.Module):
+    def __init__(self, cfg):
+        super().__init__()
+        self.norm1 = RMSNorm(cfg.d_model, cfg.eps)
+        self.attn = ContinuumSelfAttention(cfg.d_model, cfg.n_heads, cfg.rope_theta, cfg.ca_query_tile)
+        self.norm2 = RMSNorm(cfg.d_model, cfg.eps)
+        self.mlp = GELUMLP(cfg.d_model, cfg.mlp_ratio, cfg.dropout)
+
+    def forward(self, x):
+        x = x + self.attn(self.norm1(x))
+        return x + self.mlp(self.norm2(x))
+
+
+class ContinuumDecoderLM(nn.Module):
+    """Byte decoder with exact Continuum Attention
+    (cuda/continuum_attention.py:882-923)."""
+
+    def __init__(self, cfg: ContinuumDecoderConfig):
+        super().__init__()
+        self.cfg = cfg
+        self.byte_emb = nn.Embedding(cfg.vocab_size, cfg.d_model)
+        self.drop = nn.Dropout(cfg.dropout)
+        self.blocks = nn.ModuleList([CADecoderBlock(cfg) for _ in range(cfg.n_layers)])
+        self.norm_f = RMSNorm(cfg.d_model, cfg.eps)
+        self.lm_head = nn.Linear(cfg.d_model, cfg.vocab_size, bias=False)  # untied
+        self.residual_layers = cfg.n_layers
+        self.residual_init_scale = 1.0 / math.sqrt(2.0 * cfg.n_layers)
+        self.apply(self._init_weights)
+
+    def _init_weights(self, m):
+        if isinstance(m, nn.Linear):
+            std = 0.02 * self.residual_init_scale if getattr(m, "_residual_proj", False) else 0.02
+            nn.init.normal_(m.weight, mean=0, std=std)
+        elif isinstance(m, nn.Embedding):
+            nn.init.normal_(m.weight, mean=0, std=0.02)
+
+    def forward(self, input_ids, targets=None):
+        if input_ids.dim() != 2 or input_ids.shape[1] > self.cfg.block_size:
+            raise ValueError("Input must be [B,T] with T<=block_size")
+        x = self.drop(self.byte_emb(input_ids))
+        for block in self.blocks:
+            if self.cfg.grad_checkpointing and self.training:
+                x = torch.utils.checkpoint.checkpoint(block, x, use_reentrant=False)
+            else:
+                x = block(x)
+        logits = self.lm_head(self.norm_f(x))
+        out = {"logits": logits}
+        if targets is not None:
+            V = self.cfg.vocab_size
+            out["loss"] = F.cross_entropy(logits[:, :-1, :].reshape(-1, V), targets[:, 1:].reshape(-1),
+                                          reduction="mean")
+        return out
+
+    def parameter_breakdown(self):
+        return {"byte_embedding": _numel(self.byte_emb), "decoder_blocks": _numel(self.blocks),
+                "continuum_head_gains": self.cfg.n_layers * self.cfg.n_heads,
+                "final_norm": _numel(self.norm_f), "lm_head": _numel(self.lm_head)}
+
+
+def _numel(module):
+    return sum(p.numel() for p in module.parameters())
+
+
+def count_parameters(model):
+    """``{'total', 'trainable'}`` parameter counts (cuda/runtime.py:63-66)."""
+    ps = list(model.parameters())
+    return {"total": sum(p.numel() for p in ps),
+            "trainable": sum(p.numel() for p in ps if p.requires_grad)}
+
+
+def build_adamw(model, lr=3e-4, weight_decay=0.1, betas=(0.9, 0.95)):
+    """AdamW over all parameters (cuda/runtime.py:87-88, defaults
+    cuda/continuum_attention.py:960-966); the fused multi-tensor kernel when
+    the device supports it."""
+    params = list(model.parameters())
+    on_gpu = all(p.is_cuda for p in params)
+    try:
+        return torch.optim.AdamW(params, lr=lr, weight_decay=weight_decay, betas=betas, fused=on_gpu)
+    except (RuntimeError, TypeError):
+        return torch.optim.AdamW(params, lr=lr, weight_decay=weight_decay, betas=betas)
+
+
+def train_step(model, optimizer, batch, amp_dtype=torch.bfloat16, grad_clip=1.0):
+    """One optimisation step on a ``[B, T]`` byte batch (next-byte targets from
+    the batch itself, as cuda/continuum_attention.py:1205-1228): autocast
+    forward + loss, backward, clip to ``grad_clip``, AdamW.  Returns the loss
+    tensor (no host synchronisation)."""
+    optimizer.zero_grad(set_to_none=True)
+    amp = (torch.autocast(device_type="cuda", dtype=amp_dtype) if amp_dtype is not None
+           else contextlib.nullcontext())
+    with amp:
+        loss = model(batch, targets=batch)["loss"]
+    loss.backward()
+    if grad_clip and grad_clip > 0:
+        torch.nn.utils.clip_grad_norm_(model.parameters(), grad_clip)
+    optimizer.step()
+    return loss.detach()

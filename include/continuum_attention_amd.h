@@ -69,6 +69,27 @@ int ca_bwd_f32(const float* q, const float* k, const float* v, const float* log_
                float* dv, float* dlog_gain, void* workspace, size_t workspace_bytes, int B, int H,
                int T, int D, void* stream);
 
+/* ---- Weight-materialising row kernels -------------------------------------
+ * scores, grad_weights, weights and grad_scores are [BH][Q][K] fp32 (K
+ * fastest); row (b, r) is query start + r and sees keys 0 .. start + r, so
+ * start + Q <= K is required.  Entries of keys beyond a row's visible prefix
+ * are written as exact zeros.  Scores are the scaled logits (natural units). */
+
+/* Exact CA weights W and row statistics stats[BH*Q][2] = (row max m, 1/Z).
+ * Replaces: ext.forward(scores, start) -> [W, stats]
+ * (cuda/continuum_attention.py:578-590, kernel ca_weights_kernel :136-163). */
+int ca_weights_f32(const float* scores, float* weights, float* stats, int BH, int Q, int K,
+                   int start, void* stream);
+
+/* Score VJP: grad_scores = dL/dscores given grad_weights = dL/dW, with the
+ * weighted row mean computed in the kernel; also writes W when weights is not
+ * NULL.  Replaces: ext.backward_fused(scores, gw, start) -> [W, dS]
+ * (cuda/continuum_attention.py:538-554, kernel ca_backward_fused_kernel
+ * :230-293); ext.backward(scores, W, stats, gw, means, start) -> dS
+ * (:592-605) computes the same dS. */
+int ca_weights_bwd_f32(const float* scores, const float* grad_weights, float* weights,
+                       float* grad_scores, int BH, int Q, int K, int start, void* stream);
+
 /* ---- Diagnostics (no counterpart in the reference; used by bench.py) -------
  * Per-kernel timing with HIP events recorded on the launch stream around each
  * kernel launch of the calls above.  Kernel ids: 0 forward, 1 forward split

@@ -1,0 +1,228 @@
+"""GPU parity of the weight-materialising kernels and of the operator's callers.
+
+* ``ca_weights`` / ``continuous_attention_weights`` / ``ca_weights_backward``
+  (csrc/ca_weights.hip through the C ABI) against the float64 oracle
+  (oracle/ca_oracle.py: ``ca_weights``, ``ca_weights_vjp``); bars 1e-4 on
+  weights, 1e-3 on score gradients (max|x-ref|/max|ref|), exact zeros beyond
+  each row's prefix; the reference tests' weight properties
+  (test_fusion.py:27-35, test_acma.py:104-110,127-138).
+* ``CausalAttention`` with the fused operator ('hip') against the
+  materialised path ('hip_weights') and against a float64 composition with
+  the oracle; ``TinyLM`` causality (test_acma.py:118-126) and controls
+  (test_acma.py:140-146); one CA-S decoder training step and decoder logits
+  against a float64 CPU model whose attention is the oracle.
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ca_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def rel(a, b):
+    a = np.asarray(a, np.float64); b = np.asarray(b, np.float64)
+    den = np.abs(b).max()
+    return float(np.abs(a - b).max() / (den if den > 0 else 1.0))
+
+
+@pytest.mark.parametrize("T,mag", [(1, 1.0), (2, 1.0), (7, 1.0), (15, 1.0), (63, 2.0), (64, 0.0),
+                                   (65, 4.0), (257, 1.0), (1000, 3.0)])
+def test_weights_and_vjp_vs_oracle(gpu_ca, T, mag):
+    say(f"[case] weights T={T} mag={mag}")
+    g = torch.Generator().manual_seed(T)
+    s = torch.randn(2, 3, T, T, generator=g) * mag
+    gw = torch.randn(2, 3, T, T, generator=g)
+    sd = s.cuda().requires_grad_(True)
+    W = gpu_ca.continuous_attention_weights(sd)
+    (ds,) = torch.autograd.grad(W, sd, gw.cuda())
+    Wo = O.ca_weights(s.double().numpy())[0]
+    dso = O.ca_weights_vjp(s.double().numpy(), gw.double().numpy())
+    W, ds = W.detach().cpu().numpy(), ds.cpu().numpy()
+    ew, eds = rel(W, Wo), rel(ds, dso)
+    say(f"   W {ew:.2e} dS {eds:.2e}")
+    assert ew <= 1e-4 and eds <= 1e-3
+    fut = np.triu(np.ones((T, T), bool), 1)
+    assert np.all(W[..., fut] == 0.0) and np.all(ds[..., fut] == 0.0)
+    assert np.all(W >= 0.0)
+    np.testing.assert_allclose(W.sum(-1), 1.0, atol=2e-6)
+
+
+def test_weights_query_tile_offset_and_stats(gpu_ca):
+    """ext.forward(scores, start) semantics: a tile of queries start..start+Q-1
+    over K >= start+Q keys (cuda/continuum_attention.py:622-648); stats are the
+    row max and 1/Z; ext.backward_fused returns (W, dS)."""
+    say("[case] weights tile offset")
+    g = torch.Generator().manual_seed(9)
+    K, start, Q = 300, 128, 64
+    s = torch.randn(4, Q, K, generator=g) * 2.0
+    gw = torch.randn(4, Q, K, generator=g)
+    W, stats = gpu_ca.ca_weights(s.cuda(), start)
+    W2, ds = gpu_ca.ca_weights_backward(s.cuda(), gw.cuda(), start, return_weights=True)
+    qidx = np.arange(start, start + Q)
+    Wo, mo, zo = O.ca_weights(s.double().numpy(), qidx)
+    dso = O.ca_weights_vjp(s.double().numpy(), gw.double().numpy(), qidx=qidx)
+    W, W2, ds, stats = (x.cpu().numpy() for x in (W, W2, ds, stats))
+    assert rel(W, Wo) <= 1e-4 and rel(W2, Wo) <= 1e-4
+    assert rel(ds, dso) <= 1e-3
+    np.testing.assert_allclose(stats[:, 0], mo.reshape(-1), rtol=0, atol=1e-6)
+    np.testing.assert_allclose(stats[:, 1], 1.0 / zo.reshape(-1), rtol=1e-5)
+    for r in range(Q):
+        assert np.all(W[:, r, start + r + 1:] == 0.0)
+    with pytest.raises(ValueError):
+        gpu_ca.ca_weights(s[:, :, :start + Q - 1].contiguous().cuda(), start)
+
+
+def test_weight_properties_from_reference_tests(gpu_ca):
+    """test_fusion.py:27-35 (non-negative, rows sum to 1, W00 = 1),
+    test_acma.py:104-110 (scores receive finite non-zero gradients),
+    test_acma.py:127-138 (not plain softmax)."""
+    say("[case] weight properties")
+    torch.manual_seed(22)
+    s = torch.randn(2, 3, 15, 15, device="cuda")
+    W = gpu_ca.continuous_attention_weights(s)
+    assert (W >= 0).all().item()
+    torch.testing.assert_close(W.sum(-1), torch.ones_like(W.sum(-1)), atol=1e-6, rtol=1e-6)
+    torch.testing.assert_close(W[..., 0, 0], torch.ones_like(W[..., 0, 0]))
+    logits = torch.randn(2, 2, 7, 7, device="cuda", requires_grad=True)
+    w = gpu_ca.continuous_attention_weights(logits)
+    (w * torch.randn_like(w)).sum().backward()
+    assert torch.isfinite(logits.grad).all().item() and logits.grad.abs().sum().item() > 0
+    lg = torch.tensor([[[[0., 0., 0.], [0., 2., 0.], [1., -1., 3.]]]], device="cuda")
+    w = gpu_ca.continuous_attention_weights(lg)
+    causal = torch.ones(3, 3, dtype=torch.bool, device="cuda").tril()
+    std = torch.softmax(lg.masked_fill(~causal, -torch.inf), -1)
+    assert (w - std).abs().sum().item() > .01
+
+
+def _oracle_attention_np(x, attn):
+    """float64 composition of CausalAttention.forward with the oracle weights."""
+    Wqkv = attn.qkv.weight.detach().double().cpu().numpy()
+    Wout = attn.out.weight.detach().double().cpu().numpy()
+    B, T, C = x.shape
+    H, Dh = attn.heads, attn.head_dim
+    qkv = x @ Wqkv.T
+    q, k, v = (qkv[..., i * C:(i + 1) * C].reshape(B, T, H, Dh).transpose(0, 2, 1, 3) for i in range(3))
+    if attn.variant in ("B", "P"):
+        q = q / attn.fixed_tau
+    elif attn.variant in ("F", "G", "S", "H"):
+        q = q * np.exp(attn.log_qk_gain.detach().double().cpu().numpy())[None, :, None, None]
+    y = O.ca_forward(q, k, v, np.zeros(H))[0]
+    return y.transpose(0, 2, 1, 3).reshape(B, T, C) @ Wout.T
+
+
+@pytest.mark.parametrize("variant", ["P", "R", "S", "H"])
+def test_causal_attention_fused_vs_weights_vs_oracle(gpu_ca, variant):
+    say(f"[case] CausalAttention variant {variant}")
+    A = gpu_ca.architecture
+    torch.manual_seed(11)
+    x = torch.randn(2, 70, 128)
+    outs, grads = {}, {}
+    for backend in ("hip", "hip_weights"):
+        torch.manual_seed(1)
+        attn = A.CausalAttention(128, 2, 128, variant=variant, backend=backend).cuda()
+        xd = x.cuda().requires_grad_(True)
+        y = attn(xd)
+        params = [xd, attn.qkv.weight] + ([attn.log_qk_gain] if hasattr(attn, "log_qk_gain") else [])
+        grads[backend] = [gg.cpu().numpy() for gg in torch.autograd.grad((y * y).sum(), params)]
+        outs[backend] = y.detach().cpu().numpy()
+    ref = _oracle_attention_np(x.double().numpy(), attn)
+    e_f, e_w = rel(outs["hip"], ref), rel(outs["hip_weights"], ref)
+    say(f"   out fused {e_f:.2e} weights {e_w:.2e}")
+    assert e_f <= 1e-4 and e_w <= 1e-4
+    for a, b in zip(grads["hip"], grads["hip_weights"]):
+        assert rel(a, b) <= 1e-3
+
+
+def test_tinylm_no_future_leak_and_controls(gpu_ca):
+    """test_acma.py:118-126 (a prefix's logits do not see later tokens) and
+    test_acma.py:140-146 (R == S at initialisation, exactly)."""
+    say("[case] TinyLM causality")
+    A = gpu_ca.architecture
+    ids = torch.randint(0, 256, (2, 13), device="cuda")
+    mod = ids.clone()
+    mod[:, 7:] = torch.randint(0, 256, (2, 6), device="cuda")
+    for backend in ("hip", "hip_weights"):
+        for variant in ("P", "R", "S"):
+            torch.manual_seed(97)
+            m = A.TinyLM(variant=variant, backend=backend, seq_len=16, width=32, hidden=64,
+                         heads=4).cuda().eval()
+            with torch.no_grad():
+                torch.testing.assert_close(m(ids)[:, :7], m(mod)[:, :7], atol=2e-5, rtol=2e-5)
+    with torch.no_grad():
+        torch.manual_seed(97)
+        r = A.TinyLM(variant="R", seq_len=16, width=32, hidden=64, heads=4).cuda()
+        torch.manual_seed(97)
+        s = A.TinyLM(variant="S", seq_len=16, width=32, hidden=64, heads=4).cuda()
+        torch.testing.assert_close(r(ids), s(ids), atol=0, rtol=0)
+
+
+def test_tinylm_512_finite(gpu_ca):
+    """test_long.py:54-61."""
+    A = gpu_ca.architecture
+    torch.manual_seed(1729)
+    m = A.TinyLM(variant="S", seq_len=512, width=32, hidden=64, heads=4).cuda()
+    with torch.no_grad():
+        out = m(torch.randint(0, 256, (1, 512), device="cuda"))
+    assert tuple(out.shape) == (1, 512, 256) and torch.isfinite(out).all().item()
+
+
+class _OracleCA(torch.autograd.Function):
+    """Float64 CPU attention through the oracle (forward only)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, log_gain, query_tile=64):
+        y = O.ca_forward(q.numpy(), k.numpy(), v.numpy(), log_gain.detach().numpy())[0]
+        return torch.from_numpy(y)
+
+
+def test_decoder_logits_vs_float64_oracle_model(gpu_ca, monkeypatch):
+    """Small CA-S decoder: fp32 GPU logits against a float64 CPU copy of the
+    same model whose attention is the oracle."""
+    say("[case] decoder logits vs float64 oracle model")
+    Dm = gpu_ca.decoder
+    cfg = Dm.ContinuumDecoderConfig(d_model=128, n_heads=2, n_layers=2, block_size=96)
+    torch.manual_seed(4)
+    m = Dm.ContinuumDecoderLM(cfg)
+    with torch.no_grad():
+        for blk in m.blocks:
+            blk.attn.log_qk_gain.copy_(torch.tensor([0.3, -0.2]))
+    ids = torch.randint(0, 256, (2, 96))
+    with torch.no_grad():
+        got = m.cuda()(ids.cuda())["logits"].cpu().numpy()
+        m64 = Dm.ContinuumDecoderLM(cfg).double()
+        m64.load_state_dict({k: v.double().cpu() for k, v in m.state_dict().items()})
+        monkeypatch.setattr(Dm, "continuum_attention",
+                            lambda q, k, v, g, t=64: _OracleCA.apply(q, k, v, g, t))
+        ref = m64(ids)["logits"].numpy()
+    e = rel(got, ref)
+    say(f"   logits rel {e:.2e}")
+    assert e <= 1e-4
+
+
+def test_decoder_train_step_bf16(gpu_ca):
+    """One CA-S training step (bf16 autocast, fp32 CA scores): finite loss near
+    ln 256 at initialisation, finite gradients reaching every gain."""
+    say("[case] decoder train step")
+    Dm = gpu_ca.decoder
+    cfg = Dm.ContinuumDecoderConfig(d_model=256, n_heads=4, n_layers=2, block_size=256)
+    torch.manual_seed(0)
+    m = Dm.ContinuumDecoderLM(cfg).cuda()
+    opt = Dm.build_adamw(m)
+    batch = torch.randint(0, 256, (2, 256), device="cuda")
+    g0 = [b.attn.log_qk_gain.detach().clone() for b in m.blocks]
+    loss = Dm.train_step(m, opt, batch)
+    torch.cuda.synchronize()
+    assert abs(loss.item() - np.log(256)) < 0.1
+    for b, g in zip(m.blocks, g0):
+        assert b.attn.log_qk_gain.grad is not None
+        assert torch.isfinite(b.attn.log_qk_gain.grad).all().item()
+        assert not torch.equal(b.attn.log_qk_gain.detach(), g)  # the step moved the gains

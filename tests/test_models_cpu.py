@@ -1,0 +1,164 @@
+"""CPU checks of the operator's callers (continuum-attention_amd/architecture.py
+and decoder.py): parameter budgets, initialisation, configuration errors,
+state-dict layout, RoPE, and that the CA path has no CPU fallback.
+
+Expected values come from the reference's own tests: test_acma.py:21-34,
+140-154; test_hp_only.py:13-23; test_fusion.py:17-25; cuda/test_cpu.py:25-27.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+
+@pytest.fixture(scope="module")
+def A(ca):
+    return ca.architecture
+
+
+@pytest.fixture(scope="module")
+def Dm(ca):
+    return ca.decoder
+
+
+def tiny(A, variant, backend="hip", seed=97):
+    torch.manual_seed(seed)
+    return A.TinyLM(variant=variant, backend=backend, seq_len=16, width=32, hidden=64, heads=4,
+                    fixed_tau=.30)
+
+
+@pytest.mark.parametrize("variant,T,count", [("B", 192, 5_008_640), ("P", 192, 5_008_640),
+                                             ("R", 192, 5_008_640), ("F", 192, 5_008_664),
+                                             ("S", 192, 5_008_664), ("H", 192, 5_008_664),
+                                             ("H", 512, 5_090_584), ("P", 512, 5_090_560)])
+def test_tinylm_parameter_budget(A, variant, T, count):
+    """test_acma.py:21-26, test_hp_only.py:13-23."""
+    m = A.TinyLM(variant=variant, backend="hip", seq_len=T)
+    assert A.parameters(m) == count
+
+
+def test_ca_p_four_layer_budget(A):
+    """BASELINE's CA-P configuration: 4 blocks of the TinyLM backbone at T=512."""
+    m = A.TinyLM(variant="P", seq_len=512, layers=4)
+    assert A.parameters(m) == 3_459_328
+    assert not hasattr(m, "b4")
+
+
+def test_h_variant_gain_init(A):
+    """test_hp_only.py:19-20: H starts at tau = 0.30."""
+    m = A.TinyLM(variant="H", seq_len=192)
+    assert m.b0.attn.continuous
+    assert torch.exp(-m.b0.attn.log_qk_gain).mean().item() == pytest.approx(0.3, abs=1e-6)
+
+
+def test_shared_initial_weights_equal(A):
+    """test_acma.py:28-34: every variant starts from the same weights."""
+    states = {v: tiny(A, v).state_dict() for v in ("A", "B", "F", "P", "R", "S")}
+    common = set.intersection(*(set(s) for s in states.values()))
+    assert len(common) >= 40
+    for key in common:
+        for v in states:
+            assert torch.equal(states["B"][key], states[v][key]), key
+
+
+def test_state_dict_keys_follow_reference_names(A, Dm):
+    m = tiny(A, "S")
+    keys = set(m.state_dict())
+    for k in ("tok_embed.weight", "pos_embed.weight", "b0.attn.qkv.weight", "b0.attn.out.weight",
+              "b0.attn.log_qk_gain", "b5.mlp.gate_up.weight", "b5.mlp.down.weight",
+              "b3.norm_attn.weight", "b3.norm_mlp.weight", "final_norm.weight", "lm_head.weight"):
+        assert k in keys, k
+    cfg = Dm.ContinuumDecoderConfig(d_model=64, n_heads=4, n_layers=2, block_size=32)
+    d = Dm.ContinuumDecoderLM(cfg)
+    keys = set(d.state_dict())
+    for k in ("byte_emb.weight", "blocks.0.norm1.weight", "blocks.0.attn.qkv.weight",
+              "blocks.0.attn.out.weight", "blocks.0.attn.log_qk_gain", "blocks.1.norm2.weight",
+              "blocks.1.mlp.fc1.weight", "blocks.1.mlp.fc2.weight", "norm_f.weight", "lm_head.weight"):
+        assert k in keys, k
+
+
+def test_softmax_controls_on_cpu(A):
+    """Softmax variants use torch only (test_acma.py:140-154, test_fusion.py:17-25):
+    A == F initially (gain exp(0) = 1), reference weights == SDPA path."""
+    torch.manual_seed(5)
+    ids = torch.randint(0, 256, (1, 13))
+    with torch.no_grad():
+        torch.testing.assert_close(tiny(A, "A")(ids), tiny(A, "F")(ids), atol=0, rtol=0)
+        for v in ("B", "F"):
+            torch.testing.assert_close(tiny(A, v, "reference")(ids), tiny(A, v, "mixed")(ids),
+                                       atol=3e-5, rtol=3e-5)
+
+
+def test_ca_variants_have_no_cpu_path(A, ca):
+    """The CA operator and weights run on ROCm tensors only: CPU input raises."""
+    ids = torch.randint(0, 256, (1, 9))
+    for backend in ("hip", "hip_weights"):
+        with pytest.raises(RuntimeError, match="GPU"):
+            tiny(A, "P", backend)(ids)
+    with pytest.raises(RuntimeError, match="GPU"):
+        ca.continuous_attention_weights(torch.randn(1, 1, 4, 4))
+    with pytest.raises(ValueError, match="square"):
+        ca.continuous_attention_weights(torch.randn(1, 1, 3, 4))
+
+
+def test_bad_variant_backend_and_config(A, Dm):
+    with pytest.raises(ValueError):
+        A.CausalAttention(32, 4, 16, variant="Q")
+    with pytest.raises(ValueError):
+        A.CausalAttention(32, 4, 16, variant="P", backend="cuda")
+    with pytest.raises(ValueError):
+        A.CausalAttention(30, 4, 16)
+    with pytest.raises(ValueError):
+        A.CausalAttention(32, 4, 16, fixed_tau=0.0)
+    with pytest.raises(ValueError, match="divisible"):
+        Dm.ContinuumDecoderConfig(d_model=100, n_heads=3)
+    with pytest.raises(ValueError, match="RoPE"):
+        Dm.ContinuumDecoderConfig(d_model=12, n_heads=4)
+    with pytest.raises(ValueError, match="dropout"):
+        Dm.ContinuumDecoderConfig(dropout=0.1)
+    with pytest.raises(ValueError):
+        Dm.ContinuumDecoderConfig(n_layers=0)
+    cfg = Dm.ContinuumDecoderConfig(d_model=32, n_heads=2, n_layers=1, block_size=8)
+    with pytest.raises(ValueError, match="block_size"):
+        Dm.ContinuumDecoderLM(cfg)(torch.zeros(1, 9, dtype=torch.long))
+
+
+def test_ca_s_parameter_budget(Dm):
+    """cuda/test_cpu.py:25-27: the default CA-S decoder has 101,205,120 parameters."""
+    m = Dm.ContinuumDecoderLM(Dm.ContinuumDecoderConfig())
+    assert Dm.count_parameters(m) == {"total": 101_205_120, "trainable": 101_205_120}
+    br = m.parameter_breakdown()
+    assert sum(br.values()) - br["continuum_head_gains"] == 101_205_120
+    assert br["continuum_head_gains"] == 8 * 16
+
+
+def test_ca_s_initialisation(Dm):
+    """std .02, residual projections .02/sqrt(2L), untied head, gains 0."""
+    torch.manual_seed(0)
+    cfg = Dm.ContinuumDecoderConfig(d_model=256, n_heads=4, n_layers=8, block_size=64)
+    m = Dm.ContinuumDecoderLM(cfg)
+    b = m.blocks[3]
+    assert b.attn.qkv.weight.std().item() == pytest.approx(0.02, rel=0.02)
+    assert b.mlp.fc1.weight.std().item() == pytest.approx(0.02, rel=0.02)
+    assert b.attn.out.weight.std().item() == pytest.approx(0.02 / 4.0, rel=0.03)
+    assert b.mlp.fc2.weight.std().item() == pytest.approx(0.02 / 4.0, rel=0.03)
+    assert m.lm_head.weight.data_ptr() != m.byte_emb.weight.data_ptr()
+    assert torch.equal(b.attn.log_qk_gain, torch.zeros(4))
+
+
+def test_rope_matches_complex_rotation(Dm):
+    """Interleaved RoPE equals multiplying each pair (x0 + i x1) by
+    exp(i * pos * theta^(-2k/D)) -- an independent formulation."""
+    torch.manual_seed(3)
+    B, H, T, D, theta = 2, 3, 17, 8, 10000.0
+    q, k = torch.randn(B, H, T, D, dtype=torch.float64), torch.randn(B, H, T, D, dtype=torch.float64)
+    qr, kr = Dm.apply_rope(q.float(), k.float(), theta)
+    pos = np.arange(T)[:, None]
+    freq = theta ** (-np.arange(0, D, 2) / D)
+    rot = np.exp(1j * pos * freq)
+    for x, xr in ((q, qr), (k, kr)):
+        z = x.numpy()[..., 0::2] + 1j * x.numpy()[..., 1::2]
+        z = z * rot
+        ref = np.stack([z.real, z.imag], -1).reshape(B, H, T, D)
+        np.testing.assert_allclose(xr.numpy(), ref, atol=2e-6, rtol=0)
