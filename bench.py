@@ -12,6 +12,11 @@ Prints ONE JSON line (rank 0).  `value` is the median fwd+bwd milliseconds
 recorded around each kernel launch on the launch stream during the timed
 steps; `cpu_baseline` times the CPU port of the reference's PyTorch CPU path
 (oracle/ca_cpu_port.py) on a bounded sample of the same workload.
+
+Two more BASELINE workloads ride along on the same line (skip with
+--no-models): `ca_s`, the CA-S decoder training step in tokens/s (config 4,
+the metric's "CA-S tokens/s"), and `ca_p`, the small CA-P decoder step
+(config 3); each reports its step time and the share spent in CA kernels.
 """
 from __future__ import annotations
 
@@ -79,18 +84,96 @@ def cpu_baseline(sample_heads=4, reps=3):
             "cpu_model": model, "os_cpu_count": os.cpu_count(), "affinity": threads}
 
 
+def _timed_steps(ca, step, steps, warmup):
+    """Runs `warmup` untimed and `steps` timed calls of step(i); returns
+    (ms per step from HIP events on the current stream, CA kernel ms per step)."""
+    import torch
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    ca.native.timing_enable(True)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        out = step(i)
+    e1.record()
+    torch.cuda.synchronize()
+    kt = ca.native.timing_read()
+    ca.native.timing_enable(False)
+    ca_ms = sum(t for t, c in kt.values()) / steps
+    return e0.elapsed_time(e1) / steps, ca_ms, out
+
+
+def bench_ca_s(ca, dev, steps=10, warmup=3):
+    """one CA-S decoder training step (101,205,120 params,
+    T=2048, batch 1, bf16 autocast with fp32 CA scores, AdamW + clip 1.0) on
+    uniform-random bytes, random-init weights."""
+    import torch
+    Dm = ca.decoder
+    torch.manual_seed(0)
+    cfg = Dm.ContinuumDecoderConfig()
+    model = Dm.ContinuumDecoderLM(cfg).to(dev)
+    nparams = Dm.count_parameters(model)["total"]
+    opt = Dm.build_adamw(model)
+    g = torch.Generator().manual_seed(1)
+    batches = [torch.randint(0, 256, (1, cfg.block_size), generator=g).to(dev) for _ in range(4)]
+    ms, ca_ms, loss = _timed_steps(ca, lambda i: Dm.train_step(model, opt, batches[i % 4]), steps,
+                                   warmup)
+    tokens = cfg.block_size
+    res = {"metric": "CA-S tokens/s", "tokens_per_s": round(tokens / (ms * 1e-3), 1),
+           "ms_per_step": round(ms, 3), "ca_kernels_ms_per_step": round(ca_ms, 3),
+           "steps": steps, "warmup": warmup, "params": nparams, "loss": round(float(loss), 4),
+           "dtype": "bf16 autocast, f32 CA scores", "data": "synthetic uniform bytes",
+           "config": {"workload": "CA-S decoder train step (BASELINE config 4)", "d_model": cfg.d_model,
+                      "n_layers": cfg.n_layers, "n_heads": cfg.n_heads, "T": cfg.block_size,
+                      "batch": 1, "optimizer": "AdamW lr 3e-4 wd 0.1 betas (.9,.95), clip 1.0"}}
+    del model, opt
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_ca_p(ca, dev, steps=10, warmup=3):
+    """small CA-P decoder (TinyLM backbone with 4 blocks,
+    d 256, 4 heads, fixed tau 0.30, T=512, batch 16), one fp32 step on
+    uniform-random bytes, random-init weights."""
+    import torch
+    A = ca.architecture
+    torch.manual_seed(0)
+    model = A.TinyLM(variant="P", backend="hip", seq_len=512, width=256, hidden=720, heads=4,
+                     fixed_tau=0.30, layers=4).to(dev)
+    opt = A.build_adamw(model)
+    g = torch.Generator().manual_seed(2)
+    data = [torch.randint(0, 256, (16, 513), generator=g).to(dev) for _ in range(4)]
+    ms, ca_ms, loss = _timed_steps(
+        ca, lambda i: A.train_step(model, opt, data[i % 4][:, :-1], data[i % 4][:, 1:]), steps, warmup)
+    tokens = 16 * 512
+    res = {"metric": "CA-P tokens/s", "tokens_per_s": round(tokens / (ms * 1e-3), 1),
+           "ms_per_step": round(ms, 3), "ca_kernels_ms_per_step": round(ca_ms, 3),
+           "steps": steps, "warmup": warmup, "params": A.parameters(model),
+           "loss": round(float(loss), 4), "dtype": "f32", "data": "synthetic uniform bytes",
+           "config": {"workload": "CA-P TinyLM train step (BASELINE config 3)", "layers": 4,
+                      "width": 256, "heads": 4, "T": 512, "batch": 16, "fixed_tau": 0.30}}
+    del model, opt
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-models", action="store_true",
+                    help="skip the CA-S (config 4) and CA-P (config 3) training-step legs")
+    ap.add_argument("--only", choices=["ca_s", "ca_p"], default=None,
+                    help="run only one model-step leg and print its JSON (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device copy (to scale rocprof FETCH/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
-              "the CA operator shards trivially over (batch, head) slices -- see DESIGN.md",
+              "the CA operator shards over independent (batch, head) slices with no communication",
               file=sys.stderr)
         sys.exit(2)
 
@@ -108,6 +191,10 @@ def main():
     ca = importlib.import_module("continuum-attention_amd")
     ca.native.load()
     dev = torch.device("cuda:0")
+    if args.only:
+        leg = {"ca_s": bench_ca_s, "ca_p": bench_ca_p}[args.only]
+        print(json.dumps(leg(ca, dev, steps=args.steps, warmup=args.warmup)), flush=True)
+        return
     torch.backends.cuda.matmul.allow_tf32 = False
 
     B, H, T, D = SHAPE
@@ -198,6 +285,9 @@ def main():
                 out["roofline"]["traffic"] = rec["total_bytes"]
                 out["roofline"]["traffic_source"] = (
                     f"profiles/ca_op_2x16x2048x64_hbm_traffic.md (commit {tr.get('commit')})")
+    if not args.no_models:
+        out["ca_s"] = bench_ca_s(ca, dev)
+        out["ca_p"] = bench_ca_p(ca, dev)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)

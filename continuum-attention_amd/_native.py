@@ -20,6 +20,7 @@ CA_ERR_INVALID = 1
 CA_ERR_UNSUPPORTED = 2
 CA_ERR_WORKSPACE = 3
 CA_ERR_HIP = 4
+CA_DTYPE_F32, CA_DTYPE_BF16, CA_DTYPE_F16 = 0, 1, 2
 ABI_VERSION = 1
 
 _vp = ctypes.c_void_p
@@ -37,12 +38,17 @@ SIGNATURES = {
                         _i, _i, _i, _i, _vp]),
     "ca_weights_f32": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "ca_weights_bwd_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "ca_qkv_rope_in": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "ca_qkv_rope_grad": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
+    "ca_heads_to_tokens": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _vp]),
+    "ca_tokens_to_heads": (_i, [_vp, _i, _vp, _i, _i, _i, _i, _vp]),
     "ca_timing_enable": (_i, [_i]),
     "ca_timing_read": (_i, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i), _i]),
 }
 
 KERNEL_NAMES = ("ca_fwd", "ca_fwd_combine", "ca_bwd_rowdot", "ca_bwd_dkdv", "ca_bwd_dq",
-                "ca_bwd_gain", "ca_weights", "ca_weights_bwd")
+                "ca_bwd_gain", "ca_weights", "ca_weights_bwd", "ca_qkv_in", "ca_qkv_grad",
+                "ca_relayout")
 
 _lib = None
 

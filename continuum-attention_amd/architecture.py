@@ -187,3 +187,31 @@ class TinyLM(nn.Module):
 def parameters(model):
     """Trainable parameter count (architecture.py:244-245)."""
     return sum(p.numel() for p in model.parameters() if p.requires_grad)
+
+
+def build_adamw(model, lr=4e-4, weight_decay=0.1, geometry_lr_mult=8.0):
+    """AdamW as the reference trains TinyLM (benchmark.py:189-201): learned
+    gains get ``lr * geometry_lr_mult`` and no weight decay; betas (.9, .95).
+    Uses the fused multi-tensor kernel on the GPU."""
+    gains = [p for n, p in model.named_parameters() if n.endswith("log_qk_gain")]
+    dense = [p for n, p in model.named_parameters() if not n.endswith("log_qk_gain")]
+    groups = [{"params": dense, "lr": lr, "weight_decay": weight_decay}]
+    if gains:
+        groups.append({"params": gains, "lr": lr * geometry_lr_mult, "weight_decay": 0.0})
+    fused = all(p.is_cuda for p in model.parameters())
+    try:
+        return torch.optim.AdamW(groups, betas=(0.9, 0.95), fused=fused)
+    except (RuntimeError, TypeError):
+        return torch.optim.AdamW(groups, betas=(0.9, 0.95))
+
+
+def train_step(model, optimizer, x, target, grad_clip=1.0):
+    """One TinyLM step (benchmark.py:207-214): cross-entropy of the byte
+    logits, backward, clip to ``grad_clip``, AdamW.  Returns the loss tensor."""
+    logits = model(x)
+    loss = F.cross_entropy(logits.reshape(-1, 256), target.reshape(-1))
+    optimizer.zero_grad(set_to_none=True)
+    loss.backward()
+    torch.nn.utils.clip_grad_norm_(model.parameters(), grad_clip)
+    optimizer.step()
+    return loss.detach()

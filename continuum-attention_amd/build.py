@@ -13,7 +13,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libca_hip.so")
-SOURCES = ["ca_fwd.hip", "ca_bwd.hip", "ca_weights.hip", "ca_abi.hip"]
+SOURCES = ["ca_fwd.hip", "ca_bwd.hip", "ca_weights.hip", "ca_rope.hip", "ca_abi.hip"]
 ARCH = os.environ.get("CA_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [
@@ -24,7 +24,8 @@ HIPCC_FLAGS = [
     "-ffp-contract=fast",
     # no NaN or infinity is ever produced or tested; lets fmax/fmin skip canonicalisation
     "-fno-honor-nans", "-fno-honor-infinities",
-    # packed fp32 VALU forms are disabled on this target
+    # packed fp32 VALU forms are disabled: some of them have returned wrong
+    # results on this GPU pool with no error
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     # keep MFMA accumulators in VGPRs: the dK/dV kernel otherwise shuffles
     # loop-carried tiles between AGPRs every iteration (~100 moves per tile)

@@ -263,4 +263,78 @@ int ca_weights_bwd_f32(const float* scores, const float* grad_weights, float* we
   return CA_OK;
 }
 
+static int check_prologue(const char* fn, int B, int T, int H, int D, int dtype) {
+  if (B <= 0 || T <= 0 || H <= 0 || D <= 0)
+    return fail(CA_ERR_INVALID, "%s: invalid shape B=%d T=%d H=%d D=%d", fn, B, T, H, D);
+  if (D % 4)
+    return fail(CA_ERR_UNSUPPORTED, "%s: head dim D=%d must be a multiple of 4", fn, D);
+  if (dtype != CA_DTYPE_F32 && dtype != CA_DTYPE_BF16 && dtype != CA_DTYPE_F16)
+    return fail(CA_ERR_INVALID, "%s: unknown dtype code %d", fn, dtype);
+  if ((long long)B * T * 3 * H * D > (1ll << 40))
+    return fail(CA_ERR_UNSUPPORTED, "%s: tensor too large", fn);
+  return CA_OK;
+}
+
+static bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+static size_t dtype_align(int dtype) { return dtype == CA_DTYPE_F32 ? 16 : 8; }
+
+int ca_qkv_rope_in(const void* qkv, int dtype, const float* rope_cs, float* q, float* k, float* v,
+                   int B, int T, int H, int D, void* stream) {
+  int rc = check_prologue("ca_qkv_rope_in", B, T, H, D, dtype);
+  if (rc) return rc;
+  if (!qkv || !q || !k || !v) return fail(CA_ERR_INVALID, "ca_qkv_rope_in: null pointer");
+  if (!aligned(qkv, dtype_align(dtype)) || !aligned16(q) || !aligned16(k) || !aligned16(v) ||
+      (rope_cs && !aligned16(rope_cs)))
+    return fail(CA_ERR_INVALID, "ca_qkv_rope_in: misaligned buffer");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  ca::timer_begin(ca::kQkvIn, s);
+  hipError_t e = ca::launch_qkv_in(qkv, dtype, rope_cs, q, k, v, B, T, H, D, s);
+  ca::timer_end(ca::kQkvIn, s);
+  if (e != hipSuccess) return fail(CA_ERR_HIP, "ca_qkv_rope_in launch: %s", hipGetErrorString(e));
+  return CA_OK;
+}
+
+int ca_qkv_rope_grad(const float* dq, const float* dk, const float* dv, const float* rope_cs,
+                     void* dqkv, int dtype, int B, int T, int H, int D, void* stream) {
+  int rc = check_prologue("ca_qkv_rope_grad", B, T, H, D, dtype);
+  if (rc) return rc;
+  if (!dq || !dk || !dv || !dqkv) return fail(CA_ERR_INVALID, "ca_qkv_rope_grad: null pointer");
+  if (!aligned(dqkv, dtype_align(dtype)) || !aligned16(dq) || !aligned16(dk) || !aligned16(dv) ||
+      (rope_cs && !aligned16(rope_cs)))
+    return fail(CA_ERR_INVALID, "ca_qkv_rope_grad: misaligned buffer");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  ca::timer_begin(ca::kQkvGrad, s);
+  hipError_t e = ca::launch_qkv_grad(dq, dk, dv, rope_cs, dqkv, dtype, B, T, H, D, s);
+  ca::timer_end(ca::kQkvGrad, s);
+  if (e != hipSuccess) return fail(CA_ERR_HIP, "ca_qkv_rope_grad launch: %s", hipGetErrorString(e));
+  return CA_OK;
+}
+
+static int relayout(const char* fn, const void* src, void* dst, int dtype, bool to_tokens, int B,
+                    int H, int T, int D, void* stream) {
+  int rc = check_prologue(fn, B, T, H, D, dtype);
+  if (rc) return rc;
+  if (!src || !dst) return fail(CA_ERR_INVALID, "%s: null pointer", fn);
+  const void* f32side = to_tokens ? src : dst;
+  const void* tokside = to_tokens ? dst : src;
+  if (!aligned16(f32side) || !aligned(tokside, dtype_align(dtype)))
+    return fail(CA_ERR_INVALID, "%s: misaligned buffer", fn);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  ca::timer_begin(ca::kRelayout, s);
+  hipError_t e = ca::launch_relayout(src, dst, dtype, to_tokens, B, H, T, D, s);
+  ca::timer_end(ca::kRelayout, s);
+  if (e != hipSuccess) return fail(CA_ERR_HIP, "%s launch: %s", fn, hipGetErrorString(e));
+  return CA_OK;
+}
+
+int ca_heads_to_tokens(const float* y, void* out, int dtype, int B, int H, int T, int D,
+                       void* stream) {
+  return relayout("ca_heads_to_tokens", y, out, dtype, true, B, H, T, D, stream);
+}
+
+int ca_tokens_to_heads(const void* x, int dtype, float* out, int B, int H, int T, int D,
+                       void* stream) {
+  return relayout("ca_tokens_to_heads", x, out, dtype, false, B, H, T, D, stream);
+}
+
 }  // extern "C"

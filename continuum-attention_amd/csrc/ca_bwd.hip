@@ -485,16 +485,18 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
       if (e < KF4) {
         const int key = kBwdKeys * kb - 1 + e / P::C4;
         if (key >= 0 && key < T)
-          v = reinterpret_cast<const f32x4*>(K + slice + (size_t)key * D)[e % P::C4] - kref[j];
+          v = reinterpret_cast<const f32x4*>(K + slice + (size_t)key * D)[e % P::C4];
       }
       pre[j] = v;
     }
   };
+  // the shift is applied when the prefetched rows are stored, so the loads
+  // issued a block ahead are not waited for inside the MFMA loop
   auto store_k = [&](int buf) {
 #pragma unroll
     for (int j = 0; j < KLD; ++j) {
       const int e = tid + 256 * j;
-      if (e < KF4) kst[buf][e] = pre[j];
+      if (e < KF4) kst[buf][e] = pre[j] - kref[j];
     }
   };
   auto load_a = [&](int kb, float* a) {

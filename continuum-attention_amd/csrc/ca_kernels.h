@@ -72,8 +72,12 @@ inline size_t bwd_ds_floats(int BH, int T) {
 
 // Per-kernel HIP-event timing (diagnostics; off unless ca_timing_enable(1)).
 enum KernelId {
-  kFwd = 0, kFwdCombine, kBwdRowdot, kBwdDkdv, kBwdDq, kBwdGain, kWeights, kWeightsBwd, kNumKernels
+  kFwd = 0, kFwdCombine, kBwdRowdot, kBwdDkdv, kBwdDq, kBwdGain, kWeights, kWeightsBwd, kQkvIn,
+  kQkvGrad, kRelayout, kNumKernels
 };
+
+// Element types of the prologue / epilogue buffers (CA_DTYPE_* in the ABI).
+constexpr int kDtypeF32 = 0, kDtypeBF16 = 1, kDtypeF16 = 2;
 void timer_begin(int id, hipStream_t s);
 void timer_end(int id, hipStream_t s);
 
@@ -83,6 +87,14 @@ hipError_t launch_weights(const float* scores, float* weights, float* stats, int
 hipError_t launch_weights_bwd(const float* scores, const float* grad_weights, float* weights,
                               float* grad_scores, int BH, int Q, int K, int start,
                               hipStream_t stream);
+
+// Prologue / epilogue of the decoder caller (ca_rope.hip).
+hipError_t launch_qkv_in(const void* qkv, int dtype, const float* cs, float* q, float* k, float* v,
+                         int B, int T, int H, int D, hipStream_t s);
+hipError_t launch_qkv_grad(const float* dq, const float* dk, const float* dv, const float* cs,
+                           void* dqkv, int dtype, int B, int T, int H, int D, hipStream_t s);
+hipError_t launch_relayout(const void* src, void* dst, int dtype, bool to_tokens, int B, int H,
+                           int T, int D, hipStream_t s);
 
 template <int D>
 hipError_t launch_fwd(const float* q, const float* k, const float* v, const float* log_gain,

@@ -25,7 +25,11 @@ import torch
 from torch import nn
 from torch.nn import functional as F
 
-from .ops import continuum_attention
+from . import _native
+from .ops import _mode, ca_backward, ca_forward, continuum_attention
+
+_DTYPE_CODE = {torch.float32: _native.CA_DTYPE_F32, torch.bfloat16: _native.CA_DTYPE_BF16,
+               torch.float16: _native.CA_DTYPE_F16}
 
 
 @dataclass
@@ -99,6 +103,98 @@ def apply_rope(q, k, theta):
     return q * cos + _rotate_pairs(q) * sin, k * cos + _rotate_pairs(k) * sin
 
 
+_CS_CACHE: dict = {}
+
+
+def rope_cos_sin(T, D, theta, device):
+    """fp32 table ``[T, D/2, 2]`` of (cos, sin) of ``t * theta^(-2i/D)``: the
+    reference's angles before their cast to the autocast dtype
+    (cuda/continuum_attention.py:828-830); cached per shape."""
+    key = (T, D, float(theta), device)
+    cs = _CS_CACHE.get(key)
+    if cs is None:
+        freq = 1.0 / (theta ** (torch.arange(0, D, 2, device=device, dtype=torch.float32) / D))
+        phase = torch.outer(torch.arange(T, device=device, dtype=torch.float32), freq)
+        cs = torch.stack((phase.cos(), phase.sin()), -1).contiguous()
+        if len(_CS_CACHE) > 64:
+            _CS_CACHE.clear()
+        _CS_CACHE[key] = cs
+    return cs
+
+
+def _aligned(x, nbytes):
+    x = x.contiguous()
+    return x if x.data_ptr() % nbytes == 0 else x.clone()
+
+
+class _RopeContinuumAttention(torch.autograd.Function):
+    """qkv projection output -> RoPE -> CA operator -> token-major output, with
+    the prologue and epilogue as single HIP passes (ca_qkv_rope_in /
+    ca_heads_to_tokens and their gradients) around the operator's kernels.
+    Same result as ``apply_rope`` + ``continuum_attention`` + transpose, with
+    the rotation done in fp32."""
+
+    @staticmethod
+    def forward(ctx, qkv, log_gain, theta, heads, query_tile):
+        if int(query_tile) <= 0:
+            raise ValueError("query_tile must be positive")
+        _mode()
+        if qkv.dtype not in _DTYPE_CODE:
+            raise ValueError(f"unsupported qkv dtype {qkv.dtype}")
+        if qkv.device.type != "cuda":
+            raise RuntimeError("continuum attention (continuum-attention_amd) runs on ROCm GPU "
+                               f"tensors only; got a tensor on {qkv.device}")
+        lib = _native.load()
+        Bsz, T, C3 = qkv.shape
+        C = C3 // 3
+        D = C // heads
+        dev, dt = qkv.device, _DTYPE_CODE[qkv.dtype]
+        x = _aligned(qkv.detach(), 16)
+        cs = rope_cos_sin(T, D, theta, dev)
+        q, k, v = (torch.empty(Bsz, heads, T, D, device=dev, dtype=torch.float32) for _ in range(3))
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        with torch.cuda.device(dev):
+            _native.check(lib.ca_qkv_rope_in(x.data_ptr(), dt, cs.data_ptr(), q.data_ptr(),
+                                             k.data_ptr(), v.data_ptr(), Bsz, T, heads, D, stream))
+            y, stats = ca_forward(q, k, v, log_gain)
+            out = torch.empty(Bsz, T, C, device=dev, dtype=qkv.dtype)
+            _native.check(lib.ca_heads_to_tokens(y.data_ptr(), out.data_ptr(), dt, Bsz, heads, T, D,
+                                                 stream))
+        ctx.save_for_backward(q, k, v, log_gain, y, stats, cs)
+        ctx.shape = (Bsz, T, heads, D)
+        ctx.qkv_dtype = qkv.dtype
+        return out
+
+    @staticmethod
+    def backward(ctx, gout):
+        if torch.is_grad_enabled():
+            raise RuntimeError("CA Volta analytic kernel supports first-order gradients only")
+        q, k, v, log_gain, y, stats, cs = ctx.saved_tensors
+        Bsz, T, heads, D = ctx.shape
+        lib = _native.load()
+        dev = q.device
+        g = _aligned(gout, 16)
+        if g.dtype not in _DTYPE_CODE:
+            g = g.float()
+        dyf = torch.empty(Bsz, heads, T, D, device=dev, dtype=torch.float32)
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        with torch.cuda.device(dev):
+            _native.check(lib.ca_tokens_to_heads(g.data_ptr(), _DTYPE_CODE[g.dtype], dyf.data_ptr(),
+                                                 Bsz, heads, T, D, stream))
+            dq, dk, dv, dg = ca_backward(q, k, v, log_gain, y, stats, dyf)
+            dqkv = torch.empty(Bsz, T, 3 * heads * D, device=dev, dtype=ctx.qkv_dtype)
+            _native.check(lib.ca_qkv_rope_grad(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                               cs.data_ptr(), dqkv.data_ptr(),
+                                               _DTYPE_CODE[ctx.qkv_dtype], Bsz, T, heads, D, stream))
+        return dqkv, dg.to(log_gain.dtype), None, None, None
+
+
+def rope_continuum_attention(qkv, log_gain, theta, heads, query_tile=64):
+    """``[B, T, 3C]`` qkv projection output -> ``[B, T, C]`` attention output
+    (before the output projection), in qkv's dtype; see _RopeContinuumAttention."""
+    return _RopeContinuumAttention.apply(qkv, log_gain, float(theta), int(heads), int(query_tile))
+
+
 class ContinuumSelfAttention(nn.Module):
     """qkv projection -> RoPE -> CA operator -> output projection
     (cuda/continuum_attention.py:838-854)."""
@@ -115,8 +211,16 @@ class ContinuumSelfAttention(nn.Module):
         # positive per-head score gain exp(log_qk_gain), starting at 1
         self.log_qk_gain = nn.Parameter(torch.zeros(heads))
 
+    # fused HIP prologue/epilogue around the operator on GPU tensors; False
+    # runs the reference's op-by-op composition (same operator kernels)
+    fused_prologue = True
+
     def forward(self, x):
         Bsz, T, C = x.shape
+        if self.fused_prologue and x.is_cuda:
+            y = rope_continuum_attention(self.qkv(x), self.log_qk_gain, self.rope_theta, self.heads,
+                                         self.ca_query_tile)
+            return self.out(y)
         q, k, v = self.qkv(x).view(Bsz, T, 3, self.heads, self.head_dim).permute(2, 0, 3, 1, 4).unbind(0)
         q, k = apply_rope(q, k, self.rope_theta)
         y = continuum_attention(q, k, v, self.log_qk_gain, self.ca_query_tile)

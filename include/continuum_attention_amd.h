@@ -90,6 +90,37 @@ int ca_weights_f32(const float* scores, float* weights, float* stats, int BH, in
 int ca_weights_bwd_f32(const float* scores, const float* grad_weights, float* weights,
                        float* grad_scores, int BH, int Q, int K, int start, void* stream);
 
+/* ---- Decoder prologue / epilogue -------------------------------------------
+ * Layout and RoPE steps around the operator in the decoder caller
+ * (ContinuumSelfAttention.forward, cuda/continuum_attention.py:848-854), each
+ * one pass.  Token-major buffers hold elements of type `dtype` (CA_DTYPE_*);
+ * head-major buffers are fp32 [B, H, T, D].  D must be a multiple of 4.
+ * rope_cs is the fp32 table [T][D/2][2] = (cos, sin) of t * theta^(-2i/D)
+ * for interleaved pairs (cuda/continuum_attention.py:826-835); NULL skips the
+ * rotation.  No native counterpart in the reference: these replace torch op
+ * chains. */
+enum { CA_DTYPE_F32 = 0, CA_DTYPE_BF16 = 1, CA_DTYPE_F16 = 2 };
+
+/* qkv [B, T, 3, H, D] (the qkv projection's output viewed per head) ->
+ * q, k, v fp32 [B, H, T, D], RoPE applied to q and k in fp32.  Replaces the
+ * reshape/permute/unbind and apply_rope of cuda/continuum_attention.py:
+ * 849-852 and the operator's float upcast. */
+int ca_qkv_rope_in(const void* qkv, int dtype, const float* rope_cs, float* q, float* k, float* v,
+                   int B, int T, int H, int D, void* stream);
+
+/* dqkv [B, T, 3, H, D] = (R^T dq, R^T dk, dv): the backward of ca_qkv_rope_in
+ * (autograd of the same torch chain). */
+int ca_qkv_rope_grad(const float* dq, const float* dk, const float* dv, const float* rope_cs,
+                     void* dqkv, int dtype, int B, int T, int H, int D, void* stream);
+
+/* y fp32 [B, H, T, D] -> out [B, T, H*D] (dtype), and back: the operator
+ * output's transpose/reshape/cast into the output projection
+ * (cuda/continuum_attention.py:854) and its gradient. */
+int ca_heads_to_tokens(const float* y, void* out, int dtype, int B, int H, int T, int D,
+                       void* stream);
+int ca_tokens_to_heads(const void* x, int dtype, float* out, int B, int H, int T, int D,
+                       void* stream);
+
 /* ---- Diagnostics (no counterpart in the reference; used by bench.py) -------
  * Per-kernel timing with HIP events recorded on the launch stream around each
  * kernel launch of the calls above.  Kernel ids: 0 forward, 1 forward split

@@ -98,3 +98,16 @@ def test_package_does_not_import_the_oracle():
                 src = re.sub(r'""".*?"""', "", src, flags=re.S)
                 src = re.sub(r"#.*|//.*", "", src)
                 assert "oracle" not in src, f
+
+
+@pytest.mark.parametrize("BH,Q,K,start", [(0, 4, 8, 0), (1, 0, 8, 0), (1, 4, 0, 0), (1, 4, 8, -1),
+                                          (1, 4, 8, 5), (2, 9, 8, 0)])
+def test_weights_argument_errors_before_any_launch(ca, BH, Q, K, start):
+    """start + Q > K (a query without its keys), empty or negative shapes."""
+    lib = ca.native.load()
+    p = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    assert lib.ca_weights_f32(p, p, p, BH, Q, K, start, None) == 1
+    assert lib.ca_last_error().decode().startswith("ca_weights_f32")
+    assert lib.ca_weights_bwd_f32(p, p, p, p, BH, Q, K, start, None) == 1
+    assert lib.ca_weights_f32(None, p, p, 1, 4, 8, 0, None) == 1
+    assert lib.ca_weights_bwd_f32(p, None, p, p, 1, 4, 8, 0, None) == 1

@@ -226,3 +226,89 @@ def test_decoder_train_step_bf16(gpu_ca):
         assert b.attn.log_qk_gain.grad is not None
         assert torch.isfinite(b.attn.log_qk_gain.grad).all().item()
         assert not torch.equal(b.attn.log_qk_gain.detach(), g)  # the step moved the gains
+
+
+def _unfused_attention(Dm, qkv, log_gain, theta, heads):
+    """Reference op-by-op composition: view/permute, RoPE, operator, transpose."""
+    Bsz, T, C3 = qkv.shape
+    q, k, v = qkv.view(Bsz, T, 3, heads, C3 // 3 // heads).permute(2, 0, 3, 1, 4).unbind(0)
+    q, k = Dm.apply_rope(q, k, theta)
+    y = Dm.continuum_attention(q, k, v, log_gain, 64)
+    return y.transpose(1, 2).reshape(Bsz, T, C3 // 3)
+
+
+def test_prologue_relayout_bit_exact(gpu_ca):
+    """Without rotation the prologue is a pure permute and the epilogue a
+    transpose + cast: bit-identical to torch, including bf16/fp16 rounding."""
+    say("[case] prologue relayout")
+    lib = gpu_ca.native.load()
+    Bsz, T, H, D = 2, 37, 3, 16
+    g = torch.Generator().manual_seed(3)
+    for dt, code in ((torch.float32, 0), (torch.bfloat16, 1), (torch.float16, 2)):
+        qkv = (torch.randn(Bsz, T, 3 * H * D, generator=g) * 3).to(dt).cuda()
+        q, k, v = (torch.empty(Bsz, H, T, D, device="cuda") for _ in range(3))
+        s = torch.cuda.current_stream().cuda_stream
+        assert lib.ca_qkv_rope_in(qkv.data_ptr(), code, None, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                  Bsz, T, H, D, s) == 0
+        ref = qkv.float().view(Bsz, T, 3, H, D).permute(2, 0, 3, 1, 4)
+        for got, r in zip((q, k, v), ref):
+            assert torch.equal(got, r)
+        y = torch.randn(Bsz, H, T, D, generator=g).cuda() * 7
+        out = torch.empty(Bsz, T, H * D, device="cuda", dtype=dt)
+        assert lib.ca_heads_to_tokens(y.data_ptr(), out.data_ptr(), code, Bsz, H, T, D, s) == 0
+        assert torch.equal(out, y.transpose(1, 2).reshape(Bsz, T, H * D).to(dt))
+        back = torch.empty(Bsz, H, T, D, device="cuda")
+        assert lib.ca_tokens_to_heads(out.data_ptr(), code, back.data_ptr(), Bsz, H, T, D, s) == 0
+        assert torch.equal(back, out.float().view(Bsz, T, H, D).transpose(1, 2))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_fused_rope_attention_vs_unfused(gpu_ca, dtype):
+    """The decoder's fused prologue/epilogue against the reference composition
+    (apply_rope + operator + transpose): outputs and gradients of qkv and the
+    gains.  fp32: RoPE rounding only; bf16: the composition's RoPE rounds to
+    bf16 (cuda/continuum_attention.py:826-835), the fused one stays fp32."""
+    say(f"[case] fused rope attention {dtype}")
+    Dm = gpu_ca.decoder
+    torch.manual_seed(8)
+    Bsz, T, H, D, theta = 2, 130, 4, 64, 10000.0
+    qkv = (torch.randn(Bsz, T, 3 * H * D) * 1.5).cuda().to(dtype)
+    gain = torch.tensor([0.0, 0.3, -0.2, 0.1], device="cuda")
+    dout = torch.randn(Bsz, T, H * D).cuda().to(dtype)
+    res = {}
+    for name, fn in (("fused", lambda a, b: Dm.rope_continuum_attention(a, b, theta, H)),
+                     ("unfused", lambda a, b: _unfused_attention(Dm, a, b, theta, H))):
+        a = qkv.clone().requires_grad_(True)
+        b = gain.clone().requires_grad_(True)
+        y = fn(a, b)
+        assert y.dtype == dtype and y.shape == (Bsz, T, H * D)
+        ga, gb = torch.autograd.grad(y, (a, b), dout)
+        res[name] = [t.float().cpu().numpy() for t in (y.detach(), ga, gb)]
+    tol = (2e-5, 2e-4) if dtype == torch.float32 else (2e-2, 5e-2)
+    errs = [rel(x, r) for x, r in zip(res["fused"], res["unfused"])]
+    say(f"   out {errs[0]:.2e} dqkv {errs[1]:.2e} dgain {errs[2]:.2e}")
+    assert errs[0] <= tol[0] and errs[1] <= tol[1] and errs[2] <= tol[1]
+
+
+def test_decoder_fused_prologue_matches_composition(gpu_ca):
+    """Whole decoder (fp32): fused-prologue attention vs the op-by-op path,
+    logits and every parameter gradient."""
+    say("[case] decoder fused vs composition")
+    Dm = gpu_ca.decoder
+    cfg = Dm.ContinuumDecoderConfig(d_model=128, n_heads=2, n_layers=2, block_size=64)
+    torch.manual_seed(6)
+    m = Dm.ContinuumDecoderLM(cfg).cuda()
+    ids = torch.randint(0, 256, (2, 64), device="cuda")
+    outs = {}
+    for fused in (True, False):
+        Dm.ContinuumSelfAttention.fused_prologue = fused
+        try:
+            m.zero_grad(set_to_none=True)
+            loss = m(ids, targets=ids)["loss"]
+            loss.backward()
+            outs[fused] = (loss.item(), {n: p.grad.detach().clone() for n, p in m.named_parameters()})
+        finally:
+            Dm.ContinuumSelfAttention.fused_prologue = True
+    assert abs(outs[True][0] - outs[False][0]) <= 1e-5 * abs(outs[False][0])
+    for n, gref in outs[False][1].items():
+        assert rel(outs[True][1][n].cpu().numpy(), gref.cpu().numpy()) <= 1e-3, n
