@@ -8,9 +8,9 @@ upstream grad ~ N(0,1), seed 0.  One "step" is one forward + backward of the
 operator with inputs already resident in HBM.
 
 Prints ONE JSON line (rank 0).  `value` is the median fwd+bwd milliseconds
-(lower is better).  `roofline` is for the dominant kernel, from HIP events
-recorded around each kernel launch on the launch stream during the timed
-steps; `cpu_baseline` times the CPU port of the reference's PyTorch CPU path
+(lower is better) of uninstrumented steps.  `roofline` is for the dominant
+kernel, from HIP events recorded around each kernel launch on the launch
+stream during a second run of the same steps; `cpu_baseline` times the CPU port of the reference's PyTorch CPU path
 (oracle/ca_cpu_port.py) on a bounded sample of the same workload.
 
 Two more BASELINE workloads ride along on the same line (skip with
@@ -212,8 +212,9 @@ def main():
         step()
     torch.cuda.synchronize()
 
+    # Timed region 1: whole fwd+bwd steps bracketed by events on the current
+    # stream, with no per-kernel instrumentation (this is `value`).
     fwd, bwd, tot = [], [], []
-    ca.native.timing_enable(True)
     torch.cuda.synchronize()
     t_start = time.perf_counter()
     for _ in range(args.steps):
@@ -226,12 +227,18 @@ def main():
         fwd.append(ev)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_start
-    kt = ca.native.timing_read()
-    ca.native.timing_enable(False)
     for ev in fwd:
         tot.append(ev[0].elapsed_time(ev[2]))
         bwd.append(ev[1].elapsed_time(ev[2]))
     fwd = [ev[0].elapsed_time(ev[1]) for ev in fwd]
+    # Timed region 2: the same steps with HIP events recorded around every
+    # kernel launch on the launch stream (per-kernel table and roofline).
+    ca.native.timing_enable(True)
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    kt = ca.native.timing_read()
+    ca.native.timing_enable(False)
 
     P = pairs(B, H, T)
     flops_total = 14 * D * P

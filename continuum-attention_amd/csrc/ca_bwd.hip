@@ -436,8 +436,12 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   using P = Bwd<D>;
   constexpr int KF4 = 64 * P::C4;                     // float4 per 64-row K stage
   constexpr int KLD = (KF4 + 255) / 256;              // float4 loads per thread
-  __shared__ f32x4 kst[2][KF4];
-  __shared__ float red[2 * P::NMB * 16 * 64];
+  constexpr int RED4 = 2 * P::NMB * 16 * 64 / 4;      // float4 of the final parity reduction
+  // The K stages and the final reduction buffer are live at disjoint times and
+  // share one allocation (fewer LDS bytes per work group, more resident groups).
+  __shared__ f32x4 smem[2 * KF4 > RED4 ? 2 * KF4 : RED4];
+  f32x4 (*kst)[KF4] = reinterpret_cast<f32x4 (*)[KF4]>(smem);
+  float* red = reinterpret_cast<float*>(smem);
   __shared__ float gred[2];
   const int nqt = num_q_tiles(T);
   const int nqg = dq_num_groups(T);
