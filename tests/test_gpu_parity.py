@@ -277,3 +277,63 @@ def test_config5_long_context_T8192(gpu_ca):
         f"|k.dK - dRho|: {np.max(np.abs(kdk - dr) / mag):.2e}")
     assert np.all(np.abs(qdq - dr) <= 1e-4 * mag)
     assert np.all(np.abs(kdk - dr) <= 1e-4 * mag)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_half_precision_inputs(gpu_ca, dtype):
+    """bf16/fp16 q, k, v (the reference's autocast inputs): the operator reads
+    them as fp32, returns v.dtype and gradients in the input dtypes.  Against
+    the oracle on the same rounded inputs, the only extra error is the final
+    rounding of the outputs to dtype."""
+    say(f"[case] {dtype} inputs")
+    q, k, v, rho, dy = make_inputs((1, 2, 150, 64), 41, 1.0, [0.0, 0.4])
+    qh, kh, vh = (x.to(dtype) for x in (q, k, v))
+    qd, kd, vd = (x.cuda().requires_grad_(True) for x in (qh, kh, vh))
+    rd = rho.cuda().requires_grad_(True)
+    y = gpu_ca.continuum_attention(qd, kd, vd, rd)
+    assert y.dtype == dtype
+    grads = torch.autograd.grad(y, (qd, kd, vd, rd), dy.cuda().to(dtype))
+    assert [g.dtype for g in grads] == [dtype, dtype, dtype, torch.float32]
+    q64, k64, v64 = (x.double().numpy() for x in (qh, kh, vh))
+    dy64 = dy.to(dtype).double().numpy()
+    yo = O.ca_forward(q64, k64, v64, rho.numpy())[0]
+    go = O.ca_backward(q64, k64, v64, rho.numpy(), dy64)
+    tol = 2 ** -8 if dtype == torch.bfloat16 else 2 ** -11
+    ey = rel(y.float().detach().cpu().numpy(), yo)
+    eg = [rel(g.float().cpu().numpy(), r) for g, r in zip(grads, go)]
+    say(f"   out {ey:.2e} grads {[f'{e:.1e}' for e in eg]} (dtype rounding {tol:.1e})")
+    assert ey <= tol
+    assert all(e <= tol for e in eg[:3]) and eg[3] <= GRAD_TOL
+
+
+def test_hip_graph_capture_and_replay(gpu_ca):
+    """The operator's forward and backward launch only kernels on the current
+    stream (no host sync, no memset), so they can be captured in a HIP graph.
+    The graph is replayed several times with eager work and synchronisation in
+    between; every replay must equal the eager result bitwise."""
+    say("[case] graph capture")
+    q, k, v, rho, dy = make_inputs((2, 4, 300, 64), 43, 1.0, [0.0, 0.2, -0.1, 0.3])
+    qd, kd, vd, rd, dyd = (x.cuda() for x in (q, k, v, rho, dy))
+    ref_y, ref_stats = gpu_ca.ca_forward(qd, kd, vd, rd)
+    ref_g = gpu_ca.ca_backward(qd, kd, vd, rd, ref_y, ref_stats, dyd)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):  # warm-up on the capture stream
+        gpu_ca.ca_backward(qd, kd, vd, rd, *gpu_ca.ca_forward(qd, kd, vd, rd), dyd)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y, stats = gpu_ca.ca_forward(qd, kd, vd, rd)
+        grads = gpu_ca.ca_backward(qd, kd, vd, rd, y, stats, dyd)
+    for rep in range(4):
+        junk = torch.randn(1 << 20, device="cuda") * rep  # eager work between replays
+        junk.sum().item()
+        for t in (y, *grads):
+            t.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, ref_y), rep
+        for a, b in zip(grads, ref_g):
+            assert torch.equal(a, b), rep
