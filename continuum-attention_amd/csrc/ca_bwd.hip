@@ -9,21 +9,27 @@
 // Kernels (all deterministic, no atomics):
 //   ca_bwd_rowdot   Dl_i = dY_i . y_i   (equals sum_j W_ij dW_ij; the reference
 //                   forms the same row mean at cuda/continuum_attention.py:268-269)
-//   ca_bwd_dkdv     one work group per (slice, 62-key block); 4 waves take
+//   ca_bwd_dkdv     one work group per (slice, 30-key block); 4 waves take
 //                   interleaved 32-query tiles.  Per tile: S^T = K Q^T and
-//                   dP^T = V dY^T by MFMA, W and dS in registers, then
-//                   dV^T += dY^T W and dK^T += Q^T dS by MFMA after an LDS
-//                   transpose.  dS is also written, straight from registers,
-//                   as 32x64 row blocks for the dQ pass.
-//   ca_bwd_dq       dQ = c dS K, one work group per (slice, 64 queries); its
-//                   epilogue also forms the gain partial sum_i q_i . dQ_i
-//                   (= sum_ij dS_ij s_ij, since s_ij = c q_i . k_j).
+//                   dP^T = V dY^T by MFMA (K, V slot rows from LDS shared by
+//                   the work group; Q, dY rows straight from the lane's own
+//                   prefetched registers), W and dS in registers, then
+//                   dV^T += dY^T W and dK^T += Q^T dS by MFMA (W, dS through a
+//                   transposed LDS tile; dY^T read column-wise from L2, Q^T
+//                   from the wave's staged Q tile).  dS is also written,
+//                   straight from registers, as 32x32 row blocks for the dQ
+//                   pass.  ~68 KB of LDS and <= 256 VGPRs: two work groups
+//                   share a CU and hide each other's staging, waits and
+//                   epilogue behind their MFMA phases.
+//   ca_bwd_dq       dQ = c dS (K - k_ref), one work group per (slice, 64
+//                   queries); its epilogue also forms the gain partial
+//                   sum_i q_i . dQ_i (= sum_ij dS_ij s_ij, since s_ij = c q_i . k_j).
 //   ca_bwd_gain     dRho_h = sum over batch and query groups of the partials.
 //
-// Key-block layout: the work group owns weight keys [w0, w0+62); its 64 MFMA
-// key slots are keys w0-1 .. w0+62 (slot s = key w0-1+s), so both neighbours
+// Key-block layout: the work group owns weight keys [w0, w0+30); its 32 MFMA
+// key slots are keys w0-1 .. w0+30 (slot s = key w0-1+s), so both neighbours
 // of every owned key are inside the tile.  Lane half h, register n holds slot
-// 32h+n of query q.
+// 16h+n of query q.
 #include <type_traits>
 
 #include "ca_common.h"
@@ -33,21 +39,20 @@ namespace ca {
 
 template <int D>
 struct Bwd {
-  static constexpr int DH = D / 2;
-  static constexpr int NMB = (D + 31) / 32;
-  static constexpr int C4 = D / 4;
-  static constexpr int CH = DH / 4;
-  static constexpr int LDQ = D + 4;   // padded row stride (floats) of the Q / dY tiles
-  static constexpr int LDW = 64 + 4;  // padded row stride of the W / dS tiles
-  static constexpr int WAVE_FLOATS = 2 * 32 * LDQ + 2 * 32 * LDW;
-  static constexpr int LDS_FLOATS = 4 * WAVE_FLOATS + 64 * D;  // + shared V slots
+  static constexpr int DH = D / 2;            // d values per lane half (k-range split)
+  static constexpr int NMB = (D + 31) / 32;   // 32-row d blocks of dV^T / dK^T
+  static constexpr int C4 = D / 4;            // float4 chunks per row
+  static constexpr int CH = DH / 4;           // chunks per lane half
+  static constexpr int LDQ = D + 4;           // padded row stride: K/V slot tiles and Q tile
+  static constexpr int LDX = kBwdSlots + 1;   // row stride of the [slot][query] transpose tile
+  static constexpr int SLOT_FLOATS = 32 * LDQ;
+  static constexpr int QT_FLOATS = 32 * LDQ;
+  static constexpr int XT_FLOATS = ((kBwdSlots * LDX + 3) / 4) * 4;
+  static constexpr int WAVE_FLOATS = QT_FLOATS + XT_FLOATS;
+  static constexpr int MAIN_FLOATS = 2 * SLOT_FLOATS + 4 * WAVE_FLOATS;
+  static constexpr int RED_FLOATS = 4 * NMB * 16 * 64;  // epilogue: one matrix, all waves
+  static constexpr int LDS_FLOATS = MAIN_FLOATS > RED_FLOATS ? MAIN_FLOATS : RED_FLOATS;
 };
-
-// XOR swizzle of the V-slot float4 chunks: the A-operand rows read together
-// (slots 16b+{0..3} and 32+16b+{0..3}, ...) land in distinct bank groups.
-__device__ __forceinline__ int vswz(int row, int chunks_per_half) {
-  return ((row & 3) | ((row >> 3) & 4)) & (chunks_per_half - 1);
-}
 
 // Dl_i = dY_i . y_i: one float4 chunk per thread, D/4 lanes per row.
 template <int D>
@@ -69,7 +74,7 @@ __global__ __launch_bounds__(256) void ca_bwd_rowdot_kernel(const float* __restr
 }
 
 template <int D>
-__global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
+__global__ __launch_bounds__(256, 2) void ca_bwd_dkdv_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, const float* __restrict__ stats, const float* __restrict__ dvec,
     const float* __restrict__ log_gain, float* __restrict__ dK, float* __restrict__ dV,
@@ -88,151 +93,121 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
   const int q = lane & 31;
   const int h = lane >> 5;
 
-  float* Qt = lds + w * P::WAVE_FLOATS;
-  float* dOt = Qt + 32 * P::LDQ;
-  float* Wt = dOt + 32 * P::LDQ;
-  float* dSt = Wt + 32 * P::LDW;
+  float* Ks = lds;                     // K slot rows, scaled by c log2e
+  float* Vs = lds + P::SLOT_FLOATS;    // V slot rows
+  float* Qt = lds + 2 * P::SLOT_FLOATS + w * P::WAVE_FLOATS;  // this wave's Q tile
+  float* Xt = Qt + P::QT_FLOATS;       // this wave's W / dS tile, [slot][query]
 
   const size_t slice = (size_t)bh * T * D;
-  const int head = bh % H;
-  const float cl2 = head_scale_log2(log_gain, head, D);
+  const float cl2 = head_scale_log2(log_gain, bh % H, D);
 
-  // A operands of S^T = K Q^T (registers) and dP^T = V dY^T (work-group
-  // shared LDS, XOR-swizzled float4 chunks): rows of this block's 64 slots.
-  f32x4* vsl = reinterpret_cast<f32x4*>(lds + 4 * P::WAVE_FLOATS);
-  for (int e = tid; e < 64 * P::C4; e += 256) {
-    const int row = e / P::C4, c = e % P::C4;
-    const int key = w0 - 1 + row;
-    f32x4 vv = {0.f, 0.f, 0.f, 0.f};
-    if (key >= 0 && key < T) vv = reinterpret_cast<const f32x4*>(V + slice + (size_t)key * D)[c];
-    const int half = c / P::CH, cc = c % P::CH;
-    vsl[row * P::C4 + half * P::CH + (cc ^ vswz(row, P::CH))] = vv;
-  }
-  float ka[2][P::DH];
-  int vrow[2];
-  {
-    const int i = lane & 31;
-    const int rsub = ((i >> 3) << 2) | (i & 3);
-    const int hh = (i >> 2) & 1;
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      vrow[b] = 32 * hh + 16 * b + rsub;
-      const int key = w0 - 1 + vrow[b];
-      const bool ok = key >= 0 && key < T;
-      const f32x4* kp = reinterpret_cast<const f32x4*>(K + slice + (size_t)(ok ? key : 0) * D + h * P::DH);
-#pragma unroll
-      for (int c = 0; c < P::CH; ++c) {
-        f32x4 kv = ok ? kp[c] : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) ka[b][4 * c + e] = kv[e];
-      }
+  // ---- the block's 32 K and V slot rows (slot s = key w0-1+s), shared by the waves ----
+  for (int e = tid; e < 32 * P::C4; e += 256) {
+    const int s = e / P::C4, c = e % P::C4;
+    const int key = w0 - 1 + s;
+    f32x4 kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
+    if (key >= 0 && key < T) {
+      kv = reinterpret_cast<const f32x4*>(K + slice + (size_t)key * D)[c] * cl2;
+      vv = reinterpret_cast<const f32x4*>(V + slice + (size_t)key * D)[c];
     }
+    *reinterpret_cast<f32x4*>(Ks + s * P::LDQ + 4 * c) = kv;
+    *reinterpret_cast<f32x4*>(Vs + s * P::LDQ + 4 * c) = vv;
   }
-  __syncthreads();
 
-  f32x16 accv[P::NMB][2], acck[P::NMB][2];
+  f32x16 accv[P::NMB], acck[P::NMB];
 #pragma unroll
   for (int mb = 0; mb < P::NMB; ++mb)
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        accv[mb][nb][r] = 0.f;
-        acck[mb][nb][r] = 0.f;
-      }
-  const int qt0 = w0 / 32;
+    for (int r = 0; r < 16; ++r) {
+      accv[mb][r] = 0.f;
+      acck[mb][r] = 0.f;
+    }
+  const int qt0 = w0 / 32;  // first query tile that sees an owned key
   // dS block index of (this wave's current query tile, kb)
   long long ds_blk = (long long)bh * ds_blocks_before(nqt) + ds_blocks_before(qt0 + w) + kb;
-  // Next query tile of this wave, prefetched into registers while the current
-  // tile's dV/dK MFMAs run (32 rows x D floats of Q and of dY, plus row stats).
-  constexpr int PF = (32 * P::C4 + 63) / 64;  // float4 per lane per matrix
-  f32x4 pf_q[PF], pf_o[PF];
+  // This lane's own query row half of Q and dY for the next tile (the B
+  // operands of S^T / dP^T), plus its row stats; loaded a tile ahead.
+  f32x4 pf_q[P::CH], pf_o[P::CH];
   float pf_m2 = 0.f, pf_invz = 0.f, pf_d = 0.f;
   auto prefetch = [&](int qt) {
-    const int i0 = 32 * qt;
+    const int i = 32 * qt + q;
+    const bool ok = i < T;
+    const size_t roff = slice + (size_t)(ok ? i : 0) * D + h * P::DH;
 #pragma unroll
-    for (int j = 0; j < PF; ++j) {
-      const int e = lane + 64 * j;
-      const int row = e / P::C4, c = e % P::C4;
-      const int qi = i0 + row;
-      f32x4 qv = {0.f, 0.f, 0.f, 0.f}, ov = {0.f, 0.f, 0.f, 0.f};
-      if (e < 32 * P::C4 && qi < T) {
-        qv = reinterpret_cast<const f32x4*>(Q + slice + (size_t)qi * D)[c];
-        ov = reinterpret_cast<const f32x4*>(dO + slice + (size_t)qi * D)[c];
-      }
-      pf_q[j] = qv;
-      pf_o[j] = ov;
+    for (int c = 0; c < P::CH; ++c) {
+      pf_q[c] = ok ? reinterpret_cast<const f32x4*>(Q + roff)[c] : f32x4{0.f, 0.f, 0.f, 0.f};
+      pf_o[c] = ok ? reinterpret_cast<const f32x4*>(dO + roff)[c] : f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    const int i = i0 + q;
-    pf_m2 = 0.f; pf_invz = 0.f; pf_d = 0.f;
-    if (i < T) {
-      pf_m2 = stats[((size_t)bh * T + i) * 2 + 0];
-      pf_invz = stats[((size_t)bh * T + i) * 2 + 1];
-      pf_d = dvec[(size_t)bh * T + i];
-    }
+    pf_m2 = ok ? stats[((size_t)bh * T + i) * 2 + 0] : 0.f;
+    pf_invz = ok ? stats[((size_t)bh * T + i) * 2 + 1] : 0.f;
+    pf_d = ok ? dvec[(size_t)bh * T + i] : 0.f;
   };
   if (qt0 + w < nqt) prefetch(qt0 + w);
 
+  const int arow = key_of_arow(lane);  // slot row this lane feeds to the S^T / dP^T A operand
+  const bool dok = q < D;              // D < 32 pads the d rows of dV^T / dK^T
+  const int dcol = dok ? q : 0;
+  __syncthreads();
+
   for (int qt = qt0 + w; qt < nqt; qt += 4) {
     const int i0 = 32 * qt;
-    // ---- stage this wave's Q (pre-scaled) and dY tiles from the prefetch ----
-#pragma unroll
-    for (int j = 0; j < PF; ++j) {
-      const int e = lane + 64 * j;
-      if (e < 32 * P::C4) {
-        const int row = e / P::C4, c = e % P::C4;
-        *reinterpret_cast<f32x4*>(Qt + row * P::LDQ + 4 * c) = pf_q[j] * cl2;
-        *reinterpret_cast<f32x4*>(dOt + row * P::LDQ + 4 * c) = pf_o[j];
-      }
-    }
     const int i = i0 + q;
     const float m2 = pf_m2, invz = pf_invz, dz = pf_d * pf_invz;
-    wave_lds_sync();
+
+    // ---- Q row (this lane's half) into the wave's Q tile for the dK pass ----
+#pragma unroll
+    for (int c = 0; c < P::CH; ++c)
+      *reinterpret_cast<f32x4*>(Qt + q * P::LDQ + h * P::DH + 4 * c) = pf_q[c];
 
     // ---- S^T (minus the row shift, folded into the accumulator) and dP^T ----
-    // Operands of chunk c+1 are read from LDS before the MFMAs of chunk c issue.
-    f32x16 sacc[2], pacc[2];
+    // A operands from the shared slot tiles (chunk c+1 read before the MFMAs
+    // of chunk c issue), B operands from this lane's own prefetched rows.
+    f32x16 sacc, pacc;
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        sacc[b][r] = -m2;
-        pacc[b][r] = 0.f;
-      }
+    for (int r = 0; r < 16; ++r) {
+      sacc[r] = -m2;
+      pacc[r] = 0.f;
+    }
     {
-      const f32x4* qrow = reinterpret_cast<const f32x4*>(Qt + q * P::LDQ + h * P::DH);
-      const f32x4* orow = reinterpret_cast<const f32x4*>(dOt + q * P::LDQ + h * P::DH);
-      f32x4 qv_n, ov_n, vv_n[2];
-      auto fetch = [&](int c) {
-        qv_n = qrow[c];
-        ov_n = orow[c];
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-          vv_n[b] = vsl[vrow[b] * P::C4 + h * P::CH + (c ^ vswz(vrow[b], P::CH))];
-      };
-      fetch(0);
+      const float* krow = Ks + arow * P::LDQ + h * P::DH;
+      const float* vrow = Vs + arow * P::LDQ + h * P::DH;
+      f32x4 kv_n = *reinterpret_cast<const f32x4*>(krow);
+      f32x4 vv_n = *reinterpret_cast<const f32x4*>(vrow);
 #pragma unroll
       for (int c = 0; c < P::CH; ++c) {
-        const f32x4 qv = qv_n, ov = ov_n, vv0 = vv_n[0], vv1 = vv_n[1];
-        if (c + 1 < P::CH) fetch(c + 1);
+        const f32x4 kv = kv_n, vv = vv_n;
+        if (c + 1 < P::CH) {
+          kv_n = *reinterpret_cast<const f32x4*>(krow + 4 * (c + 1));
+          vv_n = *reinterpret_cast<const f32x4*>(vrow + 4 * (c + 1));
+        }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          sacc[0] = mfma32(ka[0][4 * c + e], qv[e], sacc[0]);
-          pacc[0] = mfma32(vv0[e], ov[e], pacc[0]);
-          sacc[1] = mfma32(ka[1][4 * c + e], qv[e], sacc[1]);
-          pacc[1] = mfma32(vv1[e], ov[e], pacc[1]);
+          sacc = mfma32(kv[e], pf_q[c][e], sacc);
+          pacc = mfma32(vv[e], pf_o[c][e], pacc);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
 
-    // ---- weights and score gradients of this lane's 32 slots ----
+    // ---- dY^T operands of the dV pass (lane (d, h), step r: dY[i0+16h+r][d]),
+    //      loaded now so their latency hides behind the segment math ----
+    float ady[P::NMB][16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = i0 + 16 * h + r;
+      const bool ok = dok && row < T;
+      const float* src = dO + slice + (size_t)(ok ? row : 0) * D + dcol;
+#pragma unroll
+      for (int mb = 0; mb < P::NMB; ++mb) ady[mb][r] = ok ? src[32 * mb] : 0.f;
+    }
+
+    // ---- weights and score gradients of this lane's 16 slots ----
     // Streams over the slots; W overwrites sacc and dS overwrites pacc in place.
     // Tiles that may hold invisible keys (or key 0 / the caps) take the general
     // path; all others need no masks.
-    const int kbase = w0 - 1 + 32 * h;  // key of register 0
-    const bool need_mask = (w0 == 0) || (w0 + 62 > i0) || (i0 + 32 > T);
+    const int kbase = w0 - 1 + 16 * h;  // key of register 0
+    const bool need_mask = (w0 == 0) || (w0 + kBwdKeys > i0) || (i0 + 32 > T);
     auto segments = [&](auto general_tag) {
       constexpr bool kGeneral = decltype(general_tag)::value;
       auto slot_vis = [&](int n) {
@@ -242,16 +217,16 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
       // half 1's first segment starts at half 0's last slot
       float sl, pl, gl;
       {
-        const bool v31 = slot_vis(31);
-        const float s31 = v31 ? sacc[1][15] : 0.f;
-        const float g31 = v31 ? fmaf(pacc[1][15], invz, -dz) : 0.f;
-        sl = xhalf(s31);
+        const bool v15 = slot_vis(15);
+        const float s15 = v15 ? sacc[15] : 0.f;
+        const float g15 = v15 ? fmaf(pacc[15], invz, -dz) : 0.f;
+        sl = xhalf(s15);
         pl = fast_exp2(sl);
-        gl = xhalf(g31);
+        gl = xhalf(g15);
       }
       float r_prev = 0.f, dr_prev = 0.f, xl0 = 0.f, xdl0 = 0.f;
-      // finalises slot n from its own (s,p,g), incoming right and outgoing left shares
-      auto finish = [&](int n, float sv, float pv, float gv, float wv, float dv) {
+      // finalises slot n from its own (p, g), incoming right and outgoing left shares
+      auto finish = [&](int n, float pv, float gv, float wv, float dv) {
         if (kGeneral) {
           // half-token caps on the first key and the last visible key (both when i == 0)
           const int key = kbase + n;
@@ -260,17 +235,16 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
           wv += cap;
           dv = fmaf(cap, gv, dv);
         }
-        const int slot = 32 * h + n;
-        const bool owned = slot >= 1 && slot <= 62;
-        dv = owned ? dv : 0.f;
-        sacc[n >> 4][n & 15] = owned ? wv * invz : 0.f;
-        pacc[n >> 4][n & 15] = dv;
+        const int slot = 16 * h + n;
+        const bool owned = slot >= 1 && slot <= kBwdKeys;
+        sacc[n] = owned ? wv * invz : 0.f;
+        pacc[n] = owned ? dv : 0.f;
       };
 #pragma unroll
-      for (int n = 0; n < 32; ++n) {
+      for (int n = 0; n < 16; ++n) {
         const bool vis = slot_vis(n);
-        const float sr = vis ? sacc[n >> 4][n & 15] : 0.f;  // s - m2
-        const float gr = vis ? fmaf(pacc[n >> 4][n & 15], invz, -dz) : 0.f;
+        const float sr = vis ? sacc[n] : 0.f;  // s - m2
+        const float gr = vis ? fmaf(pacc[n], invz, -dz) : 0.f;
         const float pr = fast_exp2(sr);
         float Lv, Rv, dLv, dRv;
         seg_shares_grad(sl, sr, pl, pr, gl, gr, Lv, Rv, dLv, dRv);
@@ -285,7 +259,7 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
           xl0 = xhalf(Lv);  // half 1's first left share belongs to half 0's last slot
           xdl0 = xhalf(dLv);
         } else {
-          finish(n - 1, sl, pl, gl, r_prev + Lv, dr_prev + dLv);
+          finish(n - 1, pl, gl, r_prev + Lv, dr_prev + dLv);
         }
         r_prev = Rv;
         dr_prev = dRv;
@@ -293,137 +267,98 @@ __global__ __launch_bounds__(256) void ca_bwd_dkdv_kernel(
         pl = pr;
         gl = gr;
       }
-      finish(31, sl, pl, gl, r_prev + (h ? 0.f : xl0), dr_prev + (h ? 0.f : xdl0));
+      finish(15, pl, gl, r_prev + (h ? 0.f : xl0), dr_prev + (h ? 0.f : xdl0));
     };
     if (need_mask)
       segments(std::true_type{});
     else
       segments(std::false_type{});
 
-    // ---- dS row block for the dQ pass: row q, slots 32h..32h+31 ----
+    // ---- dS row block for the dQ pass: row q, slots 16h..16h+15 ----
     {
-      float* dst = dsbuf + ((size_t)ds_blk << 11) + q * 64 + 32 * h;
+      float* dst = dsbuf + ((size_t)ds_blk * kDsBlockFloats) + q * kBwdSlots + 16 * h;
 #pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-          *reinterpret_cast<f32x4*>(dst + 16 * b + 4 * c) =
-              f32x4{pacc[b][4 * c], pacc[b][4 * c + 1], pacc[b][4 * c + 2], pacc[b][4 * c + 3]};
+      for (int c = 0; c < 4; ++c)
+        *reinterpret_cast<f32x4*>(dst + 4 * c) =
+            f32x4{pacc[4 * c], pacc[4 * c + 1], pacc[4 * c + 2], pacc[4 * c + 3]};
       ds_blk += ds_kb_count(qt) + ds_kb_count(qt + 1) + ds_kb_count(qt + 2) + ds_kb_count(qt + 3);
     }
 
-    // ---- transpose through LDS ----
-    {
-      float* wrow = Wt + q * P::LDW + 32 * h;
-      float* drow = dSt + q * P::LDW + 32 * h;
+    // ---- acc^T[d][slot] += sum_query A[query][d] X[query][slot] ----
+    // X (W or dS, held per query lane) goes through the [slot][query] tile; at
+    // step r lane half h contributes query 16h + r.
+    auto put_x = [&](const f32x16& x) {
 #pragma unroll
-      for (int b = 0; b < 2; ++b)
+      for (int n = 0; n < 16; ++n) Xt[(16 * h + n) * P::LDX + q] = x[n];
+    };
+    const float* xcol = Xt + q * P::LDX + 16 * h;  // B operand: slot q, query 16h + r
+    put_x(sacc);
+    wave_lds_sync();
+    // the next tile's rows fly during the dV and dK MFMAs
+    if (qt + 4 < nqt) prefetch(qt + 4);
+    // dV^T += dY^T W
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          *reinterpret_cast<f32x4*>(wrow + 16 * b + 4 * c) =
-              f32x4{sacc[b][4 * c], sacc[b][4 * c + 1], sacc[b][4 * c + 2], sacc[b][4 * c + 3]};
-          *reinterpret_cast<f32x4*>(drow + 16 * b + 4 * c) =
-              f32x4{pacc[b][4 * c], pacc[b][4 * c + 1], pacc[b][4 * c + 2], pacc[b][4 * c + 3]};
-        }
+    for (int r = 0; r < 16; ++r) {
+      const float b = xcol[r];
+#pragma unroll
+      for (int mb = 0; mb < P::NMB; ++mb) accv[mb] = mfma32(ady[mb][r], b, accv[mb]);
     }
     wave_lds_sync();
-    if (qt + 4 < nqt) prefetch(qt + 4);
-
-    // ---- dV^T += dY^T W,  dK^T += Q^T dS ----
-    // Operands of query row r+1 are read from LDS before the MFMAs of row r.
+    put_x(pacc);
+    wave_lds_sync();
+    // dK^T += Q^T dS (A operand: Q tile column d, row 16h + r)
     {
-      const int col0 = q < D ? q : 0;
-      float ado_n[P::NMB], aq_n[P::NMB], bw_n[2], bd_n[2];
-      auto fetch = [&](int r) {
-        const int qr = 16 * h + r;
-#pragma unroll
-        for (int mb = 0; mb < P::NMB; ++mb) {
-          const bool dok = 32 * mb + q < D;
-          ado_n[mb] = dok ? dOt[qr * P::LDQ + 32 * mb + col0] : 0.f;
-          aq_n[mb] = dok ? Qt[qr * P::LDQ + 32 * mb + col0] : 0.f;
-        }
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-          bw_n[nb] = Wt[qr * P::LDW + 32 * nb + q];
-          bd_n[nb] = dSt[qr * P::LDW + 32 * nb + q];
-        }
-      };
-      fetch(0);
+      const float* qcol = Qt + 16 * h * P::LDQ + dcol;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        float ado[P::NMB], aq[P::NMB], bw[2], bd[2];
+        const float b = xcol[r];
 #pragma unroll
         for (int mb = 0; mb < P::NMB; ++mb) {
-          ado[mb] = ado_n[mb];
-          aq[mb] = aq_n[mb];
+          const float a = dok ? qcol[r * P::LDQ + 32 * mb] : 0.f;
+          acck[mb] = mfma32(a, b, acck[mb]);
         }
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-          bw[nb] = bw_n[nb];
-          bd[nb] = bd_n[nb];
-        }
-        if (r + 1 < 16) fetch(r + 1);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int mb = 0; mb < P::NMB; ++mb)
-#pragma unroll
-          for (int nb = 0; nb < 2; ++nb) {
-            accv[mb][nb] = mfma32(ado[mb], bw[nb], accv[mb][nb]);
-            acck[mb][nb] = mfma32(aq[mb], bd[nb], acck[mb][nb]);
-          }
-        __builtin_amdgcn_sched_barrier(0);
       }
     }
+    wave_lds_sync();
   }
 
-  // ---- reduce the 4 waves' partial dV^T / dK^T through LDS ----
-  __syncthreads();
-  constexpr int NE = P::NMB * 2 * 16;  // accumulator elements per lane per matrix
-  float* redv = lds;
-  float* redk = lds + 4 * NE * 64;
+  // ---- reduce the 4 waves' partial dV^T / dK^T through LDS, one matrix at a time ----
+  constexpr int NE = P::NMB * 16;  // accumulator elements per lane per matrix
+  constexpr int NG = P::NMB * 4;   // float4 groups per lane per matrix
+  auto reduce_store = [&](const f32x16 (&acc)[P::NMB], float* __restrict__ out, float scale) {
+    __syncthreads();
 #pragma unroll
-  for (int mb = 0; mb < P::NMB; ++mb)
+    for (int mb = 0; mb < P::NMB; ++mb)
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
+      for (int r = 0; r < 16; ++r) lds[(w * NE + mb * 16 + r) * 64 + lane] = acc[mb][r];
+    __syncthreads();
+    // column q of the accumulator is slot q; register group r4 holds d = 32mb + 8r4 + 4h + 0..3
+    for (int gi = w; gi < NG; gi += 4) {
+      const int mb = gi / 4, r4 = gi % 4;
+      const int key = w0 - 1 + q;
+      const int d0 = 32 * mb + 8 * r4 + 4 * h;
+      f32x4 sum = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int e = (mb * 2 + nb) * 16 + r;
-        redv[(w * NE + e) * 64 + lane] = accv[mb][nb][r];
-        redk[(w * NE + e) * 64 + lane] = acck[mb][nb][r];
-      }
-  __syncthreads();
-  // groups of 4 consecutive d (one float4 store) are split across the waves
-  constexpr int NG = P::NMB * 2 * 4;
-  for (int gi = w; gi < NG; gi += 4) {
-    const int mb = gi / 8, nb = (gi / 4) % 2, r4 = gi % 4;
-    const int slot = 32 * nb + q;
-    const int key = w0 - 1 + slot;
-    const int d0 = 32 * mb + 8 * r4 + 4 * h;
-    f32x4 sv = {0.f, 0.f, 0.f, 0.f}, sk = {0.f, 0.f, 0.f, 0.f};
+      for (int ww = 0; ww < 4; ++ww)
 #pragma unroll
-    for (int ww = 0; ww < 4; ++ww)
-#pragma unroll
-      for (int e4 = 0; e4 < 4; ++e4) {
-        const int e = (mb * 2 + nb) * 16 + 4 * r4 + e4;
-        sv[e4] += redv[(ww * NE + e) * 64 + lane];
-        sk[e4] += redk[(ww * NE + e) * 64 + lane];
-      }
-    if (slot >= 1 && slot <= 62 && key < T && d0 < D) {
-      *reinterpret_cast<f32x4*>(dV + slice + (size_t)key * D + d0) = sv;
-      *reinterpret_cast<f32x4*>(dK + slice + (size_t)key * D + d0) = sk * kLn2;
+        for (int e4 = 0; e4 < 4; ++e4) sum[e4] += lds[(ww * NE + mb * 16 + 4 * r4 + e4) * 64 + lane];
+      if (q >= 1 && q <= kBwdKeys && key < T && d0 < D)
+        *reinterpret_cast<f32x4*>(out + slice + (size_t)key * D + d0) = sum * scale;
     }
-  }
+  };
+  reduce_store(accv, dV, 1.0f);
+  reduce_store(acck, dK, cl2 * kLn2);
 }
 
-// dQ = c dS K as a tiled GEMM over the dS row blocks written by ca_bwd_dkdv.
-// Work group: 64 queries (two 32-query tiles) of one slice.  Per key block kb
-// the 64 K rows of its slots (keys 62kb-1 .. 62kb+62) are staged in LDS
-// (double-buffered) and shared by all four waves: wave w takes query tile
-// w&1 and the slot half w>>1 of the MFMA k-range (lane half h supplies slots
-// 32h + s at k-step s).  Halo slots and invisible keys carry dS = 0, so no
-// masks are needed.  The dS operand of the next block is prefetched into
-// registers.  The two halves are summed through LDS at the end (fixed
-// order), and the epilogue writes the work group's gain partial
+// dQ = c dS (K - k_ref) as a tiled GEMM over the 32x32 dS blocks written by
+// ca_bwd_dkdv.  Work group: 64 queries (two 32-query tiles) of one slice; wave
+// w takes query tile w&1 and the key blocks of parity w>>1.  Per stage the 32
+// K rows of two consecutive key blocks (slots 30kb-1 .. 30kb+30 each) are
+// staged in LDS (double-buffered) and shared by all four waves; lane half h
+// supplies slots 16h + s at k-step s.  Halo slots and invisible keys carry
+// dS = 0, so no masks are needed.  The dS operand of the wave's next block is
+// prefetched into registers.  The two parities are summed through LDS at the
+// end (fixed order), and the epilogue writes the work group's gain partial
 // sum_i q_i . dQ_i (fixed order).
 template <int D>
 __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict__ dsbuf,
@@ -434,8 +369,8 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
                                                         float* __restrict__ gain_part, int BH,
                                                         int H, int T) {
   using P = Bwd<D>;
-  constexpr int KF4 = 64 * P::C4;                     // float4 per 64-row K stage
-  constexpr int KLD = (KF4 + 255) / 256;              // float4 loads per thread
+  constexpr int KF4 = 2 * kBwdSlots * P::C4;  // float4 per stage (two key blocks)
+  constexpr int KLD = (KF4 + 255) / 256;      // float4 loads per thread
   constexpr int RED4 = 2 * P::NMB * 16 * 64 / 4;      // float4 of the final parity reduction
   // The K stages and the final reduction buffer are live at disjoint times and
   // share one allocation (fewer LDS bytes per work group, more resident groups).
@@ -456,10 +391,11 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   const float c = head_scale_log2(log_gain, bh % H, D) * kLn2;
   // key blocks met by this wave's tile and by the work group's last tile
   const int my_kb = wave_on ? min(ds_kb_count(qt), nkb) : 0;
-  const int iters = min(ds_kb_count(min(2 * qg + 1, nqt - 1)), nkb);
-  const float* arow = dsbuf +
-                      (((size_t)bh * ds_blocks_before(nqt) + ds_blocks_before(wave_on ? qt : 0)) << 11) +
-                      q * 64 + 32 * h + 16 * par;
+  const int last_kb = min(ds_kb_count(min(2 * qg + 1, nqt - 1)), nkb);
+  const int iters = (last_kb + 1) / 2;
+  const float* arow =
+      dsbuf + ((size_t)bh * ds_blocks_before(nqt) + ds_blocks_before(wave_on ? qt : 0)) * kDsBlockFloats +
+      q * kBwdSlots + 16 * h;
 
   f32x16 acc[P::NMB];
 #pragma unroll
@@ -481,13 +417,14 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
     for (int j = 0; j < KLD; ++j) kref[j] = kr[(tid + 256 * j) % P::C4];
   }
   f32x4 pre[KLD];
-  auto load_k = [&](int kb) {
+  auto load_k = [&](int it) {
 #pragma unroll
     for (int j = 0; j < KLD; ++j) {
       const int e = tid + 256 * j;
       f32x4 v = {0.f, 0.f, 0.f, 0.f};
       if (e < KF4) {
-        const int key = kBwdKeys * kb - 1 + e / P::C4;
+        const int row = e / P::C4;  // 32 * (block in stage) + slot
+        const int key = kBwdKeys * (2 * it + (row >> 5)) - 1 + (row & 31);
         if (key >= 0 && key < T)
           v = reinterpret_cast<const f32x4*>(K + slice + (size_t)key * D)[e % P::C4];
       }
@@ -495,7 +432,7 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
     }
   };
   // the shift is applied when the prefetched rows are stored, so the loads
-  // issued a block ahead are not waited for inside the MFMA loop
+  // issued a stage ahead are not waited for inside the MFMA loop
   auto store_k = [&](int buf) {
 #pragma unroll
     for (int j = 0; j < KLD; ++j) {
@@ -503,8 +440,8 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
       if (e < KF4) kst[buf][e] = pre[j] - kref[j];
     }
   };
-  auto load_a = [&](int kb, float* a) {
-    const f32x4* src = reinterpret_cast<const f32x4*>(arow + ((size_t)kb << 11));
+  auto load_a = [&](int kbm, float* a) {
+    const f32x4* src = reinterpret_cast<const f32x4*>(arow + (size_t)kbm * kDsBlockFloats);
 #pragma unroll
     for (int c4 = 0; c4 < 4; ++c4) {
       const f32x4 v4 = src[c4];
@@ -513,7 +450,7 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   };
 
   float a_next[16];
-  if (my_kb > 0) load_a(0, a_next);
+  if (par < my_kb) load_a(par, a_next);
   load_k(0);
   store_k(0);
   __syncthreads();
@@ -521,17 +458,18 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   for (int it = 0; it < iters; ++it) {
     const int buf = it & 1;
     if (it + 1 < iters) load_k(it + 1);
-    if (it < my_kb) {
+    const int kbm = 2 * it + par;
+    if (kbm < my_kb) {
       float a[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) a[r] = a_next[r];
-      if (it + 1 < my_kb) load_a(it + 1, a_next);
-      const float* kb = reinterpret_cast<const float*>(&kst[buf][0]) + (32 * h + 16 * par) * D + dcol;
+      if (kbm + 2 < my_kb) load_a(kbm + 2, a_next);
+      const float* kbp = reinterpret_cast<const float*>(&kst[buf][0]) + (32 * par + 16 * h) * D + dcol;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
 #pragma unroll
         for (int nb = 0; nb < P::NMB; ++nb) {
-          const float b = (32 * nb + q < D) ? kb[r * D + 32 * nb] : 0.f;
+          const float b = (32 * nb + q < D) ? kbp[r * D + 32 * nb] : 0.f;
           acc[nb] = mfma32(a[r], b, acc[nb]);
         }
       }

@@ -27,8 +27,11 @@ inline size_t fwd_part_floats(int BH, int T, int C) {
   return (size_t)BH * smax * T * 66;  // D <= 64 outputs + (m, Z); sized for the largest D
 }
 
-// Backward: key blocks owned by one dK/dV work group.
-constexpr int kBwdKeys = 62;
+// Backward: key blocks owned by one dK/dV work group.  A block owns 30 keys
+// and feeds 32 MFMA slots (slot s = key 30*kb - 1 + s), so both neighbours of
+// every owned key are inside the tile.
+constexpr int kBwdKeys = 30;
+constexpr int kBwdSlots = 32;
 __host__ __device__ inline int bwd_num_key_blocks(int T) { return (T + kBwdKeys - 1) / kBwdKeys; }
 __host__ __device__ inline int num_q_tiles(int T) { return (T + 31) / 32; }
 // dQ work groups (64 queries each) per slice; also the gain partials per slice.
@@ -58,16 +61,17 @@ __host__ __device__ inline long long floor_sum(long long n, long long m, long lo
   return ans;
 }
 
-// dS blocks for the dQ pass: one 32-query x 64-slot block (row-major, slot s
-// of key block kb is key 62*kb - 1 + s) for every query tile qt and key block
-// kb that meets it (62*kb <= 32*qt + 31).  Blocks are stored qt-major, kb
-// ascending, so a dQ work group reads its rows contiguously.
+// dS blocks for the dQ pass: one 32-query x 32-slot block (row-major) for
+// every query tile qt and key block kb that meets it (30*kb <= 32*qt + 31).
+// Blocks are stored qt-major, kb ascending, so a dQ work group reads its rows
+// contiguously.  Blocks past the last key block are counted but never touched.
+constexpr int kDsBlockFloats = 32 * kBwdSlots;
 __host__ __device__ inline int ds_kb_count(int qt) { return (32 * qt + 31) / kBwdKeys + 1; }
 __host__ __device__ inline long long ds_blocks_before(int qt) {
   return qt <= 0 ? 0 : qt + floor_sum(qt, kBwdKeys, 32, 31);
 }
 inline size_t bwd_ds_floats(int BH, int T) {
-  return (size_t)BH * (size_t)ds_blocks_before(num_q_tiles(T)) * 2048;
+  return (size_t)BH * (size_t)ds_blocks_before(num_q_tiles(T)) * kDsBlockFloats;
 }
 
 // Per-kernel HIP-event timing (diagnostics; off unless ca_timing_enable(1)).
