@@ -15,8 +15,8 @@
 //                   the work group; Q, dY rows straight from the lane's own
 //                   prefetched registers), W and dS in registers, then
 //                   dV^T += dY^T W and dK^T += Q^T dS by MFMA (W, dS through a
-//                   transposed LDS tile; dY^T read column-wise from L2, Q^T
-//                   from the wave's staged Q tile).  dS is also written,
+//                   transposed LDS tile; dY^T, then Q^T, read column-wise
+//                   from the wave's row tile).  dS is also written,
 //                   straight from registers, as 32x32 row blocks for the dQ
 //                   pass.  ~68 KB of LDS and <= 256 VGPRs: two work groups
 //                   share a CU and hide each other's staging, waits and
@@ -95,8 +95,8 @@ __global__ __launch_bounds__(256, 2) void ca_bwd_dkdv_kernel(
 
   float* Ks = lds;                     // K slot rows, scaled by c log2e
   float* Vs = lds + P::SLOT_FLOATS;    // V slot rows
-  float* Qt = lds + 2 * P::SLOT_FLOATS + w * P::WAVE_FLOATS;  // this wave's Q tile
-  float* Xt = Qt + P::QT_FLOATS;       // this wave's W / dS tile, [slot][query]
+  float* At = lds + 2 * P::SLOT_FLOATS + w * P::WAVE_FLOATS;  // this wave's dY, then Q, tile
+  float* Xt = At + P::QT_FLOATS;       // this wave's W / dS tile, [slot][query]
 
   const size_t slice = (size_t)bh * T * D;
   const float cl2 = head_scale_log2(log_gain, bh % H, D);
@@ -126,23 +126,29 @@ __global__ __launch_bounds__(256, 2) void ca_bwd_dkdv_kernel(
   // dS block index of (this wave's current query tile, kb)
   long long ds_blk = (long long)bh * ds_blocks_before(nqt) + ds_blocks_before(qt0 + w) + kb;
   // This lane's own query row half of Q and dY for the next tile (the B
-  // operands of S^T / dP^T), plus its row stats; loaded a tile ahead.
+  // operands of S^T / dP^T), plus its row stats; loaded a tile ahead, dY and
+  // stats as soon as the current ones are consumed, Q after its tile is staged.
   f32x4 pf_q[P::CH], pf_o[P::CH];
   float pf_m2 = 0.f, pf_invz = 0.f, pf_d = 0.f;
-  auto prefetch = [&](int qt) {
+  auto prefetch_rows = [&](int qt, const float* __restrict__ src, f32x4* dst) {
     const int i = 32 * qt + q;
     const bool ok = i < T;
-    const size_t roff = slice + (size_t)(ok ? i : 0) * D + h * P::DH;
+    const f32x4* rp = reinterpret_cast<const f32x4*>(src + slice + (size_t)(ok ? i : 0) * D + h * P::DH);
 #pragma unroll
-    for (int c = 0; c < P::CH; ++c) {
-      pf_q[c] = ok ? reinterpret_cast<const f32x4*>(Q + roff)[c] : f32x4{0.f, 0.f, 0.f, 0.f};
-      pf_o[c] = ok ? reinterpret_cast<const f32x4*>(dO + roff)[c] : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int c = 0; c < P::CH; ++c) dst[c] = ok ? rp[c] : f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  auto prefetch_stats = [&](int qt) {
+    const int i = 32 * qt + q;
+    const bool ok = i < T;
     pf_m2 = ok ? stats[((size_t)bh * T + i) * 2 + 0] : 0.f;
     pf_invz = ok ? stats[((size_t)bh * T + i) * 2 + 1] : 0.f;
     pf_d = ok ? dvec[(size_t)bh * T + i] : 0.f;
   };
-  if (qt0 + w < nqt) prefetch(qt0 + w);
+  if (qt0 + w < nqt) {
+    prefetch_rows(qt0 + w, Q, pf_q);
+    prefetch_rows(qt0 + w, dO, pf_o);
+    prefetch_stats(qt0 + w);
+  }
 
   const int arow = key_of_arow(lane);  // slot row this lane feeds to the S^T / dP^T A operand
   const bool dok = q < D;              // D < 32 pads the d rows of dV^T / dK^T
@@ -154,10 +160,10 @@ __global__ __launch_bounds__(256, 2) void ca_bwd_dkdv_kernel(
     const int i = i0 + q;
     const float m2 = pf_m2, invz = pf_invz, dz = pf_d * pf_invz;
 
-    // ---- Q row (this lane's half) into the wave's Q tile for the dK pass ----
+    // ---- dY row (this lane's half) into the wave's tile for the dV pass ----
 #pragma unroll
     for (int c = 0; c < P::CH; ++c)
-      *reinterpret_cast<f32x4*>(Qt + q * P::LDQ + h * P::DH + 4 * c) = pf_q[c];
+      *reinterpret_cast<f32x4*>(At + q * P::LDQ + h * P::DH + 4 * c) = pf_o[c];
 
     // ---- S^T (minus the row shift, folded into the accumulator) and dP^T ----
     // A operands from the shared slot tiles (chunk c+1 read before the MFMAs
@@ -188,18 +194,6 @@ __global__ __launch_bounds__(256, 2) void ca_bwd_dkdv_kernel(
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-    }
-
-    // ---- dY^T operands of the dV pass (lane (d, h), step r: dY[i0+16h+r][d]),
-    //      loaded now so their latency hides behind the segment math ----
-    float ady[P::NMB][16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = i0 + 16 * h + r;
-      const bool ok = dok && row < T;
-      const float* src = dO + slice + (size_t)(ok ? row : 0) * D + dcol;
-#pragma unroll
-      for (int mb = 0; mb < P::NMB; ++mb) ady[mb][r] = ok ? src[32 * mb] : 0.f;
     }
 
     // ---- weights and score gradients of this lane's 16 slots ----
@@ -285,40 +279,42 @@ __global__ __launch_bounds__(256, 2) void ca_bwd_dkdv_kernel(
     }
 
     // ---- acc^T[d][slot] += sum_query A[query][d] X[query][slot] ----
-    // X (W or dS, held per query lane) goes through the [slot][query] tile; at
-    // step r lane half h contributes query 16h + r.
+    // X (W or dS, held per query lane) goes through the [slot][query] tile, A
+    // (dY, then Q) is read column-wise from the wave's row tile; at step r
+    // lane half h contributes query 16h + r.
     auto put_x = [&](const f32x16& x) {
 #pragma unroll
       for (int n = 0; n < 16; ++n) Xt[(16 * h + n) * P::LDX + q] = x[n];
     };
-    const float* xcol = Xt + q * P::LDX + 16 * h;  // B operand: slot q, query 16h + r
-    put_x(sacc);
-    wave_lds_sync();
-    // the next tile's rows fly during the dV and dK MFMAs
-    if (qt + 4 < nqt) prefetch(qt + 4);
-    // dV^T += dY^T W
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float b = xcol[r];
-#pragma unroll
-      for (int mb = 0; mb < P::NMB; ++mb) accv[mb] = mfma32(ady[mb][r], b, accv[mb]);
-    }
-    wave_lds_sync();
-    put_x(pacc);
-    wave_lds_sync();
-    // dK^T += Q^T dS (A operand: Q tile column d, row 16h + r)
-    {
-      const float* qcol = Qt + 16 * h * P::LDQ + dcol;
+    const float* xcol = Xt + q * P::LDX + 16 * h;    // B operand: slot q, query 16h + r
+    const float* acol = At + 16 * h * P::LDQ + dcol;  // A operand: row 16h + r, column d
+    auto mma_x = [&](f32x16 (&acc)[P::NMB]) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float b = xcol[r];
 #pragma unroll
         for (int mb = 0; mb < P::NMB; ++mb) {
-          const float a = dok ? qcol[r * P::LDQ + 32 * mb] : 0.f;
-          acck[mb] = mfma32(a, b, acck[mb]);
+          const float a = dok ? acol[r * P::LDQ + 32 * mb] : 0.f;
+          acc[mb] = mfma32(a, b, acc[mb]);
         }
       }
+    };
+    put_x(sacc);
+    wave_lds_sync();
+    // the next tile's dY row and stats fly during the dV and dK MFMAs
+    if (qt + 4 < nqt) {
+      prefetch_rows(qt + 4, dO, pf_o);
+      prefetch_stats(qt + 4);
     }
+    mma_x(accv);  // dV^T += dY^T W
+    wave_lds_sync();
+    put_x(pacc);
+#pragma unroll
+    for (int c = 0; c < P::CH; ++c)
+      *reinterpret_cast<f32x4*>(At + q * P::LDQ + h * P::DH + 4 * c) = pf_q[c];
+    wave_lds_sync();
+    if (qt + 4 < nqt) prefetch_rows(qt + 4, Q, pf_q);
+    mma_x(acck);  // dK^T += Q^T dS
     wave_lds_sync();
   }
 
