@@ -161,8 +161,9 @@ def bench_ca_p(ca, dev, steps=10, warmup=3):
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=20,
+                    help="untimed steps first (the GPU clock ramps up over the first ~10)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-models", action="store_true",
                     help="skip the CA-S (config 4) and CA-P (config 3) training-step legs")
