@@ -38,8 +38,9 @@ def test_library_exports_every_header_symbol(ca):
 
 def test_workspace_sizes(ca):
     lib = ca.native.load()
-    # one 128-query group fits one forward split: no partials needed
-    assert lib.ca_fwd_workspace_bytes(2, 16, 512, 64) == 0
+    # every 128-query group fits one forward split (<= 12 key tiles): no partials
+    assert lib.ca_fwd_workspace_bytes(2, 16, 384, 64) == 0
+    assert lib.ca_fwd_workspace_bytes(2, 16, 512, 64) > 0
     assert lib.ca_fwd_workspace_bytes(2, 16, 2048, 64) > 0
     nqt = 2048 // 32
     ds_bytes = 2 * 16 * (nqt * (nqt + 1) // 2) * 1024 * 4
