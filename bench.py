@@ -167,6 +167,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-models", action="store_true",
                     help="skip the CA-S (config 4) and CA-P (config 3) training-step legs")
+    ap.add_argument("--shape", default=None,
+                    help="B,H,T,D of the operator leg (diagnostics; default is BASELINE config 2)")
     ap.add_argument("--only", choices=["ca_s", "ca_p"], default=None,
                     help="run only one model-step leg and print its JSON (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -198,11 +200,12 @@ def main():
         return
     torch.backends.cuda.matmul.allow_tf32 = False
 
-    B, H, T, D = SHAPE
+    shape = tuple(int(x) for x in args.shape.split(",")) if args.shape else SHAPE
+    B, H, T, D = shape
     g = torch.Generator().manual_seed(0)
-    q, k, v = (torch.randn(SHAPE, generator=g).to(dev).requires_grad_(True) for _ in range(3))
+    q, k, v = (torch.randn(shape, generator=g).to(dev).requires_grad_(True) for _ in range(3))
     rho = torch.zeros(H, device=dev, requires_grad=True)
-    dy = torch.randn(SHAPE, generator=g).to(dev)
+    dy = torch.randn(shape, generator=g).to(dev)
 
     def step():
         y = ca.continuum_attention(q, k, v, rho, 128)
@@ -268,8 +271,8 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic N(0,1) q,k,v,dY, seed 0",
-        "config": {"workload": "CA operator fwd+bwd [B,H,T,D]=[2,16,2048,64] fp32, causal, "
-                               "log_gain=0 (BASELINE config 2)",
+        "config": {"workload": (f"CA operator fwd+bwd [B,H,T,D]=[{B},{H},{T},{D}] fp32, causal, "
+                                "log_gain=0" + (" (BASELINE config 2)" if shape == SHAPE else "")),
                    "B": B, "H": H, "T": T, "D": D, "query_tile": 128},
         "fwd_ms": round(statistics.median(fwd), 4),
         "bwd_ms": round(statistics.median(bwd), 4),

@@ -5,6 +5,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
+#include <atomic>
 #include <vector>
 
 #include "../../include/continuum_attention_amd.h"
@@ -47,16 +49,39 @@ int check_shape(int B, int H, int T, int D) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// The dQ pass splits its work items when its grid would not fill the device
+// (ca::dq_split).  The workspace is sized for a split whenever the grid is
+// below kDqSplitBound work groups, so its size does not depend on the device;
+// the device's own resident count (at most this bound) picks the split.
+constexpr int kDqSplitBound = 2048;
+
+int dq_resident_groups() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < 64) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c) return c;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  const int r = std::min(cus * ca::kDqGroupsPerCu, kDqSplitBound);
+  if (dev >= 0 && dev < 64) cache[dev].store(r, std::memory_order_relaxed);
+  return r;
+}
+
 struct BwdLayout {
-  size_t ds, dvec, gain, total;
+  size_t ds, dvec, gain, dqpart, total;
 };
-BwdLayout bwd_layout(int B, int H, int T) {
+BwdLayout bwd_layout(int B, int H, int T, int D) {
   const int BH = B * H;
+  const ca::DqSplit sp = ca::dq_split(BH, T, kDqSplitBound);  // the largest split
   BwdLayout L;
   L.ds = 0;
   L.dvec = align256(ca::bwd_ds_floats(BH, T) * sizeof(float));
   L.gain = L.dvec + align256((size_t)BH * T * sizeof(float));
-  L.total = L.gain + align256((size_t)BH * ca::dq_num_groups(T) * sizeof(float));
+  L.dqpart = L.gain + align256((size_t)BH * sp.items * sizeof(float));
+  L.total = L.dqpart + align256((size_t)BH * sp.part_items * 64 * D * sizeof(float));
   return L;
 }
 
@@ -186,9 +211,8 @@ int ca_fwd_f32(const float* q, const float* k, const float* v, const float* log_
 }
 
 size_t ca_bwd_workspace_bytes(int B, int H, int T, int D) {
-  if (B <= 0 || H <= 0 || T <= 0) return 0;
-  (void)D;
-  return bwd_layout(B, H, T).total;
+  if (B <= 0 || H <= 0 || T <= 0 || D <= 0) return 0;
+  return bwd_layout(B, H, T, D).total;
 }
 
 int ca_bwd_f32(const float* q, const float* k, const float* v, const float* log_gain,
@@ -202,7 +226,7 @@ int ca_bwd_f32(const float* q, const float* k, const float* v, const float* log_
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dout) || !aligned16(dk) ||
       !aligned16(dv))
     return fail(CA_ERR_INVALID, "q, k, v, dout, dk and dv must be 16-byte aligned");
-  const BwdLayout L = bwd_layout(B, H, T);
+  const BwdLayout L = bwd_layout(B, H, T, D);
   if (!workspace || workspace_bytes < L.total)
     return fail(CA_ERR_WORKSPACE, "backward workspace of %zu bytes required, %zu given", L.total,
                 workspace_bytes);
@@ -211,13 +235,15 @@ int ca_bwd_f32(const float* q, const float* k, const float* v, const float* log_
   float* dsbuf = reinterpret_cast<float*>(ws + L.ds);
   float* dvec = reinterpret_cast<float*>(ws + L.dvec);
   float* gain = reinterpret_cast<float*>(ws + L.gain);
+  float* dqpart = reinterpret_cast<float*>(ws + L.dqpart);
+  const ca::DqSplit sp = ca::dq_split(B * H, T, dq_resident_groups());
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;
   switch (D) {
-    case 8: e = ca::launch_bwd<8>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, dsbuf, dvec, gain, B, H, T, s); break;
-    case 16: e = ca::launch_bwd<16>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, dsbuf, dvec, gain, B, H, T, s); break;
-    case 32: e = ca::launch_bwd<32>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, dsbuf, dvec, gain, B, H, T, s); break;
-    default: e = ca::launch_bwd<64>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, dsbuf, dvec, gain, B, H, T, s); break;
+    case 8: e = ca::launch_bwd<8>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, dsbuf, dvec, gain, dqpart, sp, B, H, T, s); break;
+    case 16: e = ca::launch_bwd<16>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, dsbuf, dvec, gain, dqpart, sp, B, H, T, s); break;
+    case 32: e = ca::launch_bwd<32>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, dsbuf, dvec, gain, dqpart, sp, B, H, T, s); break;
+    default: e = ca::launch_bwd<64>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, dsbuf, dvec, gain, dqpart, sp, B, H, T, s); break;
   }
   if (e != hipSuccess) return fail(CA_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
   return CA_OK;

@@ -347,23 +347,27 @@ __global__ __launch_bounds__(256, 2) void ca_bwd_dkdv_kernel(
 }
 
 // dQ = c dS (K - k_ref) as a tiled GEMM over the 32x32 dS blocks written by
-// ca_bwd_dkdv.  Work group: 64 queries (two 32-query tiles) of one slice; wave
-// w takes query tile w&1 and the key blocks of parity w>>1.  Per stage the 32
-// K rows of two consecutive key blocks (slots 30kb-1 .. 30kb+30 each) are
-// staged in LDS (double-buffered) and shared by all four waves; lane half h
-// supplies slots 16h + s at k-step s.  Halo slots and invisible keys carry
-// dS = 0, so no masks are needed.  The dS operand of the wave's next block is
-// prefetched into registers.  The two parities are summed through LDS at the
-// end (fixed order), and the epilogue writes the work group's gain partial
-// sum_i q_i . dQ_i (fixed order).
+// ca_bwd_dkdv.  Work item: one chunk of the key blocks of a 64-query group
+// (two 32-query tiles) of one slice; wave w takes query tile w&1 and the
+// chunk's key blocks of parity w>>1.  Per stage the 32 K rows of two
+// consecutive key blocks (slots 30kb-1 .. 30kb+30 each) are staged in LDS
+// (double-buffered) and shared by all four waves; lane half h supplies slots
+// 16h + s at k-step s.  Halo slots and invisible keys carry dS = 0, so no
+// masks are needed.  The dS operand of the wave's next block is prefetched
+// into registers.  The two parities are summed through LDS at the end (fixed
+// order).  A single-chunk group writes dQ; the chunks of a longer group write
+// partial tiles that ca_bwd_gain_merge sums.  Every item writes its gain
+// partial sum_i q_i . dQ_i(chunk) (linear in dQ, so the partials add up).
 template <int D>
 __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict__ dsbuf,
                                                         const float* __restrict__ Q,
                                                         const float* __restrict__ K,
                                                         const float* __restrict__ log_gain,
                                                         float* __restrict__ dQ,
+                                                        float* __restrict__ dq_part,
                                                         float* __restrict__ gain_part, int BH,
-                                                        int H, int T) {
+                                                        int H, int T, int chunk, int n_items,
+                                                        int n_part) {
   using P = Bwd<D>;
   constexpr int KF4 = 2 * kBwdSlots * P::C4;  // float4 per stage (two key blocks)
   constexpr int KLD = (KF4 + 255) / 256;      // float4 loads per thread
@@ -375,20 +379,29 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   float* red = reinterpret_cast<float*>(smem);
   __shared__ float gred[2];
   const int nqt = num_q_tiles(T);
-  const int nqg = dq_num_groups(T);
   const int nkb = bwd_num_key_blocks(T);
   const int bh = blockIdx.x % BH;
-  const int qg = nqg - 1 - blockIdx.x / BH;  // heaviest (longest rows) first
+  const int item = blockIdx.x / BH;
+  // item -> (group, chunk), heaviest groups first
+  int qg = dq_num_groups(T) - 1, ch = item, nch = dq_group_chunks(qg, T, chunk);
+  while (ch >= nch && qg > 0) {
+    ch -= nch;
+    --qg;
+    nch = dq_group_chunks(qg, T, chunk);
+  }
+  const int gblocks = dq_group_blocks(qg, T);
+  const int clen = (gblocks + nch - 1) / nch;
+  const int kb_lo = ch * clen;
+  const int kb_hi = min(kb_lo + clen, gblocks);
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, q = lane & 31, h = lane >> 5;
   const int qsub = w & 1, par = w >> 1;
   const int qt = 2 * qg + qsub;
   const bool wave_on = qt < nqt;
   const size_t slice = (size_t)bh * T * D;
   const float c = head_scale_log2(log_gain, bh % H, D) * kLn2;
-  // key blocks met by this wave's tile and by the work group's last tile
-  const int my_kb = wave_on ? min(ds_kb_count(qt), nkb) : 0;
-  const int last_kb = min(ds_kb_count(min(2 * qg + 1, nqt - 1)), nkb);
-  const int iters = (last_kb + 1) / 2;
+  // key blocks of this chunk met by the wave's tile
+  const int my_end = wave_on ? min(min(ds_kb_count(qt), nkb), kb_hi) : 0;
+  const int iters = kb_hi > kb_lo ? (kb_hi - kb_lo + 1) / 2 : 0;
   const float* arow =
       dsbuf + ((size_t)bh * ds_blocks_before(nqt) + ds_blocks_before(wave_on ? qt : 0)) * kDsBlockFloats +
       q * kBwdSlots + 16 * h;
@@ -405,7 +418,8 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   // neighbouring keys nearly coincide the products stay small instead of
   // cancelling in fp32 (|k| ~ 1 against |k_j - k_ref| ~ 1e-2 in the
   // near-duplicate-key case), and the gain partial sum_i q_i . dQ_i inherits
-  // the same accuracy.
+  // the same accuracy.  All chunks of a group use the same k_ref, so the
+  // k_ref terms cancel in the sum of the chunk partials.
   f32x4 kref[KLD];
   {
     const f32x4* kr = reinterpret_cast<const f32x4*>(K + slice + (size_t)(64 * qg) * D);
@@ -420,7 +434,7 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
       f32x4 v = {0.f, 0.f, 0.f, 0.f};
       if (e < KF4) {
         const int row = e / P::C4;  // 32 * (block in stage) + slot
-        const int key = kBwdKeys * (2 * it + (row >> 5)) - 1 + (row & 31);
+        const int key = kBwdKeys * (kb_lo + 2 * it + (row >> 5)) - 1 + (row & 31);
         if (key >= 0 && key < T)
           v = reinterpret_cast<const f32x4*>(K + slice + (size_t)key * D)[e % P::C4];
       }
@@ -446,7 +460,7 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   };
 
   float a_next[16];
-  if (par < my_kb) load_a(par, a_next);
+  if (kb_lo + par < my_end) load_a(kb_lo + par, a_next);
   load_k(0);
   store_k(0);
   __syncthreads();
@@ -454,12 +468,12 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   for (int it = 0; it < iters; ++it) {
     const int buf = it & 1;
     if (it + 1 < iters) load_k(it + 1);
-    const int kbm = 2 * it + par;
-    if (kbm < my_kb) {
+    const int kbm = kb_lo + 2 * it + par;
+    if (kbm < my_end) {
       float a[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) a[r] = a_next[r];
-      if (kbm + 2 < my_kb) load_a(kbm + 2, a_next);
+      if (kbm + 2 < my_end) load_a(kbm + 2, a_next);
       const float* kbp = reinterpret_cast<const float*>(&kst[buf][0]) + (32 * par + 16 * h) * D + dcol;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -495,44 +509,74 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   if (par == 0) {
     float g = 0.f;
     if (wave_on) {
+      // single-chunk groups write dQ; chunk partials are item-indexed tiles
+      // [64 queries][D] (items of multi-chunk groups are numbered first)
+      float* dst = nch == 1 ? dQ + slice + (size_t)(64 * qg) * D
+                            : dq_part + ((size_t)bh * n_part + item) * 64 * D;
 #pragma unroll
       for (int nb = 0; nb < P::NMB; ++nb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const float sum = acc[nb][r] + red[((qsub * P::NMB + nb) * 16 + r) * 64 + lane];
-          const int row = 32 * qt + 8 * (r >> 2) + 4 * h + (r & 3);
+          const int rloc = 32 * qsub + 8 * (r >> 2) + 4 * h + (r & 3);
           const int d = 32 * nb + q;
           const float val = sum * c;
           g = fmaf(qv[nb][r], val, g);
-          if (row < T && d < D) dQ[slice + (size_t)row * D + d] = val;
+          if (64 * qg + rloc < T && d < D) dst[(size_t)rloc * D + d] = val;
         }
     }
     g = wave_sum(g);
     if (lane == 0) gred[qsub] = g;
   }
   __syncthreads();
-  if (tid == 0) gain_part[(size_t)bh * nqg + qg] = gred[0] + gred[1];
+  if (tid == 0) gain_part[(size_t)bh * n_items + item] = gred[0] + gred[1];
 }
 
-// dRho_h = sum over batch and query groups of the per-group partials; one
-// wave per head, fixed summation order.
-__global__ __launch_bounds__(64) void ca_bwd_gain_kernel(const float* __restrict__ gain_part,
-                                                         float* __restrict__ dlog_gain, int B,
-                                                         int H, int ngroups) {
-  const int h = blockIdx.x;
-  const int lane = threadIdx.x;
-  float acc = 0.f;
-  for (int b = 0; b < B; ++b)
-    for (int k = lane; k < ngroups; k += 64) acc += gain_part[((size_t)b * H + h) * ngroups + k];
-  acc = wave_sum(acc);
-  if (lane == 0) dlog_gain[h] = acc;
+// Work groups [0, H): dRho_h = sum over batch and dQ items of the gain
+// partials (fixed order).  Work groups H + BH*gi + bh: dQ of multi-chunk
+// group nqg-1-gi of slice bh, the sum of its chunk partials in chunk order.
+template <int D>
+__global__ __launch_bounds__(256) void ca_bwd_gain_merge_kernel(
+    const float* __restrict__ gain_part, const float* __restrict__ dq_part,
+    float* __restrict__ dlog_gain, float* __restrict__ dQ, int B, int H, int T, int chunk,
+    int n_items, int n_part) {
+  const int tid = threadIdx.x;
+  if (blockIdx.x < H) {
+    __shared__ float wsum[4];
+    const int h = blockIdx.x;
+    float acc = 0.f;
+    for (int b = 0; b < B; ++b)
+      for (int k = tid; k < n_items; k += 256) acc += gain_part[((size_t)b * H + h) * n_items + k];
+    acc = wave_sum(acc);
+    if ((tid & 63) == 0) wsum[tid >> 6] = acc;
+    __syncthreads();
+    if (tid == 0) dlog_gain[h] = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+    return;
+  }
+  constexpr int C4 = D / 4;
+  const int BH = B * H;
+  const int m = blockIdx.x - H;
+  const int bh = m % BH, gi = m / BH;
+  const int qg = dq_num_groups(T) - 1 - gi;
+  int first = 0;  // item index of the group's chunk 0
+  for (int g = dq_num_groups(T) - 1; g > qg; --g) first += dq_group_chunks(g, T, chunk);
+  const int nch = dq_group_chunks(qg, T, chunk);
+  const f32x4* part = reinterpret_cast<const f32x4*>(dq_part + ((size_t)bh * n_part + first) * 64 * D);
+  f32x4* out = reinterpret_cast<f32x4*>(dQ + ((size_t)bh * T + 64 * qg) * D);
+  for (int e = tid; e < 64 * C4; e += 256) {
+    if (64 * qg + e / C4 >= T) break;
+    f32x4 s = part[e];
+    for (int ch = 1; ch < nch; ++ch) s += part[(size_t)ch * 16 * D + e];
+    out[e] = s;
+  }
 }
 
 template <int D>
 hipError_t launch_bwd(const float* q, const float* k, const float* v, const float* log_gain,
                       const float* o, const float* stats, const float* dout, float* dq, float* dk,
                       float* dv, float* dlog_gain, float* dsbuf, float* dvec, float* gain_part,
-                      int B, int H, int T, hipStream_t stream) {
+                      float* dq_part, const DqSplit& sp, int B, int H, int T,
+                      hipStream_t stream) {
   using P = Bwd<D>;
   const int BH = B * H;
   const int rows = BH * T;
@@ -551,15 +595,16 @@ hipError_t launch_bwd(const float* q, const float* k, const float* v, const floa
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   timer_begin(kBwdDq, stream);
-  const int nqg = dq_num_groups(T);
-  hipLaunchKernelGGL(ca_bwd_dq_kernel<D>, dim3(nqg * BH), dim3(256), 0, stream, dsbuf, q, k,
-                     log_gain, dq, gain_part, BH, H, T);
+  hipLaunchKernelGGL(ca_bwd_dq_kernel<D>, dim3(sp.items * BH), dim3(256), 0, stream, dsbuf, q, k,
+                     log_gain, dq, dq_part, gain_part, BH, H, T, sp.chunk, sp.items,
+                     sp.part_items);
   timer_end(kBwdDq, stream);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   timer_begin(kBwdGain, stream);
-  hipLaunchKernelGGL(ca_bwd_gain_kernel, dim3(H), dim3(64), 0, stream, gain_part, dlog_gain, B,
-                     H, nqg);
+  hipLaunchKernelGGL(ca_bwd_gain_merge_kernel<D>, dim3(H + BH * sp.multi_groups), dim3(256), 0,
+                     stream, gain_part, dq_part, dlog_gain, dq, B, H, T, sp.chunk, sp.items,
+                     sp.part_items);
   timer_end(kBwdGain, stream);
   return hipGetLastError();
 }
@@ -580,8 +625,8 @@ template hipError_t set_bwd_attrs<64>();
 #define CA_INST_BWD(DD)                                                                        \
   template hipError_t launch_bwd<DD>(const float*, const float*, const float*, const float*,   \
                                      const float*, const float*, const float*, float*, float*, \
-                                     float*, float*, float*, float*, float*, int, int, int,    \
-                                     hipStream_t);
+                                     float*, float*, float*, float*, float*, float*,           \
+                                     const DqSplit&, int, int, int, hipStream_t);
 CA_INST_BWD(8)
 CA_INST_BWD(16)
 CA_INST_BWD(32)

@@ -34,7 +34,7 @@ constexpr int kBwdKeys = 30;
 constexpr int kBwdSlots = 32;
 __host__ __device__ inline int bwd_num_key_blocks(int T) { return (T + kBwdKeys - 1) / kBwdKeys; }
 __host__ __device__ inline int num_q_tiles(int T) { return (T + 31) / 32; }
-// dQ work groups (64 queries each) per slice; also the gain partials per slice.
+// 64-query dQ groups per slice.
 __host__ __device__ inline int dq_num_groups(int T) { return (num_q_tiles(T) + 1) / 2; }
 
 // sum_{i=0}^{n-1} floor((a*i + b) / m) for n, m >= 1 and a, b >= 0 (Euclid-like
@@ -74,6 +74,48 @@ inline size_t bwd_ds_floats(int BH, int T) {
   return (size_t)BH * (size_t)ds_blocks_before(num_q_tiles(T)) * kDsBlockFloats;
 }
 
+// dQ work items: a 64-query group of one slice and one chunk of its key
+// blocks.  A group of n blocks is cut into ceil(n / chunk) near-equal chunks
+// (split-K) when the unsplit grid would not fill the GPU for one round, so
+// that the longest rows do not leave it waiting on a few work groups; with a
+// full grid every group is one item (chunk >= bwd_num_key_blocks).  Items are
+// numbered per slice from the last (heaviest) group down, so the chunks of
+// multi-chunk groups come first; those items write partial dQ tiles that a
+// second kernel sums in chunk order.
+constexpr int kDqChunkBlocks = 32;  // split chunk length (measured 16..48: flat)
+// key blocks met by the last query tile of group qg (the group's key range)
+__host__ __device__ inline int dq_group_blocks(int qg, int T) {
+  const int nqt = num_q_tiles(T);
+  const int last = 2 * qg + 1 < nqt ? 2 * qg + 1 : nqt - 1;
+  const int c = ds_kb_count(last), nkb = bwd_num_key_blocks(T);
+  return c < nkb ? c : nkb;
+}
+__host__ __device__ inline int dq_group_chunks(int qg, int T, int chunk) {
+  return (dq_group_blocks(qg, T) + chunk - 1) / chunk;
+}
+struct DqSplit {
+  int chunk;         // key blocks per chunk (upper bound)
+  int items;         // work items per slice
+  int part_items;    // of which write partial tiles (chunks of multi-chunk groups)
+  int multi_groups;  // groups with more than one chunk (the last ones)
+};
+// resident_groups: dQ work groups the GPU holds at once (0: never split)
+inline DqSplit dq_split(int BH, int T, int resident_groups) {
+  const bool split = (long long)dq_num_groups(T) * BH < resident_groups;
+  DqSplit s{split ? kDqChunkBlocks : bwd_num_key_blocks(T), 0, 0, 0};
+  for (int g = 0; g < dq_num_groups(T); ++g) {
+    const int n = dq_group_chunks(g, T, s.chunk);
+    s.items += n;
+    if (n > 1) {
+      s.part_items += n;
+      ++s.multi_groups;
+    }
+  }
+  return s;
+}
+// dQ work groups resident per CU (VGPR-limited: 3 waves per SIMD)
+constexpr int kDqGroupsPerCu = 3;
+
 // Per-kernel HIP-event timing (diagnostics; off unless ca_timing_enable(1)).
 enum KernelId {
   kFwd = 0, kFwdCombine, kBwdRowdot, kBwdDkdv, kBwdDq, kBwdGain, kWeights, kWeightsBwd, kQkvIn,
@@ -109,6 +151,7 @@ template <int D>
 hipError_t launch_bwd(const float* q, const float* k, const float* v, const float* log_gain,
                       const float* o, const float* stats, const float* dout, float* dq, float* dk,
                       float* dv, float* dlog_gain, float* dsbuf, float* dvec, float* gain_part,
-                      int B, int H, int T, hipStream_t stream);
+                      float* dq_part, const DqSplit& sp, int B, int H, int T,
+                      hipStream_t stream);
 
 }  // namespace ca
