@@ -50,6 +50,67 @@ __device__ __forceinline__ f32x16 mfma32(float a, float b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
+// fp32 products on the bf16 matrix cores ("bf16x6").  An fp32 value is split
+// into three bf16 limbs x = h + m + l (+ |r| <= 2^-27 |x|; round-to-nearest
+// limbs carry 9 significant bits each), and a product a*b is the sum of the
+// six limb products whose orders add to <= 2: h*h, h*m, m*h, h*l, m*m, l*h.
+// The dropped terms are <= 2^-26 |a b|, each limb product is exact and the
+// MFMA accumulates in fp32, so a dot product carries fp32-level error (below
+// that of a sequential fp32 FMA chain for D = 64) while
+// v_mfma_f32_32x32x16_bf16 does 8x the multiply-adds of the fp32
+// v_mfma_f32_32x32x2_f32 per instruction.  The six products are issued small
+// terms first.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+
+struct Limbs {  // one 8-element MFMA operand in three limbs (4 VGPRs each)
+  bf16x8 h, m, l;
+};
+
+__device__ __forceinline__ f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+// c += a * b over 16 k values, to fp32 accuracy
+__device__ __forceinline__ f32x16 mfma_x6(const Limbs& a, const Limbs& b, f32x16 c) {
+  c = mfma_bf16(a.l, b.h, c);
+  c = mfma_bf16(a.m, b.m, c);
+  c = mfma_bf16(a.h, b.l, c);
+  c = mfma_bf16(a.m, b.h, c);
+  c = mfma_bf16(a.h, b.m, c);
+  return mfma_bf16(a.h, b.h, c);
+}
+
+// two floats -> packed bf16 pair, round to nearest even; a in the low half
+__device__ __forceinline__ unsigned cvt_pk_bf16(float a, float b) {
+  unsigned r;
+  asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+// limbs of the pair (a, b): h, m, l packed pairs
+__device__ __forceinline__ void split_pair(float a, float b, unsigned& h, unsigned& m,
+                                           unsigned& l) {
+  h = cvt_pk_bf16(a, b);
+  const float ra = a - __uint_as_float(h << 16), rb = b - __uint_as_float(h & 0xffff0000u);
+  m = cvt_pk_bf16(ra, rb);
+  const float sa = ra - __uint_as_float(m << 16), sb = rb - __uint_as_float(m & 0xffff0000u);
+  l = cvt_pk_bf16(sa, sb);
+}
+// limbs of 8 floats (one MFMA operand)
+__device__ __forceinline__ Limbs split8(const float* x) {
+  u32x4 H, M, L;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    unsigned h, m, l;
+    split_pair(x[2 * p], x[2 * p + 1], h, m, l);
+    H[p] = h;
+    M[p] = m;
+    L[p] = l;
+  }
+  return Limbs{__builtin_bit_cast(bf16x8, H), __builtin_bit_cast(bf16x8, M),
+               __builtin_bit_cast(bf16x8, L)};
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 

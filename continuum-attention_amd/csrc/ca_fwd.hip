@@ -1,4 +1,4 @@
-// Continuum Attention forward (gfx950, fp32 MFMA).
+// Continuum Attention forward (gfx950, fp32 products on the bf16 matrix cores).
 //
 // Replaces, for the forward pass, the per-query-tile loop of
 // _CAExactTiled.forward (cuda/continuum_attention.py:650-694): the QK^T bmm,
@@ -8,14 +8,21 @@
 //
 // Work item: one 128-query group (4 waves x 32 queries) of one (b,h) slice and
 // one contiguous range ("split") of 32-key weight tiles.  The 4 waves share
-// double-buffered K/V tiles in LDS.  Items are launched heaviest-first; groups
-// whose key range spans several splits write un-normalised partials that
-// ca_fwd_combine merges (log-sum-exp style; deterministic order).
+// double-buffered K/V tiles in LDS, stored as bf16 limb planes (the split of
+// each fp32 value into three bf16 limbs happens once, when the tile is
+// staged).  Items are launched heaviest-first; groups whose key range spans
+// several splits write un-normalised partials that ca_fwd_combine merges
+// (log-sum-exp style; deterministic order).
 //
-// Per wave, the S^T = K Q^T tile (32 keys x 32 queries) is computed with
-// v_mfma_f32_32x32x2_f32 with keys permuted so that lane (q, h) holds 16
-// consecutive keys of query q.  Segment neighbours are then in the same
-// lane; only the segment crossing the two lane halves needs permlane32_swap.
+// Both products run as bf16x6 (six limb products per fp32 product, fp32
+// accumulation; mfma_x6) on v_mfma_f32_32x32x16_bf16.  Per wave, the S^T =
+// K Q^T tile (32 keys x 32 queries) has keys permuted so that lane (q, h)
+// holds 16 consecutive keys of query q; the K tile is stored in that row
+// order.  Segment neighbours are then in the same lane; only the segment
+// crossing the two lane halves needs permlane32_swap.  In O^T += V^T W^T the
+// MFMA's k index 8h + e of k-block kb stands for weight key 16h + 8kb + e, so
+// each lane feeds its own weights as the B operand and reads V^T (stored
+// transposed) with one 16-byte LDS read per limb.
 //
 // Weight tile t covers weight keys [32t, 32t+32); its score tile covers keys
 // [32t+1, 32t+33).  Lane half h, register n: score key 32t+1+16h+n, weight
@@ -32,17 +39,27 @@ namespace ca {
 template <int D>
 struct Fwd {
   static constexpr int DH = D / 2;            // d values per lane half in the S^T operand
+  static constexpr int KB = (DH + 7) / 8;     // 16-wide k blocks of S^T (8 d per lane half each)
   static constexpr int NMB = (D + 31) / 32;   // 32-row d blocks of O^T
   static constexpr int C4 = D / 4;            // float4 chunks per row
   static constexpr int CH = DH / 4;           // float4 chunks per lane half
   static constexpr int TILE_F4 = 32 * C4;     // float4 per 32-row tile
   static constexpr int LD_PER_THREAD = (TILE_F4 + 255) / 256;
+  static constexpr int VUNITS = 16 * C4;      // (key pair, float4 chunk) units of a V tile
+  static constexpr int VLD = (VUNITS + 255) / 256;
+  // K limb plane: row p = key key_of_arow(p); two halves of 8*KB bf16 (d values
+  // h*DH + ..., zero-padded when DH < 8) and 8 bf16 of padding, so the 16-byte
+  // A-operand reads of 8 consecutive rows hit distinct banks.
+  static constexpr int KROW = 16 * KB + 8;
+  static constexpr int KPLANE = 32 * KROW;
+  // V^T limb plane: row d holds the 32 weight keys of the tile (+8 padding).
+  static constexpr int VROW = 40;
+  static constexpr int VPLANE = D * VROW;
 };
 
-// XOR swizzle of the K tile's float4 chunks (conflict-free A-operand reads
-// for the permuted key order; see key_of_arow).
-__device__ __forceinline__ int kswz(int row, int chunks_per_half) {
-  return ((row & 3) | ((row >> 2) & 4)) & (chunks_per_half - 1);
+// LDS row of the permuted K tile that holds tile key k (inverse of key_of_arow).
+__device__ __forceinline__ int arow_of_key(int k) {
+  return (((k >> 2) & 3) << 3) | (((k >> 4) & 1) << 2) | (k & 3);
 }
 
 // Item decoding: items are (group g, split s) in descending g, then s.
@@ -86,8 +103,9 @@ __global__ __launch_bounds__(256, 2) void ca_fwd_kernel(
     const float* __restrict__ log_gain, float* __restrict__ O, float* __restrict__ stats,
     float* __restrict__ part, int BH, int H, int T, int C, int G, int smax) {
   using P = Fwd<D>;
-  __shared__ f32x4 lds_k[2][P::TILE_F4];
-  __shared__ float lds_v[2][32 * D];
+  // [buffer][limb][plane]
+  __shared__ __attribute__((aligned(16))) __bf16 lds_k[2][3][P::KPLANE];
+  __shared__ __attribute__((aligned(16))) __bf16 lds_vt[2][3][P::VPLANE];
 
   const int bh = blockIdx.x % BH;
   const int item = blockIdx.x / BH;
@@ -117,7 +135,7 @@ __global__ __launch_bounds__(256, 2) void ca_fwd_kernel(
   const int head = bh % H;
   const float cl2 = head_scale_log2(log_gain, head, D);
 
-  // B operand of S^T: lane (q,h) holds Q[i][h*DH + k] * c*log2e
+  // lane (q,h) holds Q[i][h*DH + k] * c*log2e
   float qreg[P::DH];
   {
     const f32x4* qp = reinterpret_cast<const f32x4*>(Qs + (size_t)(qvalid ? i : 0) * D + h * P::DH);
@@ -149,28 +167,59 @@ __global__ __launch_bounds__(256, 2) void ca_fwd_kernel(
     }
   }
 
+  // B operand of S^T in limbs: k block kb, element e = Q[i][h*DH + 8kb + e] * c*log2e
+  Limbs qb[P::KB];
+#pragma unroll
+  for (int kb = 0; kb < P::KB; ++kb) {
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = (8 * kb + e < P::DH) ? qreg[8 * kb + e] : 0.f;
+    qb[kb] = split8(x);
+  }
+
   f32x16 acc_o[P::NMB];
 #pragma unroll
   for (int mb = 0; mb < P::NMB; ++mb)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc_o[mb][r] = 0.f;
 
+  // Half-padded K rows (DH < 8) keep zeros in their pad slots: clear both
+  // buffers once; the tile stores never write the pads.
+  if (P::DH < 8) {
+    unsigned* z = reinterpret_cast<unsigned*>(&lds_k[0][0][0]);
+    for (int e = tid; e < 2 * 3 * P::KPLANE / 2; e += 256) z[e] = 0u;
+    __syncthreads();
+  }
+
   // ---- cooperative tile loads ------------------------------------------
-  f32x4 pre_k[P::LD_PER_THREAD], pre_v[P::LD_PER_THREAD];
+  // K: float4 chunk e -> score key 32t+1+row, d = 4c..4c+3.  V: unit u ->
+  // weight keys 32t+2pp, +1 (a key pair, so the transposed store writes
+  // packed bf16 pairs), d = 4c..4c+3.
+  f32x4 pre_k[P::LD_PER_THREAD], pre_v[P::VLD][2];
   auto load_tile = [&](int t) {
 #pragma unroll
     for (int j = 0; j < P::LD_PER_THREAD; ++j) {
       const int e = tid + 256 * j;
-      f32x4 kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
+      f32x4 kv = {0.f, 0.f, 0.f, 0.f};
       if (e < P::TILE_F4) {
         const int row = e / P::C4, c = e % P::C4;
         const int kk = 32 * t + 1 + row;  // score key
-        const int vk = 32 * t + row;      // weight key
         if (kk < T) kv = reinterpret_cast<const f32x4*>(Ks + (size_t)kk * D)[c];
-        if (vk < T) vv = reinterpret_cast<const f32x4*>(Vs + (size_t)vk * D)[c];
       }
       pre_k[j] = kv;
-      pre_v[j] = vv;
+    }
+#pragma unroll
+    for (int j = 0; j < P::VLD; ++j) {
+      const int u = tid + 256 * j;
+      f32x4 v0 = {0.f, 0.f, 0.f, 0.f}, v1 = {0.f, 0.f, 0.f, 0.f};
+      if (u < P::VUNITS) {
+        const int pp = u / P::C4, c = u % P::C4;
+        const int vk = 32 * t + 2 * pp;  // weight key
+        if (vk < T) v0 = reinterpret_cast<const f32x4*>(Vs + (size_t)vk * D)[c];
+        if (vk + 1 < T) v1 = reinterpret_cast<const f32x4*>(Vs + (size_t)(vk + 1) * D)[c];
+      }
+      pre_v[j][0] = v0;
+      pre_v[j][1] = v1;
     }
   };
   auto store_tile = [&](int buf) {
@@ -179,9 +228,30 @@ __global__ __launch_bounds__(256, 2) void ca_fwd_kernel(
       const int e = tid + 256 * j;
       if (e < P::TILE_F4) {
         const int row = e / P::C4, c = e % P::C4;
-        const int half = c / P::CH, cc = c % P::CH;
-        lds_k[buf][row * P::C4 + half * P::CH + (cc ^ kswz(row, P::CH))] = pre_k[j];
-        reinterpret_cast<f32x4*>(&lds_v[buf][0])[e] = pre_v[j];
+        const int d = 4 * c, half = d / P::DH;
+        const int off = arow_of_key(row) * P::KROW + half * 8 * P::KB + (d - half * P::DH);
+        unsigned h0, m0, l0, h1, m1, l1;
+        split_pair(pre_k[j][0], pre_k[j][1], h0, m0, l0);
+        split_pair(pre_k[j][2], pre_k[j][3], h1, m1, l1);
+        *reinterpret_cast<u32x2*>(&lds_k[buf][0][off]) = u32x2{h0, h1};
+        *reinterpret_cast<u32x2*>(&lds_k[buf][1][off]) = u32x2{m0, m1};
+        *reinterpret_cast<u32x2*>(&lds_k[buf][2][off]) = u32x2{l0, l1};
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < P::VLD; ++j) {
+      const int u = tid + 256 * j;
+      if (u < P::VUNITS) {
+        const int pp = u / P::C4, c = u % P::C4;
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          unsigned hv, mv, lv;
+          split_pair(pre_v[j][0][x], pre_v[j][1][x], hv, mv, lv);
+          const int off = (4 * c + x) * P::VROW + 2 * pp;
+          *reinterpret_cast<unsigned*>(&lds_vt[buf][0][off]) = hv;
+          *reinterpret_cast<unsigned*>(&lds_vt[buf][1][off]) = mv;
+          *reinterpret_cast<unsigned*>(&lds_vt[buf][2][off]) = lv;
+        }
       }
     }
   };
@@ -190,7 +260,7 @@ __global__ __launch_bounds__(256, 2) void ca_fwd_kernel(
   store_tile(0);
   __syncthreads();
 
-  const int arow = key_of_arow(lane);  // K-tile row this lane feeds to the A operand
+  const bool dok = q < D;  // only D < 32 pads the d block of O^T
 
   for (int t = t_b; t < t_e; ++t) {
     const int buf = (t - t_b) & 1;
@@ -206,27 +276,15 @@ __global__ __launch_bounds__(256, 2) void ca_fwd_kernel(
       f32x16 sacc;
 #pragma unroll
       for (int r = 0; r < 16; ++r) sacc[r] = -m_ref;
-      // V^T operands of this tile's PV product, read now so their LDS latency
-      // hides behind the S^T MFMAs and the segment math
-      const bool dok = q < D;  // only D < 32 pads the d block
-      float va[P::NMB][16];
       {
-        const float* vcol = &lds_v[buf][(16 * h) * D + (dok ? q : 0)];
+        const __bf16* krow = &lds_k[buf][0][q * P::KROW + h * 8 * P::KB];
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-#pragma unroll
-          for (int mb = 0; mb < P::NMB; ++mb) va[mb][r] = dok ? vcol[r * D + 32 * mb] : 0.f;
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      {
-        const f32x4* krow = &lds_k[buf][arow * P::C4 + h * P::CH];
-#pragma unroll
-        for (int c = 0; c < P::CH; ++c) {
-          f32x4 kv = krow[c ^ kswz(arow, P::CH)];
-          sacc = mfma32(kv[0], qreg[4 * c + 0], sacc);
-          sacc = mfma32(kv[1], qreg[4 * c + 1], sacc);
-          sacc = mfma32(kv[2], qreg[4 * c + 2], sacc);
-          sacc = mfma32(kv[3], qreg[4 * c + 3], sacc);
+        for (int kb = 0; kb < P::KB; ++kb) {
+          Limbs ka;
+          ka.h = *reinterpret_cast<const bf16x8*>(krow + 8 * kb);
+          ka.m = *reinterpret_cast<const bf16x8*>(krow + P::KPLANE + 8 * kb);
+          ka.l = *reinterpret_cast<const bf16x8*>(krow + 2 * P::KPLANE + 8 * kb);
+          sacc = mfma_x6(ka, qb[kb], sacc);
         }
       }
       const int kbase = 32 * t + 1 + 16 * h;  // score key of register 0
@@ -297,11 +355,23 @@ __global__ __launch_bounds__(256, 2) void ca_fwd_kernel(
       sacc[0] += r_in;
       zsum += zt + r_in;
 
-      // ---- O^T += V^T W^T ----
+      // ---- O^T += V^T W^T: k block kb, element e = weight key 16h + 8kb + e ----
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
+      for (int kb = 0; kb < 2; ++kb) {
+        float x[8];
 #pragma unroll
-        for (int mb = 0; mb < P::NMB; ++mb) acc_o[mb] = mfma32(va[mb][r], sacc[r], acc_o[mb]);
+        for (int e = 0; e < 8; ++e) x[e] = sacc[8 * kb + e];
+        const Limbs wb = split8(x);
+#pragma unroll
+        for (int mb = 0; mb < P::NMB; ++mb) {
+          const __bf16* vrow = &lds_vt[buf][0][(dok ? 32 * mb + q : 0) * P::VROW + 16 * h + 8 * kb];
+          Limbs va;
+          va.h = *reinterpret_cast<const bf16x8*>(vrow);
+          va.m = *reinterpret_cast<const bf16x8*>(vrow + P::VPLANE);
+          va.l = *reinterpret_cast<const bf16x8*>(vrow + 2 * P::VPLANE);
+          if (!dok) va = Limbs{bf16x8{}, bf16x8{}, bf16x8{}};
+          acc_o[mb] = mfma_x6(va, wb, acc_o[mb]);
+        }
       }
     };
     if (wave_active && t <= wave_tmax) {
