@@ -46,7 +46,7 @@ SIGNATURES = {
     "ca_timing_read": (_i, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i), _i]),
 }
 
-KERNEL_NAMES = ("ca_fwd", "ca_fwd_combine", "ca_bwd_rowdot", "ca_bwd_dkdv", "ca_bwd_dq",
+KERNEL_NAMES = ("ca_fwd", "ca_fwd_combine", "ca_bwd_prep", "ca_bwd_dkdv", "ca_bwd_dq",
                 "ca_bwd_gain", "ca_weights", "ca_weights_bwd", "ca_qkv_in", "ca_qkv_grad",
                 "ca_relayout")
 

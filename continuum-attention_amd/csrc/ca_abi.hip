@@ -12,11 +12,6 @@
 #include "../../include/continuum_attention_amd.h"
 #include "ca_kernels.h"
 
-namespace ca {
-template <int D>
-hipError_t set_bwd_attrs();
-}
-
 namespace {
 
 thread_local char g_err[512] = "";
@@ -71,30 +66,19 @@ int dq_resident_groups() {
 }
 
 struct BwdLayout {
-  size_t ds, dvec, gain, dqpart, total;
+  size_t ds, limbs, qstat, gain, dqpart, total;
 };
 BwdLayout bwd_layout(int B, int H, int T, int D) {
   const int BH = B * H;
   const ca::DqSplit sp = ca::dq_split(BH, T, kDqSplitBound);  // the largest split
   BwdLayout L;
   L.ds = 0;
-  L.dvec = align256(ca::bwd_ds_floats(BH, T) * sizeof(float));
-  L.gain = L.dvec + align256((size_t)BH * T * sizeof(float));
+  L.limbs = align256(ca::bwd_ds_floats(BH, T) * sizeof(float));
+  L.qstat = L.limbs + align256(ca::bwd_limb_elems(BH, T, D) * sizeof(uint16_t));
+  L.gain = L.qstat + align256((size_t)BH * T * 2 * sizeof(float));
   L.dqpart = L.gain + align256((size_t)BH * sp.items * sizeof(float));
   L.total = L.dqpart + align256((size_t)BH * sp.part_items * 64 * D * sizeof(float));
   return L;
-}
-
-bool g_attrs_done = false;
-int ensure_attrs() {
-  if (g_attrs_done) return CA_OK;
-  hipError_t e = ca::set_bwd_attrs<8>();
-  if (e == hipSuccess) e = ca::set_bwd_attrs<16>();
-  if (e == hipSuccess) e = ca::set_bwd_attrs<32>();
-  if (e == hipSuccess) e = ca::set_bwd_attrs<64>();
-  if (e != hipSuccess) return fail(CA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
-  g_attrs_done = true;
-  return CA_OK;
 }
 
 // ---- per-kernel event timing ------------------------------------------------
@@ -230,20 +214,21 @@ int ca_bwd_f32(const float* q, const float* k, const float* v, const float* log_
   if (!workspace || workspace_bytes < L.total)
     return fail(CA_ERR_WORKSPACE, "backward workspace of %zu bytes required, %zu given", L.total,
                 workspace_bytes);
-  if ((rc = ensure_attrs())) return rc;
   char* ws = static_cast<char*>(workspace);
-  float* dsbuf = reinterpret_cast<float*>(ws + L.ds);
-  float* dvec = reinterpret_cast<float*>(ws + L.dvec);
-  float* gain = reinterpret_cast<float*>(ws + L.gain);
-  float* dqpart = reinterpret_cast<float*>(ws + L.dqpart);
+  ca::BwdWork work;
+  work.dsbuf = reinterpret_cast<float*>(ws + L.ds);
+  work.limbs = reinterpret_cast<__bf16*>(ws + L.limbs);
+  work.qstat = reinterpret_cast<float*>(ws + L.qstat);
+  work.gain_part = reinterpret_cast<float*>(ws + L.gain);
+  work.dq_part = reinterpret_cast<float*>(ws + L.dqpart);
   const ca::DqSplit sp = ca::dq_split(B * H, T, dq_resident_groups());
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;
   switch (D) {
-    case 8: e = ca::launch_bwd<8>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, dsbuf, dvec, gain, dqpart, sp, B, H, T, s); break;
-    case 16: e = ca::launch_bwd<16>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, dsbuf, dvec, gain, dqpart, sp, B, H, T, s); break;
-    case 32: e = ca::launch_bwd<32>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, dsbuf, dvec, gain, dqpart, sp, B, H, T, s); break;
-    default: e = ca::launch_bwd<64>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, dsbuf, dvec, gain, dqpart, sp, B, H, T, s); break;
+    case 8: e = ca::launch_bwd<8>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, work, sp, B, H, T, s); break;
+    case 16: e = ca::launch_bwd<16>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, work, sp, B, H, T, s); break;
+    case 32: e = ca::launch_bwd<32>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, work, sp, B, H, T, s); break;
+    default: e = ca::launch_bwd<64>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, work, sp, B, H, T, s); break;
   }
   if (e != hipSuccess) return fail(CA_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
   return CA_OK;

@@ -1,4 +1,4 @@
-// Continuum Attention backward (gfx950, fp32 MFMA), analytic first-order VJP.
+// Continuum Attention backward (gfx950), analytic first-order VJP.
 //
 // Replaces the per-query-tile loop of _CAExactTiled.backward
 // (cuda/continuum_attention.py:697-766): the QK^T and dY.V^T recomputation,
@@ -7,29 +7,34 @@
 // the dV/dQ/dK/dRho contractions.
 //
 // Kernels (all deterministic, no atomics):
-//   ca_bwd_rowdot   Dl_i = dY_i . y_i   (equals sum_j W_ij dW_ij; the reference
-//                   forms the same row mean at cuda/continuum_attention.py:268-269)
-//   ca_bwd_dkdv     one work group per (slice, 30-key block); 4 waves take
-//                   interleaved 32-query tiles.  Per tile: S^T = K Q^T and
-//                   dP^T = V dY^T by MFMA (K, V slot rows from LDS shared by
-//                   the work group; Q, dY rows straight from the lane's own
-//                   prefetched registers), W and dS in registers, then
-//                   dV^T += dY^T W and dK^T += Q^T dS by MFMA (W, dS through a
-//                   transposed LDS tile; dY^T, then Q^T, read column-wise
-//                   from the wave's row tile).  dS is also written,
-//                   straight from registers, as 32x32 row blocks for the dQ
-//                   pass.  ~68 KB of LDS and <= 256 VGPRs: two work groups
-//                   share a CU and hide each other's staging, waits and
-//                   epilogue behind their MFMA phases.
-//   ca_bwd_dq       dQ = c dS (K - k_ref), one work group per (slice, 64
-//                   queries); its epilogue also forms the gain partial
-//                   sum_i q_i . dQ_i (= sum_ij dS_ij s_ij, since s_ij = c q_i . k_j).
-//   ca_bwd_gain     dRho_h = sum over batch and query groups of the partials.
+//   ca_bwd_prep     per query row: Dl_i = dY_i . y_i (the reference forms the
+//                   same row mean at cuda/continuum_attention.py:268-269),
+//                   Q_i and dY_i / Z_i split into bf16 limb planes, and
+//                   (m_i, Dl_i / Z_i).
+//   ca_bwd_dkdv     one work group per (slice, 56 keys); wave w owns 14 keys
+//                   (16 MFMA slots).  The 4 waves walk the query tiles
+//                   together: each 32-query tile of Q and dY/Z limbs is staged
+//                   once in LDS (double-buffered) and read by every wave both
+//                   row-wise (S = Q K^T, dP' = (dY/Z) V^T) and transposed
+//                   (dV^T += (dY/Z)^T W, dK^T += Q^T dS) with
+//                   ds_read_b64_tr_b16.  K and V of the wave's slots stay in
+//                   registers as bf16 limbs for the whole launch.  All four
+//                   products are bf16x6 on v_mfma_f32_16x16x32_bf16.  dS is
+//                   also spilled as 32x16 row blocks for the dQ pass.
+//   ca_bwd_dq       dQ = c dS (K - k_ref) over the spilled blocks, one work
+//                   item per (slice, 64 queries, chunk of key blocks); each
+//                   item also forms its gain partial sum_i q_i . dQ_i
+//                   (= sum_ij dS_ij s_ij, since s_ij = c q_i . k_j).
+//   ca_bwd_gain_merge  dRho_h = sum of the gain partials; sums the dQ chunk
+//                   partials of split query groups.
 //
-// Key-block layout: the work group owns weight keys [w0, w0+30); its 32 MFMA
-// key slots are keys w0-1 .. w0+30 (slot s = key w0-1+s), so both neighbours
-// of every owned key are inside the tile.  Lane half h, register n holds slot
-// 16h+n of query q.
+// Score-tile layout in ca_bwd_dkdv: the 16x16 result of S / dP' puts slot j
+// (key 14*kb - 1 + j) in lane j of each 16-lane row and queries 4*(l/16) + r
+// in its registers, so the two neighbours of a segment sit in adjacent lanes
+// of one DPP row (row_shr / row_shl).  p = 2^(s - m) stays unnormalised and
+// dY arrives pre-scaled by 1/Z, so the weight gradient g = dY.v/Z - Dl/Z comes
+// straight out of the MFMA (its accumulator starts at -Dl/Z) and dV = W^T dY
+// is formed as w^T (dY/Z) with no per-row scaling in the kernel.
 #include <type_traits>
 
 #include "ca_common.h"
@@ -39,320 +44,337 @@ namespace ca {
 
 template <int D>
 struct Bwd {
-  static constexpr int DH = D / 2;            // d values per lane half (k-range split)
-  static constexpr int NMB = (D + 31) / 32;   // 32-row d blocks of dV^T / dK^T
-  static constexpr int C4 = D / 4;            // float4 chunks per row
-  static constexpr int CH = DH / 4;           // chunks per lane half
-  static constexpr int LDQ = D + 4;           // padded row stride: K/V slot tiles and Q tile
-  static constexpr int LDX = kBwdSlots + 1;   // row stride of the [slot][query] transpose tile
-  static constexpr int SLOT_FLOATS = 32 * LDQ;
-  static constexpr int QT_FLOATS = 32 * LDQ;
-  static constexpr int XT_FLOATS = ((kBwdSlots * LDX + 3) / 4) * 4;
-  static constexpr int WAVE_FLOATS = QT_FLOATS + XT_FLOATS;
-  static constexpr int MAIN_FLOATS = 2 * SLOT_FLOATS + 4 * WAVE_FLOATS;
-  static constexpr int RED_FLOATS = 4 * NMB * 16 * 64;  // epilogue: one matrix, all waves
-  static constexpr int LDS_FLOATS = MAIN_FLOATS > RED_FLOATS ? MAIN_FLOATS : RED_FLOATS;
+  static constexpr int C4 = D / 4;             // float4 chunks per row
+  static constexpr int KB = (D + 31) / 32;     // 32-wide k blocks of S / dP'
+  static constexpr int NMB = (D + 15) / 16;    // 16-row d blocks of dV^T / dK^T
+  static constexpr int LDR = D + 8;            // bf16 row stride of a staged tile
+  static constexpr int LIMB = 32 * LDR;        // bf16 per limb plane of a tile
+  static constexpr int TILE = 6 * LIMB;        // Q limbs h, m, l then dY/Z limbs h, m, l
+  static constexpr int RCH = D / 8;            // 16-byte chunks per row and plane
+  static constexpr int CHUNKS = 6 * 32 * RCH;  // chunks staged per tile
+  static constexpr int CPT = (CHUNKS + 255) / 256;
 };
 
-// Dl_i = dY_i . y_i: one float4 chunk per thread, D/4 lanes per row.
+// One thread per (row, float4 chunk): Dl = dY . y, then the Q and dY/Z limbs
+// of the chunk and, per row, (m, Dl/Z).  `rows` = B*H*T; plane p of `limbs`
+// starts at p * rows * D.
 template <int D>
-__global__ __launch_bounds__(256) void ca_bwd_rowdot_kernel(const float* __restrict__ dout,
-                                                            const float* __restrict__ out,
-                                                            float* __restrict__ dvec, int rows) {
+__global__ __launch_bounds__(256) void ca_bwd_prep_kernel(const float* __restrict__ Q,
+                                                          const float* __restrict__ dout,
+                                                          const float* __restrict__ out,
+                                                          const float* __restrict__ stats,
+                                                          __bf16* __restrict__ limbs,
+                                                          float* __restrict__ qstat, int rows) {
   constexpr int C4 = D / 4;
   const int t = blockIdx.x * 256 + threadIdx.x;
   const int row = t / C4, c = t % C4;
-  float x = 0.f;
-  if (row < rows) {
-    const f32x4 a = reinterpret_cast<const f32x4*>(dout + (size_t)row * D)[c];
-    const f32x4 b = reinterpret_cast<const f32x4*>(out + (size_t)row * D)[c];
-    x = a[0] * b[0] + a[1] * b[1] + a[2] * b[2] + a[3] * b[3];
+  const bool ok = row < rows;
+  f32x4 dy = {0.f, 0.f, 0.f, 0.f}, y = dy, qq = dy;
+  float m = 0.f, invz = 0.f;
+  if (ok) {
+    dy = reinterpret_cast<const f32x4*>(dout + (size_t)row * D)[c];
+    y = reinterpret_cast<const f32x4*>(out + (size_t)row * D)[c];
+    qq = reinterpret_cast<const f32x4*>(Q + (size_t)row * D)[c];
+    m = stats[(size_t)row * 2 + 0];
+    invz = stats[(size_t)row * 2 + 1];
   }
+  float x = dy[0] * y[0] + dy[1] * y[1] + dy[2] * y[2] + dy[3] * y[3];
 #pragma unroll
   for (int o = C4 / 2; o >= 1; o >>= 1) x += __shfl_xor(x, o);
-  if (row < rows && c == 0) dvec[row] = x;
+  if (!ok) return;
+  const size_t plane = (size_t)rows * D;
+  const size_t off = (size_t)row * D + 4 * c;
+  auto put = [&](int p0, f32x4 v) {
+    unsigned h0, m0, l0, h1, m1, l1;
+    split_pair(v[0], v[1], h0, m0, l0);
+    split_pair(v[2], v[3], h1, m1, l1);
+    *reinterpret_cast<u32x2*>(limbs + (size_t)(p0 + 0) * plane + off) = u32x2{h0, h1};
+    *reinterpret_cast<u32x2*>(limbs + (size_t)(p0 + 1) * plane + off) = u32x2{m0, m1};
+    *reinterpret_cast<u32x2*>(limbs + (size_t)(p0 + 2) * plane + off) = u32x2{l0, l1};
+  };
+  put(0, qq);
+  put(3, dy * invz);
+  if (c == 0) {
+    qstat[(size_t)row * 2 + 0] = m;
+    qstat[(size_t)row * 2 + 1] = x * invz;
+  }
 }
 
 template <int D>
 __global__ __launch_bounds__(256, 2) void ca_bwd_dkdv_kernel(
-    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-    const float* __restrict__ dO, const float* __restrict__ stats, const float* __restrict__ dvec,
-    const float* __restrict__ log_gain, float* __restrict__ dK, float* __restrict__ dV,
-    float* __restrict__ dsbuf, int BH, int H, int T) {
+    const float* __restrict__ K, const float* __restrict__ V, const __bf16* __restrict__ limbs,
+    const float* __restrict__ qstat, const float* __restrict__ log_gain, float* __restrict__ dK,
+    float* __restrict__ dV, float* __restrict__ dsbuf, int BH, int H, int T) {
   using P = Bwd<D>;
-  extern __shared__ float lds[];
+  __shared__ __attribute__((aligned(16))) __bf16 tiles[2][P::TILE];
+  __shared__ f32x4 tstat[2][16];  // rows 2u, 2u+1: (m, Dl/Z, m, Dl/Z)
 
   const int nqt = num_q_tiles(T);
+  const int nkb = bwd_num_key_blocks(T);
   const int bh = blockIdx.x % BH;
-  const int kb = blockIdx.x / BH;  // ascending: heaviest key blocks first
-  const int w0 = kBwdKeys * kb;
+  const int wg = blockIdx.x / BH;  // ascending: heaviest first
+  const int w0 = kDkdvWaves * kBwdKeys * wg;
 
   const int tid = threadIdx.x;
-  const int w = tid >> 6;
+  const int wv = tid >> 6;
   const int lane = tid & 63;
-  const int q = lane & 31;
-  const int h = lane >> 5;
-
-  float* Ks = lds;                     // K slot rows, scaled by c log2e
-  float* Vs = lds + P::SLOT_FLOATS;    // V slot rows
-  float* At = lds + 2 * P::SLOT_FLOATS + w * P::WAVE_FLOATS;  // this wave's dY, then Q, tile
-  float* Xt = At + P::QT_FLOATS;       // this wave's W / dS tile, [slot][query]
+  const int j = lane & 15;  // slot
+  const int g = lane >> 4;  // k group / row group
+  const int kb16 = kDkdvWaves * wg + wv;
+  const int key_j = kBwdKeys * kb16 - 1 + j;  // key of this lane's slot
+  const int kmin = kBwdKeys * kb16 - 1;        // key of slot 0
 
   const size_t slice = (size_t)bh * T * D;
   const float cl2 = head_scale_log2(log_gain, bh % H, D);
 
-  // ---- the block's 32 K and V slot rows (slot s = key w0-1+s), shared by the waves ----
-  for (int e = tid; e < 32 * P::C4; e += 256) {
-    const int s = e / P::C4, c = e % P::C4;
-    const int key = w0 - 1 + s;
-    f32x4 kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
-    if (key >= 0 && key < T) {
-      kv = reinterpret_cast<const f32x4*>(K + slice + (size_t)key * D)[c] * cl2;
-      vv = reinterpret_cast<const f32x4*>(V + slice + (size_t)key * D)[c];
-    }
-    *reinterpret_cast<f32x4*>(Ks + s * P::LDQ + 4 * c) = kv;
-    *reinterpret_cast<f32x4*>(Vs + s * P::LDQ + 4 * c) = vv;
+  // Stale LDS bits must not reach an MFMA as NaN through padding columns.
+  {
+    unsigned* z = reinterpret_cast<unsigned*>(&tiles[0][0]);
+    for (int e = tid; e < 2 * P::TILE / 2; e += 256) z[e] = 0u;
   }
 
-  f32x16 accv[P::NMB], acck[P::NMB];
+  // K (scaled by c log2e) and V of this lane's slot: B operands of S / dP',
+  // k block kb, element e = d 32kb + 8g + e.
+  Limbs kl[P::KB], vl[P::KB];
 #pragma unroll
-  for (int mb = 0; mb < P::NMB; ++mb)
+  for (int kb = 0; kb < P::KB; ++kb) {
+    float xk[8], xv[8];
+    const int d0 = 32 * kb + 8 * g;
+    const bool ok = key_j >= 0 && key_j < T && d0 < D;
+    const f32x4* kp = reinterpret_cast<const f32x4*>(K + slice + (size_t)(ok ? key_j : 0) * D + (ok ? d0 : 0));
+    const f32x4* vp = reinterpret_cast<const f32x4*>(V + slice + (size_t)(ok ? key_j : 0) * D + (ok ? d0 : 0));
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      accv[mb][r] = 0.f;
-      acck[mb][r] = 0.f;
+    for (int h2 = 0; h2 < 2; ++h2) {
+      const bool ok2 = ok && d0 + 4 * h2 < D;
+      const f32x4 a = ok2 ? kp[h2] * cl2 : f32x4{0.f, 0.f, 0.f, 0.f};
+      const f32x4 b = ok2 ? vp[h2] : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xk[4 * h2 + e] = a[e];
+        xv[4 * h2 + e] = b[e];
+      }
     }
-  const int qt0 = w0 / 32;  // first query tile that sees an owned key
-  // dS block index of (this wave's current query tile, kb)
-  long long ds_blk = (long long)bh * ds_blocks_before(nqt) + ds_blocks_before(qt0 + w) + kb;
-  // This lane's own query row half of Q and dY for the next tile (the B
-  // operands of S^T / dP^T), plus its row stats; loaded a tile ahead, dY and
-  // stats as soon as the current ones are consumed, Q after its tile is staged.
-  f32x4 pf_q[P::CH], pf_o[P::CH];
-  float pf_m2 = 0.f, pf_invz = 0.f, pf_d = 0.f;
-  auto prefetch_rows = [&](int qt, const float* __restrict__ src, f32x4* dst) {
-    const int i = 32 * qt + q;
-    const bool ok = i < T;
-    const f32x4* rp = reinterpret_cast<const f32x4*>(src + slice + (size_t)(ok ? i : 0) * D + h * P::DH);
-#pragma unroll
-    for (int c = 0; c < P::CH; ++c) dst[c] = ok ? rp[c] : f32x4{0.f, 0.f, 0.f, 0.f};
-  };
-  auto prefetch_stats = [&](int qt) {
-    const int i = 32 * qt + q;
-    const bool ok = i < T;
-    pf_m2 = ok ? stats[((size_t)bh * T + i) * 2 + 0] : 0.f;
-    pf_invz = ok ? stats[((size_t)bh * T + i) * 2 + 1] : 0.f;
-    pf_d = ok ? dvec[(size_t)bh * T + i] : 0.f;
-  };
-  if (qt0 + w < nqt) {
-    prefetch_rows(qt0 + w, Q, pf_q);
-    prefetch_rows(qt0 + w, dO, pf_o);
-    prefetch_stats(qt0 + w);
+    kl[kb] = split8(xk);
+    vl[kb] = split8(xv);
   }
 
-  const int arow = key_of_arow(lane);  // slot row this lane feeds to the S^T / dP^T A operand
-  const bool dok = q < D;              // D < 32 pads the d rows of dV^T / dK^T
-  const int dcol = dok ? q : 0;
+  f32x4 accv[P::NMB], acck[P::NMB];
+#pragma unroll
+  for (int mb = 0; mb < P::NMB; ++mb) {
+    accv[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    acck[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // ---- query-tile staging (all waves), one tile ahead ----
+  const size_t plane = (size_t)BH * T * D;
+  u32x4 pre[P::CPT];
+  f32x4 pre_st = {0.f, 0.f, 0.f, 0.f};
+  auto load_tile = [&](int qt) {
+#pragma unroll
+    for (int u = 0; u < P::CPT; ++u) {
+      const int e = tid + 256 * u;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (e < P::CHUNKS) {
+        const int pl = e / (32 * P::RCH), rem = e % (32 * P::RCH);
+        const int row = rem / P::RCH, ch = rem % P::RCH;
+        const int i = 32 * qt + row;
+        if (i < T)
+          v = *reinterpret_cast<const u32x4*>(limbs + (size_t)pl * plane + slice + (size_t)i * D + 8 * ch);
+      }
+      pre[u] = v;
+    }
+    if (tid < 16) {
+      const int i = 32 * qt + 2 * tid;
+      f32x4 v = {0.f, 0.f, 0.f, 0.f};
+      const float* sp = qstat + ((size_t)bh * T + (i < T ? i : 0)) * 2;
+      if (i + 1 < T) {
+        v = *reinterpret_cast<const f32x4*>(sp);
+      } else if (i < T) {
+        v[0] = sp[0];
+        v[1] = sp[1];
+      }
+      pre_st = v;
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < P::CPT; ++u) {
+      const int e = tid + 256 * u;
+      if (e < P::CHUNKS) {
+        const int pl = e / (32 * P::RCH), rem = e % (32 * P::RCH);
+        const int row = rem / P::RCH, ch = rem % P::RCH;
+        *reinterpret_cast<u32x4*>(&tiles[buf][pl * P::LIMB + row * P::LDR + 8 * ch]) = pre[u];
+      }
+    }
+    if (tid < 16) tstat[buf][tid] = pre_st;
+  };
+
+  const int qt0 = w0 / 32;  // first query tile that sees an owned key of the work group
+  // dS block of (tile qt, this wave's block); advanced by ds_kb_count(qt) per tile
+  size_t ds_blk = (size_t)bh * ds_blocks_before(nqt) + ds_blocks_before(qt0) + kb16;
+  __syncthreads();          // LDS clear before the first store
+  if (qt0 < nqt) {
+    load_tile(qt0);
+    store_tile(0);
+  }
   __syncthreads();
 
-  for (int qt = qt0 + w; qt < nqt; qt += 4) {
+  for (int qt = qt0; qt < nqt; ++qt) {
+    const int buf = (qt - qt0) & 1;
+    if (qt + 1 < nqt) load_tile(qt + 1);
     const int i0 = 32 * qt;
-    const int i = i0 + q;
-    const float m2 = pf_m2, invz = pf_invz, dz = pf_d * pf_invz;
+    // the wave's block meets this tile (and exists)
+    const bool work = kb16 < nkb && kBwdKeys * kb16 <= i0 + 31;
+    if (work) {
+      const __bf16* Tq = &tiles[buf][0];
+      const __bf16* Ty = &tiles[buf][3 * P::LIMB];
 
-    // ---- dY row (this lane's half) into the wave's tile for the dV pass ----
+      // ---- S - m and dP' - Dl/Z (row blocks rb: queries i0 + 16rb + 4g + r) ----
+      f32x4 sacc[2], pacc[2];
 #pragma unroll
-    for (int c = 0; c < P::CH; ++c)
-      *reinterpret_cast<f32x4*>(At + q * P::LDQ + h * P::DH + 4 * c) = pf_o[c];
-
-    // ---- S^T (minus the row shift, folded into the accumulator) and dP^T ----
-    // A operands from the shared slot tiles (chunk c+1 read before the MFMAs
-    // of chunk c issue), B operands from this lane's own prefetched rows.
-    f32x16 sacc, pacc;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      sacc[r] = -m2;
-      pacc[r] = 0.f;
-    }
-    {
-      const float* krow = Ks + arow * P::LDQ + h * P::DH;
-      const float* vrow = Vs + arow * P::LDQ + h * P::DH;
-      f32x4 kv_n = *reinterpret_cast<const f32x4*>(krow);
-      f32x4 vv_n = *reinterpret_cast<const f32x4*>(vrow);
-#pragma unroll
-      for (int c = 0; c < P::CH; ++c) {
-        const f32x4 kv = kv_n, vv = vv_n;
-        if (c + 1 < P::CH) {
-          kv_n = *reinterpret_cast<const f32x4*>(krow + 4 * (c + 1));
-          vv_n = *reinterpret_cast<const f32x4*>(vrow + 4 * (c + 1));
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          sacc = mfma32(kv[e], pf_q[c][e], sacc);
-          pacc = mfma32(vv[e], pf_o[c][e], pacc);
-        }
-        __builtin_amdgcn_sched_barrier(0);
+      for (int rb = 0; rb < 2; ++rb) {
+        const f32x4 s01 = tstat[buf][8 * rb + 2 * g], s23 = tstat[buf][8 * rb + 2 * g + 1];
+        sacc[rb] = f32x4{-s01[0], -s01[2], -s23[0], -s23[2]};
+        pacc[rb] = f32x4{-s01[1], -s01[3], -s23[1], -s23[3]};
       }
-    }
+#pragma unroll
+      for (int kb = 0; kb < P::KB; ++kb) {
+        const int col = 32 * kb + 8 * g;
+        Limbs qa[2], ya[2];
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+          qa[rb] = ya[rb] = Limbs{bf16x8{}, bf16x8{}, bf16x8{}};
+          if (col < D) {
+            const int o = (16 * rb + j) * P::LDR + col;
+            qa[rb].h = *reinterpret_cast<const bf16x8*>(Tq + o);
+            qa[rb].m = *reinterpret_cast<const bf16x8*>(Tq + P::LIMB + o);
+            qa[rb].l = *reinterpret_cast<const bf16x8*>(Tq + 2 * P::LIMB + o);
+            ya[rb].h = *reinterpret_cast<const bf16x8*>(Ty + o);
+            ya[rb].m = *reinterpret_cast<const bf16x8*>(Ty + P::LIMB + o);
+            ya[rb].l = *reinterpret_cast<const bf16x8*>(Ty + 2 * P::LIMB + o);
+          }
+        }
+        // four independent accumulators per limb product
+#pragma unroll
+        for (int st = 0; st < 6; ++st) {
+          sacc[0] = mfma16_step(st, qa[0], kl[kb], sacc[0]);
+          pacc[0] = mfma16_step(st, ya[0], vl[kb], pacc[0]);
+          sacc[1] = mfma16_step(st, qa[1], kl[kb], sacc[1]);
+          pacc[1] = mfma16_step(st, ya[1], vl[kb], pacc[1]);
+        }
+      }
 
-    // ---- weights and score gradients of this lane's 16 slots ----
-    // Streams over the slots; W overwrites sacc and dS overwrites pacc in place.
-    // Tiles that may hold invisible keys (or key 0 / the caps) take the general
-    // path; all others need no masks.
-    const int kbase = w0 - 1 + 16 * h;  // key of register 0
-    const bool need_mask = (w0 == 0) || (w0 + kBwdKeys > i0) || (i0 + 32 > T);
-    auto segments = [&](auto general_tag) {
-      constexpr bool kGeneral = decltype(general_tag)::value;
-      auto slot_vis = [&](int n) {
-        const int key = kbase + n;
-        return !kGeneral || (key >= 0 && key <= i);
+      // ---- segments along the slots (adjacent lanes of each DPP row) ----
+      // Tiles where every slot key is visible to every query, with no key 0
+      // and no row past T, take the fast path; the cap of key i can then only
+      // fall on slot 15, which is not owned.
+      const bool need_mask = (kmin < 1) || (kmin + 15 > i0) || (i0 + 31 >= T);
+      float wout[2][4], dout_s[2][4];
+      auto segments = [&](auto general_tag) {
+        constexpr bool kGeneral = decltype(general_tag)::value;
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int i = i0 + 16 * rb + 4 * g + r;
+            const bool vis = !kGeneral || (key_j >= 0 && key_j <= i && i < T);
+            const float s = vis ? sacc[rb][r] : 0.f;   // s - m
+            const float gg = vis ? pacc[rb][r] : 0.f;  // g = dY.v/Z - Dl/Z
+            const float p = fast_exp2(s);
+            const float sl = row_shr1(s), pl = row_shr1(p), gl = row_shr1(gg);
+            float Lv, Rv, dLv, dRv;
+            seg_shares_grad(sl, s, pl, p, gl, gg, Lv, Rv, dLv, dRv);
+            // segment (slot j-1, slot j), both keys visible
+            bool ok = j >= 1;
+            if (kGeneral) ok = ok && key_j >= 1 && key_j <= i && i < T;
+            Lv = ok ? Lv : 0.f;
+            Rv = ok ? Rv : 0.f;
+            dLv = ok ? dLv : 0.f;
+            dRv = ok ? dRv : 0.f;
+            // left shares of segment (j, j+1) arrive from lane j+1
+            float w = Rv + row_shl1(Lv);
+            float ds = dRv + row_shl1(dLv);
+            if (kGeneral) {
+              // half-token caps on the first key and the last visible key
+              const float cap = (vis && key_j == 0 ? 0.5f * p : 0.f) + (vis && key_j == i ? 0.5f * p : 0.f);
+              w += cap;
+              ds = fmaf(cap, gg, ds);
+            }
+            const bool owned = j >= 1 && j <= kBwdKeys;
+            wout[rb][r] = owned ? w : 0.f;
+            dout_s[rb][r] = owned ? ds : 0.f;
+          }
+        }
       };
-      // half 1's first segment starts at half 0's last slot
-      float sl, pl, gl;
+      if (need_mask)
+        segments(std::true_type{});
+      else
+        segments(std::false_type{});
+
+      // ---- dS block (query tile qt, key block kb16) for the dQ pass ----
       {
-        const bool v15 = slot_vis(15);
-        const float s15 = v15 ? sacc[15] : 0.f;
-        const float g15 = v15 ? fmaf(pacc[15], invz, -dz) : 0.f;
-        sl = xhalf(s15);
-        pl = fast_exp2(sl);
-        gl = xhalf(g15);
-      }
-      float r_prev = 0.f, dr_prev = 0.f, xl0 = 0.f, xdl0 = 0.f;
-      // finalises slot n from its own (p, g), incoming right and outgoing left shares
-      auto finish = [&](int n, float pv, float gv, float wv, float dv) {
-        if (kGeneral) {
-          // half-token caps on the first key and the last visible key (both when i == 0)
-          const int key = kbase + n;
-          const bool vis = slot_vis(n);
-          const float cap = (vis && key == 0 ? 0.5f * pv : 0.f) + (vis && key == i ? 0.5f * pv : 0.f);
-          wv += cap;
-          dv = fmaf(cap, gv, dv);
-        }
-        const int slot = 16 * h + n;
-        const bool owned = slot >= 1 && slot <= kBwdKeys;
-        sacc[n] = owned ? wv * invz : 0.f;
-        pacc[n] = owned ? dv : 0.f;
-      };
+        float* dst = dsbuf + ds_blk * kDsBlockFloats;
 #pragma unroll
-      for (int n = 0; n < 16; ++n) {
-        const bool vis = slot_vis(n);
-        const float sr = vis ? sacc[n] : 0.f;  // s - m2
-        const float gr = vis ? fmaf(pacc[n], invz, -dz) : 0.f;
-        const float pr = fast_exp2(sr);
-        float Lv, Rv, dLv, dRv;
-        seg_shares_grad(sl, sr, pl, pr, gl, gr, Lv, Rv, dLv, dRv);
-        const int key = kbase + n;  // right key of this segment
-        bool ok = (n > 0) || (h == 1);
-        if (kGeneral) ok = ok && key >= 1 && key <= i;
-        Lv = ok ? Lv : 0.f;
-        Rv = ok ? Rv : 0.f;
-        dLv = ok ? dLv : 0.f;
-        dRv = ok ? dRv : 0.f;
-        if (n == 0) {
-          xl0 = xhalf(Lv);  // half 1's first left share belongs to half 0's last slot
-          xdl0 = xhalf(dLv);
-        } else {
-          finish(n - 1, pl, gl, r_prev + Lv, dr_prev + dLv);
-        }
-        r_prev = Rv;
-        dr_prev = dRv;
-        sl = sr;
-        pl = pr;
-        gl = gr;
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) dst[(16 * rb + 4 * g + r) * kBwdSlots + j] = dout_s[rb][r];
       }
-      finish(15, pl, gl, r_prev + (h ? 0.f : xl0), dr_prev + (h ? 0.f : xdl0));
-    };
-    if (need_mask)
-      segments(std::true_type{});
-    else
-      segments(std::false_type{});
 
-    // ---- dS row block for the dQ pass: row q, slots 16h..16h+15 ----
-    {
-      float* dst = dsbuf + ((size_t)ds_blk * kDsBlockFloats) + q * kBwdSlots + 16 * h;
+      // ---- dV^T += (dY/Z)^T w and dK^T += Q^T dS ----
+      // k element e of group g <-> query (e < 4 ? 4g + e : 16 + 4g + e - 4),
+      // i.e. register (rb = e / 4, r = e % 4) of this lane.
+      float xw[8], xd[8];
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
-        *reinterpret_cast<f32x4*>(dst + 4 * c) =
-            f32x4{pacc[4 * c], pacc[4 * c + 1], pacc[4 * c + 2], pacc[4 * c + 3]};
-      ds_blk += ds_kb_count(qt) + ds_kb_count(qt + 1) + ds_kb_count(qt + 2) + ds_kb_count(qt + 3);
-    }
-
-    // ---- acc^T[d][slot] += sum_query A[query][d] X[query][slot] ----
-    // X (W or dS, held per query lane) goes through the [slot][query] tile, A
-    // (dY, then Q) is read column-wise from the wave's row tile; at step r
-    // lane half h contributes query 16h + r.
-    auto put_x = [&](const f32x16& x) {
+      for (int e = 0; e < 8; ++e) {
+        xw[e] = wout[e >> 2][e & 3];
+        xd[e] = dout_s[e >> 2][e & 3];
+      }
+      const Limbs wb = split8(xw), db = split8(xd);
+      const int src_row = 4 * g + (j >> 2), src_col = 4 * (j & 3);
 #pragma unroll
-      for (int n = 0; n < 16; ++n) Xt[(16 * h + n) * P::LDX + q] = x[n];
-    };
-    const float* xcol = Xt + q * P::LDX + 16 * h;    // B operand: slot q, query 16h + r
-    const float* acol = At + 16 * h * P::LDQ + dcol;  // A operand: row 16h + r, column d
-    auto mma_x = [&](f32x16 (&acc)[P::NMB]) {
+      for (int mb = 0; mb < P::NMB; ++mb) {
+        const int o0 = src_row * P::LDR + 16 * mb + src_col;
+        const int o1 = o0 + 16 * P::LDR;
+        Limbs ya, qa;
+        ya.h = lds_read_tr8(Ty + o0, Ty + o1);
+        ya.m = lds_read_tr8(Ty + P::LIMB + o0, Ty + P::LIMB + o1);
+        ya.l = lds_read_tr8(Ty + 2 * P::LIMB + o0, Ty + 2 * P::LIMB + o1);
+        qa.h = lds_read_tr8(Tq + o0, Tq + o1);
+        qa.m = lds_read_tr8(Tq + P::LIMB + o0, Tq + P::LIMB + o1);
+        qa.l = lds_read_tr8(Tq + 2 * P::LIMB + o0, Tq + 2 * P::LIMB + o1);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float b = xcol[r];
-#pragma unroll
-        for (int mb = 0; mb < P::NMB; ++mb) {
-          const float a = dok ? acol[r * P::LDQ + 32 * mb] : 0.f;
-          acc[mb] = mfma32(a, b, acc[mb]);
+        for (int st = 0; st < 6; ++st) {
+          accv[mb] = mfma16_step(st, ya, wb, accv[mb]);
+          acck[mb] = mfma16_step(st, qa, db, acck[mb]);
         }
       }
-    };
-    put_x(sacc);
-    wave_lds_sync();
-    // the next tile's dY row and stats fly during the dV and dK MFMAs
-    if (qt + 4 < nqt) {
-      prefetch_rows(qt + 4, dO, pf_o);
-      prefetch_stats(qt + 4);
     }
-    mma_x(accv);  // dV^T += dY^T W
-    wave_lds_sync();
-    put_x(pacc);
-#pragma unroll
-    for (int c = 0; c < P::CH; ++c)
-      *reinterpret_cast<f32x4*>(At + q * P::LDQ + h * P::DH + 4 * c) = pf_q[c];
-    wave_lds_sync();
-    if (qt + 4 < nqt) prefetch_rows(qt + 4, Q, pf_q);
-    mma_x(acck);  // dK^T += Q^T dS
-    wave_lds_sync();
+    ds_blk += ds_kb_count(qt);
+    if (qt + 1 < nqt) store_tile(buf ^ 1);
+    __syncthreads();
   }
 
-  // ---- reduce the 4 waves' partial dV^T / dK^T through LDS, one matrix at a time ----
-  constexpr int NE = P::NMB * 16;  // accumulator elements per lane per matrix
-  constexpr int NG = P::NMB * 4;   // float4 groups per lane per matrix
-  auto reduce_store = [&](const f32x16 (&acc)[P::NMB], float* __restrict__ out, float scale) {
-    __syncthreads();
+  // ---- epilogue: lane (slot j, group g) holds d = 16mb + 4g + r of its key ----
+  if (j >= 1 && j <= kBwdKeys && key_j < T && kb16 < nkb) {
+    const float ck = cl2 * kLn2;
 #pragma unroll
-    for (int mb = 0; mb < P::NMB; ++mb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) lds[(w * NE + mb * 16 + r) * 64 + lane] = acc[mb][r];
-    __syncthreads();
-    // column q of the accumulator is slot q; register group r4 holds d = 32mb + 8r4 + 4h + 0..3
-    for (int gi = w; gi < NG; gi += 4) {
-      const int mb = gi / 4, r4 = gi % 4;
-      const int key = w0 - 1 + q;
-      const int d0 = 32 * mb + 8 * r4 + 4 * h;
-      f32x4 sum = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ww = 0; ww < 4; ++ww)
-#pragma unroll
-        for (int e4 = 0; e4 < 4; ++e4) sum[e4] += lds[(ww * NE + mb * 16 + 4 * r4 + e4) * 64 + lane];
-      if (q >= 1 && q <= kBwdKeys && key < T && d0 < D)
-        *reinterpret_cast<f32x4*>(out + slice + (size_t)key * D + d0) = sum * scale;
+    for (int mb = 0; mb < P::NMB; ++mb) {
+      const int d0 = 16 * mb + 4 * g;
+      if (d0 < D) {
+        *reinterpret_cast<f32x4*>(dV + slice + (size_t)key_j * D + d0) = accv[mb];
+        *reinterpret_cast<f32x4*>(dK + slice + (size_t)key_j * D + d0) = acck[mb] * ck;
+      }
     }
-  };
-  reduce_store(accv, dV, 1.0f);
-  reduce_store(acck, dK, cl2 * kLn2);
+  }
 }
 
-// dQ = c dS (K - k_ref) as a tiled GEMM over the 32x32 dS blocks written by
+// dQ = c dS (K - k_ref) as a tiled GEMM over the 32x16 dS blocks written by
 // ca_bwd_dkdv.  Work item: one chunk of the key blocks of a 64-query group
-// (two 32-query tiles) of one slice; wave w takes query tile w&1 and the
-// chunk's key blocks of parity w>>1.  Per stage the 32 K rows of two
-// consecutive key blocks (slots 30kb-1 .. 30kb+30 each) are staged in LDS
-// (double-buffered) and shared by all four waves; lane half h supplies slots
-// 16h + s at k-step s.  Halo slots and invisible keys carry dS = 0, so no
+// (two 32-query tiles) of one slice; wave w takes query tile w&1 and, of the
+// four blocks staged per stage, those of parity w>>1.  Per stage the K rows
+// of four consecutive key blocks (slots 14kb-1 .. 14kb+14 each) are staged in
+// LDS (double-buffered) and shared by all four waves; lane half h supplies
+// slot 8h + s at k-step s.  Halo slots and invisible keys carry dS = 0, so no
 // masks are needed.  The dS operand of the wave's next block is prefetched
 // into registers.  The two parities are summed through LDS at the end (fixed
 // order).  A single-chunk group writes dQ; the chunks of a longer group write
@@ -368,10 +390,11 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
                                                         float* __restrict__ gain_part, int BH,
                                                         int H, int T, int chunk, int n_items,
                                                         int n_part) {
-  using P = Bwd<D>;
-  constexpr int KF4 = 2 * kBwdSlots * P::C4;  // float4 per stage (two key blocks)
-  constexpr int KLD = (KF4 + 255) / 256;      // float4 loads per thread
-  constexpr int RED4 = 2 * P::NMB * 16 * 64 / 4;      // float4 of the final parity reduction
+  constexpr int NMB = (D + 31) / 32;
+  constexpr int C4 = D / 4;
+  constexpr int KF4 = 4 * kBwdSlots * C4;   // float4 per stage (four key blocks)
+  constexpr int KLD = (KF4 + 255) / 256;    // float4 loads per thread
+  constexpr int RED4 = 2 * NMB * 16 * 64 / 4;  // float4 of the final parity reduction
   // The K stages and the final reduction buffer are live at disjoint times and
   // share one allocation (fewer LDS bytes per work group, more resident groups).
   __shared__ f32x4 smem[2 * KF4 > RED4 ? 2 * KF4 : RED4];
@@ -401,14 +424,14 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   const float c = head_scale_log2(log_gain, bh % H, D) * kLn2;
   // key blocks of this chunk met by the wave's tile
   const int my_end = wave_on ? min(min(ds_kb_count(qt), nkb), kb_hi) : 0;
-  const int iters = kb_hi > kb_lo ? (kb_hi - kb_lo + 1) / 2 : 0;
+  const int iters = kb_hi > kb_lo ? (kb_hi - kb_lo + 3) / 4 : 0;
   const float* arow =
       dsbuf + ((size_t)bh * ds_blocks_before(nqt) + ds_blocks_before(wave_on ? qt : 0)) * kDsBlockFloats +
-      q * kBwdSlots + 16 * h;
+      q * kBwdSlots + 8 * h;
 
-  f32x16 acc[P::NMB];
+  f32x16 acc[NMB];
 #pragma unroll
-  for (int nb = 0; nb < P::NMB; ++nb)
+  for (int nb = 0; nb < NMB; ++nb)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[nb][r] = 0.f;
 
@@ -424,42 +447,42 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   {
     const f32x4* kr = reinterpret_cast<const f32x4*>(K + slice + (size_t)(64 * qg) * D);
 #pragma unroll
-    for (int j = 0; j < KLD; ++j) kref[j] = kr[(tid + 256 * j) % P::C4];
+    for (int jj = 0; jj < KLD; ++jj) kref[jj] = kr[(tid + 256 * jj) % C4];
   }
   f32x4 pre[KLD];
   auto load_k = [&](int it) {
 #pragma unroll
-    for (int j = 0; j < KLD; ++j) {
-      const int e = tid + 256 * j;
+    for (int jj = 0; jj < KLD; ++jj) {
+      const int e = tid + 256 * jj;
       f32x4 v = {0.f, 0.f, 0.f, 0.f};
       if (e < KF4) {
-        const int row = e / P::C4;  // 32 * (block in stage) + slot
-        const int key = kBwdKeys * (kb_lo + 2 * it + (row >> 5)) - 1 + (row & 31);
-        if (key >= 0 && key < T)
-          v = reinterpret_cast<const f32x4*>(K + slice + (size_t)key * D)[e % P::C4];
+        const int row = e / C4;  // 16 * (block in stage) + slot
+        const int key = kBwdKeys * (kb_lo + 4 * it + (row >> 4)) - 1 + (row & 15);
+        if (key >= 0 && key < T) v = reinterpret_cast<const f32x4*>(K + slice + (size_t)key * D)[e % C4];
       }
-      pre[j] = v;
+      pre[jj] = v;
     }
   };
   // the shift is applied when the prefetched rows are stored, so the loads
   // issued a stage ahead are not waited for inside the MFMA loop
   auto store_k = [&](int buf) {
 #pragma unroll
-    for (int j = 0; j < KLD; ++j) {
-      const int e = tid + 256 * j;
-      if (e < KF4) kst[buf][e] = pre[j] - kref[j];
+    for (int jj = 0; jj < KLD; ++jj) {
+      const int e = tid + 256 * jj;
+      if (e < KF4) kst[buf][e] = pre[jj] - kref[jj];
     }
   };
   auto load_a = [&](int kbm, float* a) {
     const f32x4* src = reinterpret_cast<const f32x4*>(arow + (size_t)kbm * kDsBlockFloats);
 #pragma unroll
-    for (int c4 = 0; c4 < 4; ++c4) {
+    for (int c4 = 0; c4 < 2; ++c4) {
       const f32x4 v4 = src[c4];
       a[4 * c4 + 0] = v4[0]; a[4 * c4 + 1] = v4[1]; a[4 * c4 + 2] = v4[2]; a[4 * c4 + 3] = v4[3];
     }
   };
 
-  float a_next[16];
+  // the wave's blocks: kb_lo + par + 2u, u = 0, 1, ... (two per stage)
+  float a_next[8];
   if (kb_lo + par < my_end) load_a(kb_lo + par, a_next);
   load_k(0);
   store_k(0);
@@ -468,19 +491,23 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   for (int it = 0; it < iters; ++it) {
     const int buf = it & 1;
     if (it + 1 < iters) load_k(it + 1);
-    const int kbm = kb_lo + 2 * it + par;
-    if (kbm < my_end) {
-      float a[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) a[r] = a_next[r];
-      if (kbm + 2 < my_end) load_a(kbm + 2, a_next);
-      const float* kbp = reinterpret_cast<const float*>(&kst[buf][0]) + (32 * par + 16 * h) * D + dcol;
+    for (int u = 0; u < 2; ++u) {
+      const int kbm = kb_lo + 4 * it + par + 2 * u;
+      if (kbm < my_end) {
+        float a[8];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
+        for (int r = 0; r < 8; ++r) a[r] = a_next[r];
+        if (kbm + 2 < my_end) load_a(kbm + 2, a_next);
+        const float* kbp =
+            reinterpret_cast<const float*>(&kst[buf][0]) + (16 * (par + 2 * u) + 8 * h) * D + dcol;
 #pragma unroll
-        for (int nb = 0; nb < P::NMB; ++nb) {
-          const float b = (32 * nb + q < D) ? kbp[r * D + 32 * nb] : 0.f;
-          acc[nb] = mfma32(a[r], b, acc[nb]);
+        for (int r = 0; r < 8; ++r) {
+#pragma unroll
+          for (int nb = 0; nb < NMB; ++nb) {
+            const float b = (32 * nb + q < D) ? kbp[r * D + 32 * nb] : 0.f;
+            acc[nb] = mfma32(a[r], b, acc[nb]);
+          }
         }
       }
     }
@@ -488,10 +515,10 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
     __syncthreads();
   }
   // Q rows for the gain partial, loaded as one batch before the reduction
-  float qv[P::NMB][16];
+  float qv[NMB][16];
   if (par == 0 && wave_on) {
 #pragma unroll
-    for (int nb = 0; nb < P::NMB; ++nb)
+    for (int nb = 0; nb < NMB; ++nb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = 32 * qt + 8 * (r >> 2) + 4 * h + (r & 3);
@@ -501,32 +528,32 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   }
   if (par == 1) {
 #pragma unroll
-    for (int nb = 0; nb < P::NMB; ++nb)
+    for (int nb = 0; nb < NMB; ++nb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) red[((qsub * P::NMB + nb) * 16 + r) * 64 + lane] = acc[nb][r];
+      for (int r = 0; r < 16; ++r) red[((qsub * NMB + nb) * 16 + r) * 64 + lane] = acc[nb][r];
   }
   __syncthreads();
   if (par == 0) {
-    float g = 0.f;
+    float gsum = 0.f;
     if (wave_on) {
       // single-chunk groups write dQ; chunk partials are item-indexed tiles
       // [64 queries][D] (items of multi-chunk groups are numbered first)
       float* dst = nch == 1 ? dQ + slice + (size_t)(64 * qg) * D
                             : dq_part + ((size_t)bh * n_part + item) * 64 * D;
 #pragma unroll
-      for (int nb = 0; nb < P::NMB; ++nb)
+      for (int nb = 0; nb < NMB; ++nb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float sum = acc[nb][r] + red[((qsub * P::NMB + nb) * 16 + r) * 64 + lane];
+          const float sum = acc[nb][r] + red[((qsub * NMB + nb) * 16 + r) * 64 + lane];
           const int rloc = 32 * qsub + 8 * (r >> 2) + 4 * h + (r & 3);
           const int d = 32 * nb + q;
           const float val = sum * c;
-          g = fmaf(qv[nb][r], val, g);
+          gsum = fmaf(qv[nb][r], val, gsum);
           if (64 * qg + rloc < T && d < D) dst[(size_t)rloc * D + d] = val;
         }
     }
-    g = wave_sum(g);
-    if (lane == 0) gred[qsub] = g;
+    gsum = wave_sum(gsum);
+    if (lane == 0) gred[qsub] = gsum;
   }
   __syncthreads();
   if (tid == 0) gain_part[(size_t)bh * n_items + item] = gred[0] + gred[1];
@@ -559,14 +586,14 @@ __global__ __launch_bounds__(256) void ca_bwd_gain_merge_kernel(
   const int bh = m % BH, gi = m / BH;
   const int qg = dq_num_groups(T) - 1 - gi;
   int first = 0;  // item index of the group's chunk 0
-  for (int g = dq_num_groups(T) - 1; g > qg; --g) first += dq_group_chunks(g, T, chunk);
+  for (int gg = dq_num_groups(T) - 1; gg > qg; --gg) first += dq_group_chunks(gg, T, chunk);
   const int nch = dq_group_chunks(qg, T, chunk);
   const f32x4* part = reinterpret_cast<const f32x4*>(dq_part + ((size_t)bh * n_part + first) * 64 * D);
   f32x4* out = reinterpret_cast<f32x4*>(dQ + ((size_t)bh * T + 64 * qg) * D);
   for (int e = tid; e < 64 * C4; e += 256) {
     if (64 * qg + e / C4 >= T) break;
     f32x4 s = part[e];
-    for (int ch = 1; ch < nch; ++ch) s += part[(size_t)ch * 16 * D + e];
+    for (int cc = 1; cc < nch; ++cc) s += part[(size_t)cc * 16 * D + e];
     out[e] = s;
   }
 }
@@ -574,59 +601,43 @@ __global__ __launch_bounds__(256) void ca_bwd_gain_merge_kernel(
 template <int D>
 hipError_t launch_bwd(const float* q, const float* k, const float* v, const float* log_gain,
                       const float* o, const float* stats, const float* dout, float* dq, float* dk,
-                      float* dv, float* dlog_gain, float* dsbuf, float* dvec, float* gain_part,
-                      float* dq_part, const DqSplit& sp, int B, int H, int T,
-                      hipStream_t stream) {
-  using P = Bwd<D>;
+                      float* dv, float* dlog_gain, const BwdWork& ws, const DqSplit& sp, int B,
+                      int H, int T, hipStream_t stream) {
   const int BH = B * H;
   const int rows = BH * T;
-  timer_begin(kBwdRowdot, stream);
-  hipLaunchKernelGGL(ca_bwd_rowdot_kernel<D>, dim3((rows * (D / 4) + 255) / 256), dim3(256), 0,
-                     stream, dout, o, dvec, rows);
-  timer_end(kBwdRowdot, stream);
+  timer_begin(kBwdPrep, stream);
+  hipLaunchKernelGGL(ca_bwd_prep_kernel<D>, dim3((rows * (D / 4) + 255) / 256), dim3(256), 0,
+                     stream, q, dout, o, stats, ws.limbs, ws.qstat, rows);
+  timer_end(kBwdPrep, stream);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const size_t lds_bytes = sizeof(float) * P::LDS_FLOATS;
-  const int nkb = bwd_num_key_blocks(T);
+  const int nwg = (bwd_num_key_blocks(T) + kDkdvWaves - 1) / kDkdvWaves;
   timer_begin(kBwdDkdv, stream);
-  hipLaunchKernelGGL(ca_bwd_dkdv_kernel<D>, dim3(nkb * BH), dim3(256), lds_bytes, stream, q, k,
-                     v, dout, stats, dvec, log_gain, dk, dv, dsbuf, BH, H, T);
+  hipLaunchKernelGGL(ca_bwd_dkdv_kernel<D>, dim3(nwg * BH), dim3(256), 0, stream, k, v, ws.limbs,
+                     ws.qstat, log_gain, dk, dv, ws.dsbuf, BH, H, T);
   timer_end(kBwdDkdv, stream);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   timer_begin(kBwdDq, stream);
-  hipLaunchKernelGGL(ca_bwd_dq_kernel<D>, dim3(sp.items * BH), dim3(256), 0, stream, dsbuf, q, k,
-                     log_gain, dq, dq_part, gain_part, BH, H, T, sp.chunk, sp.items,
+  hipLaunchKernelGGL(ca_bwd_dq_kernel<D>, dim3(sp.items * BH), dim3(256), 0, stream, ws.dsbuf, q,
+                     k, log_gain, dq, ws.dq_part, ws.gain_part, BH, H, T, sp.chunk, sp.items,
                      sp.part_items);
   timer_end(kBwdDq, stream);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   timer_begin(kBwdGain, stream);
   hipLaunchKernelGGL(ca_bwd_gain_merge_kernel<D>, dim3(H + BH * sp.multi_groups), dim3(256), 0,
-                     stream, gain_part, dq_part, dlog_gain, dq, B, H, T, sp.chunk, sp.items,
+                     stream, ws.gain_part, ws.dq_part, dlog_gain, dq, B, H, T, sp.chunk, sp.items,
                      sp.part_items);
   timer_end(kBwdGain, stream);
   return hipGetLastError();
 }
 
-template <int D>
-hipError_t set_bwd_attrs() {
-  using P = Bwd<D>;
-  return hipFuncSetAttribute(reinterpret_cast<const void*>(&ca_bwd_dkdv_kernel<D>),
-                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                             (int)(sizeof(float) * P::LDS_FLOATS));
-}
-
-template hipError_t set_bwd_attrs<8>();
-template hipError_t set_bwd_attrs<16>();
-template hipError_t set_bwd_attrs<32>();
-template hipError_t set_bwd_attrs<64>();
-
-#define CA_INST_BWD(DD)                                                                        \
-  template hipError_t launch_bwd<DD>(const float*, const float*, const float*, const float*,   \
-                                     const float*, const float*, const float*, float*, float*, \
-                                     float*, float*, float*, float*, float*, float*,           \
-                                     const DqSplit&, int, int, int, hipStream_t);
+#define CA_INST_BWD(DD)                                                                         \
+  template hipError_t launch_bwd<DD>(const float*, const float*, const float*, const float*,    \
+                                     const float*, const float*, const float*, float*, float*,  \
+                                     float*, float*, const BwdWork&, const DqSplit&, int, int,  \
+                                     int, hipStream_t);
 CA_INST_BWD(8)
 CA_INST_BWD(16)
 CA_INST_BWD(32)

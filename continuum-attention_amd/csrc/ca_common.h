@@ -81,6 +81,59 @@ __device__ __forceinline__ f32x16 mfma_x6(const Limbs& a, const Limbs& b, f32x16
   return mfma_bf16(a.h, b.h, c);
 }
 
+// 16x16x32 tile (v_mfma_f32_16x16x32_bf16): A lane l supplies row l%16,
+// k = 8*(l/16) + e; B lane l supplies column l%16, same k; the result lane l
+// holds column l%16, rows 4*(l/16) + r.
+__device__ __forceinline__ f32x4 mfma16_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16_x6(const Limbs& a, const Limbs& b, f32x4 c) {
+  c = mfma16_bf16(a.l, b.h, c);
+  c = mfma16_bf16(a.m, b.m, c);
+  c = mfma16_bf16(a.h, b.l, c);
+  c = mfma16_bf16(a.m, b.h, c);
+  c = mfma16_bf16(a.h, b.m, c);
+  return mfma16_bf16(a.h, b.h, c);
+}
+
+// One of the six limb products of mfma16_x6 (step 0..5, small terms first);
+// issuing step k on several independent accumulators before step k+1 keeps
+// dependent MFMAs apart.
+__device__ __forceinline__ f32x4 mfma16_step(int step, const Limbs& a, const Limbs& b, f32x4 c) {
+  switch (step) {
+    case 0: return mfma16_bf16(a.l, b.h, c);
+    case 1: return mfma16_bf16(a.m, b.m, c);
+    case 2: return mfma16_bf16(a.h, b.l, c);
+    case 3: return mfma16_bf16(a.m, b.h, c);
+    case 4: return mfma16_bf16(a.h, b.m, c);
+    default: return mfma16_bf16(a.h, b.h, c);
+  }
+}
+
+// Transposed LDS read (ds_read_b64_tr_b16): within each 16-lane group, lane
+// i receives element (i & 3) of the 4 bf16 that lanes 4j + (i >> 2) address,
+// for j = 0..3.  With lane i' = 4j + m pointing at row r0 + j, column c0 + 4m
+// of a row-major bf16 tile, lane i gets column c0 + i of rows r0..r0+3.  Two
+// such reads give one 8-element MFMA operand.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ bf16x8 lds_read_tr8(const __bf16* p0, const __bf16* p1) {
+  typedef __attribute__((address_space(3))) s16x4* lds_s16x4;
+  const s16x4 r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4)(p0));
+  const s16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4)(p1));
+  const s16x8 v = __builtin_shufflevector(r0, r1, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(bf16x8, v);  // whole-vector casts only
+}
+
+// Lane j of each 16-lane row receives x of lane j-1 (lane 0: 0) / of lane j+1
+// (lane 15: 0).
+__device__ __forceinline__ float row_shr1(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x111, 0xf, 0xf, true));
+}
+__device__ __forceinline__ float row_shl1(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x101, 0xf, 0xf, true));
+}
+
 // two floats -> packed bf16 pair, round to nearest even; a in the low half
 __device__ __forceinline__ unsigned cvt_pk_bf16(float a, float b) {
   unsigned r;

@@ -27,11 +27,13 @@ inline size_t fwd_part_floats(int BH, int T, int C) {
   return (size_t)BH * smax * T * 66;  // D <= 64 outputs + (m, Z); sized for the largest D
 }
 
-// Backward: key blocks owned by one dK/dV work group.  A block owns 30 keys
-// and feeds 32 MFMA slots (slot s = key 30*kb - 1 + s), so both neighbours of
-// every owned key are inside the tile.
-constexpr int kBwdKeys = 30;
-constexpr int kBwdSlots = 32;
+// Backward key blocks.  One dK/dV wave owns 14 keys and feeds 16 MFMA slots
+// (slot s = key 14*kb - 1 + s), so both neighbours of every owned key are
+// inside its block; a dK/dV work group takes kDkdvWaves consecutive blocks.
+// The dS spill for the dQ pass is stored per (32-query tile, block).
+constexpr int kBwdKeys = 14;
+constexpr int kBwdSlots = 16;
+constexpr int kDkdvWaves = 4;
 __host__ __device__ inline int bwd_num_key_blocks(int T) { return (T + kBwdKeys - 1) / kBwdKeys; }
 __host__ __device__ inline int num_q_tiles(int T) { return (T + 31) / 32; }
 // 64-query dQ groups per slice.
@@ -61,8 +63,8 @@ __host__ __device__ inline long long floor_sum(long long n, long long m, long lo
   return ans;
 }
 
-// dS blocks for the dQ pass: one 32-query x 32-slot block (row-major) for
-// every query tile qt and key block kb that meets it (30*kb <= 32*qt + 31).
+// dS blocks for the dQ pass: one 32-query x 16-slot block (row-major) for
+// every query tile qt and key block kb that meets it (14*kb <= 32*qt + 31).
 // Blocks are stored qt-major, kb ascending, so a dQ work group reads its rows
 // contiguously.  Blocks past the last key block are counted but never touched.
 constexpr int kDsBlockFloats = 32 * kBwdSlots;
@@ -82,7 +84,7 @@ inline size_t bwd_ds_floats(int BH, int T) {
 // numbered per slice from the last (heaviest) group down, so the chunks of
 // multi-chunk groups come first; those items write partial dQ tiles that a
 // second kernel sums in chunk order.
-constexpr int kDqChunkBlocks = 32;  // split chunk length (measured 16..48: flat)
+constexpr int kDqChunkBlocks = 64;  // split chunk length in key blocks (about 900 keys)
 // key blocks met by the last query tile of group qg (the group's key range)
 __host__ __device__ inline int dq_group_blocks(int qg, int T) {
   const int nqt = num_q_tiles(T);
@@ -118,7 +120,7 @@ constexpr int kDqGroupsPerCu = 3;
 
 // Per-kernel HIP-event timing (diagnostics; off unless ca_timing_enable(1)).
 enum KernelId {
-  kFwd = 0, kFwdCombine, kBwdRowdot, kBwdDkdv, kBwdDq, kBwdGain, kWeights, kWeightsBwd, kQkvIn,
+  kFwd = 0, kFwdCombine, kBwdPrep, kBwdDkdv, kBwdDq, kBwdGain, kWeights, kWeightsBwd, kQkvIn,
   kQkvGrad, kRelayout, kNumKernels
 };
 
@@ -147,11 +149,21 @@ hipError_t launch_fwd(const float* q, const float* k, const float* v, const floa
                       float* o, float* stats, float* part, int B, int H, int T, int C,
                       hipStream_t stream);
 
+// Backward workspace buffers (sizes: bwd_ds_floats, bwd_limb_elems, BH*T*2
+// qstat floats, gain partials per dQ item, dQ chunk partials).
+struct BwdWork {
+  float* dsbuf;       // dS spill, 32x16 blocks
+  __bf16* limbs;      // six bf16 planes [BH][T][D]: Q limbs h, m, l; dY/Z limbs h, m, l
+  float* qstat;       // per query row: (m, D/Z)
+  float* gain_part;   // per dQ item
+  float* dq_part;     // dQ chunk partials
+};
+inline size_t bwd_limb_elems(int BH, int T, int D) { return (size_t)6 * BH * T * D; }
+
 template <int D>
 hipError_t launch_bwd(const float* q, const float* k, const float* v, const float* log_gain,
                       const float* o, const float* stats, const float* dout, float* dq, float* dk,
-                      float* dv, float* dlog_gain, float* dsbuf, float* dvec, float* gain_part,
-                      float* dq_part, const DqSplit& sp, int B, int H, int T,
-                      hipStream_t stream);
+                      float* dv, float* dlog_gain, const BwdWork& ws, const DqSplit& sp, int B,
+                      int H, int T, hipStream_t stream);
 
 }  // namespace ca
