@@ -55,9 +55,9 @@ struct Bwd {
   static constexpr int CPT = (CHUNKS + 255) / 256;
 };
 
-// One thread per (row, float4 chunk): Dl = dY . y, then the Q and dY/Z limbs
-// of the chunk and, per row, (m, Dl/Z).  `rows` = B*H*T; plane p of `limbs`
-// starts at p * rows * D.
+// One thread per (row, 8 elements): Dl = dY . y, then the Q and dY/Z limbs of
+// the 8 elements (one 16-byte store per plane) and, per row, (m, Dl/Z).
+// `rows` = B*H*T; plane p of `limbs` starts at p * rows * D.
 template <int D>
 __global__ __launch_bounds__(256) void ca_bwd_prep_kernel(const float* __restrict__ Q,
                                                           const float* __restrict__ dout,
@@ -65,35 +65,45 @@ __global__ __launch_bounds__(256) void ca_bwd_prep_kernel(const float* __restric
                                                           const float* __restrict__ stats,
                                                           __bf16* __restrict__ limbs,
                                                           float* __restrict__ qstat, int rows) {
-  constexpr int C4 = D / 4;
+  constexpr int C8 = D / 8;
   const int t = blockIdx.x * 256 + threadIdx.x;
-  const int row = t / C4, c = t % C4;
+  const int row = t / C8, c = t % C8;
   const bool ok = row < rows;
-  f32x4 dy = {0.f, 0.f, 0.f, 0.f}, y = dy, qq = dy;
+  f32x4 dy[2], y[2], qq[2];
   float m = 0.f, invz = 0.f;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    dy[u] = y[u] = qq[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (ok) {
+      dy[u] = reinterpret_cast<const f32x4*>(dout + (size_t)row * D + 8 * c)[u];
+      y[u] = reinterpret_cast<const f32x4*>(out + (size_t)row * D + 8 * c)[u];
+      qq[u] = reinterpret_cast<const f32x4*>(Q + (size_t)row * D + 8 * c)[u];
+    }
+  }
   if (ok) {
-    dy = reinterpret_cast<const f32x4*>(dout + (size_t)row * D)[c];
-    y = reinterpret_cast<const f32x4*>(out + (size_t)row * D)[c];
-    qq = reinterpret_cast<const f32x4*>(Q + (size_t)row * D)[c];
     m = stats[(size_t)row * 2 + 0];
     invz = stats[(size_t)row * 2 + 1];
   }
-  float x = dy[0] * y[0] + dy[1] * y[1] + dy[2] * y[2] + dy[3] * y[3];
+  float x = 0.f;
 #pragma unroll
-  for (int o = C4 / 2; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+  for (int u = 0; u < 2; ++u)
+    x += dy[u][0] * y[u][0] + dy[u][1] * y[u][1] + dy[u][2] * y[u][2] + dy[u][3] * y[u][3];
+#pragma unroll
+  for (int o = C8 / 2; o >= 1; o >>= 1) x += __shfl_xor(x, o);
   if (!ok) return;
   const size_t plane = (size_t)rows * D;
-  const size_t off = (size_t)row * D + 4 * c;
-  auto put = [&](int p0, f32x4 v) {
-    unsigned h0, m0, l0, h1, m1, l1;
-    split_pair(v[0], v[1], h0, m0, l0);
-    split_pair(v[2], v[3], h1, m1, l1);
-    *reinterpret_cast<u32x2*>(limbs + (size_t)(p0 + 0) * plane + off) = u32x2{h0, h1};
-    *reinterpret_cast<u32x2*>(limbs + (size_t)(p0 + 1) * plane + off) = u32x2{m0, m1};
-    *reinterpret_cast<u32x2*>(limbs + (size_t)(p0 + 2) * plane + off) = u32x2{l0, l1};
+  const size_t off = (size_t)row * D + 8 * c;
+  auto put = [&](int p0, const f32x4* v, float scale) {
+    float e[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) e[u] = v[u >> 2][u & 3] * scale;
+    const Limbs lb = split8(e);
+    *reinterpret_cast<bf16x8*>(limbs + (size_t)(p0 + 0) * plane + off) = lb.h;
+    *reinterpret_cast<bf16x8*>(limbs + (size_t)(p0 + 1) * plane + off) = lb.m;
+    *reinterpret_cast<bf16x8*>(limbs + (size_t)(p0 + 2) * plane + off) = lb.l;
   };
-  put(0, qq);
-  put(3, dy * invz);
+  put(0, qq, 1.0f);
+  put(3, dy, invz);
   if (c == 0) {
     qstat[(size_t)row * 2 + 0] = m;
     qstat[(size_t)row * 2 + 1] = x * invz;
@@ -368,18 +378,40 @@ __global__ __launch_bounds__(256, 2) void ca_bwd_dkdv_kernel(
   }
 }
 
-// dQ = c dS (K - k_ref) as a tiled GEMM over the 32x16 dS blocks written by
-// ca_bwd_dkdv.  Work item: one chunk of the key blocks of a 64-query group
-// (two 32-query tiles) of one slice; wave w takes query tile w&1 and, of the
-// four blocks staged per stage, those of parity w>>1.  Per stage the K rows
-// of four consecutive key blocks (slots 14kb-1 .. 14kb+14 each) are staged in
-// LDS (double-buffered) and shared by all four waves; lane half h supplies
-// slot 8h + s at k-step s.  Halo slots and invisible keys carry dS = 0, so no
-// masks are needed.  The dS operand of the wave's next block is prefetched
-// into registers.  The two parities are summed through LDS at the end (fixed
-// order).  A single-chunk group writes dQ; the chunks of a longer group write
-// partial tiles that ca_bwd_gain_merge sums.  Every item writes its gain
-// partial sum_i q_i . dQ_i(chunk) (linear in dQ, so the partials add up).
+// dQ = c dS (K - k_ref) over the 32x16 dS blocks written by ca_bwd_dkdv, as
+// bf16x6 products on v_mfma_f32_16x16x32_bf16 (k = 32 slots = a pair of key
+// blocks).  Work item: one chunk of the key blocks of a 64-query group (two
+// 32-query tiles) of one slice; wave w takes query tile w&1 and, of the two
+// block pairs staged per stage, pair w>>1.  Per stage the K rows of four
+// consecutive key blocks (slots 14kb-1 .. 14kb+14 each) are staged in LDS
+// (double-buffered) as transposed bf16 limb planes [d][slot], relative to
+// k_ref, and shared by all four waves.  A operand: lane (query 16rb + l%16,
+// group g) holds dS of block (2p + g/2), slots 8(g%2) .. +7, split into limbs
+// in registers; B operand: lane (d = 16nb + l%16, g) reads the same 8 slots of
+// row d.  Halo slots and invisible keys carry dS = 0, so no masks are needed.
+// The two pair parities are summed through LDS at the end (fixed order).  A
+// single-chunk group writes dQ; the chunks of a longer group write partial
+// tiles that ca_bwd_gain_merge sums.  Every item writes its gain partial
+// sum_i q_i . dQ_i(chunk) (linear in dQ, so the partials add up).
+template <int D>
+struct DqP {
+  static constexpr int NB = (D + 15) / 16;            // 16-column d blocks of dQ
+  static constexpr int C4 = D / 4;
+  static constexpr int UNITS = 4 * 8 * C4;            // (block, slot pair, float4) per stage
+  static constexpr int UPT = (UNITS + 255) / 256;
+  static constexpr int DROWS = NB * 16;               // staged d rows (padded to 16)
+  static constexpr int PLANE = 4 * DROWS * kBwdSlots;  // bf16 per limb plane of a stage
+  static constexpr int STAGE = 3 * PLANE;
+  static constexpr int RED_FLOATS = 2 * 2 * NB * 4 * 64;  // parity reduction: [qsub][rb][nb][r][lane]
+};
+// bf16 offset of (block b, d row, slot s) in a limb plane; the 16-byte halves
+// of a row swap for rows 8..15 of every 16, so the 16 rows read together by
+// one lane group hit distinct banks.
+template <int D>
+__device__ __forceinline__ int dq_kt_off(int b, int d, int s) {
+  return (b * DqP<D>::DROWS + d) * kBwdSlots + ((((s >> 3) ^ (d >> 3)) & 1) << 3) + (s & 7);
+}
+
 template <int D>
 __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict__ dsbuf,
                                                         const float* __restrict__ Q,
@@ -390,15 +422,12 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
                                                         float* __restrict__ gain_part, int BH,
                                                         int H, int T, int chunk, int n_items,
                                                         int n_part) {
-  constexpr int NMB = (D + 31) / 32;
-  constexpr int C4 = D / 4;
-  constexpr int KF4 = 4 * kBwdSlots * C4;   // float4 per stage (four key blocks)
-  constexpr int KLD = (KF4 + 255) / 256;    // float4 loads per thread
-  constexpr int RED4 = 2 * NMB * 16 * 64 / 4;  // float4 of the final parity reduction
+  using P = DqP<D>;
+  constexpr int SMEM_BF16 = 2 * P::STAGE > 2 * P::RED_FLOATS ? 2 * P::STAGE : 2 * P::RED_FLOATS;
   // The K stages and the final reduction buffer are live at disjoint times and
-  // share one allocation (fewer LDS bytes per work group, more resident groups).
-  __shared__ f32x4 smem[2 * KF4 > RED4 ? 2 * KF4 : RED4];
-  f32x4 (*kst)[KF4] = reinterpret_cast<f32x4 (*)[KF4]>(smem);
+  // share one allocation.
+  __shared__ __attribute__((aligned(16))) __bf16 smem[SMEM_BF16];
+  __bf16* kst = smem;
   float* red = reinterpret_cast<float*>(smem);
   __shared__ float gred[2];
   const int nqt = num_q_tiles(T);
@@ -416,7 +445,7 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   const int clen = (gblocks + nch - 1) / nch;
   const int kb_lo = ch * clen;
   const int kb_hi = min(kb_lo + clen, gblocks);
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, q = lane & 31, h = lane >> 5;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
   const int qsub = w & 1, par = w >> 1;
   const int qt = 2 * qg + qsub;
   const bool wave_on = qt < nqt;
@@ -425,112 +454,134 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   // key blocks of this chunk met by the wave's tile
   const int my_end = wave_on ? min(min(ds_kb_count(qt), nkb), kb_hi) : 0;
   const int iters = kb_hi > kb_lo ? (kb_hi - kb_lo + 3) / 4 : 0;
-  const float* arow =
-      dsbuf + ((size_t)bh * ds_blocks_before(nqt) + ds_blocks_before(wave_on ? qt : 0)) * kDsBlockFloats +
-      q * kBwdSlots + 8 * h;
+  // dS of this lane: rows 16rb + l16 of the wave's tile, slots 8(g&1)..+7 of block (pair, g>>1)
+  const float* arow = dsbuf +
+                      ((size_t)bh * ds_blocks_before(nqt) + ds_blocks_before(wave_on ? qt : 0)) * kDsBlockFloats +
+                      l16 * kBwdSlots + 8 * (g & 1);
 
-  f32x16 acc[NMB];
+  f32x4 acc[2][P::NB];
 #pragma unroll
-  for (int nb = 0; nb < NMB; ++nb)
+  for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[nb][r] = 0.f;
+    for (int nb = 0; nb < P::NB; ++nb) acc[rb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Every row of dS sums to zero (the weights are invariant to a common score
   // shift), so dQ_i = c sum_j dS_ij (k_j - k_ref) for any k_ref.  The staged
   // keys are taken relative to the key at the group's first query: when
   // neighbouring keys nearly coincide the products stay small instead of
-  // cancelling in fp32 (|k| ~ 1 against |k_j - k_ref| ~ 1e-2 in the
-  // near-duplicate-key case), and the gain partial sum_i q_i . dQ_i inherits
-  // the same accuracy.  All chunks of a group use the same k_ref, so the
-  // k_ref terms cancel in the sum of the chunk partials.
-  f32x4 kref[KLD];
-  {
-    const f32x4* kr = reinterpret_cast<const f32x4*>(K + slice + (size_t)(64 * qg) * D);
+  // cancelling (|k| ~ 1 against |k_j - k_ref| ~ 1e-2 in the near-duplicate-key
+  // case), and the gain partial sum_i q_i . dQ_i inherits the same accuracy.
+  // All chunks of a group use the same k_ref, so the k_ref terms cancel in the
+  // sum of the chunk partials.
+  // Staging unit u: block b, slot pair sp (slots 2sp, 2sp+1), d = 4c4..4c4+3.
+  f32x4 kref[P::UPT], pre[P::UPT][2];
 #pragma unroll
-    for (int jj = 0; jj < KLD; ++jj) kref[jj] = kr[(tid + 256 * jj) % C4];
-  }
-  f32x4 pre[KLD];
+  for (int uu = 0; uu < P::UPT; ++uu)
+    kref[uu] = reinterpret_cast<const f32x4*>(K + slice + (size_t)(64 * qg) * D)[(tid + 256 * uu) % P::C4];
   auto load_k = [&](int it) {
 #pragma unroll
-    for (int jj = 0; jj < KLD; ++jj) {
-      const int e = tid + 256 * jj;
-      f32x4 v = {0.f, 0.f, 0.f, 0.f};
-      if (e < KF4) {
-        const int row = e / C4;  // 16 * (block in stage) + slot
-        const int key = kBwdKeys * (kb_lo + 4 * it + (row >> 4)) - 1 + (row & 15);
-        if (key >= 0 && key < T) v = reinterpret_cast<const f32x4*>(K + slice + (size_t)key * D)[e % C4];
+    for (int uu = 0; uu < P::UPT; ++uu) {
+      const int u = tid + 256 * uu;
+      f32x4 v0 = {0.f, 0.f, 0.f, 0.f}, v1 = v0;
+      if (u < P::UNITS) {
+        const int c4 = u % P::C4, sp = (u / P::C4) % 8, b = u / (8 * P::C4);
+        const int key = kBwdKeys * (kb_lo + 4 * it + b) - 1 + 2 * sp;
+        if (key >= 0 && key < T) v0 = reinterpret_cast<const f32x4*>(K + slice + (size_t)key * D)[c4];
+        if (key + 1 >= 0 && key + 1 < T) v1 = reinterpret_cast<const f32x4*>(K + slice + (size_t)(key + 1) * D)[c4];
       }
-      pre[jj] = v;
+      pre[uu][0] = v0;
+      pre[uu][1] = v1;
     }
   };
-  // the shift is applied when the prefetched rows are stored, so the loads
-  // issued a stage ahead are not waited for inside the MFMA loop
-  auto store_k = [&](int buf) {
+  // The shift is applied when the prefetched rows are stored, so the loads
+  // issued a stage ahead are not waited for inside the MFMA loop.  Slots of
+  // keys outside [0, T) stay 0 (their dS is 0 too).
+  auto store_k = [&](int buf, int it) {
 #pragma unroll
-    for (int jj = 0; jj < KLD; ++jj) {
-      const int e = tid + 256 * jj;
-      if (e < KF4) kst[buf][e] = pre[jj] - kref[jj];
-    }
-  };
-  auto load_a = [&](int kbm, float* a) {
-    const f32x4* src = reinterpret_cast<const f32x4*>(arow + (size_t)kbm * kDsBlockFloats);
+    for (int uu = 0; uu < P::UPT; ++uu) {
+      const int u = tid + 256 * uu;
+      if (u < P::UNITS) {
+        const int c4 = u % P::C4, sp = (u / P::C4) % 8, b = u / (8 * P::C4);
+        const int key = kBwdKeys * (kb_lo + 4 * it + b) - 1 + 2 * sp;
+        const f32x4 k0 = (key >= 0 && key < T) ? pre[uu][0] - kref[uu] : f32x4{0.f, 0.f, 0.f, 0.f};
+        const f32x4 k1 = (key + 1 >= 0 && key + 1 < T) ? pre[uu][1] - kref[uu] : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int c4 = 0; c4 < 2; ++c4) {
-      const f32x4 v4 = src[c4];
-      a[4 * c4 + 0] = v4[0]; a[4 * c4 + 1] = v4[1]; a[4 * c4 + 2] = v4[2]; a[4 * c4 + 3] = v4[3];
-    }
-  };
-
-  // the wave's blocks: kb_lo + par + 2u, u = 0, 1, ... (two per stage)
-  float a_next[8];
-  if (kb_lo + par < my_end) load_a(kb_lo + par, a_next);
-  load_k(0);
-  store_k(0);
-  __syncthreads();
-  const int dcol = (q < D) ? q : 0;
-  for (int it = 0; it < iters; ++it) {
-    const int buf = it & 1;
-    if (it + 1 < iters) load_k(it + 1);
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int kbm = kb_lo + 4 * it + par + 2 * u;
-      if (kbm < my_end) {
-        float a[8];
-#pragma unroll
-        for (int r = 0; r < 8; ++r) a[r] = a_next[r];
-        if (kbm + 2 < my_end) load_a(kbm + 2, a_next);
-        const float* kbp =
-            reinterpret_cast<const float*>(&kst[buf][0]) + (16 * (par + 2 * u) + 8 * h) * D + dcol;
-#pragma unroll
-        for (int r = 0; r < 8; ++r) {
-#pragma unroll
-          for (int nb = 0; nb < NMB; ++nb) {
-            const float b = (32 * nb + q < D) ? kbp[r * D + 32 * nb] : 0.f;
-            acc[nb] = mfma32(a[r], b, acc[nb]);
-          }
+        for (int x = 0; x < 4; ++x) {
+          unsigned hv, mv, lv;
+          split_pair(k0[x], k1[x], hv, mv, lv);
+          const int off = dq_kt_off<D>(b, 4 * c4 + x, 2 * sp);
+          *reinterpret_cast<unsigned*>(&kst[buf * P::STAGE + off]) = hv;
+          *reinterpret_cast<unsigned*>(&kst[buf * P::STAGE + P::PLANE + off]) = mv;
+          *reinterpret_cast<unsigned*>(&kst[buf * P::STAGE + 2 * P::PLANE + off]) = lv;
         }
       }
     }
-    if (it + 1 < iters) store_k(buf ^ 1);
+  };
+  // dS of the lane for pair p (blocks kb_lo + 2p, +1), both row blocks
+  auto load_a = [&](int p, float (&a)[2][8]) {
+    const int kbm = kb_lo + 2 * p + (g >> 1);
+    const bool ok = kbm < my_end;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const f32x4* src = reinterpret_cast<const f32x4*>(arow + (size_t)(ok ? kbm : 0) * kDsBlockFloats + 16 * rb * kBwdSlots);
+#pragma unroll
+      for (int c4 = 0; c4 < 2; ++c4) {
+        const f32x4 v4 = ok ? src[c4] : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a[rb][4 * c4 + e] = v4[e];
+      }
+    }
+  };
+
+  // Zero the d rows past D (D < 16 pads the staged rows to 16).
+  if (P::DROWS > D) {
+    for (int e = tid; e < SMEM_BF16 / 2; e += 256) reinterpret_cast<unsigned*>(smem)[e] = 0u;
     __syncthreads();
   }
-  // Q rows for the gain partial, loaded as one batch before the reduction
-  float qv[NMB][16];
-  if (par == 0 && wave_on) {
+  // the wave's pairs: par, par + 2, ... (one per stage)
+  float a_next[2][8];
+  if (kb_lo + 2 * par < my_end) load_a(par, a_next);
+  load_k(0);
+  store_k(0, 0);
+  __syncthreads();
+  for (int it = 0; it < iters; ++it) {
+    const int buf = it & 1;
+    if (it + 1 < iters) load_k(it + 1);
+    const int p = 2 * it + par;
+    if (kb_lo + 2 * p < my_end) {
+      float a[2][8];
 #pragma unroll
-    for (int nb = 0; nb < NMB; ++nb)
+      for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = 32 * qt + 8 * (r >> 2) + 4 * h + (r & 3);
-        const int d = 32 * nb + q;
-        qv[nb][r] = (row < T && d < D) ? Q[slice + (size_t)row * D + d] : 0.f;
+        for (int e = 0; e < 8; ++e) a[rb][e] = a_next[rb][e];
+      if (kb_lo + 2 * (p + 2) < my_end) load_a(p + 2, a_next);
+      const Limbs al0 = split8(a[0]), al1 = split8(a[1]);
+      const __bf16* kb_base = kst + buf * P::STAGE;
+#pragma unroll
+      for (int nb = 0; nb < P::NB; ++nb) {
+        const int off = dq_kt_off<D>(2 * par + (g >> 1), 16 * nb + l16, 8 * (g & 1));
+        Limbs bl;
+        bl.h = *reinterpret_cast<const bf16x8*>(kb_base + off);
+        bl.m = *reinterpret_cast<const bf16x8*>(kb_base + P::PLANE + off);
+        bl.l = *reinterpret_cast<const bf16x8*>(kb_base + 2 * P::PLANE + off);
+#pragma unroll
+        for (int st = 0; st < 6; ++st) {
+          acc[0][nb] = mfma16_step(st, al0, bl, acc[0][nb]);
+          acc[1][nb] = mfma16_step(st, al1, bl, acc[1][nb]);
+        }
       }
+    }
+    if (it + 1 < iters) store_k(buf ^ 1, it + 1);
+    __syncthreads();
   }
+  // lane (d = 16nb + l16, group g) holds rows 16rb + 4g + r of the tile
   if (par == 1) {
 #pragma unroll
-    for (int nb = 0; nb < NMB; ++nb)
+    for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) red[((qsub * NMB + nb) * 16 + r) * 64 + lane] = acc[nb][r];
+      for (int nb = 0; nb < P::NB; ++nb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[(((qsub * 2 + rb) * P::NB + nb) * 4 + r) * 64 + lane] = acc[rb][nb][r];
   }
   __syncthreads();
   if (par == 0) {
@@ -541,16 +592,20 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
       float* dst = nch == 1 ? dQ + slice + (size_t)(64 * qg) * D
                             : dq_part + ((size_t)bh * n_part + item) * 64 * D;
 #pragma unroll
-      for (int nb = 0; nb < NMB; ++nb)
+      for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float sum = acc[nb][r] + red[((qsub * NMB + nb) * 16 + r) * 64 + lane];
-          const int rloc = 32 * qsub + 8 * (r >> 2) + 4 * h + (r & 3);
-          const int d = 32 * nb + q;
-          const float val = sum * c;
-          gsum = fmaf(qv[nb][r], val, gsum);
-          if (64 * qg + rloc < T && d < D) dst[(size_t)rloc * D + d] = val;
-        }
+        for (int nb = 0; nb < P::NB; ++nb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float sum = acc[rb][nb][r] + red[(((qsub * 2 + rb) * P::NB + nb) * 4 + r) * 64 + lane];
+            const int rloc = 32 * qsub + 16 * rb + 4 * g + r;
+            const int d = 16 * nb + l16;
+            const float val = sum * c;
+            if (64 * qg + rloc < T && d < D) {
+              gsum = fmaf(Q[slice + (size_t)(64 * qg + rloc) * D + d], val, gsum);
+              dst[(size_t)rloc * D + d] = val;
+            }
+          }
     }
     gsum = wave_sum(gsum);
     if (lane == 0) gred[qsub] = gsum;
@@ -606,7 +661,7 @@ hipError_t launch_bwd(const float* q, const float* k, const float* v, const floa
   const int BH = B * H;
   const int rows = BH * T;
   timer_begin(kBwdPrep, stream);
-  hipLaunchKernelGGL(ca_bwd_prep_kernel<D>, dim3((rows * (D / 4) + 255) / 256), dim3(256), 0,
+  hipLaunchKernelGGL(ca_bwd_prep_kernel<D>, dim3((rows * (D / 8) + 255) / 256), dim3(256), 0,
                      stream, q, dout, o, stats, ws.limbs, ws.qstat, rows);
   timer_end(kBwdPrep, stream);
   hipError_t e = hipGetLastError();
