@@ -47,7 +47,9 @@ struct Bwd {
   static constexpr int C4 = D / 4;             // float4 chunks per row
   static constexpr int KB = (D + 31) / 32;     // 32-wide k blocks of S / dP'
   static constexpr int NMB = (D + 15) / 16;    // 16-row d blocks of dV^T / dK^T
-  static constexpr int LDR = D + 8;            // bf16 row stride of a staged tile
+  // bf16 row stride of a staged tile: 160-byte rows for D = 64 keep both the
+  // 16-row row-wise reads and the transposed reads free of bank conflicts
+  static constexpr int LDR = D + 16;
   static constexpr int LIMB = 32 * LDR;        // bf16 per limb plane of a tile
   static constexpr int TILE = 6 * LIMB;        // Q limbs h, m, l then dY/Z limbs h, m, l
   static constexpr int RCH = D / 8;            // 16-byte chunks per row and plane
@@ -384,33 +386,27 @@ __global__ __launch_bounds__(256, 2) void ca_bwd_dkdv_kernel(
 // 32-query tiles) of one slice; wave w takes query tile w&1 and, of the two
 // block pairs staged per stage, pair w>>1.  Per stage the K rows of four
 // consecutive key blocks (slots 14kb-1 .. 14kb+14 each) are staged in LDS
-// (double-buffered) as transposed bf16 limb planes [d][slot], relative to
-// k_ref, and shared by all four waves.  A operand: lane (query 16rb + l%16,
+// (double-buffered) as row-major bf16 limb planes [block][slot][d], relative
+// to k_ref, and shared by all four waves.  A operand: lane (query 16rb + l%16,
 // group g) holds dS of block (2p + g/2), slots 8(g%2) .. +7, split into limbs
-// in registers; B operand: lane (d = 16nb + l%16, g) reads the same 8 slots of
-// row d.  Halo slots and invisible keys carry dS = 0, so no masks are needed.
-// The two pair parities are summed through LDS at the end (fixed order).  A
-// single-chunk group writes dQ; the chunks of a longer group write partial
-// tiles that ca_bwd_gain_merge sums.  Every item writes its gain partial
-// sum_i q_i . dQ_i(chunk) (linear in dQ, so the partials add up).
+// in registers; B operand: lane (d = 16nb + l%16, g) gets the same 8 slots of
+// column d through two transposed reads.  Halo slots and invisible keys carry
+// dS = 0, so no masks are needed.  The two pair parities are summed through
+// LDS at the end (fixed order).  A single-chunk group writes dQ; the chunks
+// of a longer group write partial tiles that ca_bwd_gain_merge sums.  Every
+// item writes its gain partial sum_i q_i . dQ_i(chunk) (linear in dQ, so the
+// partials add up).
 template <int D>
 struct DqP {
   static constexpr int NB = (D + 15) / 16;            // 16-column d blocks of dQ
   static constexpr int C4 = D / 4;
-  static constexpr int UNITS = 4 * 8 * C4;            // (block, slot pair, float4) per stage
+  static constexpr int UNITS = 4 * kBwdSlots * C4;    // (block, slot, float4) per stage
   static constexpr int UPT = (UNITS + 255) / 256;
-  static constexpr int DROWS = NB * 16;               // staged d rows (padded to 16)
-  static constexpr int PLANE = 4 * DROWS * kBwdSlots;  // bf16 per limb plane of a stage
+  static constexpr int LDK = NB * 16 + 16;            // bf16 row stride (160 bytes for D = 64)
+  static constexpr int PLANE = 4 * kBwdSlots * LDK;   // bf16 per limb plane of a stage
   static constexpr int STAGE = 3 * PLANE;
   static constexpr int RED_FLOATS = 2 * 2 * NB * 4 * 64;  // parity reduction: [qsub][rb][nb][r][lane]
 };
-// bf16 offset of (block b, d row, slot s) in a limb plane; the 16-byte halves
-// of a row swap for rows 8..15 of every 16, so the 16 rows read together by
-// one lane group hit distinct banks.
-template <int D>
-__device__ __forceinline__ int dq_kt_off(int b, int d, int s) {
-  return (b * DqP<D>::DROWS + d) * kBwdSlots + ((((s >> 3) ^ (d >> 3)) & 1) << 3) + (s & 7);
-}
 
 template <int D>
 __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict__ dsbuf,
@@ -473,24 +469,23 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   // case), and the gain partial sum_i q_i . dQ_i inherits the same accuracy.
   // All chunks of a group use the same k_ref, so the k_ref terms cancel in the
   // sum of the chunk partials.
-  // Staging unit u: block b, slot pair sp (slots 2sp, 2sp+1), d = 4c4..4c4+3.
-  f32x4 kref[P::UPT], pre[P::UPT][2];
-#pragma unroll
-  for (int uu = 0; uu < P::UPT; ++uu)
-    kref[uu] = reinterpret_cast<const f32x4*>(K + slice + (size_t)(64 * qg) * D)[(tid + 256 * uu) % P::C4];
+  // Staging unit u: block b, slot s, d = 4c4..4c4+3.
+  // (a thread's units all have d chunk tid % C4, since 256 % C4 == 0)
+  f32x4 pre[P::UPT];
+  const f32x4 kref = reinterpret_cast<const f32x4*>(K + slice + (size_t)(64 * qg) * D)[tid % P::C4];
+  auto unit_key = [&](int u, int it) {
+    return kBwdKeys * (kb_lo + 4 * it + u / (kBwdSlots * P::C4)) - 1 + (u / P::C4) % kBwdSlots;
+  };
   auto load_k = [&](int it) {
 #pragma unroll
     for (int uu = 0; uu < P::UPT; ++uu) {
       const int u = tid + 256 * uu;
-      f32x4 v0 = {0.f, 0.f, 0.f, 0.f}, v1 = v0;
+      f32x4 v = {0.f, 0.f, 0.f, 0.f};
       if (u < P::UNITS) {
-        const int c4 = u % P::C4, sp = (u / P::C4) % 8, b = u / (8 * P::C4);
-        const int key = kBwdKeys * (kb_lo + 4 * it + b) - 1 + 2 * sp;
-        if (key >= 0 && key < T) v0 = reinterpret_cast<const f32x4*>(K + slice + (size_t)key * D)[c4];
-        if (key + 1 >= 0 && key + 1 < T) v1 = reinterpret_cast<const f32x4*>(K + slice + (size_t)(key + 1) * D)[c4];
+        const int key = unit_key(u, it);
+        if (key >= 0 && key < T) v = reinterpret_cast<const f32x4*>(K + slice + (size_t)key * D)[u % P::C4];
       }
-      pre[uu][0] = v0;
-      pre[uu][1] = v1;
+      pre[uu] = v;
     }
   };
   // The shift is applied when the prefetched rows are stored, so the loads
@@ -501,19 +496,15 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
     for (int uu = 0; uu < P::UPT; ++uu) {
       const int u = tid + 256 * uu;
       if (u < P::UNITS) {
-        const int c4 = u % P::C4, sp = (u / P::C4) % 8, b = u / (8 * P::C4);
-        const int key = kBwdKeys * (kb_lo + 4 * it + b) - 1 + 2 * sp;
-        const f32x4 k0 = (key >= 0 && key < T) ? pre[uu][0] - kref[uu] : f32x4{0.f, 0.f, 0.f, 0.f};
-        const f32x4 k1 = (key + 1 >= 0 && key + 1 < T) ? pre[uu][1] - kref[uu] : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int x = 0; x < 4; ++x) {
-          unsigned hv, mv, lv;
-          split_pair(k0[x], k1[x], hv, mv, lv);
-          const int off = dq_kt_off<D>(b, 4 * c4 + x, 2 * sp);
-          *reinterpret_cast<unsigned*>(&kst[buf * P::STAGE + off]) = hv;
-          *reinterpret_cast<unsigned*>(&kst[buf * P::STAGE + P::PLANE + off]) = mv;
-          *reinterpret_cast<unsigned*>(&kst[buf * P::STAGE + 2 * P::PLANE + off]) = lv;
-        }
+        const int key = unit_key(u, it);
+        const f32x4 kv = (key >= 0 && key < T) ? pre[uu] - kref : f32x4{0.f, 0.f, 0.f, 0.f};
+        unsigned h0, m0, l0, h1, m1, l1;
+        split_pair(kv[0], kv[1], h0, m0, l0);
+        split_pair(kv[2], kv[3], h1, m1, l1);
+        const int off = buf * P::STAGE + (u / P::C4) * P::LDK + 4 * (u % P::C4);
+        *reinterpret_cast<u32x2*>(&kst[off]) = u32x2{h0, h1};
+        *reinterpret_cast<u32x2*>(&kst[off + P::PLANE]) = u32x2{m0, m1};
+        *reinterpret_cast<u32x2*>(&kst[off + 2 * P::PLANE]) = u32x2{l0, l1};
       }
     }
   };
@@ -533,8 +524,8 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
     }
   };
 
-  // Zero the d rows past D (D < 16 pads the staged rows to 16).
-  if (P::DROWS > D) {
+  // Zero the d columns past D (D < 16 pads the staged rows to 16 columns).
+  if (D < 16) {
     for (int e = tid; e < SMEM_BF16 / 2; e += 256) reinterpret_cast<unsigned*>(smem)[e] = 0u;
     __syncthreads();
   }
@@ -557,13 +548,17 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
       if (kb_lo + 2 * (p + 2) < my_end) load_a(p + 2, a_next);
       const Limbs al0 = split8(a[0]), al1 = split8(a[1]);
       const __bf16* kb_base = kst + buf * P::STAGE;
+      // transposed reads: source lane 4j + m of group g points at slot
+      // 8(g%2) + j (+4 for the second read) of block 2par + g/2, column 16nb + 4m
+      const int srow = (2 * par + (g >> 1)) * kBwdSlots + 8 * (g & 1) + (l16 >> 2);
 #pragma unroll
       for (int nb = 0; nb < P::NB; ++nb) {
-        const int off = dq_kt_off<D>(2 * par + (g >> 1), 16 * nb + l16, 8 * (g & 1));
+        const int o0 = srow * P::LDK + 16 * nb + 4 * (l16 & 3);
+        const int o1 = o0 + 4 * P::LDK;
         Limbs bl;
-        bl.h = *reinterpret_cast<const bf16x8*>(kb_base + off);
-        bl.m = *reinterpret_cast<const bf16x8*>(kb_base + P::PLANE + off);
-        bl.l = *reinterpret_cast<const bf16x8*>(kb_base + 2 * P::PLANE + off);
+        bl.h = lds_read_tr8(kb_base + o0, kb_base + o1);
+        bl.m = lds_read_tr8(kb_base + P::PLANE + o0, kb_base + P::PLANE + o1);
+        bl.l = lds_read_tr8(kb_base + 2 * P::PLANE + o0, kb_base + 2 * P::PLANE + o1);
 #pragma unroll
         for (int st = 0; st < 6; ++st) {
           acc[0][nb] = mfma16_step(st, al0, bl, acc[0][nb]);

@@ -48,9 +48,9 @@ struct Fwd {
   static constexpr int VUNITS = 16 * C4;      // (key pair, float4 chunk) units of a V tile
   static constexpr int VLD = (VUNITS + 255) / 256;
   // K limb plane: row p = key key_of_arow(p); two halves of 8*KB bf16 (d values
-  // h*DH + ..., zero-padded when DH < 8) and 8 bf16 of padding, so the 16-byte
-  // A-operand reads of 8 consecutive rows hit distinct banks.
-  static constexpr int KROW = 16 * KB + 8;
+  // h*DH + ..., zero-padded when DH < 8) and 16 bf16 of padding (160-byte rows
+  // for D = 64: the 16-byte A-operand reads hit distinct banks).
+  static constexpr int KROW = 16 * KB + 16;
   static constexpr int KPLANE = 32 * KROW;
   // V^T limb plane: row d holds the 32 weight keys of the tile (+8 padding).
   static constexpr int VROW = 40;
