@@ -77,7 +77,7 @@ BwdLayout bwd_layout(int B, int H, int T, int D) {
   L.qstat = L.limbs + align256(ca::bwd_limb_elems(BH, T, D) * sizeof(uint16_t));
   L.gain = L.qstat + align256((size_t)BH * T * 2 * sizeof(float));
   L.dqpart = L.gain + align256((size_t)BH * sp.items * sizeof(float));
-  L.total = L.dqpart + align256((size_t)BH * sp.part_items * 64 * D * sizeof(float));
+  L.total = L.dqpart + align256((size_t)BH * sp.part_items * ca::kDqRows * D * sizeof(float));
   return L;
 }
 

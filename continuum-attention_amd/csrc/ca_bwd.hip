@@ -382,30 +382,27 @@ __global__ __launch_bounds__(256, 2) void ca_bwd_dkdv_kernel(
 
 // dQ = c dS (K - k_ref) over the 32x16 dS blocks written by ca_bwd_dkdv, as
 // bf16x6 products on v_mfma_f32_16x16x32_bf16 (k = 32 slots = a pair of key
-// blocks).  Work item: one chunk of the key blocks of a 64-query group (two
-// 32-query tiles) of one slice; wave w takes query tile w&1 and, of the two
-// block pairs staged per stage, pair w>>1.  Per stage the K rows of four
-// consecutive key blocks (slots 14kb-1 .. 14kb+14 each) are staged in LDS
-// (double-buffered) as row-major bf16 limb planes [block][slot][d], relative
-// to k_ref, and shared by all four waves.  A operand: lane (query 16rb + l%16,
-// group g) holds dS of block (2p + g/2), slots 8(g%2) .. +7, split into limbs
-// in registers; B operand: lane (d = 16nb + l%16, g) gets the same 8 slots of
-// column d through two transposed reads.  Halo slots and invisible keys carry
-// dS = 0, so no masks are needed.  The two pair parities are summed through
-// LDS at the end (fixed order).  A single-chunk group writes dQ; the chunks
-// of a longer group write partial tiles that ca_bwd_gain_merge sums.  Every
-// item writes its gain partial sum_i q_i . dQ_i(chunk) (linear in dQ, so the
-// partials add up).
+// blocks).  Work item: one chunk of the key blocks of a 128-query group (four
+// 32-query tiles, one per wave) of one slice.  Per stage the K rows of one
+// block pair (slots 14kb-1 .. 14kb+14 of each block) are staged in LDS
+// (double-buffered) as row-major bf16 limb planes [slot][d], relative to
+// k_ref, and shared by the four waves.  A operand: lane (query 16rb + l%16,
+// group g) holds dS of block g/2 of the pair, slots 8(g%2) .. +7, split into
+// limbs in registers; B operand: lane (d = 16nb + l%16, g) gets the same 8
+// slots of column d through two transposed reads.  Halo slots and invisible
+// keys carry dS = 0, so no masks are needed.  A single-chunk group writes dQ;
+// the chunks of a longer group write partial tiles that ca_bwd_gain_merge
+// sums.  Every item writes its gain partial sum_i q_i . dQ_i(chunk) (linear in
+// dQ, so the partials add up).
 template <int D>
 struct DqP {
   static constexpr int NB = (D + 15) / 16;            // 16-column d blocks of dQ
   static constexpr int C4 = D / 4;
-  static constexpr int UNITS = 4 * kBwdSlots * C4;    // (block, slot, float4) per stage
+  static constexpr int UNITS = 2 * kBwdSlots * C4;    // (slot of the pair, float4) per stage
   static constexpr int UPT = (UNITS + 255) / 256;
   static constexpr int LDK = NB * 16 + 16;            // bf16 row stride (160 bytes for D = 64)
-  static constexpr int PLANE = 4 * kBwdSlots * LDK;   // bf16 per limb plane of a stage
+  static constexpr int PLANE = 2 * kBwdSlots * LDK;   // bf16 per limb plane of a stage
   static constexpr int STAGE = 3 * PLANE;
-  static constexpr int RED_FLOATS = 2 * 2 * NB * 4 * 64;  // parity reduction: [qsub][rb][nb][r][lane]
 };
 
 template <int D>
@@ -419,13 +416,8 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
                                                         int H, int T, int chunk, int n_items,
                                                         int n_part) {
   using P = DqP<D>;
-  constexpr int SMEM_BF16 = 2 * P::STAGE > 2 * P::RED_FLOATS ? 2 * P::STAGE : 2 * P::RED_FLOATS;
-  // The K stages and the final reduction buffer are live at disjoint times and
-  // share one allocation.
-  __shared__ __attribute__((aligned(16))) __bf16 smem[SMEM_BF16];
-  __bf16* kst = smem;
-  float* red = reinterpret_cast<float*>(smem);
-  __shared__ float gred[2];
+  __shared__ __attribute__((aligned(16))) __bf16 kst[2 * P::STAGE];
+  __shared__ float gred[kDqTiles];
   const int nqt = num_q_tiles(T);
   const int nkb = bwd_num_key_blocks(T);
   const int bh = blockIdx.x % BH;
@@ -442,15 +434,14 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   const int kb_lo = ch * clen;
   const int kb_hi = min(kb_lo + clen, gblocks);
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
-  const int qsub = w & 1, par = w >> 1;
-  const int qt = 2 * qg + qsub;
+  const int qt = kDqTiles * qg + w;
   const bool wave_on = qt < nqt;
   const size_t slice = (size_t)bh * T * D;
   const float c = head_scale_log2(log_gain, bh % H, D) * kLn2;
   // key blocks of this chunk met by the wave's tile
   const int my_end = wave_on ? min(min(ds_kb_count(qt), nkb), kb_hi) : 0;
-  const int iters = kb_hi > kb_lo ? (kb_hi - kb_lo + 3) / 4 : 0;
-  // dS of this lane: rows 16rb + l16 of the wave's tile, slots 8(g&1)..+7 of block (pair, g>>1)
+  const int iters = kb_hi > kb_lo ? (kb_hi - kb_lo + 1) / 2 : 0;
+  // dS of this lane: rows 16rb + l16 of the wave's tile, slots 8(g&1)..+7 of block g>>1 of a pair
   const float* arow = dsbuf +
                       ((size_t)bh * ds_blocks_before(nqt) + ds_blocks_before(wave_on ? qt : 0)) * kDsBlockFloats +
                       l16 * kBwdSlots + 8 * (g & 1);
@@ -469,12 +460,13 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   // case), and the gain partial sum_i q_i . dQ_i inherits the same accuracy.
   // All chunks of a group use the same k_ref, so the k_ref terms cancel in the
   // sum of the chunk partials.
-  // Staging unit u: block b, slot s, d = 4c4..4c4+3.
-  // (a thread's units all have d chunk tid % C4, since 256 % C4 == 0)
+  // Staging unit u: slot u / C4 of the pair (block = slot / 16), d = 4(u % C4)..+3;
+  // a thread's units all have d chunk tid % C4, since 256 % C4 == 0.
   f32x4 pre[P::UPT];
-  const f32x4 kref = reinterpret_cast<const f32x4*>(K + slice + (size_t)(64 * qg) * D)[tid % P::C4];
+  const f32x4 kref = reinterpret_cast<const f32x4*>(K + slice + (size_t)(kDqRows * qg) * D)[tid % P::C4];
   auto unit_key = [&](int u, int it) {
-    return kBwdKeys * (kb_lo + 4 * it + u / (kBwdSlots * P::C4)) - 1 + (u / P::C4) % kBwdSlots;
+    const int s = u / P::C4;
+    return kBwdKeys * (kb_lo + 2 * it + s / kBwdSlots) - 1 + s % kBwdSlots;
   };
   auto load_k = [&](int it) {
 #pragma unroll
@@ -508,9 +500,9 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
       }
     }
   };
-  // dS of the lane for pair p (blocks kb_lo + 2p, +1), both row blocks
-  auto load_a = [&](int p, float (&a)[2][8]) {
-    const int kbm = kb_lo + 2 * p + (g >> 1);
+  // dS of the lane for stage it (blocks kb_lo + 2it, +1), both row blocks
+  auto load_a = [&](int it, float (&a)[2][8]) {
+    const int kbm = kb_lo + 2 * it + (g >> 1);
     const bool ok = kbm < my_end;
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
@@ -526,31 +518,29 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
 
   // Zero the d columns past D (D < 16 pads the staged rows to 16 columns).
   if (D < 16) {
-    for (int e = tid; e < SMEM_BF16 / 2; e += 256) reinterpret_cast<unsigned*>(smem)[e] = 0u;
+    for (int e = tid; e < P::STAGE; e += 256) reinterpret_cast<unsigned*>(kst)[e] = 0u;
     __syncthreads();
   }
-  // the wave's pairs: par, par + 2, ... (one per stage)
   float a_next[2][8];
-  if (kb_lo + 2 * par < my_end) load_a(par, a_next);
+  if (kb_lo < my_end) load_a(0, a_next);
   load_k(0);
   store_k(0, 0);
   __syncthreads();
+  // transposed reads: source lane 4j + m of group g points at slot
+  // 16(g/2) + 8(g%2) + j (+4 for the second read) of the pair, column 16nb + 4m
+  const int srow = 8 * g + (l16 >> 2);
   for (int it = 0; it < iters; ++it) {
     const int buf = it & 1;
     if (it + 1 < iters) load_k(it + 1);
-    const int p = 2 * it + par;
-    if (kb_lo + 2 * p < my_end) {
+    if (kb_lo + 2 * it < my_end) {
       float a[2][8];
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
         for (int e = 0; e < 8; ++e) a[rb][e] = a_next[rb][e];
-      if (kb_lo + 2 * (p + 2) < my_end) load_a(p + 2, a_next);
+      if (kb_lo + 2 * (it + 1) < my_end) load_a(it + 1, a_next);
       const Limbs al0 = split8(a[0]), al1 = split8(a[1]);
       const __bf16* kb_base = kst + buf * P::STAGE;
-      // transposed reads: source lane 4j + m of group g points at slot
-      // 8(g%2) + j (+4 for the second read) of block 2par + g/2, column 16nb + 4m
-      const int srow = (2 * par + (g >> 1)) * kBwdSlots + 8 * (g & 1) + (l16 >> 2);
 #pragma unroll
       for (int nb = 0; nb < P::NB; ++nb) {
         const int o0 = srow * P::LDK + 16 * nb + 4 * (l16 & 3);
@@ -569,44 +559,32 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
     if (it + 1 < iters) store_k(buf ^ 1, it + 1);
     __syncthreads();
   }
-  // lane (d = 16nb + l16, group g) holds rows 16rb + 4g + r of the tile
-  if (par == 1) {
+  // lane (d = 16nb + l16, group g) holds rows 16rb + 4g + r of the wave's tile
+  float gsum = 0.f;
+  if (wave_on) {
+    // single-chunk groups write dQ; chunk partials are item-indexed tiles
+    // [kDqRows queries][D] (items of multi-chunk groups are numbered first)
+    float* dst = nch == 1 ? dQ + slice + (size_t)(kDqRows * qg) * D
+                          : dq_part + ((size_t)bh * n_part + item) * kDqRows * D;
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
       for (int nb = 0; nb < P::NB; ++nb)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) red[(((qsub * 2 + rb) * P::NB + nb) * 4 + r) * 64 + lane] = acc[rb][nb][r];
-  }
-  __syncthreads();
-  if (par == 0) {
-    float gsum = 0.f;
-    if (wave_on) {
-      // single-chunk groups write dQ; chunk partials are item-indexed tiles
-      // [64 queries][D] (items of multi-chunk groups are numbered first)
-      float* dst = nch == 1 ? dQ + slice + (size_t)(64 * qg) * D
-                            : dq_part + ((size_t)bh * n_part + item) * 64 * D;
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-        for (int nb = 0; nb < P::NB; ++nb)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float sum = acc[rb][nb][r] + red[(((qsub * 2 + rb) * P::NB + nb) * 4 + r) * 64 + lane];
-            const int rloc = 32 * qsub + 16 * rb + 4 * g + r;
-            const int d = 16 * nb + l16;
-            const float val = sum * c;
-            if (64 * qg + rloc < T && d < D) {
-              gsum = fmaf(Q[slice + (size_t)(64 * qg + rloc) * D + d], val, gsum);
-              dst[(size_t)rloc * D + d] = val;
-            }
+        for (int r = 0; r < 4; ++r) {
+          const int rloc = 32 * w + 16 * rb + 4 * g + r;
+          const int d = 16 * nb + l16;
+          const float val = acc[rb][nb][r] * c;
+          if (kDqRows * qg + rloc < T && d < D) {
+            gsum = fmaf(Q[slice + (size_t)(kDqRows * qg + rloc) * D + d], val, gsum);
+            dst[(size_t)rloc * D + d] = val;
           }
-    }
-    gsum = wave_sum(gsum);
-    if (lane == 0) gred[qsub] = gsum;
+        }
   }
+  gsum = wave_sum(gsum);
+  if (lane == 0) gred[w] = gsum;
   __syncthreads();
-  if (tid == 0) gain_part[(size_t)bh * n_items + item] = gred[0] + gred[1];
+  if (tid == 0) gain_part[(size_t)bh * n_items + item] = (gred[0] + gred[1]) + (gred[2] + gred[3]);
 }
 
 // Work groups [0, H): dRho_h = sum over batch and dQ items of the gain
@@ -638,12 +616,12 @@ __global__ __launch_bounds__(256) void ca_bwd_gain_merge_kernel(
   int first = 0;  // item index of the group's chunk 0
   for (int gg = dq_num_groups(T) - 1; gg > qg; --gg) first += dq_group_chunks(gg, T, chunk);
   const int nch = dq_group_chunks(qg, T, chunk);
-  const f32x4* part = reinterpret_cast<const f32x4*>(dq_part + ((size_t)bh * n_part + first) * 64 * D);
-  f32x4* out = reinterpret_cast<f32x4*>(dQ + ((size_t)bh * T + 64 * qg) * D);
-  for (int e = tid; e < 64 * C4; e += 256) {
-    if (64 * qg + e / C4 >= T) break;
+  const f32x4* part = reinterpret_cast<const f32x4*>(dq_part + ((size_t)bh * n_part + first) * kDqRows * D);
+  f32x4* out = reinterpret_cast<f32x4*>(dQ + ((size_t)bh * T + kDqRows * qg) * D);
+  for (int e = tid; e < kDqRows * C4; e += 256) {
+    if (kDqRows * qg + e / C4 >= T) break;
     f32x4 s = part[e];
-    for (int cc = 1; cc < nch; ++cc) s += part[(size_t)cc * 16 * D + e];
+    for (int cc = 1; cc < nch; ++cc) s += part[(size_t)cc * kDqRows * C4 + e];
     out[e] = s;
   }
 }

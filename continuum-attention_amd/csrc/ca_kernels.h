@@ -36,8 +36,10 @@ constexpr int kBwdSlots = 16;
 constexpr int kDkdvWaves = 4;
 __host__ __device__ inline int bwd_num_key_blocks(int T) { return (T + kBwdKeys - 1) / kBwdKeys; }
 __host__ __device__ inline int num_q_tiles(int T) { return (T + 31) / 32; }
-// 64-query dQ groups per slice.
-__host__ __device__ inline int dq_num_groups(int T) { return (num_q_tiles(T) + 1) / 2; }
+// dQ work groups take kDqTiles consecutive 32-query tiles (kDqRows queries).
+constexpr int kDqTiles = 4;
+constexpr int kDqRows = 32 * kDqTiles;
+__host__ __device__ inline int dq_num_groups(int T) { return (num_q_tiles(T) + kDqTiles - 1) / kDqTiles; }
 
 // sum_{i=0}^{n-1} floor((a*i + b) / m) for n, m >= 1 and a, b >= 0 (Euclid-like
 // reduction, O(log m) steps).
@@ -88,7 +90,7 @@ constexpr int kDqChunkBlocks = 64;  // split chunk length in key blocks (about 9
 // key blocks met by the last query tile of group qg (the group's key range)
 __host__ __device__ inline int dq_group_blocks(int qg, int T) {
   const int nqt = num_q_tiles(T);
-  const int last = 2 * qg + 1 < nqt ? 2 * qg + 1 : nqt - 1;
+  const int last = kDqTiles * qg + kDqTiles - 1 < nqt ? kDqTiles * qg + kDqTiles - 1 : nqt - 1;
   const int c = ds_kb_count(last), nkb = bwd_num_key_blocks(T);
   return c < nkb ? c : nkb;
 }
