@@ -47,7 +47,7 @@ SIGNATURES = {
 }
 
 KERNEL_NAMES = ("ca_fwd", "ca_fwd_combine", "ca_bwd_prep", "ca_bwd_dkdv", "ca_bwd_dq",
-                "ca_bwd_gain", "ca_weights", "ca_weights_bwd", "ca_qkv_in", "ca_qkv_grad",
+                "ca_bwd_gain_merge", "ca_weights", "ca_weights_bwd", "ca_qkv_in", "ca_qkv_grad",
                 "ca_relayout")
 
 _lib = None

@@ -51,9 +51,10 @@ __device__ __forceinline__ f32x16 mfma32(float a, float b, f32x16 c) {
 }
 
 // fp32 products on the bf16 matrix cores ("bf16x6").  An fp32 value is split
-// into three bf16 limbs x = h + m + l (+ |r| <= 2^-27 |x|; round-to-nearest
-// limbs carry 9 significant bits each), and a product a*b is the sum of the
-// six limb products whose orders add to <= 2: h*h, h*m, m*h, h*l, m*m, l*h.
+// into three round-to-nearest bf16 limbs, x = h + m + l exactly (the 24-bit
+// significand in three 8-bit limbs, while the limbs stay in bf16's normal
+// range, |x| >= 2^-110), and a product a*b is the sum of the six limb
+// products whose orders add to <= 2: h*h, h*m, m*h, h*l, m*m, l*h.
 // The dropped terms are <= 2^-26 |a b|, each limb product is exact and the
 // MFMA accumulates in fp32, so a dot product carries fp32-level error (below
 // that of a sequential fp32 FMA chain for D = 64) while
