@@ -296,13 +296,17 @@ __global__ __launch_bounds__(256, 2) void ca_bwd_dkdv_kernel(
             const float sl = row_shr1(s), pl = row_shr1(p), gl = row_shr1(gg);
             float Lv, Rv, dLv, dRv;
             seg_shares_grad(sl, s, pl, p, gl, gg, Lv, Rv, dLv, dRv);
-            // segment (slot j-1, slot j), both keys visible
-            bool ok = j >= 1;
-            if (kGeneral) ok = ok && key_j >= 1 && key_j <= i && i < T;
-            Lv = ok ? Lv : 0.f;
-            Rv = ok ? Rv : 0.f;
-            dLv = ok ? dLv : 0.f;
-            dRv = ok ? dRv : 0.f;
+            // Segment (slot j-1, slot j), both keys visible.  Lane 0 has no
+            // left neighbour: its right shares land on slot 0, which is not
+            // owned, and its left shares are read by no lane (row_shl reads
+            // lane j+1), so only the general path needs the mask.
+            if (kGeneral) {
+              const bool ok = j >= 1 && key_j >= 1 && key_j <= i && i < T;
+              Lv = ok ? Lv : 0.f;
+              Rv = ok ? Rv : 0.f;
+              dLv = ok ? dLv : 0.f;
+              dRv = ok ? dRv : 0.f;
+            }
             // left shares of segment (j, j+1) arrive from lane j+1
             float w = Rv + row_shl1(Lv);
             float ds = dRv + row_shl1(dLv);
@@ -312,8 +316,11 @@ __global__ __launch_bounds__(256, 2) void ca_bwd_dkdv_kernel(
               w += cap;
               ds = fmaf(cap, gg, ds);
             }
+            // Slots 0 and 15 are not owned: their w only reaches output
+            // columns that are never stored, but their dS must be 0 in the
+            // spill that the dQ pass reads.
             const bool owned = j >= 1 && j <= kBwdKeys;
-            wout[rb][r] = owned ? w : 0.f;
+            wout[rb][r] = w;
             dout_s[rb][r] = owned ? ds : 0.f;
           }
         }
