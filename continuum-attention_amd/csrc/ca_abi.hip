@@ -44,11 +44,27 @@ int check_shape(int B, int H, int T, int D) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-// The dQ pass splits its work items when its grid would not fill the device
-// (ca::dq_split).  The workspace is sized for a split whenever the grid is
-// below kDqSplitBound work groups, so its size does not depend on the device;
-// the device's own resident count (at most this bound) picks the split.
+// The dQ and dK/dV passes split their work items when their grids would not
+// fill the device (ca::dq_split, ca::dkdv_split).  The workspace is sized as
+// if kDqSplitBound work groups were resident, so its size does not depend on
+// the device; the device's own resident counts (at most this bound) pick the
+// splits.
 constexpr int kDqSplitBound = 2048;
+
+int dkdv_resident_groups() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < 64) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c) return c;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  const int r = std::min(cus * ca::kDkdvGroupsPerCu, kDqSplitBound);
+  if (dev >= 0 && dev < 64) cache[dev].store(r, std::memory_order_relaxed);
+  return r;
+}
 
 int dq_resident_groups() {
   static std::atomic<int> cache[64];
@@ -66,7 +82,7 @@ int dq_resident_groups() {
 }
 
 struct BwdLayout {
-  size_t ds, limbs, qstat, gain, dqpart, total;
+  size_t ds, limbs, qstat, gain, dqpart, kvpart, total;
 };
 BwdLayout bwd_layout(int B, int H, int T, int D) {
   const int BH = B * H;
@@ -77,7 +93,9 @@ BwdLayout bwd_layout(int B, int H, int T, int D) {
   L.qstat = L.limbs + align256(ca::bwd_limb_elems(BH, T, D) * sizeof(uint16_t));
   L.gain = L.qstat + align256((size_t)BH * T * 2 * sizeof(float));
   L.dqpart = L.gain + align256((size_t)BH * sp.items * sizeof(float));
-  L.total = L.dqpart + align256((size_t)BH * sp.part_items * ca::kDqRows * D * sizeof(float));
+  L.kvpart = L.dqpart + align256((size_t)BH * sp.part_items * ca::kDqRows * D * sizeof(float));
+  const ca::DkdvSplit kvs = ca::dkdv_split(BH, T, kDqSplitBound);  // the largest split
+  L.total = L.kvpart + align256((size_t)BH * kvs.part_items * ca::kDkdvKeys * 2 * D * sizeof(float));
   return L;
 }
 
@@ -221,14 +239,16 @@ int ca_bwd_f32(const float* q, const float* k, const float* v, const float* log_
   work.qstat = reinterpret_cast<float*>(ws + L.qstat);
   work.gain_part = reinterpret_cast<float*>(ws + L.gain);
   work.dq_part = reinterpret_cast<float*>(ws + L.dqpart);
+  work.kv_part = reinterpret_cast<float*>(ws + L.kvpart);
   const ca::DqSplit sp = ca::dq_split(B * H, T, dq_resident_groups());
+  const ca::DkdvSplit kvs = ca::dkdv_split(B * H, T, dkdv_resident_groups());
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;
   switch (D) {
-    case 8: e = ca::launch_bwd<8>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, work, sp, B, H, T, s); break;
-    case 16: e = ca::launch_bwd<16>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, work, sp, B, H, T, s); break;
-    case 32: e = ca::launch_bwd<32>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, work, sp, B, H, T, s); break;
-    default: e = ca::launch_bwd<64>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, work, sp, B, H, T, s); break;
+    case 8: e = ca::launch_bwd<8>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, work, sp, kvs, B, H, T, s); break;
+    case 16: e = ca::launch_bwd<16>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, work, sp, kvs, B, H, T, s); break;
+    case 32: e = ca::launch_bwd<32>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, work, sp, kvs, B, H, T, s); break;
+    default: e = ca::launch_bwd<64>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, work, sp, kvs, B, H, T, s); break;
   }
   if (e != hipSuccess) return fail(CA_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
   return CA_OK;

@@ -116,7 +116,8 @@ template <int D>
 __global__ __launch_bounds__(256, 2) void ca_bwd_dkdv_kernel(
     const float* __restrict__ K, const float* __restrict__ V, const __bf16* __restrict__ limbs,
     const float* __restrict__ qstat, const float* __restrict__ log_gain, float* __restrict__ dK,
-    float* __restrict__ dV, float* __restrict__ dsbuf, int BH, int H, int T) {
+    float* __restrict__ dV, float* __restrict__ dsbuf, float* __restrict__ kv_part, int BH, int H,
+    int T, int chunk, int n_part) {
   using P = Bwd<D>;
   __shared__ __attribute__((aligned(16))) __bf16 tiles[2][P::TILE];
   __shared__ f32x4 tstat[2][16];  // rows 2u, 2u+1: (m, Dl/Z, m, Dl/Z)
@@ -124,8 +125,21 @@ __global__ __launch_bounds__(256, 2) void ca_bwd_dkdv_kernel(
   const int nqt = num_q_tiles(T);
   const int nkb = bwd_num_key_blocks(T);
   const int bh = blockIdx.x % BH;
-  const int wg = blockIdx.x / BH;  // ascending: heaviest first
-  const int w0 = kDkdvWaves * kBwdKeys * wg;
+  const int item = blockIdx.x / BH;  // ascending: heaviest first
+  // item -> (key-block group, chunk of its query tiles)
+  int wg = item, ch = 0, nch = 1;
+  if (chunk < nqt) {
+    const int G = dkdv_num_groups(T);
+    wg = 0;
+    ch = item;
+    nch = dkdv_group_chunks(0, T, chunk);
+    while (ch >= nch && wg < G - 1) {
+      ch -= nch;
+      ++wg;
+      nch = dkdv_group_chunks(wg, T, chunk);
+    }
+  }
+  const int w0 = kDkdvKeys * wg;
 
   const int tid = threadIdx.x;
   const int wv = tid >> 6;
@@ -221,19 +235,24 @@ __global__ __launch_bounds__(256, 2) void ca_bwd_dkdv_kernel(
     if (tid < 16) tstat[buf][tid] = pre_st;
   };
 
-  const int qt0 = w0 / 32;  // first query tile that sees an owned key of the work group
+  // query tiles of this item: a chunk of qt0 .. nqt-1, where qt0 is the first
+  // tile that sees an owned key of the work group
+  const int ntl = dkdv_group_tiles(wg, T);
+  const int clen = (ntl + nch - 1) / nch;
+  const int qt0 = w0 / 32 + ch * clen;
+  const int qt_end = min(qt0 + clen, nqt);
   // dS block of (tile qt, this wave's block); advanced by ds_kb_count(qt) per tile
   size_t ds_blk = (size_t)bh * ds_blocks_before(nqt) + ds_blocks_before(qt0) + kb16;
   __syncthreads();          // LDS clear before the first store
-  if (qt0 < nqt) {
+  if (qt0 < qt_end) {
     load_tile(qt0);
     store_tile(0);
   }
   __syncthreads();
 
-  for (int qt = qt0; qt < nqt; ++qt) {
+  for (int qt = qt0; qt < qt_end; ++qt) {
     const int buf = (qt - qt0) & 1;
-    if (qt + 1 < nqt) load_tile(qt + 1);
+    if (qt + 1 < qt_end) load_tile(qt + 1);
     const int i0 = 32 * qt;
     // the wave's block meets this tile (and exists)
     const bool work = kb16 < nkb && kBwdKeys * kb16 <= i0 + 31;
@@ -369,19 +388,24 @@ __global__ __launch_bounds__(256, 2) void ca_bwd_dkdv_kernel(
       }
     }
     ds_blk += ds_kb_count(qt);
-    if (qt + 1 < nqt) store_tile(buf ^ 1);
+    if (qt + 1 < qt_end) store_tile(buf ^ 1);
     __syncthreads();
   }
 
   // ---- epilogue: lane (slot j, group g) holds d = 16mb + 4g + r of its key ----
+  // A single-chunk group writes dK/dV; the chunks of a longer group write
+  // partials [key of the group][dV, dK][D] that ca_bwd_gain_merge sums.
   if (j >= 1 && j <= kBwdKeys && key_j < T && kb16 < nkb) {
     const float ck = cl2 * kLn2;
+    float* pv = nch == 1 ? dV + slice + (size_t)key_j * D
+                         : kv_part + (((size_t)bh * n_part + item) * kDkdvKeys + (key_j - w0)) * 2 * D;
+    float* pk = nch == 1 ? dK + slice + (size_t)key_j * D : pv + D;
 #pragma unroll
     for (int mb = 0; mb < P::NMB; ++mb) {
       const int d0 = 16 * mb + 4 * g;
       if (d0 < D) {
-        *reinterpret_cast<f32x4*>(dV + slice + (size_t)key_j * D + d0) = accv[mb];
-        *reinterpret_cast<f32x4*>(dK + slice + (size_t)key_j * D + d0) = acck[mb] * ck;
+        *reinterpret_cast<f32x4*>(pv + d0) = accv[mb];
+        *reinterpret_cast<f32x4*>(pk + d0) = acck[mb] * ck;
       }
     }
   }
@@ -597,12 +621,37 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
 // Work groups [0, H): dRho_h = sum over batch and dQ items of the gain
 // partials (fixed order).  Work groups H + BH*gi + bh: dQ of multi-chunk
 // group nqg-1-gi of slice bh, the sum of its chunk partials in chunk order.
+// Work groups after those: dK, dV of multi-chunk dK/dV group gi of slice bh,
+// the sum of its chunk partials in chunk order.
 template <int D>
 __global__ __launch_bounds__(256) void ca_bwd_gain_merge_kernel(
     const float* __restrict__ gain_part, const float* __restrict__ dq_part,
-    float* __restrict__ dlog_gain, float* __restrict__ dQ, int B, int H, int T, int chunk,
-    int n_items, int n_part) {
+    const float* __restrict__ kv_part, float* __restrict__ dlog_gain, float* __restrict__ dQ,
+    float* __restrict__ dK, float* __restrict__ dV, int B, int H, int T, int chunk, int n_items,
+    int n_part, int dq_multi, int kv_chunk, int kv_part_items) {
   const int tid = threadIdx.x;
+  const int BHt = B * H;
+  if (blockIdx.x >= H + BHt * dq_multi) {
+    constexpr int C4 = D / 4;
+    const int m = blockIdx.x - H - BHt * dq_multi;
+    const int bh = m % BHt, wg = m / BHt;
+    int first = 0;  // item index of the group's chunk 0 (multi-chunk groups come first)
+    for (int gg = 0; gg < wg; ++gg) first += dkdv_group_chunks(gg, T, kv_chunk);
+    const int nch = dkdv_group_chunks(wg, T, kv_chunk);
+    const f32x4* part =
+        reinterpret_cast<const f32x4*>(kv_part + ((size_t)bh * kv_part_items + first) * kDkdvKeys * 2 * D);
+    const int w0 = kDkdvKeys * wg;
+    for (int e = tid; e < kDkdvKeys * 2 * C4; e += 256) {
+      const int kl = e / (2 * C4), which = (e / C4) % 2, c4 = e % C4;
+      const int key = w0 + kl;
+      if (key >= T) break;
+      f32x4 s = part[e];
+      for (int cc = 1; cc < nch; ++cc) s += part[(size_t)cc * kDkdvKeys * 2 * C4 + e];
+      float* dst = (which ? dK : dV) + ((size_t)bh * T + key) * D;
+      reinterpret_cast<f32x4*>(dst)[c4] = s;
+    }
+    return;
+  }
   if (blockIdx.x < H) {
     __shared__ float wsum[4];
     const int h = blockIdx.x;
@@ -636,8 +685,8 @@ __global__ __launch_bounds__(256) void ca_bwd_gain_merge_kernel(
 template <int D>
 hipError_t launch_bwd(const float* q, const float* k, const float* v, const float* log_gain,
                       const float* o, const float* stats, const float* dout, float* dq, float* dk,
-                      float* dv, float* dlog_gain, const BwdWork& ws, const DqSplit& sp, int B,
-                      int H, int T, hipStream_t stream) {
+                      float* dv, float* dlog_gain, const BwdWork& ws, const DqSplit& sp,
+                      const DkdvSplit& kvs, int B, int H, int T, hipStream_t stream) {
   const int BH = B * H;
   const int rows = BH * T;
   timer_begin(kBwdPrep, stream);
@@ -646,10 +695,10 @@ hipError_t launch_bwd(const float* q, const float* k, const float* v, const floa
   timer_end(kBwdPrep, stream);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int nwg = (bwd_num_key_blocks(T) + kDkdvWaves - 1) / kDkdvWaves;
   timer_begin(kBwdDkdv, stream);
-  hipLaunchKernelGGL(ca_bwd_dkdv_kernel<D>, dim3(nwg * BH), dim3(256), 0, stream, k, v, ws.limbs,
-                     ws.qstat, log_gain, dk, dv, ws.dsbuf, BH, H, T);
+  hipLaunchKernelGGL(ca_bwd_dkdv_kernel<D>, dim3(kvs.items * BH), dim3(256), 0, stream, k, v,
+                     ws.limbs, ws.qstat, log_gain, dk, dv, ws.dsbuf, ws.kv_part, BH, H, T,
+                     kvs.chunk, kvs.part_items);
   timer_end(kBwdDkdv, stream);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -661,9 +710,10 @@ hipError_t launch_bwd(const float* q, const float* k, const float* v, const floa
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   timer_begin(kBwdGain, stream);
-  hipLaunchKernelGGL(ca_bwd_gain_merge_kernel<D>, dim3(H + BH * sp.multi_groups), dim3(256), 0,
-                     stream, ws.gain_part, ws.dq_part, dlog_gain, dq, B, H, T, sp.chunk, sp.items,
-                     sp.part_items);
+  hipLaunchKernelGGL(ca_bwd_gain_merge_kernel<D>,
+                     dim3(H + BH * sp.multi_groups + BH * kvs.multi_groups), dim3(256), 0, stream,
+                     ws.gain_part, ws.dq_part, ws.kv_part, dlog_gain, dq, dk, dv, B, H, T, sp.chunk,
+                     sp.items, sp.part_items, sp.multi_groups, kvs.chunk, kvs.part_items);
   timer_end(kBwdGain, stream);
   return hipGetLastError();
 }
@@ -671,8 +721,8 @@ hipError_t launch_bwd(const float* q, const float* k, const float* v, const floa
 #define CA_INST_BWD(DD)                                                                         \
   template hipError_t launch_bwd<DD>(const float*, const float*, const float*, const float*,    \
                                      const float*, const float*, const float*, float*, float*,  \
-                                     float*, float*, const BwdWork&, const DqSplit&, int, int,  \
-                                     int, hipStream_t);
+                                     float*, float*, const BwdWork&, const DqSplit&,            \
+                                     const DkdvSplit&, int, int, int, hipStream_t);
 CA_INST_BWD(8)
 CA_INST_BWD(16)
 CA_INST_BWD(32)

@@ -120,6 +120,47 @@ inline DqSplit dq_split(int BH, int T, int resident_groups) {
 // dQ work groups resident per CU (VGPR-limited: 3 waves per SIMD)
 constexpr int kDqGroupsPerCu = 3;
 
+// dK/dV work items: key-block group wg (kDkdvWaves blocks, kDkdvKeys keys) of
+// one slice and a chunk of the query tiles that see its keys.  When the grid
+// of whole groups would not fill the GPU for two rounds (small B*H), a group's
+// query range is cut into chunks of at most kDkdvChunkTiles tiles, so the
+// groups with the longest ranges do not set the launch time alone; the chunks
+// write partial dK/dV that a merge sums in chunk order.  Items are numbered
+// per slice from group 0 (the longest range) up, chunks of a group together.
+constexpr int kDkdvKeys = kDkdvWaves * kBwdKeys;
+constexpr int kDkdvChunkTiles = 24;
+constexpr int kDkdvGroupsPerCu = 2;
+__host__ __device__ inline int dkdv_num_groups(int T) {
+  return (bwd_num_key_blocks(T) + kDkdvWaves - 1) / kDkdvWaves;
+}
+__host__ __device__ inline int dkdv_group_tiles(int wg, int T) {
+  return num_q_tiles(T) - kDkdvKeys * wg / 32;  // tiles qt0 .. nqt-1
+}
+__host__ __device__ inline int dkdv_group_chunks(int wg, int T, int chunk) {
+  return (dkdv_group_tiles(wg, T) + chunk - 1) / chunk;
+}
+struct DkdvSplit {
+  int chunk;         // query tiles per chunk (upper bound)
+  int items;         // work items per slice
+  int part_items;    // of which write partial dK/dV (chunks of multi-chunk groups)
+  int multi_groups;  // groups with more than one chunk (the first ones)
+};
+// resident_groups: dK/dV work groups the GPU holds at once (0: never split)
+inline DkdvSplit dkdv_split(int BH, int T, int resident_groups) {
+  const int G = dkdv_num_groups(T);
+  const bool split = (long long)G * BH < 2LL * resident_groups;
+  DkdvSplit s{split ? kDkdvChunkTiles : num_q_tiles(T), 0, 0, 0};
+  for (int g = 0; g < G; ++g) {
+    const int n = dkdv_group_chunks(g, T, s.chunk);
+    s.items += n;
+    if (n > 1) {
+      s.part_items += n;
+      ++s.multi_groups;
+    }
+  }
+  return s;
+}
+
 // Per-kernel HIP-event timing (diagnostics; off unless ca_timing_enable(1)).
 enum KernelId {
   kFwd = 0, kFwdCombine, kBwdPrep, kBwdDkdv, kBwdDq, kBwdGain, kWeights, kWeightsBwd, kQkvIn,
@@ -159,13 +200,14 @@ struct BwdWork {
   float* qstat;       // per query row: (m, D/Z)
   float* gain_part;   // per dQ item
   float* dq_part;     // dQ chunk partials
+  float* kv_part;     // dK/dV chunk partials: [BH][part item][kDkdvKeys][2][D]
 };
 inline size_t bwd_limb_elems(int BH, int T, int D) { return (size_t)6 * BH * T * D; }
 
 template <int D>
 hipError_t launch_bwd(const float* q, const float* k, const float* v, const float* log_gain,
                       const float* o, const float* stats, const float* dout, float* dq, float* dk,
-                      float* dv, float* dlog_gain, const BwdWork& ws, const DqSplit& sp, int B,
-                      int H, int T, hipStream_t stream);
+                      float* dv, float* dlog_gain, const BwdWork& ws, const DqSplit& sp,
+                      const DkdvSplit& kvs, int B, int H, int T, hipStream_t stream);
 
 }  // namespace ca
