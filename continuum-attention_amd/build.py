@@ -13,7 +13,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libca_hip.so")
-SOURCES = ["ca_fwd.hip", "ca_bwd.hip", "ca_weights.hip", "ca_rope.hip", "ca_abi.hip"]
+SOURCES = ["ca_fwd.hip", "ca_bwd.hip", "ca_weights.hip", "ca_rope.hip", "ca_norm.hip", "ca_abi.hip"]
 ARCH = os.environ.get("CA_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [
@@ -22,7 +22,9 @@ HIPCC_FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-ffp-contract=fast",
-    # no NaN or infinity is ever produced or tested; lets fmax/fmin skip canonicalisation
+    # no output depends on a NaN or infinity (the backward's fast-path segment
+    # math may form them in lane 0, which has no left neighbour, and discards
+    # them); lets fmax/fmin skip canonicalisation
     "-fno-honor-nans", "-fno-honor-infinities",
     # packed fp32 VALU forms are disabled: some of them have returned wrong
     # results on this GPU pool with no error

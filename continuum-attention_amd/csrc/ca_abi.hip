@@ -369,4 +369,52 @@ int ca_tokens_to_heads(const void* x, int dtype, float* out, int B, int H, int T
   return relayout("ca_tokens_to_heads", x, out, dtype, false, B, H, T, D, stream);
 }
 
+static int check_norm(const char* fn, int N, int C, int dtype) {
+  if (N <= 0 || C <= 0) return fail(CA_ERR_INVALID, "%s: invalid shape N=%d C=%d", fn, N, C);
+  if (C > ca::kRmsMaxCols) return fail(CA_ERR_UNSUPPORTED, "%s: C=%d exceeds %d", fn, C, ca::kRmsMaxCols);
+  if (dtype != CA_DTYPE_F32 && dtype != CA_DTYPE_BF16 && dtype != CA_DTYPE_F16)
+    return fail(CA_ERR_INVALID, "%s: unknown dtype %d", fn, dtype);
+  if ((long long)N * C > (1ll << 31) - 1) return fail(CA_ERR_UNSUPPORTED, "%s: tensor too large", fn);
+  return CA_OK;
+}
+
+int ca_rmsnorm_fwd(const float* x, const float* weight, void* y, int ydtype, float* rstd, int N,
+                   int C, float eps, void* stream) {
+  int rc = check_norm("ca_rmsnorm_fwd", N, C, ydtype);
+  if (rc) return rc;
+  if (!x || !weight || !y || !rstd) return fail(CA_ERR_INVALID, "ca_rmsnorm_fwd: null pointer");
+  if (!(eps >= 0.f)) return fail(CA_ERR_INVALID, "ca_rmsnorm_fwd: eps must be >= 0");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  ca::timer_begin(ca::kRmsFwd, s);
+  hipError_t e = ca::launch_rmsnorm_fwd(x, weight, y, ydtype, rstd, N, C, eps, s);
+  ca::timer_end(ca::kRmsFwd, s);
+  if (e != hipSuccess) return fail(CA_ERR_HIP, "ca_rmsnorm_fwd launch: %s", hipGetErrorString(e));
+  return CA_OK;
+}
+
+size_t ca_rmsnorm_bwd_workspace_bytes(int N, int C) {
+  if (N <= 0 || C <= 0) return 0;
+  return (size_t)ca::rmsnorm_bwd_blocks(N) * C * sizeof(float);
+}
+
+int ca_rmsnorm_bwd(const void* dy, int dydtype, const float* x, const float* weight,
+                   const float* rstd, float* dx, float* dweight, void* workspace,
+                   size_t workspace_bytes, int N, int C, void* stream) {
+  int rc = check_norm("ca_rmsnorm_bwd", N, C, dydtype);
+  if (rc) return rc;
+  if (!dy || !x || !weight || !rstd || !dx || !dweight)
+    return fail(CA_ERR_INVALID, "ca_rmsnorm_bwd: null pointer");
+  const size_t need = ca_rmsnorm_bwd_workspace_bytes(N, C);
+  if (!workspace || workspace_bytes < need)
+    return fail(CA_ERR_WORKSPACE, "ca_rmsnorm_bwd: workspace of %zu bytes required, %zu given", need,
+                workspace_bytes);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  ca::timer_begin(ca::kRmsBwd, s);
+  hipError_t e = ca::launch_rmsnorm_bwd(dy, dydtype, x, weight, rstd, dx, dweight,
+                                        static_cast<float*>(workspace), N, C, s);
+  ca::timer_end(ca::kRmsBwd, s);
+  if (e != hipSuccess) return fail(CA_ERR_HIP, "ca_rmsnorm_bwd launch: %s", hipGetErrorString(e));
+  return CA_OK;
+}
+
 }  // extern "C"

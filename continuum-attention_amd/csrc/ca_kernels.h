@@ -164,13 +164,25 @@ inline DkdvSplit dkdv_split(int BH, int T, int resident_groups) {
 // Per-kernel HIP-event timing (diagnostics; off unless ca_timing_enable(1)).
 enum KernelId {
   kFwd = 0, kFwdCombine, kBwdPrep, kBwdDkdv, kBwdDq, kBwdGain, kWeights, kWeightsBwd, kQkvIn,
-  kQkvGrad, kRelayout, kNumKernels
+  kQkvGrad, kRelayout, kRmsFwd, kRmsBwd, kNumKernels
 };
 
 // Element types of the prologue / epilogue buffers (CA_DTYPE_* in the ABI).
 constexpr int kDtypeF32 = 0, kDtypeBF16 = 1, kDtypeF16 = 2;
 void timer_begin(int id, hipStream_t s);
 void timer_end(int id, hipStream_t s);
+
+// RMSNorm of the decoder caller (ca_norm.hip).  The backward splits the rows
+// over at most kRmsMaxBlocks work groups and keeps one dweight partial per group.
+constexpr int kRmsMaxBlocks = 512;
+constexpr int kRmsMaxCols = 256 * 16;
+int rmsnorm_rows_per_block(int N);
+int rmsnorm_bwd_blocks(int N);
+hipError_t launch_rmsnorm_fwd(const float* x, const float* w, void* y, int ydtype, float* rstd,
+                              int N, int C, float eps, hipStream_t s);
+hipError_t launch_rmsnorm_bwd(const void* dy, int dydtype, const float* x, const float* w,
+                              const float* rstd, float* dx, float* dw, float* dw_part, int N,
+                              int C, hipStream_t s);
 
 // Weight-materialising row kernels (ca_weights.hip).
 hipError_t launch_weights(const float* scores, float* weights, float* stats, int BH, int Q, int K,

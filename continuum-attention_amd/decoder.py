@@ -58,8 +58,59 @@ class ContinuumDecoderConfig:
             raise ValueError("The CA operator has no attention dropout; use --dropout 0.0")
 
 
+class _RMSNormFn(torch.autograd.Function):
+    """RMSNorm forward and backward as single HIP passes (ca_rmsnorm_fwd /
+    ca_rmsnorm_bwd).  The output is written in ``out_dtype``: under autocast
+    every RMSNorm output feeds a linear layer, whose autocast would round it to
+    that dtype, so the rounded value is the reference's."""
+
+    @staticmethod
+    def forward(ctx, x, weight, eps, out_dtype):
+        lib = _native.load()
+        C = x.shape[-1]
+        N = x.numel() // C
+        xc = _aligned(x.detach(), 16)
+        w = weight.detach().contiguous()
+        y = torch.empty(x.shape, device=x.device, dtype=out_dtype)
+        rstd = torch.empty(N, device=x.device, dtype=torch.float32)
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        with torch.cuda.device(x.device):
+            _native.check(lib.ca_rmsnorm_fwd(xc.data_ptr(), w.data_ptr(), y.data_ptr(),
+                                             _DTYPE_CODE[out_dtype], rstd.data_ptr(), N, C,
+                                             float(eps), stream))
+        ctx.save_for_backward(xc, w, rstd)
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        if torch.is_grad_enabled():
+            raise RuntimeError("the fused RMSNorm supports first-order gradients only")
+        xc, w, rstd = ctx.saved_tensors
+        lib = _native.load()
+        C = xc.shape[-1]
+        N = xc.numel() // C
+        g = gy.contiguous()
+        if g.dtype not in _DTYPE_CODE:
+            g = g.float()
+        dx = torch.empty_like(xc)
+        dw = torch.empty_like(w)
+        nbytes = int(lib.ca_rmsnorm_bwd_workspace_bytes(N, C))
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=xc.device)
+        stream = torch.cuda.current_stream(xc.device).cuda_stream
+        with torch.cuda.device(xc.device):
+            _native.check(lib.ca_rmsnorm_bwd(g.data_ptr(), _DTYPE_CODE[g.dtype], xc.data_ptr(),
+                                             w.data_ptr(), rstd.data_ptr(), dx.data_ptr(),
+                                             dw.data_ptr(), ws.data_ptr(), ws.numel(), N, C,
+                                             stream))
+        return dx, dw, None, None
+
+
 class RMSNorm(nn.Module):
     """weight * x / rms(x) (cuda/continuum_attention.py:817-823)."""
+
+    # fp32 GPU inputs run as one HIP pass each way (_RMSNormFn); False, or any
+    # other input, runs the reference's op-by-op composition
+    fused = True
 
     def __init__(self, dim, eps=1e-6):
         super().__init__()
@@ -67,6 +118,14 @@ class RMSNorm(nn.Module):
         self.eps = eps
 
     def forward(self, x):
+        if (self.fused and x.is_cuda and x.dtype == torch.float32
+                and self.weight.dtype == torch.float32 and x.shape[-1] <= 4096):
+            out_dtype = torch.float32
+            if torch.is_autocast_enabled("cuda"):
+                ad = torch.get_autocast_dtype("cuda")
+                if ad in (torch.bfloat16, torch.float16):
+                    out_dtype = ad
+            return _RMSNormFn.apply(x, self.weight, self.eps, out_dtype)
         return self.weight * x * torch.rsqrt(x.square().mean(-1, keepdim=True) + self.eps)
 
 

@@ -121,11 +121,30 @@ int ca_heads_to_tokens(const float* y, void* out, int dtype, int B, int H, int T
 int ca_tokens_to_heads(const void* x, int dtype, float* out, int B, int H, int T, int D,
                        void* stream);
 
+/* ---- RMSNorm of the decoder caller ----------------------------------------
+ * y = weight * x * rsqrt(mean(x^2) + eps) over rows of C values
+ * (RMSNorm.forward, cuda/continuum_attention.py:817-823, run there as a chain
+ * of torch fp32 elementwise/reduction ops and their autograd).  x [N][C] fp32,
+ * weight [C] fp32, y [N][C] of type ydtype (CA_DTYPE_*; bf16/fp16 round to
+ * nearest even, the value autocast feeds the next linear layer), rstd [N]
+ * fp32 = 1 / sqrt(mean(x^2) + eps).  C <= 4096. */
+int ca_rmsnorm_fwd(const float* x, const float* weight, void* y, int ydtype, float* rstd, int N,
+                   int C, float eps, void* stream);
+/* Bytes of device workspace ca_rmsnorm_bwd needs (per-block dweight partials). */
+size_t ca_rmsnorm_bwd_workspace_bytes(int N, int C);
+/* dx [N][C] fp32 and dweight [C] fp32 from dy [N][C] (dydtype), x, weight and
+ * the forward's rstd; dweight is summed in a fixed order. */
+int ca_rmsnorm_bwd(const void* dy, int dydtype, const float* x, const float* weight,
+                   const float* rstd, float* dx, float* dweight, void* workspace,
+                   size_t workspace_bytes, int N, int C, void* stream);
+
 /* ---- Diagnostics (no counterpart in the reference; used by bench.py) -------
  * Per-kernel timing with HIP events recorded on the launch stream around each
  * kernel launch of the calls above.  Kernel ids: 0 forward, 1 forward split
- * combine, 2 backward row dot, 3 backward dK/dV, 4 backward dQ, 5 backward
- * gain reduction.  ca_timing_enable(on) turns recording on/off and discards
+ * combine, 2 backward prep, 3 backward dK/dV, 4 backward dQ, 5 backward
+ * gain / partial merge, 6 weights, 7 weights backward, 8 qkv prologue, 9 qkv
+ * gradient, 10 relayout, 11 RMSNorm forward, 12 RMSNorm backward.
+ * ca_timing_enable(on) turns recording on/off and discards
  * unread records; ca_timing_read waits for the recorded events and returns the
  * summed milliseconds and launch counts per id (n entries), then clears them.
  * Not thread-safe; meant for single-threaded benchmarking. */

@@ -290,9 +290,49 @@ def test_fused_rope_attention_vs_unfused(gpu_ca, dtype):
     assert errs[0] <= tol[0] and errs[1] <= tol[1] and errs[2] <= tol[1]
 
 
+def _rmsnorm_composition(x, w, eps):
+    return w * x * torch.rsqrt(x.square().mean(-1, keepdim=True) + eps)
+
+
+@pytest.mark.parametrize("rows,C", [(1, 256), (37, 1024), (130, 1000), (2048, 1024), (5, 4096)])
+def test_rmsnorm_fused_vs_composition(gpu_ca, rows, C):
+    """The decoder's fused RMSNorm (ca_rmsnorm_fwd/bwd through the C ABI)
+    against the reference's torch composition (cuda/continuum_attention.py:
+    817-823) and its autograd: fp32 output and dx, dweight; bf16/fp16 outputs
+    equal the composition's rounded to that dtype (within one ulp, the
+    composition's mean is summed in another order), and dy in that dtype."""
+    Dm = gpu_ca.decoder
+    g = torch.Generator().manual_seed(rows + C)
+    x = (torch.randn(rows, C, generator=g) * 3 + 0.5).cuda()
+    w = (torch.rand(C, generator=g) + 0.5).cuda()
+    for out_dtype in (torch.float32, torch.bfloat16, torch.float16):
+        say(f"[case] rmsnorm rows={rows} C={C} {out_dtype}")
+        dy = torch.randn(rows, C, generator=g).cuda().to(out_dtype)
+        xa, wa = x.clone().requires_grad_(True), w.clone().requires_grad_(True)
+        y = Dm._RMSNormFn.apply(xa, wa, 1e-6, out_dtype)
+        assert y.dtype == out_dtype
+        dx, dw = torch.autograd.grad(y, (xa, wa), dy)
+        xb, wb = x.clone().requires_grad_(True), w.clone().requires_grad_(True)
+        yr = _rmsnorm_composition(xb, wb, 1e-6)
+        dxr, dwr = torch.autograd.grad(yr, (xb, wb), dy.float())
+        if out_dtype == torch.float32:
+            ey = rel(y.detach().cpu().numpy(), yr.detach().cpu().numpy())
+            assert ey <= 1e-6
+        else:
+            yc = yr.detach().to(out_dtype).float()
+            ulp = 2.0 ** (-7 if out_dtype == torch.bfloat16 else -10)
+            diff = (y.detach().float() - yc).abs() / yc.abs().clamp_min(1e-30)
+            ey = diff.max().item()
+            assert ey <= ulp
+        ex = rel(dx.cpu().numpy(), dxr.cpu().numpy())
+        ew = rel(dw.cpu().numpy(), dwr.cpu().numpy())
+        say(f"   y {ey:.2e} dx {ex:.2e} dweight {ew:.2e}")
+        assert ex <= 1e-5 and ew <= 1e-5
+
+
 def test_decoder_fused_prologue_matches_composition(gpu_ca):
-    """Whole decoder (fp32): fused-prologue attention vs the op-by-op path,
-    logits and every parameter gradient."""
+    """Whole decoder (fp32): fused-prologue attention and fused RMSNorm vs the
+    op-by-op path, logits and every parameter gradient."""
     say("[case] decoder fused vs composition")
     Dm = gpu_ca.decoder
     cfg = Dm.ContinuumDecoderConfig(d_model=128, n_heads=2, n_layers=2, block_size=64)
@@ -302,6 +342,7 @@ def test_decoder_fused_prologue_matches_composition(gpu_ca):
     outs = {}
     for fused in (True, False):
         Dm.ContinuumSelfAttention.fused_prologue = fused
+        Dm.RMSNorm.fused = fused
         try:
             m.zero_grad(set_to_none=True)
             loss = m(ids, targets=ids)["loss"]
@@ -309,6 +350,7 @@ def test_decoder_fused_prologue_matches_composition(gpu_ca):
             outs[fused] = (loss.item(), {n: p.grad.detach().clone() for n, p in m.named_parameters()})
         finally:
             Dm.ContinuumSelfAttention.fused_prologue = True
+            Dm.RMSNorm.fused = True
     assert abs(outs[True][0] - outs[False][0]) <= 1e-5 * abs(outs[False][0])
     for n, gref in outs[False][1].items():
         assert rel(outs[True][1][n].cpu().numpy(), gref.cpu().numpy()) <= 1e-3, n
