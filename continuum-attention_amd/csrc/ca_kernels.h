@@ -175,7 +175,7 @@ void timer_end(int id, hipStream_t s);
 // RMSNorm of the decoder caller (ca_norm.hip).  The backward splits the rows
 // over at most kRmsMaxBlocks work groups and keeps one dweight partial per group.
 constexpr int kRmsMaxBlocks = 512;
-constexpr int kRmsMaxCols = 256 * 16;
+constexpr int kRmsMaxCols = 4096;  // dynamic LDS of the backward: 16*C bytes <= 64 KB
 int rmsnorm_rows_per_block(int N);
 int rmsnorm_bwd_blocks(int N);
 hipError_t launch_rmsnorm_fwd(const float* x, const float* w, void* y, int ydtype, float* rstd,

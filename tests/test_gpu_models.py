@@ -294,7 +294,8 @@ def _rmsnorm_composition(x, w, eps):
     return w * x * torch.rsqrt(x.square().mean(-1, keepdim=True) + eps)
 
 
-@pytest.mark.parametrize("rows,C", [(1, 256), (37, 1024), (130, 1000), (2048, 1024), (5, 4096)])
+@pytest.mark.parametrize("rows,C", [(1, 256), (37, 1024), (130, 1000), (2048, 1024), (5, 4096),
+                                     (3, 257), (300, 771), (3000, 64)])
 def test_rmsnorm_fused_vs_composition(gpu_ca, rows, C):
     """The decoder's fused RMSNorm (ca_rmsnorm_fwd/bwd through the C ABI)
     against the reference's torch composition (cuda/continuum_attention.py:
