@@ -340,9 +340,11 @@ __global__ __launch_bounds__(256, 2) void ca_fwd_kernel(
         Rv = seg_ok ? Rv : 0.0f;
         float x = Lv + r_prev;
         const int wk = kbase - 1 + r;  // weight key, its score is sl
-        const float cap_last = (diag && wk == i) ? 0.5f * pl : 0.0f;   // last half-token cap
-        const float cap_first = (kGeneral && wk == 0) ? 0.5f * pl : 0.0f;          // first half-token cap
-        x += cap_last + cap_first;
+        if constexpr (kGeneral) {
+          const float cap_last = (diag && wk == i) ? 0.5f * pl : 0.0f;  // last half-token cap
+          const float cap_first = wk == 0 ? 0.5f * pl : 0.0f;           // first half-token cap
+          x += cap_last + cap_first;
+        }
         sacc[r] = x;
         zt += x;
         r_prev = Rv;
