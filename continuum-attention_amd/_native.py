@@ -45,6 +45,9 @@ SIGNATURES = {
     "ca_rmsnorm_fwd": (_i, [_vp, _vp, _vp, _i, _vp, _i, _i, ctypes.c_float, _vp]),
     "ca_rmsnorm_bwd_workspace_bytes": (_sz, [_i, _i]),
     "ca_rmsnorm_bwd": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _vp]),
+    "ca_add_rmsnorm_fwd": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _i, _i, ctypes.c_float, _vp]),
+    "ca_add_rmsnorm_bwd": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _sz, _i, _i,
+                                _vp]),
     "ca_timing_enable": (_i, [_i]),
     "ca_timing_read": (_i, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i), _i]),
 }

@@ -386,9 +386,28 @@ int ca_rmsnorm_fwd(const float* x, const float* weight, void* y, int ydtype, flo
   if (!(eps >= 0.f)) return fail(CA_ERR_INVALID, "ca_rmsnorm_fwd: eps must be >= 0");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   ca::timer_begin(ca::kRmsFwd, s);
-  hipError_t e = ca::launch_rmsnorm_fwd(x, weight, y, ydtype, rstd, N, C, eps, s);
+  hipError_t e = ca::launch_rmsnorm_fwd(x, nullptr, CA_DTYPE_F32, nullptr, weight, y, ydtype, rstd,
+                                        N, C, eps, s);
   ca::timer_end(ca::kRmsFwd, s);
   if (e != hipSuccess) return fail(CA_ERR_HIP, "ca_rmsnorm_fwd launch: %s", hipGetErrorString(e));
+  return CA_OK;
+}
+
+int ca_add_rmsnorm_fwd(const float* x, const void* res, int rdtype, float* sum_out,
+                       const float* weight, void* y, int ydtype, float* rstd, int N, int C,
+                       float eps, void* stream) {
+  int rc = check_norm("ca_add_rmsnorm_fwd", N, C, ydtype);
+  if (rc) return rc;
+  if (rdtype != CA_DTYPE_F32 && rdtype != CA_DTYPE_BF16 && rdtype != CA_DTYPE_F16)
+    return fail(CA_ERR_INVALID, "ca_add_rmsnorm_fwd: unknown dtype %d", rdtype);
+  if (!x || !res || !sum_out || !weight || !y || !rstd)
+    return fail(CA_ERR_INVALID, "ca_add_rmsnorm_fwd: null pointer");
+  if (!(eps >= 0.f)) return fail(CA_ERR_INVALID, "ca_add_rmsnorm_fwd: eps must be >= 0");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  ca::timer_begin(ca::kRmsFwd, s);
+  hipError_t e = ca::launch_rmsnorm_fwd(x, res, rdtype, sum_out, weight, y, ydtype, rstd, N, C, eps, s);
+  ca::timer_end(ca::kRmsFwd, s);
+  if (e != hipSuccess) return fail(CA_ERR_HIP, "ca_add_rmsnorm_fwd launch: %s", hipGetErrorString(e));
   return CA_OK;
 }
 
@@ -410,10 +429,33 @@ int ca_rmsnorm_bwd(const void* dy, int dydtype, const float* x, const float* wei
                 workspace_bytes);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   ca::timer_begin(ca::kRmsBwd, s);
-  hipError_t e = ca::launch_rmsnorm_bwd(dy, dydtype, x, weight, rstd, dx, dweight,
-                                        static_cast<float*>(workspace), N, C, s);
+  hipError_t e = ca::launch_rmsnorm_bwd(dy, dydtype, nullptr, x, weight, rstd, dx, nullptr,
+                                        CA_DTYPE_F32, dweight, static_cast<float*>(workspace), N, C, s);
   ca::timer_end(ca::kRmsBwd, s);
   if (e != hipSuccess) return fail(CA_ERR_HIP, "ca_rmsnorm_bwd launch: %s", hipGetErrorString(e));
+  return CA_OK;
+}
+
+int ca_add_rmsnorm_bwd(const void* dy, int dydtype, const float* dsum, const float* sum,
+                       const float* weight, const float* rstd, float* dx, void* dres, int rdtype,
+                       float* dweight, void* workspace, size_t workspace_bytes, int N, int C,
+                       void* stream) {
+  int rc = check_norm("ca_add_rmsnorm_bwd", N, C, dydtype);
+  if (rc) return rc;
+  if (rdtype != CA_DTYPE_F32 && rdtype != CA_DTYPE_BF16 && rdtype != CA_DTYPE_F16)
+    return fail(CA_ERR_INVALID, "ca_add_rmsnorm_bwd: unknown dtype %d", rdtype);
+  if (!dy || !sum || !weight || !rstd || !dx || !dres || !dweight)
+    return fail(CA_ERR_INVALID, "ca_add_rmsnorm_bwd: null pointer");
+  const size_t need = ca_rmsnorm_bwd_workspace_bytes(N, C);
+  if (!workspace || workspace_bytes < need)
+    return fail(CA_ERR_WORKSPACE, "ca_add_rmsnorm_bwd: workspace of %zu bytes required, %zu given",
+                need, workspace_bytes);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  ca::timer_begin(ca::kRmsBwd, s);
+  hipError_t e = ca::launch_rmsnorm_bwd(dy, dydtype, dsum, sum, weight, rstd, dx, dres, rdtype,
+                                        dweight, static_cast<float*>(workspace), N, C, s);
+  ca::timer_end(ca::kRmsBwd, s);
+  if (e != hipSuccess) return fail(CA_ERR_HIP, "ca_add_rmsnorm_bwd launch: %s", hipGetErrorString(e));
   return CA_OK;
 }
 

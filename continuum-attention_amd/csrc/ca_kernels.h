@@ -178,11 +178,15 @@ constexpr int kRmsMaxBlocks = 512;
 constexpr int kRmsMaxCols = 4096;  // dynamic LDS of the backward: 16*C bytes <= 64 KB
 int rmsnorm_rows_per_block(int N);
 int rmsnorm_bwd_blocks(int N);
-hipError_t launch_rmsnorm_fwd(const float* x, const float* w, void* y, int ydtype, float* rstd,
-                              int N, int C, float eps, hipStream_t s);
-hipError_t launch_rmsnorm_bwd(const void* dy, int dydtype, const float* x, const float* w,
-                              const float* rstd, float* dx, float* dw, float* dw_part, int N,
-                              int C, hipStream_t s);
+// res != nullptr: normalise s = x + res and write s to sum_out.
+hipError_t launch_rmsnorm_fwd(const float* x, const void* res, int rdtype, float* sum_out,
+                              const float* w, void* y, int ydtype, float* rstd, int N, int C,
+                              float eps, hipStream_t s);
+// dres != nullptr: x is the forward's s; dx = (norm gradient) + dsum (if
+// dsum != nullptr), also written to dres in rdtype.
+hipError_t launch_rmsnorm_bwd(const void* dy, int dydtype, const float* dsum, const float* x,
+                              const float* w, const float* rstd, float* dx, void* dres, int rdtype,
+                              float* dw, float* dw_part, int N, int C, hipStream_t s);
 
 // Weight-materialising row kernels (ca_weights.hip).
 hipError_t launch_weights(const float* scores, float* weights, float* stats, int BH, int Q, int K,

@@ -89,18 +89,28 @@ __device__ __forceinline__ void store_vec(void* base, size_t i, int dtype, const
 // One wave per row, four rows per work group; lane l holds columns
 // VEC*(l + 64*u).  KMAX > 0: the row is read once into registers (u < KMAX,
 // C <= 64*VEC*KMAX) with every load issued before the first use; KMAX = 0:
-// any C, loops that read the row twice.  No work-group barrier: a wave past
-// the last row exits.
-template <int VEC, int KMAX>
-__global__ __launch_bounds__(256) void ca_rmsnorm_fwd_kernel(const float* __restrict__ x,
-                                                             const float* __restrict__ w,
-                                                             void* __restrict__ y, int ydtype,
-                                                             float* __restrict__ rstd, int N, int C,
-                                                             float eps) {
+// any C, loops that read the row twice.  ADD: the normalised row is
+// s = x + res (res in rdtype), and s is written to sum_out (fp32).  No
+// work-group barrier: a wave past the last row exits.
+template <int VEC, int KMAX, bool ADD>
+__global__ __launch_bounds__(256) void ca_rmsnorm_fwd_kernel(
+    const float* __restrict__ x, const void* __restrict__ res, int rdtype,
+    float* __restrict__ sum_out, const float* __restrict__ w, void* __restrict__ y, int ydtype,
+    float* __restrict__ rstd, int N, int C, float eps) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= N) return;
   const size_t base = (size_t)row * C;
+  // the row's values (x, or x + res) at columns c .. c+VEC-1
+  auto load_row = [&](int c, float* v) {
+    load_vec<VEC>(x, base + c, kDtypeF32, v);
+    if constexpr (ADD) {
+      float rv[VEC];
+      load_vec<VEC>(res, base + c, rdtype, rv);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) v[e] += rv[e];
+    }
+  };
   float ss = 0.f;
   if constexpr (KMAX > 0) {
     float xv[KMAX][VEC];
@@ -108,7 +118,8 @@ __global__ __launch_bounds__(256) void ca_rmsnorm_fwd_kernel(const float* __rest
     for (int u = 0; u < KMAX; ++u) {
       const int c = (lane + 64 * u) * VEC;
       if (c < C) {
-        load_vec<VEC>(x, base + c, kDtypeF32, xv[u]);
+        load_row(c, xv[u]);
+        if constexpr (ADD) store_vec<VEC>(sum_out, base + c, kDtypeF32, xv[u]);
       } else {
 #pragma unroll
         for (int e = 0; e < VEC; ++e) xv[u][e] = 0.f;
@@ -135,7 +146,8 @@ __global__ __launch_bounds__(256) void ca_rmsnorm_fwd_kernel(const float* __rest
   } else {
     for (int c = lane * VEC; c < C; c += 64 * VEC) {
       float xv[VEC];
-      load_vec<VEC>(x, base + c, kDtypeF32, xv);
+      load_row(c, xv);
+      if constexpr (ADD) store_vec<VEC>(sum_out, base + c, kDtypeF32, xv);
 #pragma unroll
       for (int e = 0; e < VEC; ++e) ss = fmaf(xv[e], xv[e], ss);
     }
@@ -143,7 +155,7 @@ __global__ __launch_bounds__(256) void ca_rmsnorm_fwd_kernel(const float* __rest
     const float r = 1.0f / sqrtf(ss / (float)C + eps);
     for (int c = lane * VEC; c < C; c += 64 * VEC) {
       float xv[VEC], wv[VEC];
-      load_vec<VEC>(x, base + c, kDtypeF32, xv);
+      load_row(c, xv);
       load_vec<VEC>(w, c, kDtypeF32, wv);
 #pragma unroll
       for (int e = 0; e < VEC; ++e) xv[e] = wv[e] * xv[e] * r;
@@ -158,12 +170,15 @@ __global__ __launch_bounds__(256) void ca_rmsnorm_fwd_kernel(const float* __rest
 // accumulates sum(dy * xh) over its rows in its own LDS row of C floats
 // (dynamic LDS, 4*C floats); the work group's dweight partial is the sum of
 // the four rows in wave order.  KMAX as in the forward (x, dy and w of the
-// row held in registers).
-template <int VEC, int KMAX>
+// row held in registers).  ADD (x is the sum s = x + res of the forward):
+// dx += dsum (the gradient s receives from its other consumers, if any), and
+// dx is also written to dres in rdtype, the gradient of res.
+template <int VEC, int KMAX, bool ADD>
 __global__ __launch_bounds__(256) void ca_rmsnorm_bwd_kernel(
-    const void* __restrict__ dy, int dydtype, const float* __restrict__ x,
-    const float* __restrict__ w, const float* __restrict__ rstd, float* __restrict__ dx,
-    float* __restrict__ dw_part, int N, int C, int rows_per_block) {
+    const void* __restrict__ dy, int dydtype, const float* __restrict__ dsum,
+    const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ rstd,
+    float* __restrict__ dx, void* __restrict__ dres, int rdtype, float* __restrict__ dw_part,
+    int N, int C, int rows_per_block) {
   extern __shared__ float acc[];
   const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
   float* mine = acc + (size_t)wv * C;
@@ -172,6 +187,20 @@ __global__ __launch_bounds__(256) void ca_rmsnorm_bwd_kernel(
     for (int e = 0; e < VEC; ++e) mine[c + e] = 0.f;
   const int r0 = blockIdx.x * rows_per_block;
   const int r1 = min(r0 + rows_per_block, N);
+  // the gradient d of columns c .. c+VEC-1 of the row at base: stored to dx
+  // (and, with ADD, plus dsum, to dx and dres)
+  auto put = [&](size_t base, int c, float* d) {
+    if constexpr (ADD) {
+      if (dsum) {
+        float e2[VEC];
+        load_vec<VEC>(dsum, base + c, kDtypeF32, e2);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) d[e] += e2[e];
+      }
+      store_vec<VEC>(dres, base + c, rdtype, d);
+    }
+    store_vec<VEC>(dx, base + c, kDtypeF32, d);
+  };
   if constexpr (KMAX > 0) {
     float wt[KMAX][VEC];
 #pragma unroll
@@ -216,7 +245,7 @@ __global__ __launch_bounds__(256) void ca_rmsnorm_bwd_kernel(
             d[e] = r * fmaf(-xh, mean, wt[u][e] * g[u][e]);
             mine[c + e] = fmaf(g[u][e], xh, mine[c + e]);
           }
-          store_vec<VEC>(dx, base + c, kDtypeF32, d);
+          put(base, c, d);
         }
       }
     }
@@ -245,7 +274,7 @@ __global__ __launch_bounds__(256) void ca_rmsnorm_bwd_kernel(
           d[e] = r * fmaf(-xh, mean, wt[e] * g[e]);
           mine[c + e] = fmaf(g[e], xh, mine[c + e]);
         }
-        store_vec<VEC>(dx, base + c, kDtypeF32, d);
+        put(base, c, d);
       }
     }
   }
@@ -290,45 +319,65 @@ int rmsnorm_bwd_blocks(int N) {
   return (N + rpb - 1) / rpb;
 }
 
-// 16-byte alignment of every row (fp32) for the 4-wide path.
-static bool rows_vec4(const void* p, int C) {
-  return C % 4 == 0 && (reinterpret_cast<uintptr_t>(p) & 15) == 0;
-}
+static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-hipError_t launch_rmsnorm_fwd(const float* x, const float* w, void* y, int ydtype, float* rstd,
-                              int N, int C, float eps, hipStream_t s) {
-  const bool v4 = rows_vec4(x, C) && rows_vec4(w, C) && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+// The 4-wide path needs C % 4 == 0 and 16-byte aligned bases (every row of
+// an fp32 tensor is then 16-byte aligned, of a 16-bit tensor 8-byte aligned).
+template <bool ADD>
+static hipError_t rms_fwd(const float* x, const void* res, int rdtype, float* sum_out,
+                          const float* w, void* y, int ydtype, float* rstd, int N, int C,
+                          float eps, hipStream_t s) {
+  const bool v4 = C % 4 == 0 && al16(x) && al16(w) && al16(y) && (!ADD || (al16(res) && al16(sum_out)));
   const dim3 grid((N + 3) / 4);
   if (v4 && C <= 1024)
-    hipLaunchKernelGGL((ca_rmsnorm_fwd_kernel<4, 4>), grid, dim3(256), 0, s, x, w, y, ydtype, rstd, N, C, eps);
+    hipLaunchKernelGGL((ca_rmsnorm_fwd_kernel<4, 4, ADD>), grid, dim3(256), 0, s, x, res, rdtype,
+                       sum_out, w, y, ydtype, rstd, N, C, eps);
   else if (v4)
-    hipLaunchKernelGGL((ca_rmsnorm_fwd_kernel<4, 16>), grid, dim3(256), 0, s, x, w, y, ydtype, rstd, N, C, eps);
+    hipLaunchKernelGGL((ca_rmsnorm_fwd_kernel<4, 16, ADD>), grid, dim3(256), 0, s, x, res, rdtype,
+                       sum_out, w, y, ydtype, rstd, N, C, eps);
   else
-    hipLaunchKernelGGL((ca_rmsnorm_fwd_kernel<1, 0>), grid, dim3(256), 0, s, x, w, y, ydtype, rstd, N, C, eps);
+    hipLaunchKernelGGL((ca_rmsnorm_fwd_kernel<1, 0, ADD>), grid, dim3(256), 0, s, x, res, rdtype,
+                       sum_out, w, y, ydtype, rstd, N, C, eps);
   return hipGetLastError();
 }
 
-hipError_t launch_rmsnorm_bwd(const void* dy, int dydtype, const float* x, const float* w,
-                              const float* rstd, float* dx, float* dw, float* dw_part, int N,
-                              int C, hipStream_t s) {
+template <bool ADD>
+static hipError_t rms_bwd(const void* dy, int dydtype, const float* dsum, const float* x,
+                          const float* w, const float* rstd, float* dx, void* dres, int rdtype,
+                          float* dw, float* dw_part, int N, int C, hipStream_t s) {
   const int nb = rmsnorm_bwd_blocks(N);
   const int rpb = rmsnorm_rows_per_block(N);
   const size_t lds = 4 * (size_t)C * sizeof(float);
-  const bool v4 = rows_vec4(x, C) && rows_vec4(w, C) && rows_vec4(dx, C) &&
-                  (reinterpret_cast<uintptr_t>(dy) & 15) == 0;
+  const bool v4 = C % 4 == 0 && al16(dy) && al16(x) && al16(w) && al16(dx) &&
+                  (!ADD || (al16(dres) && (!dsum || al16(dsum))));
   if (v4 && C <= 1024)
-    hipLaunchKernelGGL((ca_rmsnorm_bwd_kernel<4, 4>), dim3(nb), dim3(256), lds, s, dy, dydtype, x, w,
-                       rstd, dx, dw_part, N, C, rpb);
+    hipLaunchKernelGGL((ca_rmsnorm_bwd_kernel<4, 4, ADD>), dim3(nb), dim3(256), lds, s, dy, dydtype,
+                       dsum, x, w, rstd, dx, dres, rdtype, dw_part, N, C, rpb);
   else if (v4)
-    hipLaunchKernelGGL((ca_rmsnorm_bwd_kernel<4, 16>), dim3(nb), dim3(256), lds, s, dy, dydtype, x, w,
-                       rstd, dx, dw_part, N, C, rpb);
+    hipLaunchKernelGGL((ca_rmsnorm_bwd_kernel<4, 16, ADD>), dim3(nb), dim3(256), lds, s, dy, dydtype,
+                       dsum, x, w, rstd, dx, dres, rdtype, dw_part, N, C, rpb);
   else
-    hipLaunchKernelGGL((ca_rmsnorm_bwd_kernel<1, 0>), dim3(nb), dim3(256), lds, s, dy, dydtype, x, w,
-                       rstd, dx, dw_part, N, C, rpb);
+    hipLaunchKernelGGL((ca_rmsnorm_bwd_kernel<1, 0, ADD>), dim3(nb), dim3(256), lds, s, dy, dydtype,
+                       dsum, x, w, rstd, dx, dres, rdtype, dw_part, N, C, rpb);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(ca_rmsnorm_dw_kernel, dim3((C + 15) / 16), dim3(256), 0, s, dw_part, dw, nb, C);
   return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_fwd(const float* x, const void* res, int rdtype, float* sum_out,
+                              const float* w, void* y, int ydtype, float* rstd, int N, int C,
+                              float eps, hipStream_t s) {
+  return res ? rms_fwd<true>(x, res, rdtype, sum_out, w, y, ydtype, rstd, N, C, eps, s)
+             : rms_fwd<false>(x, nullptr, kDtypeF32, nullptr, w, y, ydtype, rstd, N, C, eps, s);
+}
+
+hipError_t launch_rmsnorm_bwd(const void* dy, int dydtype, const float* dsum, const float* x,
+                              const float* w, const float* rstd, float* dx, void* dres, int rdtype,
+                              float* dw, float* dw_part, int N, int C, hipStream_t s) {
+  return dres ? rms_bwd<true>(dy, dydtype, dsum, x, w, rstd, dx, dres, rdtype, dw, dw_part, N, C, s)
+              : rms_bwd<false>(dy, dydtype, nullptr, x, w, rstd, dx, nullptr, kDtypeF32, dw, dw_part,
+                               N, C, s);
 }
 
 }  // namespace ca

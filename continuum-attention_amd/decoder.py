@@ -105,6 +105,64 @@ class _RMSNormFn(torch.autograd.Function):
         return dx, dw, None, None
 
 
+class _AddRMSNormFn(torch.autograd.Function):
+    """The decoder's residual add and the RMSNorm that reads it, s = x + res
+    and y = RMSNorm(s), as one HIP pass each way (ca_add_rmsnorm_fwd /
+    ca_add_rmsnorm_bwd).  Returns (s, y): s continues the fp32 residual stream,
+    y is written in ``out_dtype`` as in _RMSNormFn.  The backward adds the
+    gradient s receives downstream to the norm's and returns it for x (fp32)
+    and, in res's dtype, for res."""
+
+    @staticmethod
+    def forward(ctx, x, res, weight, eps, out_dtype):
+        lib = _native.load()
+        C = x.shape[-1]
+        N = x.numel() // C
+        xc = _aligned(x.detach(), 16)
+        rc = _aligned(res.detach(), 16)
+        w = weight.detach().contiguous()
+        s = torch.empty(x.shape, device=x.device, dtype=torch.float32)
+        y = torch.empty(x.shape, device=x.device, dtype=out_dtype)
+        rstd = torch.empty(N, device=x.device, dtype=torch.float32)
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        with torch.cuda.device(x.device):
+            _native.check(lib.ca_add_rmsnorm_fwd(xc.data_ptr(), rc.data_ptr(), _DTYPE_CODE[res.dtype],
+                                                 s.data_ptr(), w.data_ptr(), y.data_ptr(),
+                                                 _DTYPE_CODE[out_dtype], rstd.data_ptr(), N, C,
+                                                 float(eps), stream))
+        ctx.save_for_backward(s, w, rstd)
+        ctx.res_dtype = res.dtype
+        ctx.set_materialize_grads(False)  # an unused s (after the last block) reads no zeros
+        return s, y
+
+    @staticmethod
+    def backward(ctx, gs, gy):
+        if torch.is_grad_enabled():
+            raise RuntimeError("the fused add + RMSNorm supports first-order gradients only")
+        s, w, rstd = ctx.saved_tensors
+        lib = _native.load()
+        C = s.shape[-1]
+        N = s.numel() // C
+        g = torch.zeros_like(s) if gy is None else gy.contiguous()
+        if g.dtype not in _DTYPE_CODE:
+            g = g.float()
+        gsum = None if gs is None else gs.float().contiguous()
+        dx = torch.empty_like(s)
+        dres = torch.empty(s.shape, device=s.device, dtype=ctx.res_dtype)
+        dw = torch.empty_like(w)
+        nbytes = int(lib.ca_rmsnorm_bwd_workspace_bytes(N, C))
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=s.device)
+        stream = torch.cuda.current_stream(s.device).cuda_stream
+        with torch.cuda.device(s.device):
+            _native.check(lib.ca_add_rmsnorm_bwd(g.data_ptr(), _DTYPE_CODE[g.dtype],
+                                                 None if gsum is None else gsum.data_ptr(),
+                                                 s.data_ptr(), w.data_ptr(), rstd.data_ptr(),
+                                                 dx.data_ptr(), dres.data_ptr(),
+                                                 _DTYPE_CODE[ctx.res_dtype], dw.data_ptr(),
+                                                 ws.data_ptr(), ws.numel(), N, C, stream))
+        return dx, dres, dw, None, None
+
+
 class RMSNorm(nn.Module):
     """weight * x / rms(x) (cuda/continuum_attention.py:817-823)."""
 
@@ -117,16 +175,31 @@ class RMSNorm(nn.Module):
         self.weight = nn.Parameter(torch.ones(dim))
         self.eps = eps
 
+    def _fusable(self, x):
+        return (self.fused and x.is_cuda and x.dtype == torch.float32
+                and self.weight.dtype == torch.float32 and x.shape[-1] <= 4096)
+
+    @staticmethod
+    def _out_dtype():
+        if torch.is_autocast_enabled("cuda"):
+            ad = torch.get_autocast_dtype("cuda")
+            if ad in (torch.bfloat16, torch.float16):
+                return ad
+        return torch.float32
+
     def forward(self, x):
-        if (self.fused and x.is_cuda and x.dtype == torch.float32
-                and self.weight.dtype == torch.float32 and x.shape[-1] <= 4096):
-            out_dtype = torch.float32
-            if torch.is_autocast_enabled("cuda"):
-                ad = torch.get_autocast_dtype("cuda")
-                if ad in (torch.bfloat16, torch.float16):
-                    out_dtype = ad
-            return _RMSNormFn.apply(x, self.weight, self.eps, out_dtype)
+        if self._fusable(x):
+            return _RMSNormFn.apply(x, self.weight, self.eps, self._out_dtype())
         return self.weight * x * torch.rsqrt(x.square().mean(-1, keepdim=True) + self.eps)
+
+    def add_and_norm(self, x, res):
+        """(x + res, self(x + res)): the residual add of a decoder block and
+        the norm that reads its result, fused when the input qualifies."""
+        if (self._fusable(x) and res.shape == x.shape and res.device == x.device
+                and res.dtype in _DTYPE_CODE):
+            return _AddRMSNormFn.apply(x, res, self.weight, self.eps, self._out_dtype())
+        s = x + res
+        return s, self(s)
 
 
 _ROPE_CACHE: dict = {}
@@ -341,12 +414,23 @@ class ContinuumDecoderLM(nn.Module):
         if input_ids.dim() != 2 or input_ids.shape[1] > self.cfg.block_size:
             raise ValueError("Input must be [B,T] with T<=block_size")
         x = self.drop(self.byte_emb(input_ids))
-        for block in self.blocks:
-            if self.cfg.grad_checkpointing and self.training:
-                x = torch.utils.checkpoint.checkpoint(block, x, use_reentrant=False)
-            else:
-                x = block(x)
-        logits = self.lm_head(self.norm_f(x))
+        if self.blocks and not (self.cfg.grad_checkpointing and self.training) and self.norm_f._fusable(x):
+            # the blocks' chain x = x + attn(norm1(x)); x = x + mlp(norm2(x)),
+            # with every residual add fused into the norm that reads its sum
+            # (the next block's norm1, or norm_f after the last block)
+            h = self.blocks[0].norm1(x)
+            for n, block in enumerate(self.blocks):
+                x, h = block.norm2.add_and_norm(x, block.attn(h))
+                nxt = self.blocks[n + 1].norm1 if n + 1 < len(self.blocks) else self.norm_f
+                x, h = nxt.add_and_norm(x, block.mlp(h))
+            logits = self.lm_head(h)
+        else:
+            for block in self.blocks:
+                if self.cfg.grad_checkpointing and self.training:
+                    x = torch.utils.checkpoint.checkpoint(block, x, use_reentrant=False)
+                else:
+                    x = block(x)
+            logits = self.lm_head(self.norm_f(x))
         out = {"logits": logits}
         if targets is not None:
             V = self.cfg.vocab_size
@@ -395,6 +479,28 @@ def train_step(model, optimizer, batch, amp_dtype=torch.bfloat16, grad_clip=1.0)
         loss = model(batch, targets=batch)["loss"]
     loss.backward()
     if grad_clip and grad_clip > 0:
+        if _fused_on_gpu(optimizer):
+            # clip_grad_norm_'s scaling g * max_norm / (norm + 1e-6) (applied
+            # when that factor is < 1) is handed to the fused AdamW kernel as
+            # its gradient divisor (norm + 1e-6) / max_norm, instead of a
+            # separate multiply pass over every gradient
+            grads = [p.grad for g in optimizer.param_groups for p in g["params"] if p.grad is not None]
+            norm = torch.linalg.vector_norm(torch.stack(torch._foreach_norm(grads, 2.0)), 2.0)
+            optimizer.grad_scale = torch.clamp((norm + 1e-6) / grad_clip, min=1.0)
+            try:
+                optimizer.step()
+            finally:
+                del optimizer.grad_scale
+            return loss.detach()
         torch.nn.utils.clip_grad_norm_(model.parameters(), grad_clip)
     optimizer.step()
     return loss.detach()
+
+
+def _fused_on_gpu(optimizer):
+    """A fused torch AdamW/Adam whose parameters are all on the GPU (its
+    kernel divides every gradient by ``optimizer.grad_scale`` when set)."""
+    if not isinstance(optimizer, (torch.optim.AdamW, torch.optim.Adam)):
+        return False
+    return all(g.get("fused") for g in optimizer.param_groups) and all(
+        p.is_cuda for g in optimizer.param_groups for p in g["params"])

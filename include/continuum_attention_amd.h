@@ -137,6 +137,22 @@ size_t ca_rmsnorm_bwd_workspace_bytes(int N, int C);
 int ca_rmsnorm_bwd(const void* dy, int dydtype, const float* x, const float* weight,
                    const float* rstd, float* dx, float* dweight, void* workspace,
                    size_t workspace_bytes, int N, int C, void* stream);
+/* Residual add feeding the norm, as the decoder block chains them
+ * (x = x + branch, then RMSNorm of x; CADecoderBlock.forward and
+ * ContinuumDecoderLM.forward, cuda/continuum_attention.py:878-880, 906-911):
+ * sum_out = x + res (fp32, res of type rdtype) and y = RMSNorm(sum_out) in
+ * one pass. */
+int ca_add_rmsnorm_fwd(const float* x, const void* res, int rdtype, float* sum_out,
+                       const float* weight, void* y, int ydtype, float* rstd, int N, int C,
+                       float eps, void* stream);
+/* Its gradient: dx = RMSNorm gradient at sum (the forward's sum_out) + dsum
+ * (the gradient sum receives from its other consumers; NULL for none), fp32;
+ * dres = dx in rdtype (the residual branch's gradient); dweight as in
+ * ca_rmsnorm_bwd, same workspace size. */
+int ca_add_rmsnorm_bwd(const void* dy, int dydtype, const float* dsum, const float* sum,
+                       const float* weight, const float* rstd, float* dx, void* dres, int rdtype,
+                       float* dweight, void* workspace, size_t workspace_bytes, int N, int C,
+                       void* stream);
 
 /* ---- Diagnostics (no counterpart in the reference; used by bench.py) -------
  * Per-kernel timing with HIP events recorded on the launch stream around each

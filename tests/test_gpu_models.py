@@ -331,6 +331,84 @@ def test_rmsnorm_fused_vs_composition(gpu_ca, rows, C):
         assert ex <= 1e-5 and ew <= 1e-5
 
 
+@pytest.mark.parametrize("rows,C,rdt", [(37, 1024, torch.float32), (2048, 1024, torch.bfloat16),
+                                         (300, 771, torch.bfloat16), (5, 4096, torch.float16)])
+@pytest.mark.parametrize("use_s", [True, False])
+def test_add_rmsnorm_fused_vs_composition(gpu_ca, rows, C, rdt, use_s):
+    """ca_add_rmsnorm_fwd/bwd (the decoder's residual add fused into the norm
+    that reads it) against torch's s = x + res, RMSNorm(s) and autograd:
+    s bit-exact, y as the fused RMSNorm, gradients of x (plus the gradient s
+    receives downstream, or none), res (in its dtype) and weight."""
+    say(f"[case] add+rmsnorm rows={rows} C={C} res {rdt} s used {use_s}")
+    Dm = gpu_ca.decoder
+    g = torch.Generator().manual_seed(rows + C)
+    x = (torch.randn(rows, C, generator=g) * 2).cuda()
+    res = torch.randn(rows, C, generator=g).cuda().to(rdt)
+    w = (torch.rand(C, generator=g) + 0.5).cuda()
+    gy = torch.randn(rows, C, generator=g).cuda().to(rdt)
+    gsum = torch.randn(rows, C, generator=g).cuda()
+    xa, ra, wa = (t.clone().requires_grad_(True) for t in (x, res, w))
+    s, y = Dm._AddRMSNormFn.apply(xa, ra, wa, 1e-6, rdt)
+    outs, grads = ((s, y), (gsum, gy)) if use_s else ((y,), (gy,))
+    dx, dr, dw = torch.autograd.grad(outs, (xa, ra, wa), grads)
+    xb, rb, wb = (t.clone().requires_grad_(True) for t in (x, res, w))
+    sr = xb + rb
+    yr = _rmsnorm_composition(sr, wb, 1e-6)
+    outs_r, grads_r = ((sr, yr), (gsum, gy.float())) if use_s else ((yr,), (gy.float(),))
+    dxr, drr, dwr = torch.autograd.grad(outs_r, (xb, rb, wb), grads_r)
+    assert torch.equal(s.detach(), sr.detach())
+    assert dr.dtype == rdt
+    if rdt == torch.float32:
+        assert rel(y.detach().cpu().numpy(), yr.detach().cpu().numpy()) <= 1e-6
+    else:
+        yc = yr.detach().to(rdt).float()
+        ulp = 2.0 ** (-7 if rdt == torch.bfloat16 else -10)
+        assert ((y.detach().float() - yc).abs() / yc.abs().clamp_min(1e-30)).max().item() <= ulp
+    ex = rel(dx.cpu().numpy(), dxr.cpu().numpy())
+    er = rel(dr.float().cpu().numpy(), drr.float().cpu().numpy())
+    ew = rel(dw.cpu().numpy(), dwr.cpu().numpy())
+    say(f"   dx {ex:.2e} dres {er:.2e} dweight {ew:.2e}")
+    assert ex <= 1e-5 and ew <= 1e-5
+    assert er <= (1e-5 if rdt == torch.float32 else 4e-3)
+
+
+@pytest.mark.parametrize("clip", [0.05, 1e9])
+def test_train_step_clip_in_adamw(gpu_ca, clip):
+    """train_step hands clip_grad_norm_'s factor to the fused AdamW kernel as
+    its gradient divisor: the clipped gradients left in .grad, AdamW's first
+    moments and the parameters match torch's clip_grad_norm_ + step
+    (cuda/continuum_attention.py:1205-1228), with the clip active (0.05) and
+    inactive."""
+    say(f"[case] clip in AdamW, max_norm {clip}")
+    Dm = gpu_ca.decoder
+    cfg = Dm.ContinuumDecoderConfig(d_model=128, n_heads=2, n_layers=2, block_size=64)
+    torch.manual_seed(3)
+    ma = Dm.ContinuumDecoderLM(cfg).cuda()
+    mb = Dm.ContinuumDecoderLM(cfg).cuda()
+    mb.load_state_dict(ma.state_dict())
+    oa, ob = Dm.build_adamw(ma), Dm.build_adamw(mb)
+    assert Dm._fused_on_gpu(oa)
+    ids = torch.randint(0, 256, (2, 64), device="cuda")
+    # one step from equal parameters: equal gradients before the clip, so any
+    # difference is the clip's (a second step would compare bf16 forwards of
+    # parameters that differ in their last bits)
+    Dm.train_step(ma, oa, ids, grad_clip=clip)
+    ob.zero_grad(set_to_none=True)
+    with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+        loss = mb(ids, targets=ids)["loss"]
+    loss.backward()
+    torch.nn.utils.clip_grad_norm_(mb.parameters(), clip)
+    ob.step()
+    worst = {}
+    for (n, pa), pb in zip(ma.named_parameters(), mb.parameters()):
+        sa, sb = oa.state[pa]["exp_avg"], ob.state[pb]["exp_avg"]
+        for key, a, b in (("grad", pa.grad, pb.grad), ("exp_avg", sa, sb), ("param", pa, pb)):
+            e = ((a - b).abs().max() / b.abs().max().clamp_min(1e-30)).item()
+            worst[key] = max(worst.get(key, 0.0), e)
+    say("   " + " ".join(f"{k} {v:.1e}" for k, v in worst.items()))
+    assert worst["grad"] <= 1e-5 and worst["exp_avg"] <= 1e-5 and worst["param"] <= 1e-6
+
+
 def test_decoder_fused_prologue_matches_composition(gpu_ca):
     """Whole decoder (fp32): fused-prologue attention and fused RMSNorm vs the
     op-by-op path, logits and every parameter gradient."""
