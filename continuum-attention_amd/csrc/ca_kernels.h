@@ -78,7 +78,7 @@ inline size_t bwd_ds_floats(int BH, int T) {
   return (size_t)BH * (size_t)ds_blocks_before(num_q_tiles(T)) * kDsBlockFloats;
 }
 
-// dQ work items: a 64-query group of one slice and one chunk of its key
+// dQ work items: a 128-query group of one slice and one chunk of its key
 // blocks.  A group of n blocks is cut into ceil(n / chunk) near-equal chunks
 // (split-K) when the unsplit grid would not fill the GPU for one round, so
 // that the longest rows do not leave it waiting on a few work groups; with a
@@ -86,7 +86,8 @@ inline size_t bwd_ds_floats(int BH, int T) {
 // numbered per slice from the last (heaviest) group down, so the chunks of
 // multi-chunk groups come first; those items write partial dQ tiles that a
 // second kernel sums in chunk order.
-constexpr int kDqChunkBlocks = 64;  // split chunk length in key blocks (about 900 keys)
+constexpr int kDqChunkBlocks = 64;       // split chunk length in key blocks (about 900 keys)
+constexpr int kDqChunkBlocksShort = 48;  // when 64-block chunks still leave the GPU short of a round
 // key blocks met by the last query tile of group qg (the group's key range)
 __host__ __device__ inline int dq_group_blocks(int qg, int T) {
   const int nqt = num_q_tiles(T);
@@ -103,10 +104,8 @@ struct DqSplit {
   int part_items;    // of which write partial tiles (chunks of multi-chunk groups)
   int multi_groups;  // groups with more than one chunk (the last ones)
 };
-// resident_groups: dQ work groups the GPU holds at once (0: never split)
-inline DqSplit dq_split(int BH, int T, int resident_groups) {
-  const bool split = (long long)dq_num_groups(T) * BH < resident_groups;
-  DqSplit s{split ? kDqChunkBlocks : bwd_num_key_blocks(T), 0, 0, 0};
+inline DqSplit dq_split_chunk(int T, int chunk) {
+  DqSplit s{chunk, 0, 0, 0};
   for (int g = 0; g < dq_num_groups(T); ++g) {
     const int n = dq_group_chunks(g, T, s.chunk);
     s.items += n;
@@ -116,6 +115,14 @@ inline DqSplit dq_split(int BH, int T, int resident_groups) {
     }
   }
   return s;
+}
+// resident_groups: dQ work groups the GPU holds at once (0: never split).
+// Splitting more finely only adds work groups (and partial tiles), so the
+// workspace sized for the largest resident_groups covers every smaller one.
+inline DqSplit dq_split(int BH, int T, int resident_groups) {
+  if ((long long)dq_num_groups(T) * BH >= resident_groups) return dq_split_chunk(T, bwd_num_key_blocks(T));
+  const DqSplit s = dq_split_chunk(T, kDqChunkBlocks);
+  return (long long)s.items * BH >= resident_groups ? s : dq_split_chunk(T, kDqChunkBlocksShort);
 }
 // dQ work groups resident per CU (VGPR-limited: 3 waves per SIMD)
 constexpr int kDqGroupsPerCu = 3;
