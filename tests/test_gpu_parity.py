@@ -5,6 +5,7 @@ on outputs and <= 1e-3 on gradients (dq, dk, dv, dlog_gain); exact causality
 (outputs bitwise unchanged, future gradients exactly 0).  Every call goes
 through the C ABI (libca_hip.so via ctypes) behind continuum_attention().
 """
+import json
 import math
 import sys
 
@@ -79,6 +80,37 @@ def test_config1_cpu_operator_shape(gpu_ca):
     assert rel(y, yo) <= OUT_TOL
     for a, b in zip(grads, go):
         assert rel(a, b) <= GRAD_TOL
+
+
+def error_metrics(a, b):
+    """Errors of a against the float64 reference b: the bar's max relative
+    error (max|a-b| / max|b|), the reference benchmark's relative L2 and
+    max-abs (cuda/benchmark.py:22-31: |a-b|_2 / |a|_2), and the element-wise
+    relative error with an absolute floor of 1e-3 * rms(b)."""
+    a = np.asarray(a, np.float64); b = np.asarray(b, np.float64)
+    d = np.abs(a - b)
+    floor = 1e-3 * float(np.sqrt(np.mean(b * b))) + 1e-300
+    return {"max_rel": rel(a, b), "relative_l2": float(np.linalg.norm(d) / max(np.linalg.norm(a), 1e-9)),
+            "max_abs": float(d.max()), "elem_rel_floor": float((d / np.maximum(np.abs(b), floor)).max())}
+
+
+@pytest.mark.parametrize("shape", [(1, 2, 64, 16), (1, 4, 1024, 64)])
+def test_error_metrics_reference_style(gpu_ca, shape):
+    """Every error metric the measurement spec names, printed per tensor as
+    the reference's COMPARE lines, at config 1 and a 1024-token shape of
+    config 2's head size (seed 0, tau = 1): max relative error within the
+    bars (outputs 1e-4, gradients 1e-3) and relative L2 within the
+    reference's own 1e-3 (cuda/benchmark.py:22-31)."""
+    say(f"[case] error metrics {shape}")
+    q, k, v, rho, dy = make_inputs(shape, 0)
+    y, grads = run_hip(gpu_ca, q, k, v, rho, dy)
+    yo = O.ca_forward(q.numpy(), k.numpy(), v.numpy(), rho.numpy())[0]
+    go = O.ca_backward(q.numpy(), k.numpy(), v.numpy(), rho.numpy(), dy.numpy())
+    for name, a, b, bar in zip(("y", "dq", "dk", "dv", "drho"), [y] + grads, [yo] + list(go),
+                               [OUT_TOL] + [GRAD_TOL] * 4):
+        m = error_metrics(a, b)
+        say("COMPARE " + json.dumps({"name": name, **{k2: float(f"{v2:.3e}") for k2, v2 in m.items()}}))
+        assert m["max_rel"] <= bar and m["relative_l2"] <= min(bar, 1e-3), name
 
 
 def test_reference_ca_check_shape(gpu_ca):
