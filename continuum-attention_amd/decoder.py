@@ -26,7 +26,7 @@ from torch import nn
 from torch.nn import functional as F
 
 from . import _native
-from .ops import _mode, ca_backward, ca_forward, continuum_attention
+from .ops import SUPPORTED_HEAD_DIMS, _mode, ca_backward, ca_forward, continuum_attention
 
 _DTYPE_CODE = {torch.float32: _native.CA_DTYPE_F32, torch.bfloat16: _native.CA_DTYPE_BF16,
                torch.float16: _native.CA_DTYPE_F16}
@@ -343,13 +343,14 @@ class ContinuumSelfAttention(nn.Module):
         # positive per-head score gain exp(log_qk_gain), starting at 1
         self.log_qk_gain = nn.Parameter(torch.zeros(heads))
 
-    # fused HIP prologue/epilogue around the operator on GPU tensors; False
-    # runs the reference's op-by-op composition (same operator kernels)
+    # fused HIP prologue/epilogue around the operator on GPU tensors (head
+    # dims with fused operator kernels); False runs the reference's op-by-op
+    # composition (same operator kernels)
     fused_prologue = True
 
     def forward(self, x):
         Bsz, T, C = x.shape
-        if self.fused_prologue and x.is_cuda:
+        if self.fused_prologue and x.is_cuda and self.head_dim in SUPPORTED_HEAD_DIMS:
             y = rope_continuum_attention(self.qkv(x), self.log_qk_gain, self.rope_theta, self.heads,
                                          self.ca_query_tile)
             return self.out(y)

@@ -14,8 +14,9 @@ autograd Function ``_CAExactTiled`` (cuda/continuum_attention.py:650-783):
 Compute is float32 on the device (fp16/bf16 inputs are read as fp32, results
 cast back).  ``query_tile`` is accepted and validated; in the reference it only
 bounds the memory of the materialised ``[BH, Qt, K]`` weights
-(cuda/continuum_attention.py:957), which these kernels never materialise, so it
-does not change the arithmetic.  All ``CA_CUDA_MODE`` values select the same
+(cuda/continuum_attention.py:957), which the fused kernels (D in 8, 16, 32,
+64) never materialise, so it does not change their arithmetic; other head
+dims run the reference's query-tile structure, where it does bound memory.  All ``CA_CUDA_MODE`` values select the same
 exact fp32 path (the reference modes differ only in fp16 rounding and launch
 structure).
 
@@ -109,6 +110,87 @@ def ca_backward(q, k, v, log_gain, out, stats, dout):
     return dq, dk, dv, dg
 
 
+# ---- any head dimension: the query-tile structure over the HIP weight kernels
+#
+# Head dims without a fused kernel (D not in SUPPORTED_HEAD_DIMS) run the
+# reference operator's own structure (cuda/continuum_attention.py:666-694 and
+# :707-764) on the device: per query tile, fp32 GEMMs for the scores, W.V and
+# the gradient contractions, and the HIP weight kernels (ca_weights_f32,
+# ca_weights_bwd_f32) for the exact weights and their score VJP.  The [BH,
+# Qt, K] tile is materialised, so query_tile bounds the memory as in the
+# reference.  Matmuls run in IEEE fp32 (no reduced-precision fp32 modes).
+
+
+class _Fp32Matmul:
+    """Turns reduced-precision fp32 GEMM modes off for the enclosed calls."""
+
+    def __enter__(self):
+        self.prev = torch.backends.cuda.matmul.allow_tf32
+        torch.backends.cuda.matmul.allow_tf32 = False
+
+    def __exit__(self, *exc):
+        torch.backends.cuda.matmul.allow_tf32 = self.prev
+
+
+def _head_scale(log_gain, H, D):
+    return (torch.exp(log_gain.reshape(H).float()) * D ** -0.5).reshape(1, H, 1, 1)
+
+
+def _tile_scores(qf, kt, scale, start, end):
+    """c * q[start:end] k[:end]^T for every (b, h): [B, H, end-start, end]."""
+    return torch.matmul(qf[:, :, start:end].contiguous(), kt[:, :, :, :end].contiguous()) * scale
+
+
+def tiled_forward(q, k, v, log_gain, query_tile):
+    """fp32 output of the operator for any head dim (query-tile structure)."""
+    from .weights import ca_weights
+    _check_device(q, k, v, log_gain)
+    B, H, T, D = q.shape
+    qf, kf, vf = _as_f32(q), _as_f32(k), _as_f32(v)
+    scale = _head_scale(log_gain, H, D)
+    kt = kf.transpose(2, 3).contiguous()
+    out = torch.empty((B, H, T, D), device=q.device, dtype=torch.float32)
+    with _Fp32Matmul():
+        for start in range(0, T, query_tile):
+            end = min(T, start + query_tile)
+            s = _tile_scores(qf, kt, scale, start, end)
+            w, _ = ca_weights(s.reshape(B * H, end - start, end), start)
+            out[:, :, start:end] = torch.matmul(w.reshape(B, H, end - start, end), vf[:, :, :end])
+    return out
+
+
+def tiled_backward(q, k, v, log_gain, dout, query_tile):
+    """fp32 (dq, dk, dv, dlog_gain) for any head dim, recomputing each tile."""
+    from .weights import ca_weights_backward
+    _check_device(q, k, v, log_gain, dout)
+    B, H, T, D = q.shape
+    qf, kf, vf, gf = _as_f32(q), _as_f32(k), _as_f32(v), _as_f32(dout)
+    scale = _head_scale(log_gain, H, D)
+    kt = kf.transpose(2, 3).contiguous()
+    vt = vf.transpose(2, 3).contiguous()
+    dq = torch.zeros_like(qf)
+    dk = torch.zeros_like(kf)
+    dv = torch.zeros_like(vf)
+    dg = torch.zeros((B, H), device=q.device, dtype=torch.float32)
+    with _Fp32Matmul():
+        for start in range(0, T, query_tile):
+            end = min(T, start + query_tile)
+            n = end - start
+            s = _tile_scores(qf, kt, scale, start, end)
+            gy = gf[:, :, start:end].contiguous()
+            gw = torch.matmul(gy, vt[:, :, :, :end].contiguous())            # dL/dW
+            w, ds = ca_weights_backward(s.reshape(B * H, n, end), gw.reshape(B * H, n, end), start,
+                                        return_weights=True)
+            w = w.reshape(B, H, n, end)
+            ds = ds.reshape(B, H, n, end)
+            dv[:, :, :end] += torch.matmul(w.transpose(2, 3).contiguous(), gy)
+            dsc = ds * scale                                                    # dL/d(q.k)
+            dq[:, :, start:end] = torch.matmul(dsc, kf[:, :, :end])
+            dk[:, :, :end] += torch.matmul(dsc.transpose(2, 3).contiguous(), qf[:, :, start:end].contiguous())
+            dg += (ds * s).sum(dim=(2, 3))                                      # d/dlog_gain: s is linear in e^g
+    return dq, dk, dv, dg.sum(0)
+
+
 class _CAExactTiled(torch.autograd.Function):
     """Autograd Function with the reference's contract (cuda/continuum_attention.py:650-766)."""
 
@@ -121,25 +203,37 @@ class _CAExactTiled(torch.autograd.Function):
         if int(query_tile) <= 0:
             raise ValueError("query_tile must be positive")
         _mode()
-        with torch.autocast(device_type="cuda", enabled=False):
-            out, stats = ca_forward(q, k, v, log_gain)
-        ctx.save_for_backward(q, k, v, log_gain, out, stats)
         ctx.query_tile = int(query_tile)
+        ctx.fused = q.shape[-1] in SUPPORTED_HEAD_DIMS
+        with torch.autocast(device_type="cuda", enabled=False):
+            if ctx.fused:
+                out, stats = ca_forward(q, k, v, log_gain)
+                ctx.save_for_backward(q, k, v, log_gain, out, stats)
+            else:
+                out = tiled_forward(q, k, v, log_gain, ctx.query_tile)
+                ctx.save_for_backward(q, k, v, log_gain)
         return out.to(v.dtype)
 
     @staticmethod
     def backward(ctx, grad_y):
         if torch.is_grad_enabled():
             raise RuntimeError("CA Volta analytic kernel supports first-order gradients only")
-        q, k, v, log_gain, out, stats = ctx.saved_tensors
-        dq, dk, dv, dg = ca_backward(q, k, v, log_gain, out, stats, grad_y)
+        if ctx.fused:
+            q, k, v, log_gain, out, stats = ctx.saved_tensors
+            dq, dk, dv, dg = ca_backward(q, k, v, log_gain, out, stats, grad_y)
+        else:
+            q, k, v, log_gain = ctx.saved_tensors
+            with torch.autocast(device_type="cuda", enabled=False):
+                dq, dk, dv, dg = tiled_backward(q, k, v, log_gain, grad_y, ctx.query_tile)
         return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg.to(log_gain.dtype), None)
 
 
 def continuum_attention(q, k, v, log_gain, query_tile=64):
     """Exact causal Continuum Attention (cuda/continuum_attention.py:768-783).
 
-    q, k, v: ``[B, H, T, D]`` (same dtype, D in {8, 16, 32, 64}), log_gain: ``[H]``.
+    q, k, v: ``[B, H, T, D]`` (same dtype), log_gain: ``[H]``.  D in {8, 16,
+    32, 64} runs the fused kernels; any other D the query-tile structure over
+    the HIP weight kernels (``query_tile`` rows at a time).
     Scores are ``exp(log_gain[h]) / sqrt(D) * q.k``; keys and values are
     linearly interpolated between adjacent positions with half-token end caps
     and integrated exactly.  Returns ``[B, H, T, D]`` in ``v.dtype``.

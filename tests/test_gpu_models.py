@@ -184,12 +184,14 @@ class _OracleCA(torch.autograd.Function):
         return torch.from_numpy(y)
 
 
-def test_decoder_logits_vs_float64_oracle_model(gpu_ca, monkeypatch):
+@pytest.mark.parametrize("d_model", [128, 256])
+def test_decoder_logits_vs_float64_oracle_model(gpu_ca, monkeypatch, d_model):
     """Small CA-S decoder: fp32 GPU logits against a float64 CPU copy of the
-    same model whose attention is the oracle."""
-    say("[case] decoder logits vs float64 oracle model")
+    same model whose attention is the oracle (head dims 64: fused kernels,
+    128: the query-tile path)."""
+    say(f"[case] decoder logits vs float64 oracle model, d_model {d_model}")
     Dm = gpu_ca.decoder
-    cfg = Dm.ContinuumDecoderConfig(d_model=128, n_heads=2, n_layers=2, block_size=96)
+    cfg = Dm.ContinuumDecoderConfig(d_model=d_model, n_heads=2, n_layers=2, block_size=96)
     torch.manual_seed(4)
     m = Dm.ContinuumDecoderLM(cfg)
     with torch.no_grad():
