@@ -108,15 +108,16 @@ def _timed_steps(ca, step, steps, warmup):
 
 def bench_ca_s(ca, dev, steps=10, warmup=3):
     """one CA-S decoder training step (101,205,120 params,
-    T=2048, batch 1, bf16 autocast with fp32 CA scores, AdamW + clip 1.0) on
-    uniform-random bytes, random-init weights."""
+    T=2048, batch 1, bf16 autocast with fp32 CA scores, AdamW + clip 1.0 as
+    the library's fused HIP optimizer) on uniform-random bytes, random-init
+    weights."""
     import torch
     Dm = ca.decoder
     torch.manual_seed(0)
     cfg = Dm.ContinuumDecoderConfig()
     model = Dm.ContinuumDecoderLM(cfg).to(dev)
     nparams = Dm.count_parameters(model)["total"]
-    opt = Dm.build_adamw(model)
+    opt = Dm.build_fused_adamw(model)
     g = torch.Generator().manual_seed(1)
     batches = [torch.randint(0, 256, (1, cfg.block_size), generator=g).to(dev) for _ in range(4)]
     ms, ca_ms, loss = _timed_steps(ca, lambda i: Dm.train_step(model, opt, batches[i % 4]), steps,
@@ -128,7 +129,8 @@ def bench_ca_s(ca, dev, steps=10, warmup=3):
            "dtype": "bf16 autocast, f32 CA scores", "data": "synthetic uniform bytes",
            "config": {"workload": "CA-S decoder train step (BASELINE config 4)", "d_model": cfg.d_model,
                       "n_layers": cfg.n_layers, "n_heads": cfg.n_heads, "T": cfg.block_size,
-                      "batch": 1, "optimizer": "AdamW lr 3e-4 wd 0.1 betas (.9,.95), clip 1.0"}}
+                      "batch": 1, "optimizer": "AdamW lr 3e-4 wd 0.1 betas (.9,.95), clip 1.0 "
+                                               "(HIP clip + AdamW, bf16 shadows of the Linear weights)"}}
     del model, opt
     torch.cuda.empty_cache()
     return res

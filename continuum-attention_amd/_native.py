@@ -48,6 +48,11 @@ SIGNATURES = {
     "ca_add_rmsnorm_fwd": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _i, _i, ctypes.c_float, _vp]),
     "ca_add_rmsnorm_bwd": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _sz, _i, _i,
                                 _vp]),
+    "ca_opt_chunk_elems": (_i, []),
+    "ca_grad_clip_coef": (_i, [_vp, _i, _vp, _i, _vp, ctypes.c_float, _vp, _vp, _vp]),
+    "ca_adamw_step": (_i, [_vp, _i, _vp, _i, _vp, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+                           ctypes.c_float, ctypes.c_float, _i, _vp]),
+    "ca_bf16_shadow": (_i, [_vp, _i, _vp, _i, _vp]),
     "ca_timing_enable": (_i, [_i]),
     "ca_timing_read": (_i, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i), _i]),
 }

@@ -6,6 +6,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cmath>
 #include <atomic>
 #include <vector>
 
@@ -456,6 +457,65 @@ int ca_add_rmsnorm_bwd(const void* dy, int dydtype, const float* dsum, const flo
                                         dweight, static_cast<float*>(workspace), N, C, s);
   ca::timer_end(ca::kRmsBwd, s);
   if (e != hipSuccess) return fail(CA_ERR_HIP, "ca_add_rmsnorm_bwd launch: %s", hipGetErrorString(e));
+  return CA_OK;
+}
+
+int ca_opt_chunk_elems(void) { return ca::kOptChunk; }
+
+static int check_opt(const char* fn, const ca_opt_tensor* tensors, int ntensors, const int* chunks,
+                     int nchunks) {
+  if (!tensors || !chunks) return fail(CA_ERR_INVALID, "%s: null tensor or chunk table", fn);
+  if (ntensors <= 0 || nchunks <= 0) return fail(CA_ERR_INVALID, "%s: empty tensor or chunk table", fn);
+  if ((reinterpret_cast<uintptr_t>(tensors) & 7) || (reinterpret_cast<uintptr_t>(chunks) & 7))
+    return fail(CA_ERR_INVALID, "%s: tables must be 8-byte aligned", fn);
+  return CA_OK;
+}
+
+int ca_grad_clip_coef(const ca_opt_tensor* tensors, int ntensors, const int* chunks, int nchunks,
+                      float* partial, float max_norm, float* total_norm, float* coef,
+                      void* stream) {
+  int rc = check_opt("ca_grad_clip_coef", tensors, ntensors, chunks, nchunks);
+  if (rc) return rc;
+  if (!partial || !total_norm || !coef) return fail(CA_ERR_INVALID, "ca_grad_clip_coef: null pointer");
+  hipError_t e = ca::launch_grad_sumsq(tensors, ntensors, reinterpret_cast<const int2*>(chunks), nchunks,
+                                       partial, max_norm, total_norm, coef,
+                                       reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(CA_ERR_HIP, "ca_grad_clip_coef launch: %s", hipGetErrorString(e));
+  return CA_OK;
+}
+
+int ca_adamw_step(const ca_opt_tensor* tensors, int ntensors, const int* chunks, int nchunks,
+                  const float* coef, float lr, float beta1, float beta2, float eps,
+                  float weight_decay, int step, void* stream) {
+  int rc = check_opt("ca_adamw_step", tensors, ntensors, chunks, nchunks);
+  if (rc) return rc;
+  if (step < 1) return fail(CA_ERR_INVALID, "ca_adamw_step: step must be >= 1, got %d", step);
+  if (!(beta1 >= 0.f && beta1 < 1.f && beta2 >= 0.f && beta2 < 1.f))
+    return fail(CA_ERR_INVALID, "ca_adamw_step: betas must be in [0, 1)");
+  // bias corrections in double, as torch's AdamW computes them on the host
+  const double bc1 = 1.0 - std::pow((double)beta1, (double)step);
+  const double bc2 = 1.0 - std::pow((double)beta2, (double)step);
+  ca::CaAdamwScalars k;
+  k.decay = (float)(1.0 - (double)lr * (double)weight_decay);
+  k.one_minus_beta1 = (float)(1.0 - (double)beta1);
+  k.beta2 = beta2;
+  k.one_minus_beta2 = (float)(1.0 - (double)beta2);
+  k.bc2_sqrt = (float)std::sqrt(bc2);
+  k.eps = eps;
+  k.neg_step_size = (float)(-(double)lr / bc1);
+  hipError_t e = ca::launch_adamw(tensors, ntensors, reinterpret_cast<const int2*>(chunks), nchunks,
+                                  coef, k, reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(CA_ERR_HIP, "ca_adamw_step launch: %s", hipGetErrorString(e));
+  return CA_OK;
+}
+
+int ca_bf16_shadow(const ca_opt_tensor* tensors, int ntensors, const int* chunks, int nchunks,
+                   void* stream) {
+  int rc = check_opt("ca_bf16_shadow", tensors, ntensors, chunks, nchunks);
+  if (rc) return rc;
+  hipError_t e = ca::launch_shadow(tensors, ntensors, reinterpret_cast<const int2*>(chunks), nchunks,
+                                   reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(CA_ERR_HIP, "ca_bf16_shadow launch: %s", hipGetErrorString(e));
   return CA_OK;
 }
 

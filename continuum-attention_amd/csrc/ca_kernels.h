@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 
+#include "../../include/continuum_attention_amd.h"
+
 namespace ca {
 
 // Forward work decomposition: 128-query groups, 32-key weight tiles, splits of
@@ -194,6 +196,26 @@ hipError_t launch_rmsnorm_fwd(const float* x, const void* res, int rdtype, float
 hipError_t launch_rmsnorm_bwd(const void* dy, int dydtype, const float* dsum, const float* x,
                               const float* w, const float* rstd, float* dx, void* dres, int rdtype,
                               float* dw, float* dw_part, int N, int C, hipStream_t s);
+
+// AdamW step (ca_optim.hip): chunks of kOptChunk elements.
+constexpr int kOptChunk = 16384;
+using CaOptTensor = ca_opt_tensor;
+struct CaAdamwScalars {
+  float decay;            // 1 - lr * weight_decay
+  float one_minus_beta1;
+  float beta2;
+  float one_minus_beta2;
+  float bc2_sqrt;         // sqrt(1 - beta2^step)
+  float eps;
+  float neg_step_size;    // -lr / (1 - beta1^step)
+};
+hipError_t launch_grad_sumsq(const CaOptTensor* tensors, int ntensors, const int2* chunks,
+                             int nchunks, float* partial, float max_norm, float* total_norm,
+                             float* coef, hipStream_t s);
+hipError_t launch_adamw(const CaOptTensor* tensors, int ntensors, const int2* chunks, int nchunks,
+                        const float* coef, const CaAdamwScalars& k, hipStream_t s);
+hipError_t launch_shadow(const CaOptTensor* tensors, int ntensors, const int2* chunks, int nchunks,
+                         hipStream_t s);
 
 // Weight-materialising row kernels (ca_weights.hip).
 hipError_t launch_weights(const float* scores, float* weights, float* stats, int BH, int Q, int K,

@@ -468,17 +468,31 @@ def build_adamw(model, lr=3e-4, weight_decay=0.1, betas=(0.9, 0.95)):
         return torch.optim.AdamW(params, lr=lr, weight_decay=weight_decay, betas=betas)
 
 
+def build_fused_adamw(model, lr=3e-4, weight_decay=0.1, betas=(0.9, 0.95)):
+    """build_adamw's optimizer as the library's HIP AdamW (optim.FusedAdamW):
+    the same update over the same parameters, with bf16 shadows of every
+    nn.Linear weight so bf16 autocast runs no weight casts."""
+    from .optim import FusedAdamW
+    linears = [m for m in model.modules() if isinstance(m, nn.Linear)]
+    return FusedAdamW(model.parameters(), lr=lr, betas=betas, weight_decay=weight_decay,
+                      shadow_modules=linears)
+
+
 def train_step(model, optimizer, batch, amp_dtype=torch.bfloat16, grad_clip=1.0):
     """One optimisation step on a ``[B, T]`` byte batch (next-byte targets from
     the batch itself, as cuda/continuum_attention.py:1205-1228): autocast
     forward + loss, backward, clip to ``grad_clip``, AdamW.  Returns the loss
     tensor (no host synchronisation)."""
+    from .optim import FusedAdamW
     optimizer.zero_grad(set_to_none=True)
     amp = (torch.autocast(device_type="cuda", dtype=amp_dtype) if amp_dtype is not None
            else contextlib.nullcontext())
     with amp:
         loss = model(batch, targets=batch)["loss"]
     loss.backward()
+    if isinstance(optimizer, FusedAdamW):
+        optimizer.step(max_norm=grad_clip or 0.0)
+        return loss.detach()
     if grad_clip and grad_clip > 0:
         if _fused_on_gpu(optimizer):
             # clip_grad_norm_'s scaling g * max_norm / (norm + 1e-6) (applied

@@ -154,6 +154,43 @@ int ca_add_rmsnorm_bwd(const void* dy, int dydtype, const float* dsum, const flo
                        float* dweight, void* workspace, size_t workspace_bytes, int N, int C,
                        void* stream);
 
+/* ---- AdamW step of the decoder's training loop ------------------------------
+ * torch.optim.AdamW as the reference builds it (cuda/runtime.py:87-88) after
+ * torch.nn.utils.clip_grad_norm_ (cuda/continuum_attention.py:1205-1228),
+ * over a list of tensors described in device memory.  A tensor's gradient is
+ * fp32 or bf16 (CA_DTYPE_*); `shadow`, when not NULL, is a bf16 copy of the
+ * parameter that the step refreshes (round to nearest even: the value bf16
+ * autocast would cast the weight to).  Every pointer is 16-byte aligned.
+ * Work is split into chunks of ca_opt_chunk_elems() elements; `chunks` holds
+ * nchunks pairs (tensor index, chunk index within the tensor), covering every
+ * tensor exactly once.  No counterpart in the reference's native code (it
+ * runs torch's optimizer kernels). */
+typedef struct {
+  float* param;
+  const void* grad;
+  float* exp_avg;
+  float* exp_avg_sq;
+  unsigned short* shadow;
+  long long numel;
+  int grad_dtype;
+  int reserved;
+} ca_opt_tensor;
+int ca_opt_chunk_elems(void);
+/* Sum of squares of every gradient (partial: nchunks floats of workspace),
+ * then, on the device, total_norm = sqrt(sum) and
+ * coef = min(1, max_norm / (total_norm + 1e-6)) (1 when max_norm <= 0). */
+int ca_grad_clip_coef(const ca_opt_tensor* tensors, int ntensors, const int* chunks, int nchunks,
+                      float* partial, float max_norm, float* total_norm, float* coef,
+                      void* stream);
+/* One AdamW step (step >= 1: the bias corrections' exponent) with every
+ * gradient multiplied by *coef (coef NULL: 1). */
+int ca_adamw_step(const ca_opt_tensor* tensors, int ntensors, const int* chunks, int nchunks,
+                  const float* coef, float lr, float beta1, float beta2, float eps,
+                  float weight_decay, int step, void* stream);
+/* shadow = bf16(param) for every tensor that has a shadow. */
+int ca_bf16_shadow(const ca_opt_tensor* tensors, int ntensors, const int* chunks, int nchunks,
+                   void* stream);
+
 /* ---- Diagnostics (no counterpart in the reference; used by bench.py) -------
  * Per-kernel timing with HIP events recorded on the launch stream around each
  * kernel launch of the calls above.  Kernel ids: 0 forward, 1 forward split

@@ -112,3 +112,28 @@ def test_weights_argument_errors_before_any_launch(ca, BH, Q, K, start):
     assert lib.ca_weights_bwd_f32(p, p, p, p, BH, Q, K, start, None) == 1
     assert lib.ca_weights_f32(None, p, p, 1, 4, 8, 0, None) == 1
     assert lib.ca_weights_bwd_f32(p, None, p, p, 1, 4, 8, 0, None) == 1
+
+
+def test_opt_tensor_layout_matches_header(tmp_path):
+    """The ctypes mirror of ca_opt_tensor (optim._OptTensor) has the C
+    header's size and field offsets (compiled with gcc from the header)."""
+    import ctypes
+    import importlib
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    src = tmp_path / "layout.c"
+    fields = ["param", "grad", "exp_avg", "exp_avg_sq", "shadow", "numel", "grad_dtype", "reserved"]
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "continuum_attention_amd.h"\n'
+                   'int main(void) { printf("%zu", sizeof(ca_opt_tensor));'
+                   + "".join(f' printf(" %zu", offsetof(ca_opt_tensor, {f}));' for f in fields)
+                   + ' return 0; }\n')
+    exe = tmp_path / "layout"
+    subprocess.run([gcc, "-I", os.path.join(root, "include"), str(src), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    opt = importlib.import_module("continuum-attention_amd.optim")
+    want = [ctypes.sizeof(opt._OptTensor)] + [getattr(opt._OptTensor, f).offset for f in fields]
+    assert got == want

@@ -12,6 +12,7 @@
   (test_acma.py:140-146); one CA-S decoder training step and decoder logits
   against a float64 CPU model whose attention is the oracle.
 """
+import contextlib
 import sys
 
 import numpy as np
@@ -435,3 +436,101 @@ def test_decoder_fused_prologue_matches_composition(gpu_ca):
     assert abs(outs[True][0] - outs[False][0]) <= 1e-5 * abs(outs[False][0])
     for n, gref in outs[False][1].items():
         assert rel(outs[True][1][n].cpu().numpy(), gref.cpu().numpy()) <= 1e-3, n
+
+
+def _torch_reference_step(m, opt, ids, clip, amp):
+    opt.zero_grad(set_to_none=True)
+    ctx = torch.autocast(device_type="cuda", dtype=torch.bfloat16) if amp else contextlib.nullcontext()
+    with ctx:
+        loss = m(ids, targets=ids)["loss"]
+    loss.backward()
+    grads = [p.grad.detach().clone() for p in m.parameters()]
+    torch.nn.utils.clip_grad_norm_(m.parameters(), clip)
+    opt.step()
+    return loss.item(), grads
+
+
+@pytest.mark.parametrize("amp,clip", [(True, 0.05), (True, 1e9), (False, 0.05)])
+def test_fused_adamw_matches_torch(gpu_ca, amp, clip):
+    """optim.FusedAdamW (HIP clip + AdamW, bf16 shadows of the Linear
+    weights) against torch's clip_grad_norm_ + AdamW (cuda/runtime.py:87-88,
+    cuda/continuum_attention.py:1205-1228) on one decoder step from equal
+    parameters: the same loss, the gradients the step uses equal to torch's
+    (the bf16 shadow gradients are the values autocast upcasts), first and
+    second moments and parameters within fp32 rounding, and every shadow
+    equal to its new weight rounded to bf16."""
+    say(f"[case] FusedAdamW vs torch, autocast {amp}, clip {clip}")
+    Dm = gpu_ca.decoder
+    cfg = Dm.ContinuumDecoderConfig(d_model=128, n_heads=2, n_layers=2, block_size=64)
+    torch.manual_seed(5)
+    ma = Dm.ContinuumDecoderLM(cfg).cuda()
+    mb = Dm.ContinuumDecoderLM(cfg).cuda()
+    mb.load_state_dict(ma.state_dict())
+    oa = Dm.build_fused_adamw(ma)
+    ob = torch.optim.AdamW(mb.parameters(), lr=3e-4, weight_decay=0.1, betas=(0.9, 0.95))
+    ids = torch.randint(0, 256, (2, 64), device="cuda")
+    loss_a = Dm.train_step(ma, oa, ids, amp_dtype=torch.bfloat16 if amp else None, grad_clip=clip).item()
+    loss_b, grads_b = _torch_reference_step(mb, ob, ids, clip, amp)
+    assert loss_a == loss_b
+    for ga, gb in zip(oa.grads(), grads_b):
+        assert torch.equal(ga.float(), gb)
+    worst = {}
+    for pa, pb in zip(ma.parameters(), mb.parameters()):
+        sa, sb = oa.state[pa], ob.state[pb]
+        for key, a, b in (("exp_avg", sa["exp_avg"], sb["exp_avg"]),
+                          ("exp_avg_sq", sa["exp_avg_sq"], sb["exp_avg_sq"]), ("param", pa, pb)):
+            e = ((a - b).abs().max() / b.abs().max().clamp_min(1e-30)).item()
+            worst[key] = max(worst.get(key, 0.0), e)
+    say("   " + " ".join(f"{k} {v:.1e}" for k, v in worst.items()))
+    assert worst["exp_avg"] <= 1e-5 and worst["exp_avg_sq"] <= 1e-5 and worst["param"] <= 1e-6
+    for mod in ma.modules():
+        sh = getattr(mod, "_ca_shadow", None)
+        if sh is not None:
+            assert torch.equal(sh, mod.weight.detach().to(torch.bfloat16))
+
+
+def test_fused_adamw_shadow_refresh_and_groups(gpu_ca):
+    """A weight changed outside the optimizer (load_state_dict) is recopied
+    to its shadow before the next bf16 forward; two parameter groups (gains
+    at 8x lr without decay, as TinyLM's build_adamw) share one clip norm and
+    match torch; an LR scheduler drives the fused optimizer."""
+    say("[case] FusedAdamW shadow refresh, groups, scheduler")
+    Dm = gpu_ca.decoder
+    from importlib import import_module
+    Opt = import_module("continuum-attention_amd.optim")
+    cfg = Dm.ContinuumDecoderConfig(d_model=128, n_heads=2, n_layers=2, block_size=64)
+    torch.manual_seed(8)
+    ma = Dm.ContinuumDecoderLM(cfg).cuda()
+    mb = Dm.ContinuumDecoderLM(cfg).cuda()
+    mb.load_state_dict(ma.state_dict())
+
+    def groups(m):
+        gains = [p for n, p in m.named_parameters() if "log_qk_gain" in n]
+        rest = [p for n, p in m.named_parameters() if "log_qk_gain" not in n]
+        return [{"params": rest}, {"params": gains, "lr": 2.4e-3, "weight_decay": 0.0}]
+
+    oa = Opt.FusedAdamW(groups(ma), lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1,
+                        shadow_modules=[m for m in ma.modules() if isinstance(m, torch.nn.Linear)])
+    ob = torch.optim.AdamW(groups(mb), lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1)
+    sched = torch.optim.lr_scheduler.StepLR(oa, step_size=1, gamma=0.5)
+    ids = torch.randint(0, 256, (2, 64), device="cuda")
+    Dm.train_step(ma, oa, ids, grad_clip=0.05)
+    _torch_reference_step(mb, ob, ids, 0.05, True)
+    sched.step()
+    assert abs(oa.param_groups[0]["lr"] - 1.5e-4) < 1e-12
+    for pa, pb in zip(ma.parameters(), mb.parameters()):
+        e = ((oa.state[pa]["exp_avg"] - ob.state[pb]["exp_avg"]).abs().max()
+             / ob.state[pb]["exp_avg"].abs().max().clamp_min(1e-30)).item()
+        assert e <= 1e-5
+        assert ((pa - pb).abs().max() / pb.abs().max()).item() <= 1e-6
+    # weights replaced from outside: the next bf16 forward recopies the shadows
+    fresh = Dm.ContinuumDecoderLM(cfg).cuda()
+    ma.load_state_dict(fresh.state_dict())
+    with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+        la = ma(ids, targets=ids)["loss"].item()
+        lb = fresh(ids, targets=ids)["loss"].item()
+    assert la == lb
+    for mod in ma.modules():
+        sh = getattr(mod, "_ca_shadow", None)
+        if sh is not None:
+            assert torch.equal(sh, mod.weight.detach().to(torch.bfloat16))
