@@ -33,6 +33,7 @@ import torch
 from torch import nn
 from torch.nn import functional as F
 
+from .decoder import RMSNorm as _DecoderRMSNorm
 from .ops import continuum_attention
 from .weights import continuous_attention_weights
 
@@ -43,15 +44,16 @@ _BACKEND_MAP = {"hip": "hip", "hip_weights": "hip_weights", "reference": "hip_we
                 "metal_direct": "hip"}
 
 
-class RMSNorm(nn.Module):
-    """x / rms(x) * weight, eps 1e-5 (architecture.py:21-29)."""
+class RMSNorm(_DecoderRMSNorm):
+    """x / rms(x) * weight, eps 1e-5 (architecture.py:21-29).  On fp32 GPU
+    inputs one HIP pass each way (the decoder's fused RMSNorm kernels, also
+    for the residual add that feeds it); otherwise, or with
+    ``RMSNorm.fused = False``, the reference's composition."""
 
     def __init__(self, width, eps=1e-5):
-        super().__init__()
-        self.weight = nn.Parameter(torch.ones(width))
-        self.eps = eps
+        super().__init__(width, eps)
 
-    def forward(self, x):
+    def _composition(self, x):
         return x * torch.rsqrt(x.square().mean(dim=-1, keepdim=True) + self.eps) * self.weight
 
 
@@ -179,8 +181,18 @@ class TinyLM(nn.Module):
             raise ValueError("Sequence exceeds model seq_len")
         pos = torch.arange(length, device=tokens.device)
         x = self.tok_embed(tokens) + self.pos_embed(pos)[None, :, :]
-        for i in range(self.layers):
-            x = getattr(self, f"b{i}")(x)
+        blocks = [getattr(self, f"b{i}") for i in range(self.layers)]
+        if self.final_norm._fusable(x):
+            # the blocks' chain x = x + attn(norm_attn(x)); x = x + mlp(norm_mlp(x)),
+            # with every residual add fused into the norm that reads its sum
+            h = blocks[0].norm_attn(x)
+            for n, block in enumerate(blocks):
+                x, h = block.norm_mlp.add_and_norm(x, block.attn(h))
+                nxt = blocks[n + 1].norm_attn if n + 1 < len(blocks) else self.final_norm
+                x, h = nxt.add_and_norm(x, block.mlp(h))
+            return self.lm_head(h)
+        for block in blocks:
+            x = block(x)
         return self.lm_head(self.final_norm(x))
 
 
@@ -205,13 +217,29 @@ def build_adamw(model, lr=4e-4, weight_decay=0.1, geometry_lr_mult=8.0):
         return torch.optim.AdamW(groups, betas=(0.9, 0.95))
 
 
+def build_fused_adamw(model, lr=4e-4, weight_decay=0.1, geometry_lr_mult=8.0):
+    """build_adamw's groups and hyper-parameters as the library's HIP AdamW
+    (optim.FusedAdamW; TinyLM trains in fp32, so no bf16 weight shadows)."""
+    from .optim import FusedAdamW
+    gains = [p for n, p in model.named_parameters() if n.endswith("log_qk_gain")]
+    dense = [p for n, p in model.named_parameters() if not n.endswith("log_qk_gain")]
+    groups = [{"params": dense, "lr": lr, "weight_decay": weight_decay}]
+    if gains:
+        groups.append({"params": gains, "lr": lr * geometry_lr_mult, "weight_decay": 0.0})
+    return FusedAdamW(groups, lr=lr, betas=(0.9, 0.95), weight_decay=weight_decay)
+
+
 def train_step(model, optimizer, x, target, grad_clip=1.0):
     """One TinyLM step (benchmark.py:207-214): cross-entropy of the byte
     logits, backward, clip to ``grad_clip``, AdamW.  Returns the loss tensor."""
+    from .optim import FusedAdamW
     logits = model(x)
     loss = F.cross_entropy(logits.reshape(-1, 256), target.reshape(-1))
     optimizer.zero_grad(set_to_none=True)
     loss.backward()
+    if isinstance(optimizer, FusedAdamW):
+        optimizer.step(max_norm=grad_clip or 0.0)
+        return loss.detach()
     torch.nn.utils.clip_grad_norm_(model.parameters(), grad_clip)
     optimizer.step()
     return loss.detach()

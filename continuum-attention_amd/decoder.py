@@ -187,10 +187,13 @@ class RMSNorm(nn.Module):
                 return ad
         return torch.float32
 
+    def _composition(self, x):
+        return self.weight * x * torch.rsqrt(x.square().mean(-1, keepdim=True) + self.eps)
+
     def forward(self, x):
         if self._fusable(x):
             return _RMSNormFn.apply(x, self.weight, self.eps, self._out_dtype())
-        return self.weight * x * torch.rsqrt(x.square().mean(-1, keepdim=True) + self.eps)
+        return self._composition(x)
 
     def add_and_norm(self, x, res):
         """(x + res, self(x + res)): the residual add of a decoder block and

@@ -534,3 +534,44 @@ def test_fused_adamw_shadow_refresh_and_groups(gpu_ca):
         sh = getattr(mod, "_ca_shadow", None)
         if sh is not None:
             assert torch.equal(sh, mod.weight.detach().to(torch.bfloat16))
+
+
+def test_tinylm_fused_norms_and_adamw(gpu_ca):
+    """TinyLM (CA-P family) with its RMSNorms and residual adds fused (one
+    HIP pass each) against the reference's composition: logits and every
+    parameter gradient; then one step of the HIP AdamW (TinyLM's groups:
+    gains at 8x lr without decay) against torch's clip_grad_norm_ + AdamW
+    (benchmark.py:189-214)."""
+    say("[case] TinyLM fused norms + HIP AdamW")
+    A = gpu_ca.architecture
+    Dm = gpu_ca.decoder
+    torch.manual_seed(12)
+    m = A.TinyLM(variant="H", backend="hip", seq_len=128, layers=2).cuda()
+    x = torch.randint(0, 256, (2, 128), device="cuda")
+    outs = {}
+    for fused in (True, False):
+        Dm.RMSNorm.fused = fused
+        try:
+            m.zero_grad(set_to_none=True)
+            logits = m(x)
+            torch.nn.functional.cross_entropy(logits.reshape(-1, 256), x.reshape(-1)).backward()
+            outs[fused] = (logits.detach().clone(), [p.grad.detach().clone() for p in m.parameters()])
+        finally:
+            Dm.RMSNorm.fused = True
+    el = rel(outs[True][0].cpu().numpy(), outs[False][0].cpu().numpy())
+    eg = max(rel(a.cpu().numpy(), b.cpu().numpy()) for a, b in zip(outs[True][1], outs[False][1]))
+    say(f"   logits {el:.2e} grads {eg:.2e}")
+    assert el <= 1e-5 and eg <= 1e-4
+    ma = A.TinyLM(variant="H", backend="hip", seq_len=128, layers=2).cuda()
+    mb = A.TinyLM(variant="H", backend="hip", seq_len=128, layers=2).cuda()
+    mb.load_state_dict(ma.state_dict())
+    oa, ob = A.build_fused_adamw(ma), A.build_adamw(mb)
+    la = A.train_step(ma, oa, x, x, grad_clip=0.05).item()
+    Dm.RMSNorm.fused = True
+    lb = A.train_step(mb, ob, x, x, grad_clip=0.05).item()
+    assert la == lb
+    for pa, pb in zip(ma.parameters(), mb.parameters()):
+        e = ((oa.state[pa]["exp_avg"] - ob.state[pb]["exp_avg"]).abs().max()
+             / ob.state[pb]["exp_avg"].abs().max().clamp_min(1e-30)).item()
+        assert e <= 1e-5
+        assert ((pa - pb).abs().max() / pb.abs().max()).item() <= 1e-6
