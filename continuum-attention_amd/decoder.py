@@ -515,6 +515,65 @@ def train_step(model, optimizer, batch, amp_dtype=torch.bfloat16, grad_clip=1.0)
     return loss.detach()
 
 
+class GraphedTrainStep:
+    """train_step with the forward and backward captured once as a HIP graph
+    and replayed each step (the optimizer step runs eagerly after the replay:
+    optim.FusedAdamW's clip + update, or clip_grad_norm_ + a torch optimizer).
+
+    The decoder step launches a few hundred kernels, many of a few
+    microseconds; replaying them as one graph removes the per-launch host
+    work between them.  ``batch`` fixes the input shape; each call copies its
+    batch into the captured input.  Forward and backward are warmed up (twice,
+    on a side stream, without an optimizer step: parameters are unchanged)
+    before capture, as graph capture requires.  While the object is used the
+    gradients are the captured graph's buffers: they are overwritten by each
+    replay and must not be set to None (do not call ``zero_grad``).  A
+    replay uses the parameters and the bf16 shadows as they are in memory,
+    so in-place changes to them between steps are seen; hyper-parameters of
+    the eager optimizer step can change freely."""
+
+    def __init__(self, model, optimizer, batch, amp_dtype=torch.bfloat16, grad_clip=1.0, warmup=2):
+        from .optim import FusedAdamW
+        self.model, self.optimizer = model, optimizer
+        self.amp_dtype, self.grad_clip = amp_dtype, grad_clip
+        self.fused = isinstance(optimizer, FusedAdamW)
+        self.static_batch = batch.detach().clone()
+        dev = batch.device
+        _native.timing_enable(False)
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            for _ in range(warmup):
+                optimizer.zero_grad(set_to_none=True)
+                self._forward_backward()
+        torch.cuda.current_stream(dev).wait_stream(side)
+        optimizer.zero_grad(set_to_none=True)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.static_loss = self._forward_backward()
+
+    def _forward_backward(self):
+        amp = (torch.autocast(device_type="cuda", dtype=self.amp_dtype, cache_enabled=False)
+               if self.amp_dtype is not None else contextlib.nullcontext())
+        with amp:
+            loss = self.model(self.static_batch, targets=self.static_batch)["loss"]
+        loss.backward()
+        return loss.detach()
+
+    def __call__(self, batch):
+        """One training step on ``batch``; returns the loss (a device tensor
+        that the next call overwrites)."""
+        self.static_batch.copy_(batch)
+        self.graph.replay()
+        if self.fused:
+            self.optimizer.step(max_norm=self.grad_clip or 0.0)
+        else:
+            if self.grad_clip and self.grad_clip > 0:
+                torch.nn.utils.clip_grad_norm_(self.model.parameters(), self.grad_clip)
+            self.optimizer.step()
+        return self.static_loss
+
+
 def _fused_on_gpu(optimizer):
     """A fused torch AdamW/Adam whose parameters are all on the GPU (its
     kernel divides every gradient by ``optimizer.grad_scale`` when set)."""
