@@ -93,6 +93,9 @@ class FusedAdamW(torch.optim.Optimizer):
             mod._ca_shadow_version = w._version
             self.shadow[id(w)] = sh
         self._groups = []
+        devices = {p.device for group in self.param_groups for p in group["params"]}
+        if len(devices) != 1:
+            raise ValueError("FusedAdamW: all parameters must be on one GPU")
         for group in self.param_groups:
             tensors = list(group["params"])
             for p in tensors:
