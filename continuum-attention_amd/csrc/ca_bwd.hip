@@ -11,7 +11,7 @@
 //                   same row mean at cuda/continuum_attention.py:268-269),
 //                   Q_i and dY_i / Z_i split into bf16 limb planes, and
 //                   (m_i, Dl_i / Z_i).
-//   ca_bwd_dkdv     one work group per (slice, 56 keys); wave w owns 14 keys
+//   ca_bwd_dkdv     (ca_bwd_dkdv.hip) one work group per (slice, 56 keys); wave w owns 14 keys
 //                   (16 MFMA slots).  The 4 waves walk the query tiles
 //                   together: each 32-query tile of Q and dY/Z limbs is staged
 //                   once in LDS (double-buffered) and read by every wave both
@@ -22,7 +22,7 @@
 //                   products are bf16x6 on v_mfma_f32_16x16x32_bf16.  dS is
 //                   also spilled as 32x16 row blocks for the dQ pass.
 //   ca_bwd_dq       dQ = c dS (K - k_ref) over the spilled blocks, one work
-//                   item per (slice, 64 queries, chunk of key blocks); each
+//                   item per (slice, 128 queries, chunk of key blocks); each
 //                   item also forms its gain partial sum_i q_i . dQ_i
 //                   (= sum_ij dS_ij s_ij, since s_ij = c q_i . k_j).
 //   ca_bwd_gain_merge  dRho_h = sum of the gain partials; sums the dQ chunk
@@ -42,20 +42,6 @@
 
 namespace ca {
 
-template <int D>
-struct Bwd {
-  static constexpr int C4 = D / 4;             // float4 chunks per row
-  static constexpr int KB = (D + 31) / 32;     // 32-wide k blocks of S / dP'
-  static constexpr int NMB = (D + 15) / 16;    // 16-row d blocks of dV^T / dK^T
-  // bf16 row stride of a staged tile: 160-byte rows for D = 64 keep both the
-  // 16-row row-wise reads and the transposed reads free of bank conflicts
-  static constexpr int LDR = D + 16;
-  static constexpr int LIMB = 32 * LDR;        // bf16 per limb plane of a tile
-  static constexpr int TILE = 6 * LIMB;        // Q limbs h, m, l then dY/Z limbs h, m, l
-  static constexpr int RCH = D / 8;            // 16-byte chunks per row and plane
-  static constexpr int CHUNKS = 6 * 32 * RCH;  // chunks staged per tile
-  static constexpr int CPT = (CHUNKS + 255) / 256;
-};
 
 // One thread per (row, 8 elements): Dl = dY . y, then the Q and dY/Z limbs of
 // the 8 elements (one 16-byte store per plane) and, per row, (m, Dl/Z).
@@ -109,305 +95,6 @@ __global__ __launch_bounds__(256) void ca_bwd_prep_kernel(const float* __restric
   if (c == 0) {
     qstat[(size_t)row * 2 + 0] = m;
     qstat[(size_t)row * 2 + 1] = x * invz;
-  }
-}
-
-template <int D>
-__global__ __launch_bounds__(256, 2) void ca_bwd_dkdv_kernel(
-    const float* __restrict__ K, const float* __restrict__ V, const __bf16* __restrict__ limbs,
-    const float* __restrict__ qstat, const float* __restrict__ log_gain, float* __restrict__ dK,
-    float* __restrict__ dV, float* __restrict__ dsbuf, float* __restrict__ kv_part, int BH, int H,
-    int T, int chunk, int n_part) {
-  using P = Bwd<D>;
-  __shared__ __attribute__((aligned(16))) __bf16 tiles[2][P::TILE];
-  __shared__ f32x4 tstat[2][16];  // rows 2u, 2u+1: (m, Dl/Z, m, Dl/Z)
-
-  const int nqt = num_q_tiles(T);
-  const int nkb = bwd_num_key_blocks(T);
-  const int bh = blockIdx.x % BH;
-  const int item = blockIdx.x / BH;  // ascending: heaviest first
-  // item -> (key-block group, chunk of its query tiles)
-  int wg = item, ch = 0, nch = 1;
-  if (chunk < nqt) {
-    const int G = dkdv_num_groups(T);
-    wg = 0;
-    ch = item;
-    nch = dkdv_group_chunks(0, T, chunk);
-    while (ch >= nch && wg < G - 1) {
-      ch -= nch;
-      ++wg;
-      nch = dkdv_group_chunks(wg, T, chunk);
-    }
-  }
-  const int w0 = kDkdvKeys * wg;
-
-  const int tid = threadIdx.x;
-  const int wv = tid >> 6;
-  const int lane = tid & 63;
-  const int j = lane & 15;  // slot
-  const int g = lane >> 4;  // k group / row group
-  const int kb16 = kDkdvWaves * wg + wv;
-  const int key_j = kBwdKeys * kb16 - 1 + j;  // key of this lane's slot
-  const int kmin = kBwdKeys * kb16 - 1;        // key of slot 0
-
-  const size_t slice = (size_t)bh * T * D;
-  const float cl2 = head_scale_log2(log_gain, bh % H, D);
-
-  // Stale LDS bits must not reach an MFMA as NaN through padding columns.
-  {
-    unsigned* z = reinterpret_cast<unsigned*>(&tiles[0][0]);
-    for (int e = tid; e < 2 * P::TILE / 2; e += 256) z[e] = 0u;
-  }
-
-  // K (scaled by c log2e) and V of this lane's slot: B operands of S / dP',
-  // k block kb, element e = d 32kb + 8g + e.
-  Limbs kl[P::KB], vl[P::KB];
-#pragma unroll
-  for (int kb = 0; kb < P::KB; ++kb) {
-    float xk[8], xv[8];
-    const int d0 = 32 * kb + 8 * g;
-    const bool ok = key_j >= 0 && key_j < T && d0 < D;
-    const f32x4* kp = reinterpret_cast<const f32x4*>(K + slice + (size_t)(ok ? key_j : 0) * D + (ok ? d0 : 0));
-    const f32x4* vp = reinterpret_cast<const f32x4*>(V + slice + (size_t)(ok ? key_j : 0) * D + (ok ? d0 : 0));
-#pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2) {
-      const bool ok2 = ok && d0 + 4 * h2 < D;
-      const f32x4 a = ok2 ? kp[h2] * cl2 : f32x4{0.f, 0.f, 0.f, 0.f};
-      const f32x4 b = ok2 ? vp[h2] : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        xk[4 * h2 + e] = a[e];
-        xv[4 * h2 + e] = b[e];
-      }
-    }
-    kl[kb] = split8(xk);
-    vl[kb] = split8(xv);
-  }
-
-  f32x4 accv[P::NMB], acck[P::NMB];
-#pragma unroll
-  for (int mb = 0; mb < P::NMB; ++mb) {
-    accv[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    acck[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-
-  // ---- query-tile staging (all waves), one tile ahead ----
-  const size_t plane = (size_t)BH * T * D;
-  u32x4 pre[P::CPT];
-  f32x4 pre_st = {0.f, 0.f, 0.f, 0.f};
-  auto load_tile = [&](int qt) {
-#pragma unroll
-    for (int u = 0; u < P::CPT; ++u) {
-      const int e = tid + 256 * u;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (e < P::CHUNKS) {
-        const int pl = e / (32 * P::RCH), rem = e % (32 * P::RCH);
-        const int row = rem / P::RCH, ch = rem % P::RCH;
-        const int i = 32 * qt + row;
-        if (i < T)
-          v = *reinterpret_cast<const u32x4*>(limbs + (size_t)pl * plane + slice + (size_t)i * D + 8 * ch);
-      }
-      pre[u] = v;
-    }
-    if (tid < 16) {
-      const int i = 32 * qt + 2 * tid;
-      f32x4 v = {0.f, 0.f, 0.f, 0.f};
-      const float* sp = qstat + ((size_t)bh * T + (i < T ? i : 0)) * 2;
-      if (i + 1 < T) {
-        v = *reinterpret_cast<const f32x4*>(sp);
-      } else if (i < T) {
-        v[0] = sp[0];
-        v[1] = sp[1];
-      }
-      pre_st = v;
-    }
-  };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int u = 0; u < P::CPT; ++u) {
-      const int e = tid + 256 * u;
-      if (e < P::CHUNKS) {
-        const int pl = e / (32 * P::RCH), rem = e % (32 * P::RCH);
-        const int row = rem / P::RCH, ch = rem % P::RCH;
-        *reinterpret_cast<u32x4*>(&tiles[buf][pl * P::LIMB + row * P::LDR + 8 * ch]) = pre[u];
-      }
-    }
-    if (tid < 16) tstat[buf][tid] = pre_st;
-  };
-
-  // query tiles of this item: a chunk of qt0 .. nqt-1, where qt0 is the first
-  // tile that sees an owned key of the work group
-  const int ntl = dkdv_group_tiles(wg, T);
-  const int clen = (ntl + nch - 1) / nch;
-  const int qt0 = w0 / 32 + ch * clen;
-  const int qt_end = min(qt0 + clen, nqt);
-  // dS block of (tile qt, this wave's block); advanced by ds_kb_count(qt) per tile
-  size_t ds_blk = (size_t)bh * ds_blocks_before(nqt) + ds_blocks_before(qt0) + kb16;
-  __syncthreads();          // LDS clear before the first store
-  if (qt0 < qt_end) {
-    load_tile(qt0);
-    store_tile(0);
-  }
-  __syncthreads();
-
-  for (int qt = qt0; qt < qt_end; ++qt) {
-    const int buf = (qt - qt0) & 1;
-    if (qt + 1 < qt_end) load_tile(qt + 1);
-    const int i0 = 32 * qt;
-    // the wave's block meets this tile (and exists)
-    const bool work = kb16 < nkb && kBwdKeys * kb16 <= i0 + 31;
-    if (work) {
-      const __bf16* Tq = &tiles[buf][0];
-      const __bf16* Ty = &tiles[buf][3 * P::LIMB];
-
-      // ---- S - m and dP' - Dl/Z (row blocks rb: queries i0 + 16rb + 4g + r) ----
-      f32x4 sacc[2], pacc[2];
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        const f32x4 s01 = tstat[buf][8 * rb + 2 * g], s23 = tstat[buf][8 * rb + 2 * g + 1];
-        sacc[rb] = f32x4{-s01[0], -s01[2], -s23[0], -s23[2]};
-        pacc[rb] = f32x4{-s01[1], -s01[3], -s23[1], -s23[3]};
-      }
-#pragma unroll
-      for (int kb = 0; kb < P::KB; ++kb) {
-        const int col = 32 * kb + 8 * g;
-        Limbs qa[2], ya[2];
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
-          qa[rb] = ya[rb] = Limbs{bf16x8{}, bf16x8{}, bf16x8{}};
-          if (col < D) {
-            const int o = (16 * rb + j) * P::LDR + col;
-            qa[rb].h = *reinterpret_cast<const bf16x8*>(Tq + o);
-            qa[rb].m = *reinterpret_cast<const bf16x8*>(Tq + P::LIMB + o);
-            qa[rb].l = *reinterpret_cast<const bf16x8*>(Tq + 2 * P::LIMB + o);
-            ya[rb].h = *reinterpret_cast<const bf16x8*>(Ty + o);
-            ya[rb].m = *reinterpret_cast<const bf16x8*>(Ty + P::LIMB + o);
-            ya[rb].l = *reinterpret_cast<const bf16x8*>(Ty + 2 * P::LIMB + o);
-          }
-        }
-        // four independent accumulators per limb product
-#pragma unroll
-        for (int st = 0; st < 6; ++st) {
-          sacc[0] = mfma16_step(st, qa[0], kl[kb], sacc[0]);
-          pacc[0] = mfma16_step(st, ya[0], vl[kb], pacc[0]);
-          sacc[1] = mfma16_step(st, qa[1], kl[kb], sacc[1]);
-          pacc[1] = mfma16_step(st, ya[1], vl[kb], pacc[1]);
-        }
-      }
-
-      // ---- segments along the slots (adjacent lanes of each DPP row) ----
-      // Tiles where every slot key is visible to every query, with no key 0
-      // and no row past T, take the fast path; the cap of key i can then only
-      // fall on slot 15, which is not owned.
-      const bool need_mask = (kmin < 1) || (kmin + 15 > i0) || (i0 + 31 >= T);
-      float wout[2][4], dout_s[2][4];
-      auto segments = [&](auto general_tag) {
-        constexpr bool kGeneral = decltype(general_tag)::value;
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int i = i0 + 16 * rb + 4 * g + r;
-            const bool vis = !kGeneral || (key_j >= 0 && key_j <= i && i < T);
-            const float s = vis ? sacc[rb][r] : 0.f;   // s - m
-            const float gg = vis ? pacc[rb][r] : 0.f;  // g = dY.v/Z - Dl/Z
-            const float p = fast_exp2(s);
-            const float sl = row_shr1(s), pl = row_shr1(p), gl = row_shr1(gg);
-            float Lv, Rv, dLv, dRv;
-            seg_shares_grad(sl, s, pl, p, gl, gg, Lv, Rv, dLv, dRv);
-            // Segment (slot j-1, slot j), both keys visible.  Lane 0 has no
-            // left neighbour: its right shares land on slot 0, which is not
-            // owned, and its left shares are read by no lane (row_shl reads
-            // lane j+1), so only the general path needs the mask.
-            if (kGeneral) {
-              const bool ok = j >= 1 && key_j >= 1 && key_j <= i && i < T;
-              Lv = ok ? Lv : 0.f;
-              Rv = ok ? Rv : 0.f;
-              dLv = ok ? dLv : 0.f;
-              dRv = ok ? dRv : 0.f;
-            }
-            // left shares of segment (j, j+1) arrive from lane j+1
-            float w = Rv + row_shl1(Lv);
-            float ds = dRv + row_shl1(dLv);
-            if (kGeneral) {
-              // half-token caps on the first key and the last visible key
-              const float cap = (vis && key_j == 0 ? 0.5f * p : 0.f) + (vis && key_j == i ? 0.5f * p : 0.f);
-              w += cap;
-              ds = fmaf(cap, gg, ds);
-            }
-            // Slots 0 and 15 are not owned: their w only reaches output
-            // columns that are never stored, but their dS must be 0 in the
-            // spill that the dQ pass reads.
-            const bool owned = j >= 1 && j <= kBwdKeys;
-            wout[rb][r] = w;
-            dout_s[rb][r] = owned ? ds : 0.f;
-          }
-        }
-      };
-      if (need_mask)
-        segments(std::true_type{});
-      else
-        segments(std::false_type{});
-
-      // ---- dS block (query tile qt, key block kb16) for the dQ pass ----
-      {
-        float* dst = dsbuf + ds_blk * kDsBlockFloats;
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) dst[(16 * rb + 4 * g + r) * kBwdSlots + j] = dout_s[rb][r];
-      }
-
-      // ---- dV^T += (dY/Z)^T w and dK^T += Q^T dS ----
-      // k element e of group g <-> query (e < 4 ? 4g + e : 16 + 4g + e - 4),
-      // i.e. register (rb = e / 4, r = e % 4) of this lane.
-      float xw[8], xd[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        xw[e] = wout[e >> 2][e & 3];
-        xd[e] = dout_s[e >> 2][e & 3];
-      }
-      const Limbs wb = split8(xw), db = split8(xd);
-      const int src_row = 4 * g + (j >> 2), src_col = 4 * (j & 3);
-#pragma unroll
-      for (int mb = 0; mb < P::NMB; ++mb) {
-        const int o0 = src_row * P::LDR + 16 * mb + src_col;
-        const int o1 = o0 + 16 * P::LDR;
-        Limbs ya, qa;
-        ya.h = lds_read_tr8(Ty + o0, Ty + o1);
-        ya.m = lds_read_tr8(Ty + P::LIMB + o0, Ty + P::LIMB + o1);
-        ya.l = lds_read_tr8(Ty + 2 * P::LIMB + o0, Ty + 2 * P::LIMB + o1);
-        qa.h = lds_read_tr8(Tq + o0, Tq + o1);
-        qa.m = lds_read_tr8(Tq + P::LIMB + o0, Tq + P::LIMB + o1);
-        qa.l = lds_read_tr8(Tq + 2 * P::LIMB + o0, Tq + 2 * P::LIMB + o1);
-#pragma unroll
-        for (int st = 0; st < 6; ++st) {
-          accv[mb] = mfma16_step(st, ya, wb, accv[mb]);
-          acck[mb] = mfma16_step(st, qa, db, acck[mb]);
-        }
-      }
-    }
-    ds_blk += ds_kb_count(qt);
-    if (qt + 1 < qt_end) store_tile(buf ^ 1);
-    __syncthreads();
-  }
-
-  // ---- epilogue: lane (slot j, group g) holds d = 16mb + 4g + r of its key ----
-  // A single-chunk group writes dK/dV; the chunks of a longer group write
-  // partials [key of the group][dV, dK][D] that ca_bwd_gain_merge sums.
-  if (j >= 1 && j <= kBwdKeys && key_j < T && kb16 < nkb) {
-    const float ck = cl2 * kLn2;
-    float* pv = nch == 1 ? dV + slice + (size_t)key_j * D
-                         : kv_part + (((size_t)bh * n_part + item) * kDkdvKeys + (key_j - w0)) * 2 * D;
-    float* pk = nch == 1 ? dK + slice + (size_t)key_j * D : pv + D;
-#pragma unroll
-    for (int mb = 0; mb < P::NMB; ++mb) {
-      const int d0 = 16 * mb + 4 * g;
-      if (d0 < D) {
-        *reinterpret_cast<f32x4*>(pv + d0) = accv[mb];
-        *reinterpret_cast<f32x4*>(pk + d0) = acck[mb] * ck;
-      }
-    }
   }
 }
 
@@ -696,11 +383,8 @@ hipError_t launch_bwd(const float* q, const float* k, const float* v, const floa
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   timer_begin(kBwdDkdv, stream);
-  hipLaunchKernelGGL(ca_bwd_dkdv_kernel<D>, dim3(kvs.items * BH), dim3(256), 0, stream, k, v,
-                     ws.limbs, ws.qstat, log_gain, dk, dv, ws.dsbuf, ws.kv_part, BH, H, T,
-                     kvs.chunk, kvs.part_items);
+  e = launch_bwd_dkdv<D>(k, v, ws, log_gain, dk, dv, kvs, BH, H, T, stream);
   timer_end(kBwdDkdv, stream);
-  e = hipGetLastError();
   if (e != hipSuccess) return e;
   timer_begin(kBwdDq, stream);
   hipLaunchKernelGGL(ca_bwd_dq_kernel<D>, dim3(sp.items * BH), dim3(256), 0, stream, ws.dsbuf, q,

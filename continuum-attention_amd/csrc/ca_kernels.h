@@ -247,6 +247,12 @@ struct BwdWork {
   float* dq_part;     // dQ chunk partials
   float* kv_part;     // dK/dV chunk partials: [BH][part item][kDkdvKeys][2][D]
 };
+
+// dK/dV kernel of the backward (ca_bwd_dkdv.hip, its own translation unit).
+template <int D>
+hipError_t launch_bwd_dkdv(const float* k, const float* v, const BwdWork& ws, const float* log_gain,
+                           float* dk, float* dv, const DkdvSplit& kvs, int BH, int H, int T,
+                           hipStream_t stream);
 inline size_t bwd_limb_elems(int BH, int T, int D) { return (size_t)6 * BH * T * D; }
 
 template <int D>
