@@ -362,6 +362,44 @@ def test_config5_long_context_T8192(gpu_ca):
     assert np.all(np.abs(kdk - dr) <= 1e-4 * mag)
 
 
+def test_long_context_T16384(gpu_ca):
+    """Twice config 5's length, beyond the reference's fused-kernel limit
+    (T <= 2048, cuda/continuum_attention.py:664-665): [1,2,16384,64] with one
+    near-duplicate-key head (config 5 head 0) and one large-delta head (head
+    8).  Forward and dQ on sampled rows, exact dK/dV/dQ of the last 256 keys,
+    and sum dV = sum dY, sum dK = 0, sum q.dQ = sum k.dK = dRho per head."""
+    say("[case] long context [1,2,16384,64]")
+    T = 16384
+    q, k, v, rho, dy = config5_inputs(3, T)
+    sel = [0, 8]
+    q, k, v, dy = (x[:, sel].contiguous() for x in (q, k, v, dy))
+    rho = rho[sel].contiguous()
+    y, (dq, dk, dv, dr) = run_hip(gpu_ca, q, k, v, rho, dy)
+    assert np.all(np.isfinite(y)) and all(np.all(np.isfinite(x)) for x in (dq, dk, dv, dr))
+    qn, kn, vn, dyn, rn = q.numpy(), k.numpy(), v.numpy(), dy.numpy(), rho.numpy()
+    rng = np.random.default_rng(9)
+    rows = np.unique(np.concatenate([[0, 1, 31, 32, 2047, 2048, 8191, 8192, 12000, T - 2, T - 1],
+                                     rng.integers(0, T, 6)]))
+    for h in (0, 1):
+        yr = O.ca_forward_rows(qn, kn, vn, rn, 0, h, rows)
+        dqr = O.ca_backward_rows(qn, kn, vn, rn, dyn, 0, h, rows)[0]
+        ey, eq = rel(y[0, h][rows], yr), rel(dq[0, h][rows], dqr)
+        suffix = np.arange(T - 256, T)
+        dq_s, dk_s, dv_s, _ = O.ca_backward_rows(qn, kn, vn, rn, dyn, 0, h, suffix)
+        ek, ev = rel(dk[0, h, suffix], dk_s[suffix]), rel(dv[0, h, suffix], dv_s[suffix])
+        say(f"   head {h}: rows out {ey:.2e} dq {eq:.2e}; last 256 keys dk {ek:.2e} dv {ev:.2e}")
+        assert ey <= OUT_TOL and eq <= GRAD_TOL and ek <= GRAD_TOL and ev <= GRAD_TOL
+    d64 = lambda a: np.asarray(a, np.float64)
+    scale_v = d64(np.abs(dyn)).sum(2).max()
+    assert np.abs(d64(dv).sum(2) - d64(dyn).sum(2)).max() <= 1e-5 * scale_v
+    dks = np.abs(d64(dk).sum(2)).max(-1)[0]
+    assert np.all(dks <= 1e-4 * np.abs(d64(dk)).sum(2).max(-1)[0])
+    qdq = (d64(qn) * dq).sum(axis=(0, 2, 3))
+    kdk = (d64(kn) * dk).sum(axis=(0, 2, 3))
+    mag = (np.abs(d64(qn) * dq)).sum(axis=(0, 2, 3))
+    assert np.all(np.abs(qdq - dr) <= 1e-4 * mag) and np.all(np.abs(kdk - dr) <= 1e-4 * mag)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_half_precision_inputs(gpu_ca, dtype):
     """bf16/fp16 q, k, v (the reference's autocast inputs): the operator reads
