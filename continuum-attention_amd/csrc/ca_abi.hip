@@ -34,8 +34,8 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 int check_shape(int B, int H, int T, int D) {
   if (B <= 0 || H <= 0 || T <= 0)
     return fail(CA_ERR_INVALID, "invalid shape B=%d H=%d T=%d (all must be positive)", B, H, T);
-  if (D != 8 && D != 16 && D != 32 && D != 64)
-    return fail(CA_ERR_UNSUPPORTED, "head dim D=%d not supported (HIP kernels cover D in {8,16,32,64})", D);
+  if (D != 8 && D != 16 && D != 32 && D != 64 && D != 128)
+    return fail(CA_ERR_UNSUPPORTED, "head dim D=%d not supported (HIP kernels cover D in {8,16,32,64,128})", D);
   if ((long long)B * H * T * D > (1ll << 31) - 1)
     return fail(CA_ERR_UNSUPPORTED, "tensor of %lld elements exceeds the 2^31 element limit",
                 (long long)B * H * T * D);
@@ -183,8 +183,7 @@ const char* ca_last_error(void) { return g_err; }
 
 size_t ca_fwd_workspace_bytes(int B, int H, int T, int D) {
   if (B <= 0 || H <= 0 || T <= 0) return 0;
-  (void)D;
-  return ca::fwd_part_floats(B * H, T, kSplitTiles) * sizeof(float);
+  return ca::fwd_part_floats(B * H, T, kSplitTiles, D) * sizeof(float);
 }
 
 int ca_fwd_f32(const float* q, const float* k, const float* v, const float* log_gain, float* out,
@@ -207,7 +206,8 @@ int ca_fwd_f32(const float* q, const float* k, const float* v, const float* log_
     case 8: e = ca::launch_fwd<8>(q, k, v, log_gain, out, stats, part, B, H, T, kSplitTiles, s); break;
     case 16: e = ca::launch_fwd<16>(q, k, v, log_gain, out, stats, part, B, H, T, kSplitTiles, s); break;
     case 32: e = ca::launch_fwd<32>(q, k, v, log_gain, out, stats, part, B, H, T, kSplitTiles, s); break;
-    default: e = ca::launch_fwd<64>(q, k, v, log_gain, out, stats, part, B, H, T, kSplitTiles, s); break;
+    case 64: e = ca::launch_fwd<64>(q, k, v, log_gain, out, stats, part, B, H, T, kSplitTiles, s); break;
+    default: e = ca::launch_fwd<128>(q, k, v, log_gain, out, stats, part, B, H, T, kSplitTiles, s); break;
   }
   if (e != hipSuccess) return fail(CA_ERR_HIP, "forward launch: %s", hipGetErrorString(e));
   return CA_OK;
@@ -241,15 +241,20 @@ int ca_bwd_f32(const float* q, const float* k, const float* v, const float* log_
   work.gain_part = reinterpret_cast<float*>(ws + L.gain);
   work.dq_part = reinterpret_cast<float*>(ws + L.dqpart);
   work.kv_part = reinterpret_cast<float*>(ws + L.kvpart);
-  const ca::DqSplit sp = ca::dq_split(B * H, T, dq_resident_groups());
-  const ca::DkdvSplit kvs = ca::dkdv_split(B * H, T, dkdv_resident_groups());
+  // D = 128 kernels hold fewer work groups per CU (dK/dV one instead of two,
+  // dQ two instead of three: register and LDS budgets)
+  const int dq_res = D > 64 ? dq_resident_groups() * 2 / 3 : dq_resident_groups();
+  const int kv_res = D > 64 ? dkdv_resident_groups() / 2 : dkdv_resident_groups();
+  const ca::DqSplit sp = ca::dq_split(B * H, T, dq_res);
+  const ca::DkdvSplit kvs = ca::dkdv_split(B * H, T, kv_res);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;
   switch (D) {
     case 8: e = ca::launch_bwd<8>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, work, sp, kvs, B, H, T, s); break;
     case 16: e = ca::launch_bwd<16>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, work, sp, kvs, B, H, T, s); break;
     case 32: e = ca::launch_bwd<32>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, work, sp, kvs, B, H, T, s); break;
-    default: e = ca::launch_bwd<64>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, work, sp, kvs, B, H, T, s); break;
+    case 64: e = ca::launch_bwd<64>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, work, sp, kvs, B, H, T, s); break;
+    default: e = ca::launch_bwd<128>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, work, sp, kvs, B, H, T, s); break;
   }
   if (e != hipSuccess) return fail(CA_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
   return CA_OK;

@@ -411,5 +411,6 @@ CA_INST_BWD(8)
 CA_INST_BWD(16)
 CA_INST_BWD(32)
 CA_INST_BWD(64)
+CA_INST_BWD(128)
 
 }  // namespace ca

@@ -34,7 +34,7 @@ struct Bwd {
 };
 
 template <int D>
-__global__ __launch_bounds__(256, 2) void ca_bwd_dkdv_kernel(
+__global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
     const float* __restrict__ K, const float* __restrict__ V, const __bf16* __restrict__ limbs,
     const float* __restrict__ qstat, const float* __restrict__ log_gain, float* __restrict__ dK,
     float* __restrict__ dV, float* __restrict__ dsbuf, float* __restrict__ kv_part, int BH, int H,
@@ -350,6 +350,7 @@ CA_INSTANTIATE_DKDV(8)
 CA_INSTANTIATE_DKDV(16)
 CA_INSTANTIATE_DKDV(32)
 CA_INSTANTIATE_DKDV(64)
+CA_INSTANTIATE_DKDV(128)
 #undef CA_INSTANTIATE_DKDV
 
 }  // namespace ca

@@ -98,7 +98,7 @@ __device__ __forceinline__ float halo_dot(const float* qreg, const float* __rest
 }
 
 template <int D>
-__global__ __launch_bounds__(256, 2) void ca_fwd_kernel(
+__global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ log_gain, float* __restrict__ O, float* __restrict__ stats,
     float* __restrict__ part, int BH, int H, int T, int C, int G, int smax) {
@@ -505,6 +505,8 @@ template hipError_t launch_fwd<16>(const float*, const float*, const float*, con
                                    float*, float*, int, int, int, int, hipStream_t);
 template hipError_t launch_fwd<32>(const float*, const float*, const float*, const float*, float*,
                                    float*, float*, int, int, int, int, hipStream_t);
+template hipError_t launch_fwd<128>(const float*, const float*, const float*, const float*, float*,
+                                    float*, float*, int, int, int, int, hipStream_t);
 template hipError_t launch_fwd<64>(const float*, const float*, const float*, const float*, float*,
                                    float*, float*, int, int, int, int, hipStream_t);
 

@@ -23,10 +23,10 @@ inline int fwd_num_items(int T, int C) {
   for (int g = 0; g < G; ++g) n += (fwd_group_tiles(g, T) + C - 1) / C;
   return n;
 }
-inline size_t fwd_part_floats(int BH, int T, int C) {
+inline size_t fwd_part_floats(int BH, int T, int C, int D) {
   const int smax = fwd_max_splits(T, C);
   if (smax <= 1) return 0;
-  return (size_t)BH * smax * T * 66;  // D <= 64 outputs + (m, Z); sized for the largest D
+  return (size_t)BH * smax * T * (D + 2);  // D outputs + (m, Z) per row and split
 }
 
 // Backward key blocks.  One dK/dV wave owns 14 keys and feeds 16 MFMA slots

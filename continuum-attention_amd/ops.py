@@ -15,7 +15,7 @@ Compute is float32 on the device (fp16/bf16 inputs are read as fp32, results
 cast back).  ``query_tile`` is accepted and validated; in the reference it only
 bounds the memory of the materialised ``[BH, Qt, K]`` weights
 (cuda/continuum_attention.py:957), which the fused kernels (D in 8, 16, 32,
-64) never materialise, so it does not change their arithmetic; other head
+64, 128) never materialise, so it does not change their arithmetic; other head
 dims run the reference's query-tile structure, where it does bound memory.  All ``CA_CUDA_MODE`` values select the same
 exact fp32 path (the reference modes differ only in fp16 rounding and launch
 structure).
@@ -32,7 +32,7 @@ import torch
 from . import _native
 
 _MODES = ("dense", "prefix", "fused", "prefix_v5", "prefix_v6")
-SUPPORTED_HEAD_DIMS = (8, 16, 32, 64)
+SUPPORTED_HEAD_DIMS = (8, 16, 32, 64, 128)
 
 
 def _mode() -> str:
@@ -232,7 +232,7 @@ def continuum_attention(q, k, v, log_gain, query_tile=64):
     """Exact causal Continuum Attention (cuda/continuum_attention.py:768-783).
 
     q, k, v: ``[B, H, T, D]`` (same dtype), log_gain: ``[H]``.  D in {8, 16,
-    32, 64} runs the fused kernels; any other D the query-tile structure over
+    32, 64, 128} runs the fused kernels; any other D the query-tile structure over
     the HIP weight kernels (``query_tile`` rows at a time).
     Scores are ``exp(log_gain[h]) / sqrt(D) * q.k``; keys and values are
     linearly interpolated between adjacent positions with half-token end caps

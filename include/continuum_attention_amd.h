@@ -47,7 +47,7 @@ size_t ca_fwd_workspace_bytes(int B, int H, int T, int D);
 /* Forward: out = W(S) v with S = exp(log_gain[h]) / sqrt(D) * q k^T, exact CA
  * weights W (segment moments, half-token caps, causal).  Also writes per-row
  * statistics stats[B*H*T][2] = (row shift in log2 units, 1/Z) that
- * ca_bwd_f32 consumes.  log_gain has H entries.  D in {8, 16, 32, 64}.
+ * ca_bwd_f32 consumes.  log_gain has H entries.  D in {8, 16, 32, 64, 128}.
  * Replaces: _CAExactTiled.forward (cuda/continuum_attention.py:651-694) with
  * ext.forward / ext.forward_half / ext.direct_output
  * (cuda/continuum_attention.py:460-471, 556-590). */

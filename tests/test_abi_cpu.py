@@ -49,7 +49,7 @@ def test_workspace_sizes(ca):
 
 
 @pytest.mark.parametrize("shape,code", [((0, 1, 8, 64), 1), ((1, 1, 0, 64), 1),
-                                        ((1, 1, 8, 128), 2), ((1, 1, 8, 24), 2)])
+                                        ((1, 1, 8, 256), 2), ((1, 1, 8, 24), 2)])
 def test_argument_errors_before_any_launch(ca, shape, code):
     lib = ca.native.load()
     p = ctypes.c_void_p(4096)  # never dereferenced: validation fails first

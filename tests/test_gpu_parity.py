@@ -133,7 +133,7 @@ def test_ragged_lengths(gpu_ca, T):
     check_case(gpu_ca, (1, 2, T, 64), 100 + T, 1.0, [0.0, 0.3], f"ragged T={T}")
 
 
-@pytest.mark.parametrize("D", [8, 16, 32, 64])
+@pytest.mark.parametrize("D", [8, 16, 32, 64, 128])
 def test_head_dims(gpu_ca, D):
     check_case(gpu_ca, (2, 2, 129, D), 7 + D, 1.0, [0.0, math.log(1 / 0.3)], f"D={D}")
 
