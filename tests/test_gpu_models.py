@@ -188,8 +188,7 @@ class _OracleCA(torch.autograd.Function):
 @pytest.mark.parametrize("d_model", [128, 256])
 def test_decoder_logits_vs_float64_oracle_model(gpu_ca, monkeypatch, d_model):
     """Small CA-S decoder: fp32 GPU logits against a float64 CPU copy of the
-    same model whose attention is the oracle (head dims 64: fused kernels,
-    128: the query-tile path)."""
+    same model whose attention is the oracle (head dims 64 and 128)."""
     say(f"[case] decoder logits vs float64 oracle model, d_model {d_model}")
     Dm = gpu_ca.decoder
     cfg = Dm.ContinuumDecoderConfig(d_model=d_model, n_heads=2, n_layers=2, block_size=96)

@@ -138,15 +138,16 @@ def test_head_dims(gpu_ca, D):
     check_case(gpu_ca, (2, 2, 129, D), 7 + D, 1.0, [0.0, math.log(1 / 0.3)], f"D={D}")
 
 
-@pytest.mark.parametrize("D,T,tile,dtype", [(128, 200, 64, torch.float32), (96, 129, 32, torch.float32),
+@pytest.mark.parametrize("D,T,tile,dtype", [(80, 200, 64, torch.float32), (96, 129, 32, torch.float32),
                                              (48, 65, 16, torch.float32), (24, 100, 128, torch.float32),
                                              (4, 33, 7, torch.float32), (128, 1, 64, torch.float32),
                                              (128, 130, 37, torch.bfloat16)])
 def test_any_head_dim_query_tiles(gpu_ca, D, T, tile, dtype):
-    """Head dims without fused kernels run the reference's query-tile
-    structure on the device (fp32 GEMMs + the HIP weight kernels): outputs
-    and all four gradients against the oracle, across tile boundaries and a
-    tile that does not divide T, nonzero gains, and bf16 inputs."""
+    """Head dims without fused kernels (80, 96, 48, 24, 4) run the
+    reference's query-tile structure on the device (fp32 GEMMs + the HIP
+    weight kernels); D = 128 runs the fused kernels.  Outputs and all four
+    gradients against the oracle, across tile boundaries and a tile that does
+    not divide T, nonzero gains, and bf16 inputs."""
     say(f"[case] any head dim D={D} T={T} query_tile={tile} {dtype}")
     q, k, v, rho, dy = make_inputs((2, 2, T, D), 300 + D + T, 1.0, [0.2, -0.4])
     q, k, v, dy = (x.to(dtype).float() for x in (q, k, v, dy))
