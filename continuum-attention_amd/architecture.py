@@ -34,7 +34,8 @@ from torch import nn
 from torch.nn import functional as F
 
 from .decoder import RMSNorm as _DecoderRMSNorm
-from .ops import continuum_attention
+from .decoder import rope_continuum_attention
+from .ops import SUPPORTED_HEAD_DIMS, continuum_attention
 from .weights import continuous_attention_weights
 
 VARIANTS = ("A", "B", "F", "G", "P", "R", "S", "H")
@@ -111,8 +112,24 @@ class CausalAttention(nn.Module):
         q, k, v = self._qkv(x)
         return self._weights(q, k, v)
 
+    # fused HIP prologue/epilogue (qkv -> fp32 heads -> operator -> tokens) on
+    # GPU tensors for the continuous variants on the 'hip' backend, with the
+    # variant's q scale passed as the operator's log-gain; False runs the
+    # reference's composition (same operator kernels)
+    fused_prologue = True
+
+    def _log_gain(self, device):
+        if self.variant in ("F", "G", "S", "H"):
+            return self.log_qk_gain
+        g = math.log(1.0 / self.fixed_tau) if self.variant in ("B", "P") else 0.0
+        return torch.full((self.heads,), g, device=device, dtype=torch.float32)
+
     def forward(self, x):
         Bsz, T, _ = x.shape
+        if (self.fused_prologue and self.continuous and self.path == "hip" and x.is_cuda
+                and self.head_dim in SUPPORTED_HEAD_DIMS and self.head_dim % 4 == 0):
+            y = rope_continuum_attention(self.qkv(x), self._log_gain(x.device), None, self.heads)
+            return self.out(y)
         q, k, v = self._qkv(x)
         if self.continuous and self.path == "hip":
             zero = torch.zeros(self.heads, device=q.device, dtype=torch.float32)

@@ -244,13 +244,18 @@ _CS_CACHE: dict = {}
 def rope_cos_sin(T, D, theta, device):
     """fp32 table ``[T, D/2, 2]`` of (cos, sin) of ``t * theta^(-2i/D)``: the
     reference's angles before their cast to the autocast dtype
-    (cuda/continuum_attention.py:828-830); cached per shape."""
-    key = (T, D, float(theta), device)
+    (cuda/continuum_attention.py:828-830); ``theta=None`` gives the identity
+    rotation (cos 1, sin 0, exact in the prologue); cached per shape."""
+    key = (T, D, None if theta is None else float(theta), device)
     cs = _CS_CACHE.get(key)
     if cs is None:
-        freq = 1.0 / (theta ** (torch.arange(0, D, 2, device=device, dtype=torch.float32) / D))
-        phase = torch.outer(torch.arange(T, device=device, dtype=torch.float32), freq)
-        cs = torch.stack((phase.cos(), phase.sin()), -1).contiguous()
+        if theta is None:
+            cs = torch.stack((torch.ones(T, D // 2, device=device), torch.zeros(T, D // 2, device=device)),
+                             -1).contiguous()
+        else:
+            freq = 1.0 / (theta ** (torch.arange(0, D, 2, device=device, dtype=torch.float32) / D))
+            phase = torch.outer(torch.arange(T, device=device, dtype=torch.float32), freq)
+            cs = torch.stack((phase.cos(), phase.sin()), -1).contiguous()
         if len(_CS_CACHE) > 64:
             _CS_CACHE.clear()
         _CS_CACHE[key] = cs
@@ -326,8 +331,10 @@ class _RopeContinuumAttention(torch.autograd.Function):
 
 def rope_continuum_attention(qkv, log_gain, theta, heads, query_tile=64):
     """``[B, T, 3C]`` qkv projection output -> ``[B, T, C]`` attention output
-    (before the output projection), in qkv's dtype; see _RopeContinuumAttention."""
-    return _RopeContinuumAttention.apply(qkv, log_gain, float(theta), int(heads), int(query_tile))
+    (before the output projection), in qkv's dtype; see _RopeContinuumAttention.
+    ``theta=None``: no rotary embedding (the prologue only splits the heads)."""
+    return _RopeContinuumAttention.apply(qkv, log_gain, None if theta is None else float(theta),
+                                         int(heads), int(query_tile))
 
 
 class ContinuumSelfAttention(nn.Module):

@@ -603,3 +603,36 @@ def test_graphed_train_step_matches_eager(gpu_ca):
         worst = max(((pa - pb).abs().max() / pb.abs().max()).item()
                     for pa, pb in zip(ma.parameters(), mb.parameters()))
         assert worst <= 1e-6, worst
+
+
+@pytest.mark.parametrize("variant", ["P", "R", "S", "H"])
+def test_tinylm_fused_prologue_matches_composition(gpu_ca, variant):
+    """TinyLM's continuous variants with the fused qkv -> heads prologue (the
+    variant's q scale passed as the operator's log-gain, no rotation) against
+    the reference's composition (q scaled, heads split and copied): logits and
+    every parameter gradient, the learned gains' included."""
+    say(f"[case] TinyLM {variant} fused prologue vs composition")
+    A = gpu_ca.architecture
+    torch.manual_seed(31)
+    m = A.TinyLM(variant=variant, backend="hip", seq_len=96, layers=2).cuda()
+    if variant in ("S", "H"):
+        with torch.no_grad():
+            for n, p in m.named_parameters():
+                if n.endswith("log_qk_gain"):
+                    p.add_(torch.linspace(-0.3, 0.3, p.numel(), device="cuda"))
+    x = torch.randint(0, 256, (2, 96), device="cuda")
+    outs = {}
+    for fused in (True, False):
+        A.CausalAttention.fused_prologue = fused
+        try:
+            m.zero_grad(set_to_none=True)
+            logits = m(x)
+            torch.nn.functional.cross_entropy(logits.reshape(-1, 256), x.reshape(-1)).backward()
+            outs[fused] = (logits.detach().clone(), {n: p.grad.detach().clone() for n, p in m.named_parameters()})
+        finally:
+            A.CausalAttention.fused_prologue = True
+    el = rel(outs[True][0].cpu().numpy(), outs[False][0].cpu().numpy())
+    eg = {n: rel(outs[True][1][n].cpu().numpy(), outs[False][1][n].cpu().numpy()) for n in outs[True][1]}
+    worst = max(eg.values())
+    say(f"   logits {el:.2e} worst grad {worst:.2e} ({max(eg, key=eg.get)})")
+    assert el <= 1e-5 and worst <= 1e-4
