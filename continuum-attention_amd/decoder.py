@@ -522,37 +522,84 @@ def train_step(model, optimizer, batch, amp_dtype=torch.bfloat16, grad_clip=1.0)
     return loss.detach()
 
 
+# torch's embedding backward sums rows without sorting for at most this many
+# indices; above it (and always with scale_grad_by_freq) it sorts and runs
+# rocprim's partition, which records a hipMemsetAsync of its selected counters
+# into a captured graph.  Replays do not reliably redo such memset nodes; with
+# stale counters the partition writes past its output buffer.
+_GRAPH_SAFE_EMBEDDING_INDICES = 3072
+
+
+@contextlib.contextmanager
+def _embedding_graph_guard(model):
+    """Raises ValueError from the forward of any trainable nn.Embedding of
+    ``model`` whose backward would take torch's sorting path."""
+
+    def check(name):
+        def hook(mod, args):
+            ids = args[0]
+            if mod.weight.requires_grad and not mod.sparse and (
+                    ids.numel() > _GRAPH_SAFE_EMBEDDING_INDICES or mod.scale_grad_by_freq):
+                raise ValueError(
+                    f"GraphedTrainStep: embedding '{name}' looks up {ids.numel()} indices; the "
+                    f"backward of more than {_GRAPH_SAFE_EMBEDDING_INDICES} (or with "
+                    "scale_grad_by_freq) records a memset node that graph replays do not "
+                    "reliably redo; train this model with the eager step")
+        return hook
+
+    handles = [m.register_forward_pre_hook(check(n)) for n, m in model.named_modules()
+               if isinstance(m, nn.Embedding)]
+    try:
+        yield
+    finally:
+        for h in handles:
+            h.remove()
+
+
 class GraphedTrainStep:
-    """train_step with the forward and backward captured once as a HIP graph
-    and replayed each step (the optimizer step runs eagerly after the replay:
-    optim.FusedAdamW's clip + update, or clip_grad_norm_ + a torch optimizer).
+    """A training step with the forward and backward captured once as a HIP
+    graph and replayed each step (the optimizer step runs eagerly after the
+    replay: optim.FusedAdamW's clip + update, or clip_grad_norm_ + a torch
+    optimizer).
 
-    The decoder step launches a few hundred kernels, many of a few
-    microseconds; replaying them as one graph removes the per-launch host
-    work between them.  ``batch`` fixes the input shape; each call copies its
-    batch into the captured input.  Forward and backward are warmed up (twice,
-    on a side stream, without an optimizer step: parameters are unchanged)
-    before capture, as graph capture requires.  While the object is used the
-    gradients are the captured graph's buffers: they are overwritten by each
-    replay and must not be set to None (do not call ``zero_grad``).  A
-    replay uses the parameters and the bf16 shadows as they are in memory,
-    so in-place changes to them between steps are seen; hyper-parameters of
-    the eager optimizer step can change freely."""
+    ``batch`` is a tensor or a tuple of tensors fixing the input shapes; each
+    call copies its inputs into the captured ones.  ``loss_fn(model, *inputs)``
+    returns the scalar loss; by default the decoder's next-byte loss
+    ``model(ids, targets=ids)["loss"]``.  Forward and backward are warmed up
+    (twice, on a side stream, without an optimizer step: parameters are
+    unchanged) before capture, as graph capture requires.  While the object
+    is used the gradients are the captured graph's buffers: they are
+    overwritten by each replay and must not be set to None (do not call
+    ``zero_grad``).  A replay uses the parameters and the bf16 shadows as they
+    are in memory, so in-place changes to them between steps are seen;
+    hyper-parameters of the eager optimizer step can change freely.
 
-    def __init__(self, model, optimizer, batch, amp_dtype=torch.bfloat16, grad_clip=1.0, warmup=2):
+    Models whose nn.Embedding backward takes torch's sorting path (more than
+    3072 indices per lookup, or scale_grad_by_freq) are refused with
+    ValueError before capture: that path records a memset node that graph
+    replays do not reliably redo."""
+
+    def __init__(self, model, optimizer, batch, amp_dtype=torch.bfloat16, grad_clip=1.0, warmup=2,
+                 loss_fn=None):
         from .optim import FusedAdamW
         self.model, self.optimizer = model, optimizer
         self.amp_dtype, self.grad_clip = amp_dtype, grad_clip
         self.fused = isinstance(optimizer, FusedAdamW)
-        self.static_batch = batch.detach().clone()
-        dev = batch.device
+        self.loss_fn = loss_fn or (lambda m, ids: m(ids, targets=ids)["loss"])
+        inputs = batch if isinstance(batch, (tuple, list)) else (batch,)
+        self.static_inputs = tuple(t.detach().clone() for t in inputs)
+        dev = self.static_inputs[0].device
         _native.timing_enable(False)
         side = torch.cuda.Stream(device=dev)
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side):
-            for _ in range(warmup):
+            for i in range(max(warmup, 1)):
                 optimizer.zero_grad(set_to_none=True)
-                self._forward_backward()
+                if i == 0:
+                    with _embedding_graph_guard(model):
+                        self._forward_backward()
+                else:
+                    self._forward_backward()
         torch.cuda.current_stream(dev).wait_stream(side)
         optimizer.zero_grad(set_to_none=True)
         self.graph = torch.cuda.CUDAGraph()
@@ -563,14 +610,16 @@ class GraphedTrainStep:
         amp = (torch.autocast(device_type="cuda", dtype=self.amp_dtype, cache_enabled=False)
                if self.amp_dtype is not None else contextlib.nullcontext())
         with amp:
-            loss = self.model(self.static_batch, targets=self.static_batch)["loss"]
+            loss = self.loss_fn(self.model, *self.static_inputs)
         loss.backward()
         return loss.detach()
 
-    def __call__(self, batch):
-        """One training step on ``batch``; returns the loss (a device tensor
-        that the next call overwrites)."""
-        self.static_batch.copy_(batch)
+    def __call__(self, *batch):
+        """One training step on ``batch`` (the same tensors, in the same order,
+        as at construction); returns the loss (a device tensor that the next
+        call overwrites)."""
+        for dst, src in zip(self.static_inputs, batch):
+            dst.copy_(src)
         self.graph.replay()
         if self.fused:
             self.optimizer.step(max_norm=self.grad_clip or 0.0)

@@ -18,6 +18,7 @@ import sys
 import numpy as np
 import pytest
 import torch
+import torch.nn.functional as F
 
 from oracle import ca_oracle as O
 
@@ -603,6 +604,41 @@ def test_graphed_train_step_matches_eager(gpu_ca):
         worst = max(((pa - pb).abs().max() / pb.abs().max()).item()
                     for pa, pb in zip(ma.parameters(), mb.parameters()))
         assert worst <= 1e-6, worst
+
+
+def test_graphed_tinylm_step_matches_eager(gpu_ca):
+    """GraphedTrainStep with a caller's loss (TinyLM's next-byte cross-entropy
+    on (inputs, targets)), fp32 without autocast, a tied head and FusedAdamW's
+    two parameter groups under a global clip, against the eager step over
+    three replays; 3072 token lookups per step, the most whose embedding
+    backward is captured (a larger batch is refused before capture)."""
+    say("[case] graphed TinyLM step vs eager (B 6, T 512)")
+    A, Dm = gpu_ca.architecture, gpu_ca.decoder
+    torch.manual_seed(31)
+    kw = dict(variant="P", backend="hip", seq_len=512, width=64, hidden=128, heads=4,
+              fixed_tau=0.30, layers=2)
+    ma, mb = A.TinyLM(**kw).cuda(), A.TinyLM(**kw).cuda()
+    mb.load_state_dict(ma.state_dict())
+    oa, ob = A.build_fused_adamw(ma), A.build_fused_adamw(mb)
+    g = torch.Generator().manual_seed(32)
+    data = [torch.randint(0, 256, (6, 513), generator=g).cuda() for _ in range(3)]
+    loss_fn = lambda m, x, t: F.cross_entropy(m(x).reshape(-1, 256), t.reshape(-1))
+    step = Dm.GraphedTrainStep(ma, oa, (data[0][:, :-1], data[0][:, 1:]), amp_dtype=None,
+                               grad_clip=0.5, loss_fn=loss_fn)
+    for n, d in enumerate(data):
+        la = step(d[:, :-1], d[:, 1:]).item()
+        torch.cuda.synchronize()
+        lb = A.train_step(mb, ob, d[:, :-1], d[:, 1:], grad_clip=0.5).item()
+        torch.cuda.synchronize()
+        say(f"   step {n}: graphed {la:.6f} eager {lb:.6f}")
+        assert abs(la - lb) <= 1e-6 * abs(lb)
+        worst = max(((pa - pb).abs().max() / pb.abs().max()).item()
+                    for pa, pb in zip(ma.parameters(), mb.parameters()))
+        assert worst <= 1e-6, worst
+    say("[case] graphed TinyLM step refused at B 16 (8192 lookups)")
+    big = torch.randint(0, 256, (16, 513), generator=g).cuda()
+    with pytest.raises(ValueError, match="tok_embed.*8192 indices"):
+        Dm.GraphedTrainStep(mb, ob, (big[:, :-1], big[:, 1:]), amp_dtype=None, loss_fn=loss_fn)
 
 
 @pytest.mark.parametrize("variant", ["P", "R", "S", "H"])

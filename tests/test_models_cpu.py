@@ -162,3 +162,20 @@ def test_rope_matches_complex_rotation(Dm):
         z = z * rot
         ref = np.stack([z.real, z.imag], -1).reshape(B, H, T, D)
         np.testing.assert_allclose(xr.numpy(), ref, atol=2e-6, rtol=0)
+
+
+def test_graphed_step_refuses_sorting_embedding_backward(A, Dm):
+    """GraphedTrainStep's capture guard: an nn.Embedding lookup of more than
+    3072 indices (torch's sorting backward, whose captured memset node graph
+    replays do not reliably redo) raises before any capture; 3072 passes."""
+    m = tiny(A, "A")  # softmax control: runs on the CPU
+    with torch.no_grad():
+        with Dm._embedding_graph_guard(m):
+            m(torch.randint(0, 256, (192, 16)))  # 3072 indices per lookup
+        with pytest.raises(ValueError, match="tok_embed.*3088 indices"):
+            with Dm._embedding_graph_guard(m):
+                m(torch.randint(0, 256, (193, 16)))
+        m(torch.randint(0, 256, (193, 16)))  # hooks removed after the guard
+        m.tok_embed.weight.requires_grad_(False)  # no backward: nothing to refuse
+        with Dm._embedding_graph_guard(m):
+            m(torch.randint(0, 256, (193, 16)))
