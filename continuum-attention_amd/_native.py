@@ -7,10 +7,11 @@ loudly when it is missing -- there is no fallback path.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 
-import torch  # noqa: F401  -- must be imported first: the library binds torch's HIP runtime
+import torch  # must be imported first: the library binds torch's HIP runtime
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libca_hip.so")
@@ -70,6 +71,26 @@ class CAError(RuntimeError):
     def __init__(self, code: int, message: str):
         super().__init__(message)
         self.code = code
+
+
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def stream_handle(dev: torch.device) -> int:
+    """The current HIP stream of ``dev`` as the handle the C ABI takes: the
+    value of ``torch.cuda.current_stream(dev).cuda_stream``, read without
+    building a Stream object (that costs microseconds per launch)."""
+    if _raw_stream is not None and dev.index is not None:
+        return _raw_stream(dev.index)
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def on_device(dev: torch.device):
+    """``torch.cuda.device(dev)``, or a no-op context when ``dev`` is already
+    the current device (the library launches on the current device)."""
+    if dev.index is None or dev.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(dev)
 
 
 def load() -> ctypes.CDLL:

@@ -73,8 +73,8 @@ class _RMSNormFn(torch.autograd.Function):
         w = weight.detach().contiguous()
         y = torch.empty(x.shape, device=x.device, dtype=out_dtype)
         rstd = torch.empty(N, device=x.device, dtype=torch.float32)
-        stream = torch.cuda.current_stream(x.device).cuda_stream
-        with torch.cuda.device(x.device):
+        stream = _native.stream_handle(x.device)
+        with _native.on_device(x.device):
             _native.check(lib.ca_rmsnorm_fwd(xc.data_ptr(), w.data_ptr(), y.data_ptr(),
                                              _DTYPE_CODE[out_dtype], rstd.data_ptr(), N, C,
                                              float(eps), stream))
@@ -96,8 +96,8 @@ class _RMSNormFn(torch.autograd.Function):
         dw = torch.empty_like(w)
         nbytes = int(lib.ca_rmsnorm_bwd_workspace_bytes(N, C))
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=xc.device)
-        stream = torch.cuda.current_stream(xc.device).cuda_stream
-        with torch.cuda.device(xc.device):
+        stream = _native.stream_handle(xc.device)
+        with _native.on_device(xc.device):
             _native.check(lib.ca_rmsnorm_bwd(g.data_ptr(), _DTYPE_CODE[g.dtype], xc.data_ptr(),
                                              w.data_ptr(), rstd.data_ptr(), dx.data_ptr(),
                                              dw.data_ptr(), ws.data_ptr(), ws.numel(), N, C,
@@ -124,8 +124,8 @@ class _AddRMSNormFn(torch.autograd.Function):
         s = torch.empty(x.shape, device=x.device, dtype=torch.float32)
         y = torch.empty(x.shape, device=x.device, dtype=out_dtype)
         rstd = torch.empty(N, device=x.device, dtype=torch.float32)
-        stream = torch.cuda.current_stream(x.device).cuda_stream
-        with torch.cuda.device(x.device):
+        stream = _native.stream_handle(x.device)
+        with _native.on_device(x.device):
             _native.check(lib.ca_add_rmsnorm_fwd(xc.data_ptr(), rc.data_ptr(), _DTYPE_CODE[res.dtype],
                                                  s.data_ptr(), w.data_ptr(), y.data_ptr(),
                                                  _DTYPE_CODE[out_dtype], rstd.data_ptr(), N, C,
@@ -152,8 +152,8 @@ class _AddRMSNormFn(torch.autograd.Function):
         dw = torch.empty_like(w)
         nbytes = int(lib.ca_rmsnorm_bwd_workspace_bytes(N, C))
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=s.device)
-        stream = torch.cuda.current_stream(s.device).cuda_stream
-        with torch.cuda.device(s.device):
+        stream = _native.stream_handle(s.device)
+        with _native.on_device(s.device):
             _native.check(lib.ca_add_rmsnorm_bwd(g.data_ptr(), _DTYPE_CODE[g.dtype],
                                                  None if gsum is None else gsum.data_ptr(),
                                                  s.data_ptr(), w.data_ptr(), rstd.data_ptr(),
@@ -292,8 +292,8 @@ class _RopeContinuumAttention(torch.autograd.Function):
         x = _aligned(qkv.detach(), 16)
         cs = rope_cos_sin(T, D, theta, dev)
         q, k, v = (torch.empty(Bsz, heads, T, D, device=dev, dtype=torch.float32) for _ in range(3))
-        stream = torch.cuda.current_stream(dev).cuda_stream
-        with torch.cuda.device(dev):
+        stream = _native.stream_handle(dev)
+        with _native.on_device(dev):
             _native.check(lib.ca_qkv_rope_in(x.data_ptr(), dt, cs.data_ptr(), q.data_ptr(),
                                              k.data_ptr(), v.data_ptr(), Bsz, T, heads, D, stream))
             y, stats = ca_forward(q, k, v, log_gain)
@@ -317,8 +317,8 @@ class _RopeContinuumAttention(torch.autograd.Function):
         if g.dtype not in _DTYPE_CODE:
             g = g.float()
         dyf = torch.empty(Bsz, heads, T, D, device=dev, dtype=torch.float32)
-        stream = torch.cuda.current_stream(dev).cuda_stream
-        with torch.cuda.device(dev):
+        stream = _native.stream_handle(dev)
+        with _native.on_device(dev):
             _native.check(lib.ca_tokens_to_heads(g.data_ptr(), _DTYPE_CODE[g.dtype], dyf.data_ptr(),
                                                  Bsz, heads, T, D, stream))
             dq, dk, dv, dg = ca_backward(q, k, v, log_gain, y, stats, dyf)

@@ -25,6 +25,7 @@ otherwise.  CPU checking code lives in ``oracle/`` (tests only).
 """
 from __future__ import annotations
 
+import functools
 import os
 
 import torch
@@ -53,7 +54,17 @@ def _as_f32(x: torch.Tensor) -> torch.Tensor:
 
 
 def _stream(dev: torch.device) -> int:
-    return torch.cuda.current_stream(dev).cuda_stream
+    return _native.stream_handle(dev)
+
+
+@functools.lru_cache(maxsize=256)
+def _fwd_workspace_bytes(B: int, H: int, T: int, D: int) -> int:
+    return int(_native.load().ca_fwd_workspace_bytes(B, H, T, D))
+
+
+@functools.lru_cache(maxsize=256)
+def _bwd_workspace_bytes(B: int, H: int, T: int, D: int) -> int:
+    return int(_native.load().ca_bwd_workspace_bytes(B, H, T, D))
 
 
 def _check_device(*ts: torch.Tensor) -> torch.device:
@@ -80,9 +91,9 @@ def ca_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, log_gain: torc
     qf, kf, vf, gf = _as_f32(q), _as_f32(k), _as_f32(v), _as_f32(log_gain.reshape(H))
     out = torch.empty((B, H, T, D), device=dev, dtype=torch.float32)
     stats = torch.empty((B * H * T, 2), device=dev, dtype=torch.float32)
-    nbytes = lib.ca_fwd_workspace_bytes(B, H, T, D)
+    nbytes = _fwd_workspace_bytes(B, H, T, D)
     ws = torch.empty(max(nbytes, 1), device=dev, dtype=torch.uint8)
-    with torch.cuda.device(dev):
+    with _native.on_device(dev):
         _native.check(lib.ca_fwd_f32(qf.data_ptr(), kf.data_ptr(), vf.data_ptr(), gf.data_ptr(),
                                      out.data_ptr(), stats.data_ptr(), ws.data_ptr(), nbytes,
                                      B, H, T, D, _stream(dev)))
@@ -100,9 +111,9 @@ def ca_backward(q, k, v, log_gain, out, stats, dout):
     dk = torch.empty_like(dq)
     dv = torch.empty_like(dq)
     dg = torch.empty(H, device=dev, dtype=torch.float32)
-    nbytes = lib.ca_bwd_workspace_bytes(B, H, T, D)
+    nbytes = _bwd_workspace_bytes(B, H, T, D)
     ws = torch.empty(nbytes, device=dev, dtype=torch.uint8)
-    with torch.cuda.device(dev):
+    with _native.on_device(dev):
         _native.check(lib.ca_bwd_f32(qf.data_ptr(), kf.data_ptr(), vf.data_ptr(), gf.data_ptr(),
                                      of.data_ptr(), sf.data_ptr(), df.data_ptr(), dq.data_ptr(),
                                      dk.data_ptr(), dv.data_ptr(), dg.data_ptr(), ws.data_ptr(),

@@ -180,7 +180,7 @@ class FusedAdamW(torch.optim.Optimizer):
                 closure()
         self.step_count += 1
         groups = [g for g in self._groups if g["tensors"]]
-        stream = torch.cuda.current_stream(groups[0]["tensors"][0].device).cuda_stream
+        stream = _native.stream_handle(groups[0]["tensors"][0].device)
         for g in groups:
             self._fill_table(g)
         coef = None

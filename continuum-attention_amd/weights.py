@@ -57,9 +57,9 @@ def ca_weights(scores: torch.Tensor, start: int = 0):
     s = _f32c(scores)
     W = torch.empty_like(s)
     stats = torch.empty((BH * Q, 2), device=s.device, dtype=torch.float32)
-    with torch.cuda.device(s.device):
+    with _native.on_device(s.device):
         _native.check(lib.ca_weights_f32(s.data_ptr(), W.data_ptr(), stats.data_ptr(), BH, Q, K,
-                                         int(start), torch.cuda.current_stream(s.device).cuda_stream))
+                                         int(start), _native.stream_handle(s.device)))
     return W, stats
 
 
@@ -82,11 +82,11 @@ def ca_weights_backward(scores: torch.Tensor, grad_weights: torch.Tensor, start:
     gw = _f32c(grad_weights)
     ds = torch.empty_like(s)
     W = torch.empty_like(s) if return_weights else None
-    with torch.cuda.device(s.device):
+    with _native.on_device(s.device):
         _native.check(lib.ca_weights_bwd_f32(s.data_ptr(), gw.data_ptr(),
                                              W.data_ptr() if W is not None else None,
                                              ds.data_ptr(), BH, Q, K, int(start),
-                                             torch.cuda.current_stream(s.device).cuda_stream))
+                                             _native.stream_handle(s.device)))
     return (W, ds) if return_weights else ds
 
 

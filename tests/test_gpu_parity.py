@@ -459,3 +459,26 @@ def test_hip_graph_capture_and_replay(gpu_ca):
         assert torch.equal(y, ref_y), rep
         for a, b in zip(grads, ref_g):
             assert torch.equal(a, b), rep
+
+
+def test_stream_handle_follows_current_stream(gpu_ca):
+    """The launch stream handle equals torch's current stream on the default
+    stream and under a side stream (forward and the autograd backward launched
+    there give the default stream's results)."""
+    say("[case] stream handle")
+    N = gpu_ca.native
+    dev = torch.device("cuda", torch.cuda.current_device())
+    assert N.stream_handle(dev) == torch.cuda.current_stream(dev).cuda_stream
+    q, k, v, rho, dy = (x.cuda() for x in make_inputs((1, 2, 200, 32), 44, 1.0, [0.1, -0.2]))
+    ref = run_hip(gpu_ca, q, k, v, rho, dy)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        assert N.stream_handle(dev) == s.cuda_stream != torch.cuda.default_stream(dev).cuda_stream
+        got = run_hip(gpu_ca, q, k, v, rho, dy)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    assert np.array_equal(got[0], ref[0])
+    for a, b in zip(got[1], ref[1]):
+        assert np.array_equal(a, b)
