@@ -194,7 +194,10 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
   // ---- cooperative tile loads ------------------------------------------
   // K: float4 chunk e -> score key 32t+1+row, d = 4c..4c+3.  V: unit u ->
   // weight keys 32t+2pp, +1 (a key pair, so the transposed store writes
-  // packed bf16 pairs), d = 4c..4c+3.
+  // packed bf16 pairs), d = 4c..4c+3, with pp = u % 16 the fast index: the 16
+  // lanes of one c write 16 consecutive words of each V^T row, and the four c
+  // of a wave rows 80 words apart, so the stores of a wave hit 64 distinct
+  // banks (the loads still read whole 64-byte row segments).
   f32x4 pre_k[P::LD_PER_THREAD], pre_v[P::VLD][2];
   auto load_tile = [&](int t) {
 #pragma unroll
@@ -213,7 +216,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
       const int u = tid + 256 * j;
       f32x4 v0 = {0.f, 0.f, 0.f, 0.f}, v1 = {0.f, 0.f, 0.f, 0.f};
       if (u < P::VUNITS) {
-        const int pp = u / P::C4, c = u % P::C4;
+        const int pp = u % 16, c = u / 16;
         const int vk = 32 * t + 2 * pp;  // weight key
         if (vk < T) v0 = reinterpret_cast<const f32x4*>(Vs + (size_t)vk * D)[c];
         if (vk + 1 < T) v1 = reinterpret_cast<const f32x4*>(Vs + (size_t)(vk + 1) * D)[c];
@@ -242,7 +245,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
     for (int j = 0; j < P::VLD; ++j) {
       const int u = tid + 256 * j;
       if (u < P::VUNITS) {
-        const int pp = u / P::C4, c = u % P::C4;
+        const int pp = u % 16, c = u / 16;
 #pragma unroll
         for (int x = 0; x < 4; ++x) {
           unsigned hv, mv, lv;
