@@ -112,7 +112,7 @@ def _timed_steps(ca, step, steps, warmup):
     return ms, ca_ms, out
 
 
-def bench_ca_s(ca, dev, steps=10, warmup=3):
+def bench_ca_s(ca, dev, steps=20, warmup=5):
     """one CA-S decoder training step (101,205,120 params,
     T=2048, batch 1, bf16 autocast with fp32 CA scores, AdamW + clip 1.0 as
     the library's fused HIP optimizer) on uniform-random bytes, random-init
@@ -142,7 +142,7 @@ def bench_ca_s(ca, dev, steps=10, warmup=3):
     return res
 
 
-def bench_ca_p(ca, dev, steps=10, warmup=3):
+def bench_ca_p(ca, dev, steps=30, warmup=10):
     """small CA-P decoder (TinyLM backbone with 4 blocks,
     d 256, 4 heads, fixed tau 0.30, T=512, batch 16), one fp32 step on
     uniform-random bytes, random-init weights."""
