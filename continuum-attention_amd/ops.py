@@ -216,6 +216,16 @@ class _CAExactTiled(torch.autograd.Function):
         _mode()
         ctx.query_tile = int(query_tile)
         ctx.fused = q.shape[-1] in SUPPORTED_HEAD_DIMS
+        ctx.empty = False
+        if q.shape[2] == 0:
+            # the reference's query-tile loop has no tile to concatenate (:670-694)
+            raise RuntimeError("continuum_attention: empty sequence (T = 0)")
+        if q.shape[0] * q.shape[1] == 0:
+            # an empty batch: the reference's tile loop yields empty tiles
+            _check_device(q, k, v, log_gain)
+            ctx.empty = True
+            ctx.save_for_backward(q, k, v, log_gain)
+            return torch.empty(q.shape, device=q.device, dtype=v.dtype)
         with torch.autocast(device_type="cuda", enabled=False):
             if ctx.fused:
                 out, stats = ca_forward(q, k, v, log_gain)
@@ -229,6 +239,10 @@ class _CAExactTiled(torch.autograd.Function):
     def backward(ctx, grad_y):
         if torch.is_grad_enabled():
             raise RuntimeError("CA Volta analytic kernel supports first-order gradients only")
+        if ctx.empty:
+            q, k, v, log_gain = ctx.saved_tensors
+            return (torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v),
+                    torch.zeros_like(log_gain), None)
         if ctx.fused:
             q, k, v, log_gain, out, stats = ctx.saved_tensors
             dq, dk, dv, dg = ca_backward(q, k, v, log_gain, out, stats, grad_y)

@@ -482,3 +482,20 @@ def test_stream_handle_follows_current_stream(gpu_ca):
     assert np.array_equal(got[0], ref[0])
     for a, b in zip(got[1], ref[1]):
         assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("shape", [(0, 2, 16, 64), (2, 0, 16, 64), (0, 1, 5, 24)])
+def test_empty_batch(gpu_ca, shape):
+    """An empty batch (B or H = 0) gives empty outputs and gradients, as the
+    reference's tile loop does; T = 0 raises (its concatenation of no tiles)."""
+    say(f"[case] empty batch {shape}")
+    q, k, v = (torch.randn(shape, device="cuda", requires_grad=True) for _ in range(3))
+    rho = torch.zeros(shape[1], device="cuda", requires_grad=True)
+    y = gpu_ca.continuum_attention(q, k, v, rho)
+    assert y.shape == q.shape and y.dtype == v.dtype
+    grads = torch.autograd.grad(y.sum(), (q, k, v, rho), allow_unused=True)
+    for g, t in zip(grads, (q, k, v, rho)):
+        assert g is None or g.shape == t.shape
+    z = torch.randn(1, 1, 0, 64, device="cuda")
+    with pytest.raises(RuntimeError, match="T = 0"):
+        gpu_ca.continuum_attention(z, z, z, torch.zeros(1, device="cuda"))
