@@ -121,10 +121,20 @@ inline DqSplit dq_split_chunk(int T, int chunk) {
 // resident_groups: dQ work groups the GPU holds at once (0: never split).
 // Splitting more finely only adds work groups (and partial tiles), so the
 // workspace sized for the largest resident_groups covers every smaller one.
+// Shorter chunks while the grid would fill less than half a round (few
+// slices, short rows): more dQ work groups, at the price of more partials to
+// merge, which outweighs the gain once half a round is filled.
+constexpr int kDqChunkSmall[] = {32, 24, 16};
 inline DqSplit dq_split(int BH, int T, int resident_groups) {
   if ((long long)dq_num_groups(T) * BH >= resident_groups) return dq_split_chunk(T, bwd_num_key_blocks(T));
-  const DqSplit s = dq_split_chunk(T, kDqChunkBlocks);
-  return (long long)s.items * BH >= resident_groups ? s : dq_split_chunk(T, kDqChunkBlocksShort);
+  DqSplit s = dq_split_chunk(T, kDqChunkBlocks);
+  if ((long long)s.items * BH >= resident_groups) return s;
+  s = dq_split_chunk(T, kDqChunkBlocksShort);
+  for (int c : kDqChunkSmall) {
+    if (2LL * s.items * BH >= resident_groups) break;
+    s = dq_split_chunk(T, c);
+  }
+  return s;
 }
 // dQ work groups resident per CU (VGPR-limited: 3 waves per SIMD)
 constexpr int kDqGroupsPerCu = 3;
@@ -155,17 +165,29 @@ struct DkdvSplit {
   int multi_groups;  // groups with more than one chunk (the first ones)
 };
 // resident_groups: dK/dV work groups the GPU holds at once (0: never split)
-inline DkdvSplit dkdv_split(int BH, int T, int resident_groups) {
-  const int G = dkdv_num_groups(T);
-  const bool split = (long long)G * BH < 2LL * resident_groups;
-  DkdvSplit s{split ? kDkdvChunkTiles : num_q_tiles(T), 0, 0, 0};
-  for (int g = 0; g < G; ++g) {
-    const int n = dkdv_group_chunks(g, T, s.chunk);
+inline DkdvSplit dkdv_split_chunk(int T, int chunk) {
+  DkdvSplit s{chunk, 0, 0, 0};
+  for (int g = 0; g < dkdv_num_groups(T); ++g) {
+    const int n = dkdv_group_chunks(g, T, chunk);
     s.items += n;
     if (n > 1) {
       s.part_items += n;
       ++s.multi_groups;
     }
+  }
+  return s;
+}
+// Shorter chunks while kDkdvChunkTiles leaves less than one round (fewer
+// would only add partials and merge work): the first length whose items fill
+// a round is taken, else the last.
+constexpr int kDkdvChunkSmall[] = {16, 12, 8, 6};
+inline DkdvSplit dkdv_split(int BH, int T, int resident_groups) {
+  const long long want = 2LL * resident_groups;
+  if ((long long)dkdv_num_groups(T) * BH >= want) return dkdv_split_chunk(T, num_q_tiles(T));
+  DkdvSplit s = dkdv_split_chunk(T, kDkdvChunkTiles);
+  for (int c : kDkdvChunkSmall) {
+    if ((long long)s.items * BH >= resident_groups) break;
+    s = dkdv_split_chunk(T, c);
   }
   return s;
 }
