@@ -26,8 +26,10 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
-constexpr int kSplitTiles = 12;  // forward split length in 32-key tiles (measured: 12 balances
-                                 // small grids against split-partial traffic)
+// The forward workspace is sized for the split ca::fwd_split_tiles picks when
+// this many work groups are resident (the shortest the device can pick), so
+// its size is a function of the shape alone.
+constexpr int kFwdSplitBound = 1024;
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
@@ -65,6 +67,20 @@ int dkdv_resident_groups() {
   const int r = std::min(cus * ca::kDkdvGroupsPerCu, kDqSplitBound);
   if (dev >= 0 && dev < 64) cache[dev].store(r, std::memory_order_relaxed);
   return r;
+}
+
+// forward work groups resident on the current device (2 per CU, 1 for D > 64)
+int fwd_resident_groups(int D) {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  int cus = 0;
+  if (dev >= 0 && dev < 64) cus = cache[dev].load(std::memory_order_relaxed);
+  if (!cus) {
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    if (dev >= 0 && dev < 64) cache[dev].store(cus, std::memory_order_relaxed);
+  }
+  return std::min(cus * (D > 64 ? 1 : 2), kFwdSplitBound);
 }
 
 int dq_resident_groups() {
@@ -183,7 +199,8 @@ const char* ca_last_error(void) { return g_err; }
 
 size_t ca_fwd_workspace_bytes(int B, int H, int T, int D) {
   if (B <= 0 || H <= 0 || T <= 0) return 0;
-  return ca::fwd_part_floats(B * H, T, kSplitTiles, D) * sizeof(float);
+  return ca::fwd_part_floats(B * H, T, ca::fwd_split_tiles(B * H, T, kFwdSplitBound), D) *
+         sizeof(float);
 }
 
 int ca_fwd_f32(const float* q, const float* k, const float* v, const float* log_gain, float* out,
@@ -202,12 +219,14 @@ int ca_fwd_f32(const float* q, const float* k, const float* v, const float* log_
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;
   float* part = static_cast<float*>(workspace);
+  // the device's own residency: a split no shorter than the workspace's
+  const int C = ca::fwd_split_tiles(B * H, T, fwd_resident_groups(D));
   switch (D) {
-    case 8: e = ca::launch_fwd<8>(q, k, v, log_gain, out, stats, part, B, H, T, kSplitTiles, s); break;
-    case 16: e = ca::launch_fwd<16>(q, k, v, log_gain, out, stats, part, B, H, T, kSplitTiles, s); break;
-    case 32: e = ca::launch_fwd<32>(q, k, v, log_gain, out, stats, part, B, H, T, kSplitTiles, s); break;
-    case 64: e = ca::launch_fwd<64>(q, k, v, log_gain, out, stats, part, B, H, T, kSplitTiles, s); break;
-    default: e = ca::launch_fwd<128>(q, k, v, log_gain, out, stats, part, B, H, T, kSplitTiles, s); break;
+    case 8: e = ca::launch_fwd<8>(q, k, v, log_gain, out, stats, part, B, H, T, C, s); break;
+    case 16: e = ca::launch_fwd<16>(q, k, v, log_gain, out, stats, part, B, H, T, C, s); break;
+    case 32: e = ca::launch_fwd<32>(q, k, v, log_gain, out, stats, part, B, H, T, C, s); break;
+    case 64: e = ca::launch_fwd<64>(q, k, v, log_gain, out, stats, part, B, H, T, C, s); break;
+    default: e = ca::launch_fwd<128>(q, k, v, log_gain, out, stats, part, B, H, T, C, s); break;
   }
   if (e != hipSuccess) return fail(CA_ERR_HIP, "forward launch: %s", hipGetErrorString(e));
   return CA_OK;

@@ -23,6 +23,22 @@ inline int fwd_num_items(int T, int C) {
   for (int g = 0; g < G; ++g) n += (fwd_group_tiles(g, T) + C - 1) / C;
   return n;
 }
+// Split length: 12 tiles; for short rows (at most four 128-query groups) 8,
+// 6 or 4 while the grid of BH * items would not fill `resident` work groups.
+// Measured: with longer rows the shorter splits leave the forward's time
+// unchanged and only add combine traffic.
+constexpr int kFwdSplitTiles = 12;
+constexpr int kFwdSplitSmall[] = {8, 6, 4};
+constexpr int kFwdSplitShortT = 512;
+inline int fwd_split_tiles(int BH, int T, int resident) {
+  int C = kFwdSplitTiles;
+  if (T > kFwdSplitShortT) return C;
+  for (int c : kFwdSplitSmall) {
+    if ((long long)fwd_num_items(T, C) * BH >= resident) break;
+    C = c;
+  }
+  return C;
+}
 inline size_t fwd_part_floats(int BH, int T, int C, int D) {
   const int smax = fwd_max_splits(T, C);
   if (smax <= 1) return 0;

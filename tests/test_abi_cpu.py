@@ -38,9 +38,12 @@ def test_library_exports_every_header_symbol(ca):
 
 def test_workspace_sizes(ca):
     lib = ca.native.load()
-    # every 128-query group fits one forward split (<= 12 key tiles): no partials
-    assert lib.ca_fwd_workspace_bytes(2, 16, 384, 64) == 0
+    # every 128-query group fits one forward split (<= 12 key tiles) and the
+    # grid fills the device: no partials
+    assert lib.ca_fwd_workspace_bytes(16, 32, 384, 64) == 0
     assert lib.ca_fwd_workspace_bytes(2, 16, 512, 64) > 0
+    # a small grid takes shorter splits (4 tiles: 3 splits of the 12-tile group)
+    assert lib.ca_fwd_workspace_bytes(2, 16, 384, 64) == 2 * 16 * 3 * 384 * 66 * 4
     assert lib.ca_fwd_workspace_bytes(2, 16, 2048, 64) > 0
     nqt = 2048 // 32
     ds_bytes = 2 * 16 * (nqt * (nqt + 1) // 2) * 1024 * 4
