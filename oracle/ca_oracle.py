@@ -18,7 +18,8 @@ Every array here is float64.  Rows are addressed by an explicit query index so
 that the same code checks a full ``[T, T]`` problem or a few sampled rows of a
 T=8192 problem (row ``i`` of W and dS depends only on row ``i`` of S).
 
-Pinning (see tests/test_oracle_*.py): trapezoid quadrature of the segment
+Pinning (tests/test_oracle.py; the kernels' scalar forms in
+tests/test_device_math.py): trapezoid quadrature of the segment
 integrals and of the full per-query integral (the known-answer input of
 test_acma.py:49-69), the uniform/softmax limit, single-token W=1, offset
 invariance, row sums, exact future zeros, float64 autograd through an
