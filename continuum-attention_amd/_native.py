@@ -54,13 +54,15 @@ SIGNATURES = {
     "ca_adamw_step": (_i, [_vp, _i, _vp, _i, _vp, ctypes.c_float, ctypes.c_float, ctypes.c_float,
                            ctypes.c_float, ctypes.c_float, _i, _vp]),
     "ca_bf16_shadow": (_i, [_vp, _i, _vp, _i, _vp]),
+    "ca_swiglu_fwd_f32": (_i, [_vp, _vp, _i, _i, _vp]),
+    "ca_swiglu_bwd_f32": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
     "ca_timing_enable": (_i, [_i]),
     "ca_timing_read": (_i, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i), _i]),
 }
 
 KERNEL_NAMES = ("ca_fwd", "ca_fwd_combine", "ca_bwd_prep", "ca_bwd_dkdv", "ca_bwd_dq",
                 "ca_bwd_gain_merge", "ca_weights", "ca_weights_bwd", "ca_qkv_in", "ca_qkv_grad",
-                "ca_relayout", "ca_rmsnorm_fwd", "ca_rmsnorm_bwd")
+                "ca_relayout", "ca_rmsnorm_fwd", "ca_rmsnorm_bwd", "ca_swiglu_fwd", "ca_swiglu_bwd")
 
 _lib = None
 

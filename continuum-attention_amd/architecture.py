@@ -33,6 +33,7 @@ import torch
 from torch import nn
 from torch.nn import functional as F
 
+from . import _native
 from .decoder import RMSNorm as _DecoderRMSNorm
 from .decoder import rope_continuum_attention
 from .ops import SUPPORTED_HEAD_DIMS, continuum_attention
@@ -141,14 +142,58 @@ class CausalAttention(nn.Module):
         return self.out(y.transpose(1, 2).reshape(Bsz, T, self.width))
 
 
+class _SwiGLUFn(torch.autograd.Function):
+    """silu(gate) * value over the halves of u = [gate | value] as one HIP
+    pass each way (ca_swiglu_fwd_f32 / ca_swiglu_bwd_f32); the backward writes
+    the gradient of u whole, so no concatenation of the halves' gradients."""
+
+    @staticmethod
+    def forward(ctx, u):
+        lib = _native.load()
+        H = u.shape[-1] // 2
+        N = u.numel() // (2 * H)
+        uc = u.detach()
+        h = torch.empty(u.shape[:-1] + (H,), device=u.device, dtype=torch.float32)
+        with _native.on_device(u.device):
+            _native.check(lib.ca_swiglu_fwd_f32(uc.data_ptr(), h.data_ptr(), N, H,
+                                                _native.stream_handle(u.device)))
+        ctx.save_for_backward(uc)
+        return h
+
+    @staticmethod
+    def backward(ctx, dh):
+        if torch.is_grad_enabled():
+            raise RuntimeError("the fused SwiGLU supports first-order gradients only")
+        (uc,) = ctx.saved_tensors
+        lib = _native.load()
+        H = uc.shape[-1] // 2
+        N = uc.numel() // (2 * H)
+        g = dh.float().contiguous()
+        if g.data_ptr() % 16:
+            g = g.clone()
+        du = torch.empty_like(uc)
+        with _native.on_device(uc.device):
+            _native.check(lib.ca_swiglu_bwd_f32(uc.data_ptr(), g.data_ptr(), du.data_ptr(), N, H,
+                                                _native.stream_handle(uc.device)))
+        return du
+
+
 class SwiGLU(nn.Module):
+    """SwiGLU MLP (architecture.py:180-188).  On fp32 GPU activations the
+    gate runs as _SwiGLUFn; ``SwiGLU.fused = False`` restores the composition."""
+    fused = True
+
     def __init__(self, width, hidden):
         super().__init__()
         self.gate_up = nn.Linear(width, 2 * hidden, bias=False)
         self.down = nn.Linear(hidden, width, bias=False)
 
     def forward(self, x):
-        gate, value = self.gate_up(x).chunk(2, dim=-1)
+        u = self.gate_up(x)
+        if (self.fused and u.is_cuda and u.dtype == torch.float32 and u.is_contiguous()
+                and u.shape[-1] % 8 == 0 and u.data_ptr() % 16 == 0 and u.numel() > 0):
+            return self.down(_SwiGLUFn.apply(u))
+        gate, value = u.chunk(2, dim=-1)
         return self.down(F.silu(gate) * value)
 
 

@@ -394,6 +394,38 @@ int ca_tokens_to_heads(const void* x, int dtype, float* out, int B, int H, int T
   return relayout("ca_tokens_to_heads", x, out, dtype, false, B, H, T, D, stream);
 }
 
+static int check_swiglu(const char* fn, const void* a, const void* b, const void* c, int N,
+                        int H) {
+  if (N <= 0 || H <= 0 || H % 4) return fail(CA_ERR_INVALID, "%s: invalid shape N=%d H=%d (H %% 4 == 0)", fn, N, H);
+  if ((long long)N * 2 * H > (1ll << 40)) return fail(CA_ERR_UNSUPPORTED, "%s: tensor too large", fn);
+  if (!a || !b || !c) return fail(CA_ERR_INVALID, "%s: null pointer", fn);
+  if (!aligned16(a) || !aligned16(b) || !aligned16(c))
+    return fail(CA_ERR_INVALID, "%s: pointers must be 16-byte aligned", fn);
+  return CA_OK;
+}
+
+int ca_swiglu_fwd_f32(const float* u, float* h, int N, int H, void* stream) {
+  int rc = check_swiglu("ca_swiglu_fwd_f32", u, h, h, N, H);
+  if (rc) return rc;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  ca::timer_begin(ca::kSwigluFwd, s);
+  hipError_t e = ca::launch_swiglu_fwd(u, h, N, H, s);
+  ca::timer_end(ca::kSwigluFwd, s);
+  if (e != hipSuccess) return fail(CA_ERR_HIP, "ca_swiglu_fwd_f32 launch: %s", hipGetErrorString(e));
+  return CA_OK;
+}
+
+int ca_swiglu_bwd_f32(const float* u, const float* dh, float* du, int N, int H, void* stream) {
+  int rc = check_swiglu("ca_swiglu_bwd_f32", u, dh, du, N, H);
+  if (rc) return rc;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  ca::timer_begin(ca::kSwigluBwd, s);
+  hipError_t e = ca::launch_swiglu_bwd(u, dh, du, N, H, s);
+  ca::timer_end(ca::kSwigluBwd, s);
+  if (e != hipSuccess) return fail(CA_ERR_HIP, "ca_swiglu_bwd_f32 launch: %s", hipGetErrorString(e));
+  return CA_OK;
+}
+
 static int check_norm(const char* fn, int N, int C, int dtype) {
   if (N <= 0 || C <= 0) return fail(CA_ERR_INVALID, "%s: invalid shape N=%d C=%d", fn, N, C);
   if (C > ca::kRmsMaxCols) return fail(CA_ERR_UNSUPPORTED, "%s: C=%d exceeds %d", fn, C, ca::kRmsMaxCols);

@@ -211,7 +211,7 @@ inline DkdvSplit dkdv_split(int BH, int T, int resident_groups) {
 // Per-kernel HIP-event timing (diagnostics; off unless ca_timing_enable(1)).
 enum KernelId {
   kFwd = 0, kFwdCombine, kBwdPrep, kBwdDkdv, kBwdDq, kBwdGain, kWeights, kWeightsBwd, kQkvIn,
-  kQkvGrad, kRelayout, kRmsFwd, kRmsBwd, kNumKernels
+  kQkvGrad, kRelayout, kRmsFwd, kRmsBwd, kSwigluFwd, kSwigluBwd, kNumKernels
 };
 
 // Element types of the prologue / epilogue buffers (CA_DTYPE_* in the ABI).
@@ -234,6 +234,12 @@ hipError_t launch_rmsnorm_fwd(const float* x, const void* res, int rdtype, float
 hipError_t launch_rmsnorm_bwd(const void* dy, int dydtype, const float* dsum, const float* x,
                               const float* w, const float* rstd, float* dx, void* dres, int rdtype,
                               float* dw, float* dw_part, int N, int C, hipStream_t s);
+
+// SwiGLU gate of the TinyLM MLP (ca_swiglu.hip): u [N][2H] = [g | v],
+// h [N][H] = silu(g) * v, du [N][2H]; H % 4 == 0, 16-byte aligned rows.
+hipError_t launch_swiglu_fwd(const float* u, float* h, int N, int H, hipStream_t s);
+hipError_t launch_swiglu_bwd(const float* u, const float* dh, float* du, int N, int H,
+                             hipStream_t s);
 
 // AdamW step (ca_optim.hip): chunks of kOptChunk elements.
 constexpr int kOptChunk = 16384;

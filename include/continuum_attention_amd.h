@@ -121,6 +121,16 @@ int ca_heads_to_tokens(const float* y, void* out, int dtype, int B, int H, int T
 int ca_tokens_to_heads(const void* x, int dtype, float* out, int B, int H, int T, int D,
                        void* stream);
 
+/* ---- SwiGLU gate of the TinyLM MLP ----------------------------------------
+ * No reference counterpart: F.silu(gate) * value of SwiGLU.forward
+ * (architecture.py:186-188), run there as torch's silu and multiply kernels,
+ * and their autograd with the chunk's gradient concatenation.  u [N][2H] fp32
+ * = [gate | value] (the gate_up projection's output), h [N][H] fp32, dh
+ * [N][H], du [N][2H] = [d gate | d value]; H % 4 == 0, pointers 16-byte
+ * aligned. */
+int ca_swiglu_fwd_f32(const float* u, float* h, int N, int H, void* stream);
+int ca_swiglu_bwd_f32(const float* u, const float* dh, float* du, int N, int H, void* stream);
+
 /* ---- RMSNorm of the decoder caller ----------------------------------------
  * y = weight * x * rsqrt(mean(x^2) + eps) over rows of C values
  * (RMSNorm.forward, cuda/continuum_attention.py:817-823, run there as a chain

@@ -672,3 +672,56 @@ def test_tinylm_fused_prologue_matches_composition(gpu_ca, variant):
     worst = max(eg.values())
     say(f"   logits {el:.2e} worst grad {worst:.2e} ({max(eg, key=eg.get)})")
     assert el <= 1e-5 and worst <= 1e-4
+
+
+@pytest.mark.parametrize("N,H,scale", [(37, 4, 1.0), (8192, 720, 1.0), (300, 256, 30.0),
+                                       (5, 16, 120.0)])
+def test_fused_swiglu_matches_composition(gpu_ca, N, H, scale):
+    """The fused SwiGLU gate (ca_swiglu_fwd_f32 / ca_swiglu_bwd_f32) against
+    torch's silu(gate) * value and its autograd: same formulas in the same
+    order, so equal to a few ulp; |g| > 88 (scale 120) checks the capped
+    exponent, where torch's silu gives -0 and the kernel a denormal.  Bar:
+    1e-6 as max|x - ref| / max|ref| on h and du."""
+    say(f"[case] fused SwiGLU N={N} H={H} scale={scale}")
+    A = gpu_ca.architecture
+    torch.manual_seed(N + H)
+    u = (torch.randn(N, 2 * H, device="cuda") * scale).requires_grad_(True)
+    dh = torch.randn(N, H, device="cuda")
+    h = A._SwiGLUFn.apply(u)
+    (du,) = torch.autograd.grad(h, u, dh)
+    u2 = u.detach().clone().requires_grad_(True)
+    g, v = u2.chunk(2, dim=-1)
+    h2 = F.silu(g) * v
+    (du2,) = torch.autograd.grad(h2, u2, dh)
+    # per tensor, max|x - ref| / max|ref|: element-wise the two differ
+    # relatively where values are tiny (silu of g << 0, whose exp argument
+    # reduction errs by about |g| ulp) or where 1 + g (1 - s) cancels (g near
+    # -1.28, a one-ulp difference in s amplified)
+    eh = rel(h.detach().cpu().numpy(), h2.detach().cpu().numpy())
+    e = rel(du.cpu().numpy(), du2.cpu().numpy())
+    say(f"   h max rel {eh:.2e}, du max rel {e:.2e}")
+    assert eh <= 1e-6 and e <= 1e-6
+
+
+def test_tinylm_fused_swiglu_step(gpu_ca):
+    """A TinyLM (variant P, fp32) loss and every parameter gradient with the
+    fused SwiGLU gate against SwiGLU.fused = False (torch's composition)."""
+    say("[case] TinyLM fused SwiGLU vs composition")
+    A = gpu_ca.architecture
+    torch.manual_seed(41)
+    m = A.TinyLM(variant="P", backend="hip", seq_len=128, width=64, hidden=96, heads=4,
+                 fixed_tau=0.30, layers=2).cuda()
+    ids = torch.randint(0, 256, (3, 129), device="cuda")
+    out = {}
+    try:
+        for fused in (True, False):
+            A.SwiGLU.fused = fused
+            m.zero_grad(set_to_none=True)
+            loss = F.cross_entropy(m(ids[:, :-1]).reshape(-1, 256), ids[:, 1:].reshape(-1))
+            loss.backward()
+            out[fused] = (loss.item(), [p.grad.clone() for p in m.parameters()])
+    finally:
+        A.SwiGLU.fused = True
+    assert abs(out[True][0] - out[False][0]) <= 1e-6 * abs(out[False][0])
+    for a, b in zip(out[True][1], out[False][1]):
+        torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-7)
