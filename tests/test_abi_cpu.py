@@ -140,3 +140,23 @@ def test_opt_tensor_layout_matches_header(tmp_path):
     opt = importlib.import_module("continuum-attention_amd.optim")
     want = [ctypes.sizeof(opt._OptTensor)] + [getattr(opt._OptTensor, f).offset for f in fields]
     assert got == want
+
+
+@pytest.mark.parametrize("N,H", [(0, 8), (4, 0), (4, 6), (-1, 8)])
+def test_swiglu_argument_errors_before_any_launch(ca, N, H):
+    """ca_swiglu_fwd_f32 / ca_swiglu_bwd_f32 reject empty or negative shapes
+    and H not a multiple of 4, before touching the pointers."""
+    lib = ca.native.load()
+    p = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    assert lib.ca_swiglu_fwd_f32(p, p, N, H, None) == 1
+    assert lib.ca_last_error().decode().startswith("ca_swiglu_fwd_f32")
+    assert lib.ca_swiglu_bwd_f32(p, p, p, N, H, None) == 1
+
+
+def test_swiglu_null_and_misaligned_pointers(ca):
+    lib = ca.native.load()
+    p, odd = ctypes.c_void_p(4096), ctypes.c_void_p(4100)
+    assert lib.ca_swiglu_fwd_f32(None, p, 4, 8, None) == 1
+    assert b"null" in lib.ca_last_error()
+    assert lib.ca_swiglu_bwd_f32(p, odd, p, 4, 8, None) == 1
+    assert b"aligned" in lib.ca_last_error()
