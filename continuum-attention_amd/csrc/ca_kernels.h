@@ -152,7 +152,9 @@ inline DqSplit dq_split(int BH, int T, int resident_groups) {
   }
   return s;
 }
-// dQ work groups resident per CU (VGPR-limited: 3 waves per SIMD)
+// dQ work groups per CU the split heuristic counts as resident: 3, although
+// the D = 64 kernel's 126 VGPRs allow 4 (counting 4 picks 48-block chunks at
+// [2,16,2048,64] and measured 4% slower)
 constexpr int kDqGroupsPerCu = 3;
 
 // dK/dV work items: key-block group wg (kDkdvWaves blocks, kDkdvKeys keys) of
