@@ -123,7 +123,13 @@ class CausalAttention(nn.Module):
         if self.variant in ("F", "G", "S", "H"):
             return self.log_qk_gain
         g = math.log(1.0 / self.fixed_tau) if self.variant in ("B", "P") else 0.0
-        return torch.full((self.heads,), g, device=device, dtype=torch.float32)
+        # a constant: kept per (device, value), not rebuilt every step
+        cache = self.__dict__.setdefault("_gain_cache", {})
+        key = (device, self.heads, g)
+        t = cache.get(key)
+        if t is None:
+            t = cache[key] = torch.full((self.heads,), g, device=device, dtype=torch.float32)
+        return t
 
     def forward(self, x):
         Bsz, T, _ = x.shape
