@@ -10,8 +10,9 @@ operator with inputs already resident in HBM.
 Prints ONE JSON line (rank 0).  `value` is the median fwd+bwd milliseconds
 (lower is better) of uninstrumented steps.  `roofline` is for the dominant
 kernel, from HIP events recorded around each kernel launch on the launch
-stream during a second run of the same steps; `cpu_baseline` times the CPU port of the reference's PyTorch CPU path
-(oracle/ca_cpu_port.py) on a bounded sample of the same workload.
+stream during a second run of the same steps; `cpu_baseline` times the CPU
+port of the reference's PyTorch CPU path (oracle/ca_cpu_port.py) on the same
+workload in full (and on config 1).
 
 Two more BASELINE workloads ride along on the same line (skip with
 --no-models): `ca_s`, the CA-S decoder training step in tokens/s (config 4,
@@ -48,16 +49,38 @@ def kernel_flops_per_pair(D):
             "ca_bwd_dq": 2 * D}     # dQ = dS K
 
 
-def cpu_baseline(sample_heads=4, reps=3):
+def _cpu_model():
+    """The host CPU's model name (lscpu, else /proc/cpuinfo)."""
+    import subprocess
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.strip().startswith("Model name"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def _time_port(P, shape, seed_order, reps):
+    """Median forward and backward seconds of the CPU port on one shape."""
     import torch
-    from oracle import ca_cpu_port as P
-    threads = len(os.sched_getaffinity(0))
-    torch.set_num_threads(threads)
-    B, H, T, D = SHAPE
-    g = torch.Generator().manual_seed(0)
-    q, k, v, dy = (torch.randn(1, sample_heads, T, D, generator=g) for _ in range(4))
-    rho = torch.zeros(sample_heads)
+    B, H, T, D = shape
+    if seed_order:
+        torch.manual_seed(0)  # BASELINE config 1: manual_seed(0), then q, k, v, dY
+        q, k, v, dy = (torch.randn(shape) for _ in range(4))
+    else:
+        g = torch.Generator().manual_seed(0)
+        q, k, v, dy = (torch.randn(shape, generator=g) for _ in range(4))
+    rho = torch.zeros(H)
     P.port_forward(q, k, v, rho, 128)  # warm-up
+    P.port_backward(q, k, v, rho, dy, 128)
     fw, bw = [], []
     for _ in range(reps):
         t0 = time.perf_counter()
@@ -67,23 +90,30 @@ def cpu_baseline(sample_heads=4, reps=3):
         t2 = time.perf_counter()
         fw.append(t1 - t0)
         bw.append(t2 - t1)
-    scale = (B * H) / sample_heads
-    total_ms = (statistics.median(fw) + statistics.median(bw)) * 1e3 * scale
-    model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {"value": round(total_ms, 1), "unit": "ms per fwd+bwd (extrapolated)",
+    return statistics.median(fw), statistics.median(bw)
+
+
+def cpu_baseline(reps=3):
+    """The reference's PyTorch CPU path (its restatement in
+    oracle/ca_cpu_port.py, query_tile=128) timed on this host's cores at
+    BASELINE config 2 in full, and at config 1."""
+    import torch
+    from oracle import ca_cpu_port as P
+    affinity = len(os.sched_getaffinity(0))
+    torch.set_num_threads(affinity)
+    f2, b2 = _time_port(P, SHAPE, False, reps)
+    f1, b1 = _time_port(P, (1, 2, 64, 16), True, 20)
+    return {"value": round((f2 + b2) * 1e3, 1), "unit": "ms per fwd+bwd",
             "cores": torch.get_num_threads(), "kind": "port",
-            "sample": (f"[1,{sample_heads},{T},{D}] fp32 fwd+bwd, query_tile=128, median of {reps} "
-                       f"after 1 warm-up, x{scale:g} for the [2,16,2048,64] workload"),
-            "fwd_ms": round(statistics.median(fw) * 1e3 * scale, 1),
-            "bwd_ms": round(statistics.median(bw) * 1e3 * scale, 1),
-            "cpu_model": model, "os_cpu_count": os.cpu_count(), "affinity": threads}
+            "sample": (f"BASELINE config 2 in full ([2,16,2048,64] fp32 fwd+bwd, seed 0, "
+                       f"query_tile=128), median of {reps} after 1 warm-up"),
+            "fwd_ms": round(f2 * 1e3, 1), "bwd_ms": round(b2 * 1e3, 1),
+            "config1": {"shape": [1, 2, 64, 16], "fwd_ms": round(f1 * 1e3, 3),
+                        "bwd_ms": round(b1 * 1e3, 3), "sample": "median of 20 after 1 warm-up"},
+            "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count(), "affinity": affinity,
+            "torch_threads": torch.get_num_threads(),
+            "note": "threads = the affinity set; the reference launcher's OMP_NUM_THREADS=2 "
+                    "(cuda/run.sh:8) is overridden"}
 
 
 def _timed_steps(ca, step, steps, warmup):

@@ -17,8 +17,8 @@ from . import _native as native
 from .ops import (SUPPORTED_HEAD_DIMS, _CAExactTiled, ca_backward, ca_forward,
                   continuum_attention)
 from .weights import ca_weights, ca_weights_backward, continuous_attention_weights
-from . import architecture, decoder, optim
+from . import architecture, decoder, ops, optim
 
 __all__ = ["continuum_attention", "_CAExactTiled", "ca_forward", "ca_backward", "native",
            "SUPPORTED_HEAD_DIMS", "ca_weights", "ca_weights_backward",
-           "continuous_attention_weights", "architecture", "decoder", "optim"]
+           "continuous_attention_weights", "architecture", "decoder", "ops", "optim"]

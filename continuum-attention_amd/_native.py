@@ -58,6 +58,7 @@ SIGNATURES = {
     "ca_swiglu_bwd_f32": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
     "ca_timing_enable": (_i, [_i]),
     "ca_timing_read": (_i, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i), _i]),
+    "ca_debug_set_splits": (_i, [_i, _i, _i]),
 }
 
 KERNEL_NAMES = ("ca_fwd", "ca_fwd_combine", "ca_bwd_prep", "ca_bwd_dkdv", "ca_bwd_dq",

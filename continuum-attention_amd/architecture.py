@@ -7,8 +7,13 @@ state-dict keys are the reference's, so its checkpoints load unchanged and the
 parameter budgets agree (5,008,640 / 5,008,664 at seq_len 192, test_acma.py:
 21-26; 5,090,560 / 5,090,584 at 512, test_hp_only.py:13-23).
 
-Backends for the continuous variants (all run the HIP kernels, none has a CPU
-path):
+The weight-level functions of the reference module are here too:
+``segment_integral_coefficients(delta) -> (L, mu)`` (architecture.py:32-62)
+and ``continuous_attention_weights(logits)`` (architecture.py:65-105), so the
+reference's tests import them from this module unchanged.
+
+Backends for the continuous variants on GPU tensors (CPU tensors run the
+operator's and the weights' CPU path, as the reference's modules do):
 
 * ``'hip'``: the fused operator ``continuum_attention`` (no ``[T, T]`` tensor);
   the variant's q scaling (``1/tau`` or ``exp(log_qk_gain)``) is applied to q
@@ -37,7 +42,32 @@ from . import _native
 from .decoder import RMSNorm as _DecoderRMSNorm
 from .decoder import rope_continuum_attention
 from .ops import SUPPORTED_HEAD_DIMS, continuum_attention
+from .cpu import _C_J0, _C_RIGHT, _SERIES_BELOW, _series
 from .weights import continuous_attention_weights
+
+__all__ = ["segment_integral_coefficients", "continuous_attention_weights", "RMSNorm",
+           "CausalAttention", "SwiGLU", "Block", "TinyLM", "parameters", "build_adamw",
+           "build_fused_adamw", "train_step", "VARIANTS"]
+
+
+def segment_integral_coefficients(delta):
+    """``(L, mu)`` for segments with endpoint logits a, b and ``delta = b - a``
+    (architecture.py:32-62): ``exp(max(a, b)) * L`` is the segment's mass,
+    ``L = (1 - e^-|delta|) / |delta|`` = J0(-|delta|) (1 at 0), and
+    ``mu = J1(delta) / J0(delta)`` is the share of the right endpoint (1/2 at
+    0), with ``J_n(x) = int_0^1 u^n e^(x u) du``.  Below |delta| = 1 both are
+    20-term power series (J0, J1 coefficients 1/(k+1)!, 1/(k!(k+2))), above it
+    the closed forms; torch ops on any device, differentiable."""
+    t = delta.abs()
+    small = t < _SERIES_BELOW
+    ts = torch.where(small, t, torch.zeros_like(t))
+    tc = torch.where(small, torch.ones_like(t), t)
+    L = torch.where(small, _series(-ts, _C_J0), -torch.expm1(-tc) / tc)
+    ds = torch.where(small, delta, torch.zeros_like(delta))
+    mu_series = _series(ds, _C_RIGHT) / _series(ds, _C_J0)
+    mu_hi = 1.0 / (-torch.expm1(-tc)) - 1.0 / tc             # mu at +|delta|
+    mu = torch.where(small, mu_series, torch.where(delta >= 0, mu_hi, 1.0 - mu_hi))
+    return L, mu
 
 VARIANTS = ("A", "B", "F", "G", "P", "R", "S", "H")
 _BACKEND_MAP = {"hip": "hip", "hip_weights": "hip_weights", "reference": "hip_weights",

@@ -22,10 +22,6 @@ HIPCC_FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-ffp-contract=fast",
-    # no output depends on a NaN or infinity (the backward's fast-path segment
-    # math may form them in lane 0, which has no left neighbour, and discards
-    # them); lets fmax/fmin skip canonicalisation
-    "-fno-honor-nans", "-fno-honor-infinities",
     # packed fp32 VALU forms are disabled: some of them have returned wrong
     # results on this GPU pool with no error
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
@@ -37,10 +33,21 @@ HIPCC_FLAGS = [
 ]
 
 
+# The attention kernels compute no output from a NaN or infinity they form
+# themselves (the backward's fast-path segment math may form one in lane 0,
+# which has no left neighbour, and discards it), so they are built assuming
+# finite values, which lets fmax/fmin skip canonicalisation.  NaN or infinite
+# inputs still propagate through their arithmetic (tests pin that).  The
+# other sources (norms, optimizer, SwiGLU, weight rows) keep IEEE semantics:
+# a diverging run's non-finite values must behave there as in torch.
+_FINITE_MATH = ["-fno-honor-nans", "-fno-honor-infinities"]
+
 # Per-source flags: the dK/dV kernel schedules better with LLVM's max-ILP
 # machine-scheduler strategy (about 2% faster); the other kernels are slower
 # with it, so it applies to that translation unit only.
-SOURCE_FLAGS = {"ca_bwd_dkdv.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]}
+SOURCE_FLAGS = {"ca_fwd.hip": _FINITE_MATH,
+                "ca_bwd.hip": _FINITE_MATH,
+                "ca_bwd_dkdv.hip": _FINITE_MATH + ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]}
 
 
 def hipcc() -> str:

@@ -98,12 +98,38 @@ int dq_resident_groups() {
   return r;
 }
 
+// Forced split lengths (ca_debug_set_splits; 0 = automatic).  When one is
+// set, the workspace sizes and the launches both use it, so the two agree.
+struct SplitOverride {
+  int fwd_tiles = 0, dq_blocks = 0, dkdv_tiles = 0;
+};
+SplitOverride g_split;
+
+// Forward split length: for_sizing picks the shortest split any device can
+// choose (the workspace bound), otherwise the current device's choice.
+int fwd_split(int BH, int T, int D, bool for_sizing) {
+  if (g_split.fwd_tiles > 0) return g_split.fwd_tiles;
+  return ca::fwd_split_tiles(BH, T, for_sizing ? kFwdSplitBound : fwd_resident_groups(D));
+}
+ca::DqSplit dq_split_for(int BH, int T, int D, bool for_sizing) {
+  if (g_split.dq_blocks > 0) return ca::dq_split_chunk(T, g_split.dq_blocks);
+  // D = 128 kernels hold fewer dQ work groups per CU (two instead of three)
+  const int res = for_sizing ? kDqSplitBound : (D > 64 ? dq_resident_groups() * 2 / 3 : dq_resident_groups());
+  return ca::dq_split(BH, T, res);
+}
+ca::DkdvSplit dkdv_split_for(int BH, int T, int D, bool for_sizing) {
+  if (g_split.dkdv_tiles > 0) return ca::dkdv_split_chunk(T, g_split.dkdv_tiles);
+  // D = 128: one dK/dV work group per CU instead of two (registers and LDS)
+  const int res = for_sizing ? kDqSplitBound : (D > 64 ? dkdv_resident_groups() / 2 : dkdv_resident_groups());
+  return ca::dkdv_split(BH, T, res);
+}
+
 struct BwdLayout {
   size_t ds, limbs, qstat, gain, dqpart, kvpart, total;
 };
 BwdLayout bwd_layout(int B, int H, int T, int D) {
   const int BH = B * H;
-  const ca::DqSplit sp = ca::dq_split(BH, T, kDqSplitBound);  // the largest split
+  const ca::DqSplit sp = dq_split_for(BH, T, D, true);  // the largest split
   BwdLayout L;
   L.ds = 0;
   L.limbs = align256(ca::bwd_ds_floats(BH, T) * sizeof(float));
@@ -111,7 +137,7 @@ BwdLayout bwd_layout(int B, int H, int T, int D) {
   L.gain = L.qstat + align256((size_t)BH * T * 2 * sizeof(float));
   L.dqpart = L.gain + align256((size_t)BH * sp.items * sizeof(float));
   L.kvpart = L.dqpart + align256((size_t)BH * sp.part_items * ca::kDqRows * D * sizeof(float));
-  const ca::DkdvSplit kvs = ca::dkdv_split(BH, T, kDqSplitBound);  // the largest split
+  const ca::DkdvSplit kvs = dkdv_split_for(BH, T, D, true);  // the largest split
   L.total = L.kvpart + align256((size_t)BH * kvs.part_items * ca::kDkdvKeys * 2 * D * sizeof(float));
   return L;
 }
@@ -193,14 +219,22 @@ int ca_timing_read(double* total_ms, int* launches, int n) {
 }
 
 
+int ca_debug_set_splits(int fwd_split_tiles, int dq_chunk_blocks, int dkdv_chunk_tiles) {
+  if (fwd_split_tiles < 0 || dq_chunk_blocks < 0 || dkdv_chunk_tiles < 0)
+    return fail(CA_ERR_INVALID, "ca_debug_set_splits: lengths must be >= 0 (0 = automatic)");
+  g_split.fwd_tiles = fwd_split_tiles;
+  g_split.dq_blocks = dq_chunk_blocks;
+  g_split.dkdv_tiles = dkdv_chunk_tiles;
+  return CA_OK;
+}
+
 int ca_abi_version(void) { return CA_ABI_VERSION; }
 
 const char* ca_last_error(void) { return g_err; }
 
 size_t ca_fwd_workspace_bytes(int B, int H, int T, int D) {
   if (B <= 0 || H <= 0 || T <= 0) return 0;
-  return ca::fwd_part_floats(B * H, T, ca::fwd_split_tiles(B * H, T, kFwdSplitBound), D) *
-         sizeof(float);
+  return ca::fwd_part_floats(B * H, T, fwd_split(B * H, T, D, true), D) * sizeof(float);
 }
 
 int ca_fwd_f32(const float* q, const float* k, const float* v, const float* log_gain, float* out,
@@ -220,7 +254,7 @@ int ca_fwd_f32(const float* q, const float* k, const float* v, const float* log_
   hipError_t e;
   float* part = static_cast<float*>(workspace);
   // the device's own residency: a split no shorter than the workspace's
-  const int C = ca::fwd_split_tiles(B * H, T, fwd_resident_groups(D));
+  const int C = fwd_split(B * H, T, D, false);
   switch (D) {
     case 8: e = ca::launch_fwd<8>(q, k, v, log_gain, out, stats, part, B, H, T, C, s); break;
     case 16: e = ca::launch_fwd<16>(q, k, v, log_gain, out, stats, part, B, H, T, C, s); break;
@@ -245,9 +279,9 @@ int ca_bwd_f32(const float* q, const float* k, const float* v, const float* log_
   if (rc) return rc;
   if (!q || !k || !v || !log_gain || !out || !stats || !dout || !dq || !dk || !dv || !dlog_gain)
     return fail(CA_ERR_INVALID, "null tensor pointer");
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dout) || !aligned16(dk) ||
-      !aligned16(dv))
-    return fail(CA_ERR_INVALID, "q, k, v, dout, dk and dv must be 16-byte aligned");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) || !aligned16(dout) ||
+      !aligned16(dq) || !aligned16(dk) || !aligned16(dv))
+    return fail(CA_ERR_INVALID, "q, k, v, out, dout, dq, dk and dv must be 16-byte aligned");
   const BwdLayout L = bwd_layout(B, H, T, D);
   if (!workspace || workspace_bytes < L.total)
     return fail(CA_ERR_WORKSPACE, "backward workspace of %zu bytes required, %zu given", L.total,
@@ -260,12 +294,8 @@ int ca_bwd_f32(const float* q, const float* k, const float* v, const float* log_
   work.gain_part = reinterpret_cast<float*>(ws + L.gain);
   work.dq_part = reinterpret_cast<float*>(ws + L.dqpart);
   work.kv_part = reinterpret_cast<float*>(ws + L.kvpart);
-  // D = 128 kernels hold fewer work groups per CU (dK/dV one instead of two,
-  // dQ two instead of three: register and LDS budgets)
-  const int dq_res = D > 64 ? dq_resident_groups() * 2 / 3 : dq_resident_groups();
-  const int kv_res = D > 64 ? dkdv_resident_groups() / 2 : dkdv_resident_groups();
-  const ca::DqSplit sp = ca::dq_split(B * H, T, dq_res);
-  const ca::DkdvSplit kvs = ca::dkdv_split(B * H, T, kv_res);
+  const ca::DqSplit sp = dq_split_for(B * H, T, D, false);
+  const ca::DkdvSplit kvs = dkdv_split_for(B * H, T, D, false);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;
   switch (D) {

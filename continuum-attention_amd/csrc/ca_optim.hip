@@ -109,8 +109,10 @@ __global__ __launch_bounds__(256) void ca_clip_coef_kernel(const float* __restri
   if (threadIdx.x == 0) {
     const float norm = sqrtf((red[0] + red[1]) + (red[2] + red[3]));
     total_norm[0] = norm;
+    // clip_grad_norm_'s clamp(max_norm / (norm + 1e-6), max=1): an infinite
+    // norm gives 0, a NaN norm gives NaN (the comparison is false for NaN)
     const float c = max_norm / (norm + 1e-6f);
-    coef[0] = max_norm > 0.f ? (c < 1.f ? c : 1.f) : 1.f;
+    coef[0] = max_norm > 0.f ? (c >= 1.f ? 1.f : c) : 1.f;
   }
 }
 

@@ -20,8 +20,12 @@ dims run the reference's query-tile structure, where it does bound memory.  All 
 exact fp32 path (the reference modes differ only in fp16 rounding and launch
 structure).
 
-There is no CPU path here: the operator runs on ROCm devices only and raises
-otherwise.  CPU checking code lives in ``oracle/`` (tests only).
+GPU tensors run the HIP kernels only (a missing library raises; there is no
+fallback).  CPU tensors run ``cpu.py``, this package's own float32
+formulation of the reference's CPU branch (``ext=None``,
+cuda/continuum_attention.py:658, 688, 737-751), with the reference's CPU-side
+errors: ``CA_CUDA_MODE`` prefix_v5/prefix_v6 need CUDA fp16 tensors, and
+'fused' needs T <= 2048, D <= 128 and fp16/fp32 values (:662-665).
 """
 from __future__ import annotations
 
@@ -31,6 +35,7 @@ import os
 import torch
 
 from . import _native
+from . import cpu as _cpu
 
 _MODES = ("dense", "prefix", "fused", "prefix_v5", "prefix_v6")
 SUPPORTED_HEAD_DIMS = (8, 16, 32, 64, 128)
@@ -65,6 +70,18 @@ def _fwd_workspace_bytes(B: int, H: int, T: int, D: int) -> int:
 @functools.lru_cache(maxsize=256)
 def _bwd_workspace_bytes(B: int, H: int, T: int, D: int) -> int:
     return int(_native.load().ca_bwd_workspace_bytes(B, H, T, D))
+
+
+def set_split_override(fwd_split_tiles: int = 0, dq_chunk_blocks: int = 0,
+                       dkdv_chunk_tiles: int = 0) -> None:
+    """Forces the kernels' work-split lengths (0 = automatic; see
+    ``ca_debug_set_splits`` in the C header).  For tests: the automatic
+    choice depends on the device's CU count, so a forced length runs each one
+    at a small shape.  Clears the cached workspace sizes, which follow it."""
+    _native.check(_native.load().ca_debug_set_splits(int(fwd_split_tiles), int(dq_chunk_blocks),
+                                                     int(dkdv_chunk_tiles)))
+    _fwd_workspace_bytes.cache_clear()
+    _bwd_workspace_bytes.cache_clear()
 
 
 def _check_device(*ts: torch.Tensor) -> torch.device:
@@ -213,19 +230,33 @@ class _CAExactTiled(torch.autograd.Function):
             raise ValueError(f"CA expects [B,H,T,D] tensors, got shape {tuple(q.shape)}")
         if int(query_tile) <= 0:
             raise ValueError("query_tile must be positive")
-        _mode()
+        mode = _mode()
         ctx.query_tile = int(query_tile)
         ctx.fused = q.shape[-1] in SUPPORTED_HEAD_DIMS
         ctx.empty = False
+        ctx.on_cpu = q.device.type == "cpu"
+        if ctx.on_cpu:
+            T, D = q.shape[2], q.shape[3]
+            if mode in ("prefix_v5", "prefix_v6"):
+                raise ValueError("CA v5/v6 paths require CUDA FP16 Q/K/V and T<=2048")
+            if mode == "fused" and (T > 2048 or D > 128 or v.dtype not in (torch.float16, torch.float32)):
+                raise ValueError("CA fused forward supports T<=2048, D<=128, FP16/FP32 values")
+            for t in (k, v, log_gain):
+                if t.device != q.device:
+                    raise RuntimeError("continuum_attention: all tensors must be on the same device")
         if q.shape[2] == 0:
             # the reference's query-tile loop has no tile to concatenate (:670-694)
             raise RuntimeError("continuum_attention: empty sequence (T = 0)")
         if q.shape[0] * q.shape[1] == 0:
             # an empty batch: the reference's tile loop yields empty tiles
-            _check_device(q, k, v, log_gain)
+            if not ctx.on_cpu:
+                _check_device(q, k, v, log_gain)
             ctx.empty = True
             ctx.save_for_backward(q, k, v, log_gain)
             return torch.empty(q.shape, device=q.device, dtype=v.dtype)
+        if ctx.on_cpu:
+            ctx.save_for_backward(q, k, v, log_gain)
+            return _cpu.forward(q, k, v, log_gain, ctx.query_tile)
         with torch.autocast(device_type="cuda", enabled=False):
             if ctx.fused:
                 out, stats = ca_forward(q, k, v, log_gain)
@@ -243,7 +274,10 @@ class _CAExactTiled(torch.autograd.Function):
             q, k, v, log_gain = ctx.saved_tensors
             return (torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v),
                     torch.zeros_like(log_gain), None)
-        if ctx.fused:
+        if ctx.on_cpu:
+            q, k, v, log_gain = ctx.saved_tensors
+            dq, dk, dv, dg = _cpu.backward(q, k, v, log_gain, grad_y, ctx.query_tile)
+        elif ctx.fused:
             q, k, v, log_gain, out, stats = ctx.saved_tensors
             dq, dk, dv, dg = ca_backward(q, k, v, log_gain, out, stats, grad_y)
         else:
@@ -256,9 +290,10 @@ class _CAExactTiled(torch.autograd.Function):
 def continuum_attention(q, k, v, log_gain, query_tile=64):
     """Exact causal Continuum Attention (cuda/continuum_attention.py:768-783).
 
-    q, k, v: ``[B, H, T, D]`` (same dtype), log_gain: ``[H]``.  D in {8, 16,
-    32, 64, 128} runs the fused kernels; any other D the query-tile structure over
-    the HIP weight kernels (``query_tile`` rows at a time).
+    q, k, v: ``[B, H, T, D]`` (same dtype), log_gain: ``[H]``.  On the GPU,
+    D in {8, 16, 32, 64, 128} runs the fused kernels and any other D the
+    query-tile structure over the HIP weight kernels (``query_tile`` rows at a
+    time); CPU tensors run the float32 CPU path (``cpu.py``).
     Scores are ``exp(log_gain[h]) / sqrt(D) * q.k``; keys and values are
     linearly interpolated between adjacent positions with half-token end caps
     and integrated exactly.  Returns ``[B, H, T, D]`` in ``v.dtype``.

@@ -20,10 +20,16 @@ library's kernels (``ca_grad_clip_coef``, ``ca_adamw_step``):
 The fp32 weights stay the parameters (state dicts are unchanged); a shadow is
 recopied whenever its weight's version counter shows a change made outside
 the optimizer (``load_state_dict``, in-place edits).  Gradients of shadowed
-weights live on the shadow (``shadow.grad``), not on the weight's ``.grad``;
-``FusedAdamW.grads()`` lists the gradient each tensor's step uses.  The update
-is torch's AdamW formula in fp32 (one global step count: every parameter is
-expected to receive a gradient each step, as in the decoders).
+weights are collected by the optimizer, not left on the weight's ``.grad``:
+a hook takes each backward's bf16 gradient off the shadow as soon as autograd
+has stored it.  One backward per step keeps that bf16 tensor (the value
+autocast's cast backward would upcast); gradient accumulation over several
+backwards (the reference's ``grad_accum`` micro-steps,
+cuda/continuum_attention.py:1194-1207) sums them in an fp32 buffer, as torch
+sums upcast gradients into an fp32 ``.grad``, never rounding the running sum
+to bf16.  ``FusedAdamW.grads()`` lists the gradient each tensor's step uses.
+The update is torch's AdamW formula in fp32 (one global step count: every
+parameter is expected to receive a gradient each step, as in the decoders).
 """
 from __future__ import annotations
 
@@ -92,6 +98,8 @@ class FusedAdamW(torch.optim.Optimizer):
             mod._ca_shadow = sh
             mod._ca_shadow_version = w._version
             self.shadow[id(w)] = sh
+            sh.register_post_accumulate_grad_hook(self._collect_shadow_grad)
+        self._shadow_grads = {}  # id(shadow) -> bf16 gradient (one backward) or fp32 sum
         self._groups = []
         devices = {p.device for group in self.param_groups for p in group["params"]}
         if len(devices) != 1:
@@ -121,9 +129,32 @@ class FusedAdamW(torch.optim.Optimizer):
         self._coef = torch.empty(1, device=dev, dtype=torch.float32)
 
     # ---- gradients -----------------------------------------------------
+    def _collect_shadow_grad(self, sh):
+        """Post-accumulate hook of a shadow: moves the gradient autograd just
+        stored on it into the optimizer.  The shadow's .grad is then empty
+        again, so the next backward stores its gradient afresh instead of
+        adding it to a bf16 sum; from the second backward on the gradients
+        are summed in fp32."""
+        g = sh.grad
+        if g is None:
+            return
+        sh.grad = None
+        key = id(sh)
+        prev = self._shadow_grads.get(key)
+        if prev is None:
+            self._shadow_grads[key] = g
+        elif prev.dtype == torch.float32:
+            prev.add_(g)
+        else:
+            self._shadow_grads[key] = prev.float().add_(g)
+
     def _grad_of(self, p):
         sh = self.shadow.get(id(p))
-        gs = sh.grad if sh is not None else None
+        gs = None
+        if sh is not None:
+            gs = self._shadow_grads.get(id(sh))
+            if sh.grad is not None:  # stored without the hook (e.g. assigned by hand)
+                gs = sh.grad if gs is None else gs.float().add_(sh.grad)
         if gs is not None and p.grad is not None:
             raise RuntimeError("FusedAdamW: a weight has both a bf16-shadow and an fp32 gradient")
         return gs if gs is not None else p.grad
@@ -133,6 +164,9 @@ class FusedAdamW(torch.optim.Optimizer):
         return [self._grad_of(p) for g in self._groups for p in g["tensors"]]
 
     def zero_grad(self, set_to_none: bool = True):
+        # collected shadow gradients are dropped either way: the next backward
+        # starts a new sum, which equals adding to zeros
+        self._shadow_grads.clear()
         for g in self._groups:
             for p in g["tensors"]:
                 for t in (p, self.shadow.get(id(p))):

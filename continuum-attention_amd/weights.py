@@ -11,15 +11,20 @@
   ``[..., T, T]`` logits, differentiable (its backward is the analytic VJP
   kernel).  Same ``ValueError`` for non-square logits.
 
-All arithmetic runs in the HIP row kernels (csrc/ca_weights.hip) through the C
-ABI; inputs of any float dtype are computed in float32 and results are
-returned in the input dtype.  CPU tensors raise: there is no CPU path.
+On GPU tensors all arithmetic runs in the HIP row kernels
+(csrc/ca_weights.hip) through the C ABI; inputs of any float dtype are
+computed in float32 and results are returned in the input dtype.
+``continuous_attention_weights`` on CPU tensors runs ``cpu.py`` in the logits'
+own dtype and stays differentiable to any order, as the reference's torch
+composition is; ``ca_weights`` / ``ca_weights_backward`` (the CUDA
+extension's entry points in the reference) take GPU tensors only.
 """
 from __future__ import annotations
 
 import torch
 
 from . import _native
+from . import cpu as _cpu
 
 
 def _f32c(x: torch.Tensor) -> torch.Tensor:
@@ -102,6 +107,11 @@ class _CAWeights(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_w):
+        if torch.is_grad_enabled():
+            # the analytic VJP kernel is not itself differentiable: a graph
+            # built through it (create_graph=True) would be silently cut
+            raise RuntimeError("continuous_attention_weights on the GPU supports first-order "
+                               "gradients only")
         (logits,) = ctx.saved_tensors
         ds = ca_weights_backward(logits, grad_w, 0)
         return ds.to(logits.dtype)
@@ -114,4 +124,6 @@ def continuous_attention_weights(logits: torch.Tensor) -> torch.Tensor:
     T = logits.size(-1)
     if logits.size(-2) != T:
         raise ValueError("This benchmark requires square full-sequence causal attention")
+    if logits.device.type == "cpu":
+        return _cpu.continuous_attention_weights(logits)
     return _CAWeights.apply(logits)

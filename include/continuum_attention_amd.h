@@ -7,6 +7,9 @@
  * asynchronous on `stream` (NULL = the default stream) and returns CA_OK or an
  * error code whose text ca_last_error() returns (thread-local).
  *
+ * Every tensor pointer of ca_fwd_f32 and ca_bwd_f32 (q, k, v, out, dout, dq,
+ * dk, dv) must be 16-byte aligned: the kernels move rows as 16-byte vectors.
+ *
  * This library replaces the native half of the reference operator
  * (akhadangi/continuum-attention):
  *   - the pybind extension built by _ca_cuda_extension
@@ -213,6 +216,16 @@ int ca_bf16_shadow(const ca_opt_tensor* tensors, int ntensors, const int* chunks
  * Not thread-safe; meant for single-threaded benchmarking. */
 int ca_timing_enable(int on);
 int ca_timing_read(double* total_ms, int* launches, int n);
+
+/* Forces the work-split lengths of ca_fwd_f32 / ca_bwd_f32 (0 = automatic,
+ * the default): forward split length in 32-key tiles, dQ chunk length in
+ * 14-key blocks, dK/dV chunk length in 32-query tiles.  While set, the
+ * workspace-size functions return the sizes for the forced lengths, so size
+ * queries and calls must see the same setting.  Process-wide, not
+ * thread-safe; no counterpart in the reference: it lets tests run every
+ * split length the automatic choice can pick (which depends on the device's
+ * CU count) at small shapes. */
+int ca_debug_set_splits(int fwd_split_tiles, int dq_chunk_blocks, int dkdv_chunk_tiles);
 
 #ifdef __cplusplus
 }

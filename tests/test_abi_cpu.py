@@ -85,12 +85,24 @@ def test_python_errors_follow_reference_contract(ca, monkeypatch):
     monkeypatch.setenv("CA_CUDA_MODE", "bogus")
     with pytest.raises(ValueError, match="CA_CUDA_MODE"):
         ca.continuum_attention(q, q, q, torch.zeros(1))
-    monkeypatch.setenv("CA_CUDA_MODE", "prefix_v6")
-    # no CPU path: CPU tensors are rejected loudly instead of falling back
-    with pytest.raises(RuntimeError, match="ROCm GPU tensors only"):
-        ca.continuum_attention(q, q, q, torch.zeros(1))
+    # CPU tensors: the reference's CPU-side errors (cuda/continuum_attention.py:662-665)
+    for mode in ("prefix_v5", "prefix_v6"):
+        monkeypatch.setenv("CA_CUDA_MODE", mode)
+        with pytest.raises(ValueError, match="v5/v6 paths require CUDA FP16"):
+            ca.continuum_attention(q, q, q, torch.zeros(1))
+    monkeypatch.setenv("CA_CUDA_MODE", "fused")
+    with pytest.raises(ValueError, match="fused forward supports T<=2048"):
+        z = torch.zeros(1, 1, 2049, 16)
+        ca.continuum_attention(z, z, z, torch.zeros(1))
+    with pytest.raises(ValueError, match="fused forward supports"):
+        ca.continuum_attention(q.double(), q.double(), q.double(), torch.zeros(1))
+    monkeypatch.setenv("CA_CUDA_MODE", "prefix")
     with pytest.raises(ValueError, match="query_tile"):
         ca.continuum_attention(q, q, q, torch.zeros(1), 0)
+    # other devices are neither the HIP nor the CPU path
+    m = torch.zeros(1, 1, 4, 16, device="meta")
+    with pytest.raises(RuntimeError, match="ROCm GPU tensors only"):
+        ca.continuum_attention(m, m, m, torch.zeros(1, device="meta"))
 
 
 def test_package_does_not_import_the_oracle():

@@ -725,3 +725,65 @@ def test_tinylm_fused_swiglu_step(gpu_ca):
     assert abs(out[True][0] - out[False][0]) <= 1e-6 * abs(out[False][0])
     for a, b in zip(out[True][1], out[False][1]):
         torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-7)
+
+
+@pytest.mark.parametrize("micro", [2, 8])
+def test_fused_adamw_gradient_accumulation(gpu_ca, micro):
+    """The reference's grad_accum loop (cuda/continuum_attention.py:1194-1207:
+    loss / grad_accum, one backward per micro-batch, then clip and step)
+    under bf16 autocast: the gradients FusedAdamW steps with are the fp32
+    sums of the micro-batches' bf16 weight gradients, bit for bit what torch
+    accumulates in each fp32 .grad, and the updated parameters agree with
+    torch's clip_grad_norm_ + AdamW to fp32 rounding."""
+    say(f"[case] FusedAdamW gradient accumulation over {micro} backwards")
+    Dm = gpu_ca.decoder
+    cfg = Dm.ContinuumDecoderConfig(d_model=128, n_heads=2, n_layers=2, block_size=64)
+    torch.manual_seed(11)
+    ma = Dm.ContinuumDecoderLM(cfg).cuda()
+    mb = Dm.ContinuumDecoderLM(cfg).cuda()
+    mb.load_state_dict(ma.state_dict())
+    oa = Dm.build_fused_adamw(ma)
+    ob = torch.optim.AdamW(mb.parameters(), lr=3e-4, weight_decay=0.1, betas=(0.9, 0.95))
+    batches = [torch.randint(0, 256, (2, 64), device="cuda") for _ in range(micro)]
+    for m, o in ((ma, oa), (mb, ob)):
+        o.zero_grad(set_to_none=True)
+        for ids in batches:
+            with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+                loss = m(ids, targets=ids)["loss"] / micro
+            loss.backward()
+    grads_b = [p.grad.detach().clone() for p in mb.parameters()]
+    for ga, gb in zip(oa.grads(), grads_b):
+        assert ga.dtype == torch.float32 and torch.equal(ga, gb)
+    oa.step(max_norm=1.0)
+    torch.nn.utils.clip_grad_norm_(mb.parameters(), 1.0)
+    ob.step()
+    worst = max(((pa - pb).abs().max() / pb.abs().max()).item()
+                for pa, pb in zip(ma.parameters(), mb.parameters()))
+    say(f"   parameters after the step: {worst:.1e}")
+    assert worst <= 1e-6
+
+
+@pytest.mark.parametrize("bad", [float("inf"), float("nan")])
+def test_clip_and_adamw_with_non_finite_gradient(gpu_ca, bad):
+    """A diverging step: one gradient element is inf or NaN.  The HIP clip
+    and AdamW give torch's total norm (inf / NaN), clip factor (0 / NaN) and
+    updated parameters (NaN where torch's are NaN, equal elsewhere)."""
+    say(f"[case] clip + AdamW with a {bad} gradient")
+    torch.manual_seed(12)
+    shapes = [(64, 33), (1000,), (7,)]
+    pa = [torch.randn(s, device="cuda") for s in shapes]
+    pb = [p.clone() for p in pa]
+    grads = [torch.randn(s, device="cuda") for s in shapes]
+    grads[1][123] = bad
+    for p, q, gr in zip(pa, pb, grads):
+        p.grad = gr.clone()
+        q.grad = gr.clone()
+    oa = gpu_ca.optim.FusedAdamW(pa, lr=1e-3, betas=(0.9, 0.95), weight_decay=0.1)
+    ob = torch.optim.AdamW(pb, lr=1e-3, betas=(0.9, 0.95), weight_decay=0.1)
+    norm_a = oa.step(max_norm=1.0)
+    norm_b = torch.nn.utils.clip_grad_norm_(pb, 1.0)
+    ob.step()
+    torch.testing.assert_close(norm_a.reshape(()), norm_b, equal_nan=True)
+    for a, b in zip(pa, pb):
+        assert torch.equal(torch.isnan(a), torch.isnan(b))
+        torch.testing.assert_close(a, b, atol=1e-6, rtol=1e-6, equal_nan=True)

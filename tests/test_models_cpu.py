@@ -1,6 +1,6 @@
 """CPU checks of the operator's callers (continuum-attention_amd/architecture.py
 and decoder.py): parameter budgets, initialisation, configuration errors,
-state-dict layout, RoPE, and that the CA path has no CPU fallback.
+state-dict layout, RoPE, and the CA variants on CPU tensors.
 
 Expected values come from the reference's own tests: test_acma.py:21-34,
 140-154; test_hp_only.py:13-23; test_fusion.py:17-25; cuda/test_cpu.py:25-27.
@@ -90,16 +90,20 @@ def test_softmax_controls_on_cpu(A):
                                        atol=3e-5, rtol=3e-5)
 
 
-def test_ca_variants_have_no_cpu_path(A, ca):
-    """The CA operator and weights run on ROCm tensors only: CPU input raises."""
-    ids = torch.randint(0, 256, (1, 9))
-    for backend in ("hip", "hip_weights"):
-        with pytest.raises(RuntimeError, match="GPU"):
-            tiny(A, "P", backend)(ids)
-    with pytest.raises(RuntimeError, match="GPU"):
-        ca.continuous_attention_weights(torch.randn(1, 1, 4, 4))
+def test_ca_variants_run_on_cpu(A, ca):
+    """CPU tensors run the CA variants as the reference's modules do: the
+    fused-operator backend and the weights backend agree, and the weight-level
+    entry points keep the GPU-only ones GPU-only."""
+    ids = torch.randint(0, 256, (2, 9))
+    for v in ("P", "R", "S", "H"):
+        a = tiny(A, v, "hip")(ids)
+        b = tiny(A, v, "hip_weights")(ids)
+        assert torch.isfinite(a).all()
+        torch.testing.assert_close(a, b, atol=2e-5, rtol=2e-5)
     with pytest.raises(ValueError, match="square"):
         ca.continuous_attention_weights(torch.randn(1, 1, 3, 4))
+    with pytest.raises(RuntimeError, match="GPU tensors only"):
+        ca.ca_weights(torch.randn(1, 4, 4))
 
 
 def test_bad_variant_backend_and_config(A, Dm):
