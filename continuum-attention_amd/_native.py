@@ -37,6 +37,8 @@ SIGNATURES = {
     "ca_bwd_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "ca_bwd_f32": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
                         _i, _i, _i, _i, _vp]),
+    "ca_bwd_f32_noalloc": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                _i, _i, _i, _i, _vp]),
     "ca_weights_f32": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "ca_weights_bwd_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "ca_qkv_rope_in": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),

@@ -167,6 +167,14 @@ hipEvent_t pool_event() {
 }  // namespace
 
 namespace ca {
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
 void timer_begin(int id, hipStream_t s) {
   if (!g_timing) return;
   g_open_start = pool_event();

@@ -220,6 +220,8 @@ enum KernelId {
 constexpr int kDtypeF32 = 0, kDtypeBF16 = 1, kDtypeF16 = 2;
 void timer_begin(int id, hipStream_t s);
 void timer_end(int id, hipStream_t s);
+// Sets the calling thread's ca_last_error() text; returns `code`.
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 
 // RMSNorm of the decoder caller (ca_norm.hip).  The backward splits the rows
 // over at most kRmsMaxBlocks work groups and keeps one dweight partial per group.

@@ -72,6 +72,23 @@ int ca_bwd_f32(const float* q, const float* k, const float* v, const float* log_
                float* dv, float* dlog_gain, void* workspace, size_t workspace_bytes, int B, int H,
                int T, int D, void* stream);
 
+/* Size of the static scratch array of ca_bwd_f32_noalloc, in MiB. */
+#define CA_NOALLOC_SCRATCH_MB 512
+
+/* ca_bwd_f32 without a workspace argument: the workspace is a static device
+ * array of CA_NOALLOC_SCRATCH_MB MiB that the library holds on each device it
+ * runs on until the process ends.  No counterpart in the reference: for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  It allocates
+ * nothing; shapes whose ca_bwd_workspace_bytes exceeds the array fail with
+ * CA_ERR_WORKSPACE before any launch.  All calls on one device share its
+ * array, so calls that overlap in time on one device (other streams, other
+ * threads) race and must be serialised by the caller. */
+int ca_bwd_f32_noalloc(const float* q, const float* k, const float* v, const float* log_gain,
+                       const float* out, const float* stats, const float* dout, float* dq,
+                       float* dk, float* dv, float* dlog_gain, int B, int H, int T, int D,
+                       void* stream);
+
 /* ---- Weight-materialising row kernels -------------------------------------
  * scores, grad_weights, weights and grad_scores are [BH][Q][K] fp32 (K
  * fastest); row (b, r) is query start + r and sees keys 0 .. start + r, so

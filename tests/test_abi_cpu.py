@@ -172,3 +172,14 @@ def test_swiglu_null_and_misaligned_pointers(ca):
     assert b"null" in lib.ca_last_error()
     assert lib.ca_swiglu_bwd_f32(p, odd, p, 4, 8, None) == 1
     assert b"aligned" in lib.ca_last_error()
+
+
+def test_noalloc_backward_checks_before_any_launch(ca):
+    """ca_bwd_f32_noalloc refuses, with no HIP call, shapes whose workspace
+    exceeds its static array and invalid shapes."""
+    lib = ca.native.load()
+    p = ctypes.c_void_p(16)
+    assert lib.ca_bwd_workspace_bytes(4, 16, 4096, 64) > 512 << 20
+    assert lib.ca_bwd_f32_noalloc(p, p, p, p, p, p, p, p, p, p, p, 4, 16, 4096, 64, None) == 3
+    assert b"scratch" in lib.ca_last_error()
+    assert lib.ca_bwd_f32_noalloc(p, p, p, p, p, p, p, p, p, p, p, 0, 16, 64, 64, None) == 1
