@@ -41,10 +41,8 @@ SIGNATURES = {
                                 _i, _i, _i, _i, _vp]),
     "ca_weights_f32": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "ca_weights_bwd_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
-    "ca_qkv_rope_in": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
-    "ca_qkv_rope_grad": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
-    "ca_heads_to_tokens": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _vp]),
-    "ca_tokens_to_heads": (_i, [_vp, _i, _vp, _i, _i, _i, _i, _vp]),
+    "ca_fwd_qkv": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp]),
+    "ca_bwd_qkv": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp]),
     "ca_rmsnorm_fwd": (_i, [_vp, _vp, _vp, _i, _vp, _i, _i, ctypes.c_float, _vp]),
     "ca_rmsnorm_bwd_workspace_bytes": (_sz, [_i, _i]),
     "ca_rmsnorm_bwd": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _vp]),
@@ -64,8 +62,8 @@ SIGNATURES = {
 }
 
 KERNEL_NAMES = ("ca_fwd", "ca_fwd_combine", "ca_bwd_prep", "ca_bwd_dkdv", "ca_bwd_dq",
-                "ca_bwd_gain_merge", "ca_weights", "ca_weights_bwd", "ca_qkv_in", "ca_qkv_grad",
-                "ca_relayout", "ca_rmsnorm_fwd", "ca_rmsnorm_bwd", "ca_swiglu_fwd", "ca_swiglu_bwd")
+                "ca_bwd_gain_merge", "ca_weights", "ca_weights_bwd", "ca_rmsnorm_fwd",
+                "ca_rmsnorm_bwd", "ca_swiglu_fwd", "ca_swiglu_bwd")
 
 _lib = None
 

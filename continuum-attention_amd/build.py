@@ -13,7 +13,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libca_hip.so")
-SOURCES = ["ca_fwd.hip", "ca_bwd.hip", "ca_bwd_dkdv.hip", "ca_weights.hip", "ca_rope.hip", "ca_norm.hip",
+SOURCES = ["ca_fwd.hip", "ca_bwd.hip", "ca_bwd_dkdv.hip", "ca_weights.hip", "ca_norm.hip",
            "ca_optim.hip", "ca_swiglu.hip", "ca_abi.hip", "ca_noalloc.hip"]
 ARCH = os.environ.get("CA_OFFLOAD_ARCH", "gfx950")
 

@@ -245,51 +245,60 @@ size_t ca_fwd_workspace_bytes(int B, int H, int T, int D) {
   return ca::fwd_part_floats(B * H, T, fwd_split(B * H, T, D, true), D) * sizeof(float);
 }
 
-int ca_fwd_f32(const float* q, const float* k, const float* v, const float* log_gain, float* out,
-               float* stats, void* workspace, size_t workspace_bytes, int B, int H, int T, int D,
-               void* stream) {
-  int rc = check_shape(B, H, T, D);
-  if (rc) return rc;
-  if (!q || !k || !v || !log_gain || !out || !stats)
-    return fail(CA_ERR_INVALID, "null tensor pointer");
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
-    return fail(CA_ERR_INVALID, "q, k, v and out must be 16-byte aligned");
-  const size_t need = ca_fwd_workspace_bytes(B, H, T, D);
-  if (workspace_bytes < need || (need && !workspace))
-    return fail(CA_ERR_WORKSPACE, "forward workspace of %zu bytes required, %zu given", need,
-                workspace_bytes);
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  hipError_t e;
-  float* part = static_cast<float*>(workspace);
-  // the device's own residency: a split no shorter than the workspace's
-  const int C = fwd_split(B * H, T, D, false);
-  switch (D) {
-    case 8: e = ca::launch_fwd<8>(q, k, v, log_gain, out, stats, part, B, H, T, C, s); break;
-    case 16: e = ca::launch_fwd<16>(q, k, v, log_gain, out, stats, part, B, H, T, C, s); break;
-    case 32: e = ca::launch_fwd<32>(q, k, v, log_gain, out, stats, part, B, H, T, C, s); break;
-    case 64: e = ca::launch_fwd<64>(q, k, v, log_gain, out, stats, part, B, H, T, C, s); break;
-    default: e = ca::launch_fwd<128>(q, k, v, log_gain, out, stats, part, B, H, T, C, s); break;
-  }
-  if (e != hipSuccess) return fail(CA_ERR_HIP, "forward launch: %s", hipGetErrorString(e));
-  return CA_OK;
-}
-
 size_t ca_bwd_workspace_bytes(int B, int H, int T, int D) {
   if (B <= 0 || H <= 0 || T <= 0 || D <= 0) return 0;
   return bwd_layout(B, H, T, D).total;
 }
 
-int ca_bwd_f32(const float* q, const float* k, const float* v, const float* log_gain,
-               const float* out, const float* stats, const float* dout, float* dq, float* dk,
-               float* dv, float* dlog_gain, void* workspace, size_t workspace_bytes, int B, int H,
-               int T, int D, void* stream) {
-  int rc = check_shape(B, H, T, D);
-  if (rc) return rc;
-  if (!q || !k || !v || !log_gain || !out || !stats || !dout || !dq || !dk || !dv || !dlog_gain)
-    return fail(CA_ERR_INVALID, "null tensor pointer");
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) || !aligned16(dout) ||
-      !aligned16(dq) || !aligned16(dk) || !aligned16(dv))
-    return fail(CA_ERR_INVALID, "q, k, v, out, dout, dq, dk and dv must be 16-byte aligned");
+}  // extern "C"
+
+namespace {
+
+template <class E>
+hipError_t fwd_launch(int D, const ca::FwdIO& io, float* part, int B, int H, int T, int C,
+                      hipStream_t s) {
+  switch (D) {
+    case 8: return ca::launch_fwd<8, E>(io, part, B, H, T, C, s);
+    case 16: return ca::launch_fwd<16, E>(io, part, B, H, T, C, s);
+    case 32: return ca::launch_fwd<32, E>(io, part, B, H, T, C, s);
+    case 64: return ca::launch_fwd<64, E>(io, part, B, H, T, C, s);
+    default: return ca::launch_fwd<128, E>(io, part, B, H, T, C, s);
+  }
+}
+
+template <class E>
+hipError_t bwd_launch(int D, const ca::BwdIO& io, const ca::BwdWork& w, const ca::DqSplit& sp,
+                      const ca::DkdvSplit& kvs, int B, int H, int T, hipStream_t s) {
+  switch (D) {
+    case 8: return ca::launch_bwd<8, E>(io, w, sp, kvs, B, H, T, s);
+    case 16: return ca::launch_bwd<16, E>(io, w, sp, kvs, B, H, T, s);
+    case 32: return ca::launch_bwd<32, E>(io, w, sp, kvs, B, H, T, s);
+    case 64: return ca::launch_bwd<64, E>(io, w, sp, kvs, B, H, T, s);
+    default: return ca::launch_bwd<128, E>(io, w, sp, kvs, B, H, T, s);
+  }
+}
+
+// Shape, workspace and launch of the forward, once the operands are views.
+int fwd_common(const ca::FwdIO& io, int dtype, void* workspace, size_t workspace_bytes, int B,
+               int H, int T, int D, void* stream) {
+  const size_t need = ca_fwd_workspace_bytes(B, H, T, D);
+  if (workspace_bytes < need || (need && !workspace))
+    return fail(CA_ERR_WORKSPACE, "forward workspace of %zu bytes required, %zu given", need,
+                workspace_bytes);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  float* part = static_cast<float*>(workspace);
+  // the device's own residency: a split no shorter than the workspace's
+  const int C = fwd_split(B * H, T, D, false);
+  hipError_t e;
+  if (dtype == CA_DTYPE_BF16) e = fwd_launch<__bf16>(D, io, part, B, H, T, C, s);
+  else if (dtype == CA_DTYPE_F16) e = fwd_launch<_Float16>(D, io, part, B, H, T, C, s);
+  else e = fwd_launch<float>(D, io, part, B, H, T, C, s);
+  if (e != hipSuccess) return fail(CA_ERR_HIP, "forward launch: %s", hipGetErrorString(e));
+  return CA_OK;
+}
+
+int bwd_common(const ca::BwdIO& io, int dtype, void* workspace, size_t workspace_bytes, int B,
+               int H, int T, int D, void* stream) {
   const BwdLayout L = bwd_layout(B, H, T, D);
   if (!workspace || workspace_bytes < L.total)
     return fail(CA_ERR_WORKSPACE, "backward workspace of %zu bytes required, %zu given", L.total,
@@ -306,15 +315,105 @@ int ca_bwd_f32(const float* q, const float* k, const float* v, const float* log_
   const ca::DkdvSplit kvs = dkdv_split_for(B * H, T, D, false);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;
-  switch (D) {
-    case 8: e = ca::launch_bwd<8>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, work, sp, kvs, B, H, T, s); break;
-    case 16: e = ca::launch_bwd<16>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, work, sp, kvs, B, H, T, s); break;
-    case 32: e = ca::launch_bwd<32>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, work, sp, kvs, B, H, T, s); break;
-    case 64: e = ca::launch_bwd<64>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, work, sp, kvs, B, H, T, s); break;
-    default: e = ca::launch_bwd<128>(q, k, v, log_gain, out, stats, dout, dq, dk, dv, dlog_gain, work, sp, kvs, B, H, T, s); break;
-  }
+  if (dtype == CA_DTYPE_BF16) e = bwd_launch<__bf16>(D, io, work, sp, kvs, B, H, T, s);
+  else if (dtype == CA_DTYPE_F16) e = bwd_launch<_Float16>(D, io, work, sp, kvs, B, H, T, s);
+  else e = bwd_launch<float>(D, io, work, sp, kvs, B, H, T, s);
   if (e != hipSuccess) return fail(CA_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
   return CA_OK;
+}
+
+// fp32 [B,H,T,D] tensor as a view
+ca::View heads_view(const void* p, int H, int T, int D) {
+  return ca::View{const_cast<void*>(p), (long long)H * T * D, (long long)T * D, (long long)D};
+}
+size_t dtype_size(int dtype) { return dtype == CA_DTYPE_F32 ? 4 : 2; }
+// part `part` (of `parts`) of a token-major [B,T,parts,H,D] tensor as a view
+ca::View tokens_view(const void* p, int dtype, int part, int parts, int T, int H, int D) {
+  char* base = static_cast<char*>(const_cast<void*>(p)) + (size_t)part * H * D * dtype_size(dtype);
+  return ca::View{base, (long long)T * parts * H * D, (long long)D, (long long)parts * H * D};
+}
+bool aligned_to(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+int ca_fwd_f32(const float* q, const float* k, const float* v, const float* log_gain, float* out,
+               float* stats, void* workspace, size_t workspace_bytes, int B, int H, int T, int D,
+               void* stream) {
+  int rc = check_shape(B, H, T, D);
+  if (rc) return rc;
+  if (!q || !k || !v || !log_gain || !out || !stats)
+    return fail(CA_ERR_INVALID, "null tensor pointer");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+    return fail(CA_ERR_INVALID, "q, k, v and out must be 16-byte aligned");
+  ca::FwdIO io{heads_view(q, H, T, D), heads_view(k, H, T, D), heads_view(v, H, T, D), nullptr,
+               log_gain, out, ca::View{nullptr, 0, 0, 0}, stats};
+  return fwd_common(io, CA_DTYPE_F32, workspace, workspace_bytes, B, H, T, D, stream);
+}
+
+int ca_bwd_f32(const float* q, const float* k, const float* v, const float* log_gain,
+               const float* out, const float* stats, const float* dout, float* dq, float* dk,
+               float* dv, float* dlog_gain, void* workspace, size_t workspace_bytes, int B, int H,
+               int T, int D, void* stream) {
+  int rc = check_shape(B, H, T, D);
+  if (rc) return rc;
+  if (!q || !k || !v || !log_gain || !out || !stats || !dout || !dq || !dk || !dv || !dlog_gain)
+    return fail(CA_ERR_INVALID, "null tensor pointer");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) || !aligned16(dout) ||
+      !aligned16(dq) || !aligned16(dk) || !aligned16(dv))
+    return fail(CA_ERR_INVALID, "q, k, v, out, dout, dq, dk and dv must be 16-byte aligned");
+  ca::BwdIO io{heads_view(q, H, T, D), heads_view(k, H, T, D), heads_view(v, H, T, D), nullptr,
+               log_gain, out, stats, heads_view(dout, H, T, D), heads_view(dq, H, T, D),
+               heads_view(dk, H, T, D), heads_view(dv, H, T, D), dlog_gain};
+  return bwd_common(io, CA_DTYPE_F32, workspace, workspace_bytes, B, H, T, D, stream);
+}
+
+static int check_qkv(const char* fn, int dtype, const void* qkv, const float* rope_cs,
+                     const float* y, const void* tok) {
+  if (dtype != CA_DTYPE_F32 && dtype != CA_DTYPE_BF16 && dtype != CA_DTYPE_F16)
+    return fail(CA_ERR_INVALID, "%s: unknown dtype code %d", fn, dtype);
+  const size_t a = dtype == CA_DTYPE_F32 ? 16 : 8;
+  if (!aligned_to(qkv, a) || !aligned_to(tok, a) || !aligned16(y) ||
+      (rope_cs && !aligned16(rope_cs)))
+    return fail(CA_ERR_INVALID, "%s: misaligned buffer (qkv and the token-major output %zu-byte, "
+                "y and rope_cs 16-byte)", fn, a);
+  return CA_OK;
+}
+
+int ca_fwd_qkv(const void* qkv, int dtype, const float* rope_cs, const float* log_gain, float* y,
+               void* out, float* stats, void* workspace, size_t workspace_bytes, int B, int T,
+               int H, int D, void* stream) {
+  int rc = check_shape(B, H, T, D);
+  if (rc) return rc;
+  if (!qkv || !log_gain || !y || !out || !stats)
+    return fail(CA_ERR_INVALID, "ca_fwd_qkv: null pointer");
+  rc = check_qkv("ca_fwd_qkv", dtype, qkv, rope_cs, y, out);
+  if (rc) return rc;
+  ca::FwdIO io{tokens_view(qkv, dtype, 0, 3, T, H, D), tokens_view(qkv, dtype, 1, 3, T, H, D),
+               tokens_view(qkv, dtype, 2, 3, T, H, D), rope_cs, log_gain, y,
+               tokens_view(out, dtype, 0, 1, T, H, D), stats};
+  return fwd_common(io, dtype, workspace, workspace_bytes, B, H, T, D, stream);
+}
+
+int ca_bwd_qkv(const void* qkv, int dtype, const float* rope_cs, const float* log_gain,
+               const float* y, const float* stats, const void* dout, void* dqkv,
+               float* dlog_gain, void* workspace, size_t workspace_bytes, int B, int T, int H,
+               int D, void* stream) {
+  int rc = check_shape(B, H, T, D);
+  if (rc) return rc;
+  if (!qkv || !log_gain || !y || !stats || !dout || !dqkv || !dlog_gain)
+    return fail(CA_ERR_INVALID, "ca_bwd_qkv: null pointer");
+  rc = check_qkv("ca_bwd_qkv", dtype, qkv, rope_cs, y, dout);
+  if (rc) return rc;
+  if (!aligned_to(dqkv, dtype == CA_DTYPE_F32 ? 16 : 8))
+    return fail(CA_ERR_INVALID, "ca_bwd_qkv: misaligned dqkv");
+  ca::BwdIO io{tokens_view(qkv, dtype, 0, 3, T, H, D), tokens_view(qkv, dtype, 1, 3, T, H, D),
+               tokens_view(qkv, dtype, 2, 3, T, H, D), rope_cs, log_gain, y, stats,
+               tokens_view(dout, dtype, 0, 1, T, H, D), tokens_view(dqkv, dtype, 0, 3, T, H, D),
+               tokens_view(dqkv, dtype, 1, 3, T, H, D), tokens_view(dqkv, dtype, 2, 3, T, H, D),
+               dlog_gain};
+  return bwd_common(io, dtype, workspace, workspace_bytes, B, H, T, D, stream);
 }
 
 static int check_rows(const char* fn, int BH, int Q, int K, int start) {
@@ -356,80 +455,6 @@ int ca_weights_bwd_f32(const float* scores, const float* grad_weights, float* we
   if (e != hipSuccess)
     return fail(CA_ERR_HIP, "ca_weights_bwd_f32 launch: %s", hipGetErrorString(e));
   return CA_OK;
-}
-
-static int check_prologue(const char* fn, int B, int T, int H, int D, int dtype) {
-  if (B <= 0 || T <= 0 || H <= 0 || D <= 0)
-    return fail(CA_ERR_INVALID, "%s: invalid shape B=%d T=%d H=%d D=%d", fn, B, T, H, D);
-  if (D % 4)
-    return fail(CA_ERR_UNSUPPORTED, "%s: head dim D=%d must be a multiple of 4", fn, D);
-  if (dtype != CA_DTYPE_F32 && dtype != CA_DTYPE_BF16 && dtype != CA_DTYPE_F16)
-    return fail(CA_ERR_INVALID, "%s: unknown dtype code %d", fn, dtype);
-  if ((long long)B * T * 3 * H * D > (1ll << 40))
-    return fail(CA_ERR_UNSUPPORTED, "%s: tensor too large", fn);
-  return CA_OK;
-}
-
-static bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
-static size_t dtype_align(int dtype) { return dtype == CA_DTYPE_F32 ? 16 : 8; }
-
-int ca_qkv_rope_in(const void* qkv, int dtype, const float* rope_cs, float* q, float* k, float* v,
-                   int B, int T, int H, int D, void* stream) {
-  int rc = check_prologue("ca_qkv_rope_in", B, T, H, D, dtype);
-  if (rc) return rc;
-  if (!qkv || !q || !k || !v) return fail(CA_ERR_INVALID, "ca_qkv_rope_in: null pointer");
-  if (!aligned(qkv, dtype_align(dtype)) || !aligned16(q) || !aligned16(k) || !aligned16(v) ||
-      (rope_cs && !aligned16(rope_cs)))
-    return fail(CA_ERR_INVALID, "ca_qkv_rope_in: misaligned buffer");
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  ca::timer_begin(ca::kQkvIn, s);
-  hipError_t e = ca::launch_qkv_in(qkv, dtype, rope_cs, q, k, v, B, T, H, D, s);
-  ca::timer_end(ca::kQkvIn, s);
-  if (e != hipSuccess) return fail(CA_ERR_HIP, "ca_qkv_rope_in launch: %s", hipGetErrorString(e));
-  return CA_OK;
-}
-
-int ca_qkv_rope_grad(const float* dq, const float* dk, const float* dv, const float* rope_cs,
-                     void* dqkv, int dtype, int B, int T, int H, int D, void* stream) {
-  int rc = check_prologue("ca_qkv_rope_grad", B, T, H, D, dtype);
-  if (rc) return rc;
-  if (!dq || !dk || !dv || !dqkv) return fail(CA_ERR_INVALID, "ca_qkv_rope_grad: null pointer");
-  if (!aligned(dqkv, dtype_align(dtype)) || !aligned16(dq) || !aligned16(dk) || !aligned16(dv) ||
-      (rope_cs && !aligned16(rope_cs)))
-    return fail(CA_ERR_INVALID, "ca_qkv_rope_grad: misaligned buffer");
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  ca::timer_begin(ca::kQkvGrad, s);
-  hipError_t e = ca::launch_qkv_grad(dq, dk, dv, rope_cs, dqkv, dtype, B, T, H, D, s);
-  ca::timer_end(ca::kQkvGrad, s);
-  if (e != hipSuccess) return fail(CA_ERR_HIP, "ca_qkv_rope_grad launch: %s", hipGetErrorString(e));
-  return CA_OK;
-}
-
-static int relayout(const char* fn, const void* src, void* dst, int dtype, bool to_tokens, int B,
-                    int H, int T, int D, void* stream) {
-  int rc = check_prologue(fn, B, T, H, D, dtype);
-  if (rc) return rc;
-  if (!src || !dst) return fail(CA_ERR_INVALID, "%s: null pointer", fn);
-  const void* f32side = to_tokens ? src : dst;
-  const void* tokside = to_tokens ? dst : src;
-  if (!aligned16(f32side) || !aligned(tokside, dtype_align(dtype)))
-    return fail(CA_ERR_INVALID, "%s: misaligned buffer", fn);
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  ca::timer_begin(ca::kRelayout, s);
-  hipError_t e = ca::launch_relayout(src, dst, dtype, to_tokens, B, H, T, D, s);
-  ca::timer_end(ca::kRelayout, s);
-  if (e != hipSuccess) return fail(CA_ERR_HIP, "%s launch: %s", fn, hipGetErrorString(e));
-  return CA_OK;
-}
-
-int ca_heads_to_tokens(const float* y, void* out, int dtype, int B, int H, int T, int D,
-                       void* stream) {
-  return relayout("ca_heads_to_tokens", y, out, dtype, true, B, H, T, D, stream);
-}
-
-int ca_tokens_to_heads(const void* x, int dtype, float* out, int B, int H, int T, int D,
-                       void* stream) {
-  return relayout("ca_tokens_to_heads", x, out, dtype, false, B, H, T, D, stream);
 }
 
 static int check_swiglu(const char* fn, const void* a, const void* b, const void* c, int N,

@@ -46,26 +46,31 @@ namespace ca {
 // One thread per (row, 8 elements): Dl = dY . y, then the Q and dY/Z limbs of
 // the 8 elements (one 16-byte store per plane) and, per row, (m, Dl/Z).
 // `rows` = B*H*T; plane p of `limbs` starts at p * rows * D.
-template <int D>
-__global__ __launch_bounds__(256) void ca_bwd_prep_kernel(const float* __restrict__ Q,
-                                                          const float* __restrict__ dout,
+template <int D, class E>
+__global__ __launch_bounds__(256) void ca_bwd_prep_kernel(View Qv, const float* __restrict__ rope,
+                                                          View dYv,
                                                           const float* __restrict__ out,
                                                           const float* __restrict__ stats,
                                                           __bf16* __restrict__ limbs,
-                                                          float* __restrict__ qstat, int rows) {
+                                                          float* __restrict__ qstat, int H, int T,
+                                                          int rows) {
   constexpr int C8 = D / 8;
-  const int t = blockIdx.x * 256 + threadIdx.x;
-  const int row = t / C8, c = t % C8;
+  const int tix = blockIdx.x * 256 + threadIdx.x;
+  const int row = tix / C8, c = tix % C8;
   const bool ok = row < rows;
+  const int bh = ok ? row / T : 0, t = ok ? row % T : 0;
+  const E* qp = view_slice<const E>(Qv, bh, H) + (long long)t * Qv.rstride + 8 * c;
+  const E* dp = view_slice<const E>(dYv, bh, H) + (long long)t * dYv.rstride + 8 * c;
   f32x4 dy[2], y[2], qq[2];
   float m = 0.f, invz = 0.f;
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
     dy[u] = y[u] = qq[u] = f32x4{0.f, 0.f, 0.f, 0.f};
     if (ok) {
-      dy[u] = reinterpret_cast<const f32x4*>(dout + (size_t)row * D + 8 * c)[u];
+      dy[u] = ld4(dp + 4 * u);
       y[u] = reinterpret_cast<const f32x4*>(out + (size_t)row * D + 8 * c)[u];
-      qq[u] = reinterpret_cast<const f32x4*>(Q + (size_t)row * D + 8 * c)[u];
+      qq[u] = ld4(qp + 4 * u);
+      if (rope) qq[u] = rope4(qq[u], rope_entry(rope, t, D, 8 * c + 4 * u), false);
     }
   }
   if (ok) {
@@ -123,13 +128,11 @@ struct DqP {
   static constexpr int STAGE = 3 * PLANE;
 };
 
-template <int D>
-__global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict__ dsbuf,
-                                                        const float* __restrict__ Q,
-                                                        const float* __restrict__ K,
+template <int D, class E, bool ROPE>
+__global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict__ dsbuf, View Qv,
+                                                        View Kv, const float* __restrict__ rope,
                                                         const float* __restrict__ log_gain,
-                                                        float* __restrict__ dQ,
-                                                        float* __restrict__ dq_part,
+                                                        View dQv, float* __restrict__ dq_part,
                                                         float* __restrict__ gain_part, int BH,
                                                         int H, int T, int chunk, int n_items,
                                                         int n_part) {
@@ -154,7 +157,6 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
   const int qt = kDqTiles * qg + w;
   const bool wave_on = qt < nqt;
-  const size_t slice = (size_t)bh * T * D;
   const float c = head_scale_log2(log_gain, bh % H, D) * kLn2;
   // key blocks of this chunk met by the wave's tile
   const int my_end = wave_on ? min(min(ds_kb_count(qt), nkb), kb_hi) : 0;
@@ -180,8 +182,19 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   // sum of the chunk partials.
   // Staging unit u: slot u / C4 of the pair (block = slot / 16), d = 4(u % C4)..+3;
   // a thread's units all have d chunk tid % C4, since 256 % C4 == 0.
-  f32x4 pre[P::UPT];
-  const f32x4 kref = reinterpret_cast<const f32x4*>(K + slice + (size_t)(kDqRows * qg) * D)[tid % P::C4];
+  // rows of K (RoPE applied when `rope`): loaded raw a stage ahead and
+  // converted, rotated and shifted when stored
+  if (!ROPE) rope = nullptr;  // lets the compiler drop every rotation
+  const E* __restrict__ Ks = view_slice<const E>(Kv, bh, H);
+  const long long krs = Kv.rstride;
+  auto k_row4 = [&](int key, int d0) {
+    f32x4 x = ld4(Ks + (long long)key * krs + d0);
+    return rope ? rope4(x, rope_entry(rope, key, D, d0), false) : x;
+  };
+  typedef typename Raw4<E>::type R4;
+  R4 pre[P::UPT];
+  f32x4 pre_cs[ROPE ? P::UPT : 1];
+  const f32x4 kref = k_row4(kDqRows * qg, 4 * (tid % P::C4));
   auto unit_key = [&](int u, int it) {
     const int s = u / P::C4;
     return kBwdKeys * (kb_lo + 2 * it + s / kBwdSlots) - 1 + s % kBwdSlots;
@@ -190,12 +203,17 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
 #pragma unroll
     for (int uu = 0; uu < P::UPT; ++uu) {
       const int u = tid + 256 * uu;
-      f32x4 v = {0.f, 0.f, 0.f, 0.f};
+      R4 v = {};
+      f32x4 cs = {1.f, 0.f, 1.f, 0.f};
       if (u < P::UNITS) {
         const int key = unit_key(u, it);
-        if (key >= 0 && key < T) v = reinterpret_cast<const f32x4*>(K + slice + (size_t)key * D)[u % P::C4];
+        if (key >= 0 && key < T) {
+          v = ld_raw4(Ks + (long long)key * krs + 4 * (u % P::C4));
+          if (ROPE) cs = rope_entry(rope, key, D, 4 * (u % P::C4));
+        }
       }
       pre[uu] = v;
+      if constexpr (ROPE) pre_cs[uu] = cs;
     }
   };
   // The shift is applied when the prefetched rows are stored, so the loads
@@ -207,7 +225,9 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
       const int u = tid + 256 * uu;
       if (u < P::UNITS) {
         const int key = unit_key(u, it);
-        const f32x4 kv = (key >= 0 && key < T) ? pre[uu] - kref : f32x4{0.f, 0.f, 0.f, 0.f};
+        f32x4 kx = raw_to_f32(pre[uu], Ks);
+        if constexpr (ROPE) kx = rope4(kx, pre_cs[uu], false);
+        const f32x4 kv = (key >= 0 && key < T) ? kx - kref : f32x4{0.f, 0.f, 0.f, 0.f};
         unsigned h0, m0, l0, h1, m1, l1;
         split_pair(kv[0], kv[1], h0, m0, l0);
         split_pair(kv[2], kv[3], h1, m1, l1);
@@ -277,13 +297,18 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
     if (it + 1 < iters) store_k(buf ^ 1, it + 1);
     __syncthreads();
   }
-  // lane (d = 16nb + l16, group g) holds rows 16rb + 4g + r of the wave's tile
+  // lane (d = 16nb + l16, group g) holds rows 16rb + 4g + r of the wave's
+  // tile; the other column of d's RoPE pair (d ^ 1) is in lane l16 ^ 1
   float gsum = 0.f;
   if (wave_on) {
     // single-chunk groups write dQ; chunk partials are item-indexed tiles
-    // [kDqRows queries][D] (items of multi-chunk groups are numbered first)
-    float* dst = nch == 1 ? dQ + slice + (size_t)(kDqRows * qg) * D
-                          : dq_part + ((size_t)bh * n_part + item) * kDqRows * D;
+    // [kDqRows queries][D] (items of multi-chunk groups are numbered first),
+    // summed and rotated back by the merge
+    const bool single = nch == 1;
+    float* part = dq_part + ((size_t)bh * n_part + item) * kDqRows * D;
+    const E* Qs = view_slice<const E>(Qv, bh, H);
+    E* dQs = view_slice<E>(dQv, bh, H);
+    const bool odd = l16 & 1;
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
@@ -291,11 +316,31 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int rloc = 32 * w + 16 * rb + 4 * g + r;
+          const int row = kDqRows * qg + rloc;
           const int d = 16 * nb + l16;
           const float val = acc[rb][nb][r] * c;
-          if (kDqRows * qg + rloc < T && d < D) {
-            gsum = fmaf(Q[slice + (size_t)(kDqRows * qg + rloc) * D + d], val, gsum);
-            dst[(size_t)rloc * D + d] = val;
+          const float val_pair = __shfl_xor(val, 1);
+          if (row < T && d < D) {
+            const E* qrow = Qs + (long long)row * Qv.rstride;
+            float qd = ld1(qrow + d);
+            float cs_c = 1.f, cs_s = 0.f;
+            if (rope) {
+              const float* e = rope + (long long)row * D + (d & ~1);
+              cs_c = e[0];
+              cs_s = e[1];
+              const float qp = ld1(qrow + (d ^ 1));
+              qd = odd ? fmaf(qd, cs_c, qp * cs_s) : fmaf(qd, cs_c, -qp * cs_s);
+            }
+            gsum = fmaf(qd, val, gsum);
+            if (single) {
+              // transposed rotation back to the un-rotated q
+              const float o = rope ? (odd ? fmaf(val, cs_c, -val_pair * cs_s)
+                                          : fmaf(val, cs_c, val_pair * cs_s))
+                                   : val;
+              st1(dQs + (long long)row * dQv.rstride + d, o);
+            } else {
+              part[(size_t)rloc * D + d] = val;
+            }
           }
         }
   }
@@ -310,12 +355,12 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
 // group nqg-1-gi of slice bh, the sum of its chunk partials in chunk order.
 // Work groups after those: dK, dV of multi-chunk dK/dV group gi of slice bh,
 // the sum of its chunk partials in chunk order.
-template <int D>
+template <int D, class E>
 __global__ __launch_bounds__(256) void ca_bwd_gain_merge_kernel(
     const float* __restrict__ gain_part, const float* __restrict__ dq_part,
-    const float* __restrict__ kv_part, float* __restrict__ dlog_gain, float* __restrict__ dQ,
-    float* __restrict__ dK, float* __restrict__ dV, int B, int H, int T, int chunk, int n_items,
-    int n_part, int dq_multi, int kv_chunk, int kv_part_items) {
+    const float* __restrict__ kv_part, const float* __restrict__ rope,
+    float* __restrict__ dlog_gain, View dQv, View dKv, View dVv, int B, int H, int T, int chunk,
+    int n_items, int n_part, int dq_multi, int kv_chunk, int kv_part_items) {
   const int tid = threadIdx.x;
   const int BHt = B * H;
   if (blockIdx.x >= H + BHt * dq_multi) {
@@ -334,8 +379,9 @@ __global__ __launch_bounds__(256) void ca_bwd_gain_merge_kernel(
       if (key >= T) break;
       f32x4 s = part[e];
       for (int cc = 1; cc < nch; ++cc) s += part[(size_t)cc * kDkdvKeys * 2 * C4 + e];
-      float* dst = (which ? dK : dV) + ((size_t)bh * T + key) * D;
-      reinterpret_cast<f32x4*>(dst)[c4] = s;
+      const View& ov = which ? dKv : dVv;
+      if (which && rope) s = rope4(s, rope_entry(rope, key, D, 4 * c4), true);
+      st4(view_slice<E>(ov, bh, H) + (long long)key * ov.rstride + 4 * c4, s);
     }
     return;
   }
@@ -360,57 +406,61 @@ __global__ __launch_bounds__(256) void ca_bwd_gain_merge_kernel(
   for (int gg = dq_num_groups(T) - 1; gg > qg; --gg) first += dq_group_chunks(gg, T, chunk);
   const int nch = dq_group_chunks(qg, T, chunk);
   const f32x4* part = reinterpret_cast<const f32x4*>(dq_part + ((size_t)bh * n_part + first) * kDqRows * D);
-  f32x4* out = reinterpret_cast<f32x4*>(dQ + ((size_t)bh * T + kDqRows * qg) * D);
+  E* dQs = view_slice<E>(dQv, bh, H);
   for (int e = tid; e < kDqRows * C4; e += 256) {
-    if (kDqRows * qg + e / C4 >= T) break;
+    const int row = kDqRows * qg + e / C4, c4 = e % C4;
+    if (row >= T) break;
     f32x4 s = part[e];
     for (int cc = 1; cc < nch; ++cc) s += part[(size_t)cc * kDqRows * C4 + e];
-    out[e] = s;
+    if (rope) s = rope4(s, rope_entry(rope, row, D, 4 * c4), true);
+    st4(dQs + (long long)row * dQv.rstride + 4 * c4, s);
   }
 }
 
-template <int D>
-hipError_t launch_bwd(const float* q, const float* k, const float* v, const float* log_gain,
-                      const float* o, const float* stats, const float* dout, float* dq, float* dk,
-                      float* dv, float* dlog_gain, const BwdWork& ws, const DqSplit& sp,
-                      const DkdvSplit& kvs, int B, int H, int T, hipStream_t stream) {
+template <int D, class E>
+hipError_t launch_bwd(const BwdIO& io, const BwdWork& ws, const DqSplit& sp, const DkdvSplit& kvs,
+                      int B, int H, int T, hipStream_t stream) {
   const int BH = B * H;
   const int rows = BH * T;
   timer_begin(kBwdPrep, stream);
-  hipLaunchKernelGGL(ca_bwd_prep_kernel<D>, dim3((rows * (D / 8) + 255) / 256), dim3(256), 0,
-                     stream, q, dout, o, stats, ws.limbs, ws.qstat, rows);
+  hipLaunchKernelGGL((ca_bwd_prep_kernel<D, E>), dim3((rows * (D / 8) + 255) / 256), dim3(256), 0,
+                     stream, io.q, io.rope, io.dout, io.y, io.stats, ws.limbs, ws.qstat, H, T, rows);
   timer_end(kBwdPrep, stream);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   timer_begin(kBwdDkdv, stream);
-  e = launch_bwd_dkdv<D>(k, v, ws, log_gain, dk, dv, kvs, BH, H, T, stream);
+  e = launch_bwd_dkdv<D, E>(io, ws, kvs, BH, H, T, stream);
   timer_end(kBwdDkdv, stream);
   if (e != hipSuccess) return e;
   timer_begin(kBwdDq, stream);
-  hipLaunchKernelGGL(ca_bwd_dq_kernel<D>, dim3(sp.items * BH), dim3(256), 0, stream, ws.dsbuf, q,
-                     k, log_gain, dq, ws.dq_part, ws.gain_part, BH, H, T, sp.chunk, sp.items,
-                     sp.part_items);
+  if (io.rope)
+    hipLaunchKernelGGL((ca_bwd_dq_kernel<D, E, true>), dim3(sp.items * BH), dim3(256), 0, stream,
+                       ws.dsbuf, io.q, io.k, io.rope, io.log_gain, io.dq, ws.dq_part, ws.gain_part,
+                       BH, H, T, sp.chunk, sp.items, sp.part_items);
+  else
+    hipLaunchKernelGGL((ca_bwd_dq_kernel<D, E, false>), dim3(sp.items * BH), dim3(256), 0, stream,
+                       ws.dsbuf, io.q, io.k, io.rope, io.log_gain, io.dq, ws.dq_part, ws.gain_part,
+                       BH, H, T, sp.chunk, sp.items, sp.part_items);
   timer_end(kBwdDq, stream);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   timer_begin(kBwdGain, stream);
-  hipLaunchKernelGGL(ca_bwd_gain_merge_kernel<D>,
+  hipLaunchKernelGGL((ca_bwd_gain_merge_kernel<D, E>),
                      dim3(H + BH * sp.multi_groups + BH * kvs.multi_groups), dim3(256), 0, stream,
-                     ws.gain_part, ws.dq_part, ws.kv_part, dlog_gain, dq, dk, dv, B, H, T, sp.chunk,
-                     sp.items, sp.part_items, sp.multi_groups, kvs.chunk, kvs.part_items);
+                     ws.gain_part, ws.dq_part, ws.kv_part, io.rope, io.dlog_gain, io.dq, io.dk, io.dv,
+                     B, H, T, sp.chunk, sp.items, sp.part_items, sp.multi_groups, kvs.chunk,
+                     kvs.part_items);
   timer_end(kBwdGain, stream);
   return hipGetLastError();
 }
 
-#define CA_INST_BWD(DD)                                                                         \
-  template hipError_t launch_bwd<DD>(const float*, const float*, const float*, const float*,    \
-                                     const float*, const float*, const float*, float*, float*,  \
-                                     float*, float*, const BwdWork&, const DqSplit&,            \
-                                     const DkdvSplit&, int, int, int, hipStream_t);
-CA_INST_BWD(8)
-CA_INST_BWD(16)
-CA_INST_BWD(32)
-CA_INST_BWD(64)
-CA_INST_BWD(128)
+#define CA_INST_BWD(DD, EE)                                                                     \
+  template hipError_t launch_bwd<DD, EE>(const BwdIO&, const BwdWork&, const DqSplit&,          \
+                                         const DkdvSplit&, int, int, int, hipStream_t);
+#define CA_INST_BWD_ALL(EE) \
+  CA_INST_BWD(8, EE) CA_INST_BWD(16, EE) CA_INST_BWD(32, EE) CA_INST_BWD(64, EE) CA_INST_BWD(128, EE)
+CA_INST_BWD_ALL(float)
+CA_INST_BWD_ALL(__bf16)
+CA_INST_BWD_ALL(_Float16)
 
 }  // namespace ca

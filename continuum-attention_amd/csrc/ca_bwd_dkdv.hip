@@ -33,12 +33,12 @@ struct Bwd {
   static constexpr int CPT = (CHUNKS + 255) / 256;
 };
 
-template <int D>
+template <int D, class E>
 __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
-    const float* __restrict__ K, const float* __restrict__ V, const __bf16* __restrict__ limbs,
-    const float* __restrict__ qstat, const float* __restrict__ log_gain, float* __restrict__ dK,
-    float* __restrict__ dV, float* __restrict__ dsbuf, float* __restrict__ kv_part, int BH, int H,
-    int T, int chunk, int n_part) {
+    View Kv, View Vv, const float* __restrict__ rope, const __bf16* __restrict__ limbs,
+    const float* __restrict__ qstat, const float* __restrict__ log_gain, View dKv, View dVv,
+    float* __restrict__ dsbuf, float* __restrict__ kv_part, int BH, int H, int T, int chunk,
+    int n_part) {
   using P = Bwd<D>;
   __shared__ __attribute__((aligned(16))) __bf16 tiles[2][P::TILE];
   __shared__ f32x4 tstat[2][16];  // rows 2u, 2u+1: (m, Dl/Z, m, Dl/Z)
@@ -80,21 +80,24 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
     for (int e = tid; e < 2 * P::TILE / 2; e += 256) z[e] = 0u;
   }
 
-  // K (scaled by c log2e) and V of this lane's slot: B operands of S / dP',
-  // k block kb, element e = d 32kb + 8g + e.
+  // K (RoPE applied when `rope`, then scaled by c log2e) and V of this lane's
+  // slot: B operands of S / dP', k block kb, element e = d 32kb + 8g + e.
   Limbs kl[P::KB], vl[P::KB];
 #pragma unroll
   for (int kb = 0; kb < P::KB; ++kb) {
     float xk[8], xv[8];
     const int d0 = 32 * kb + 8 * g;
     const bool ok = key_j >= 0 && key_j < T && d0 < D;
-    const f32x4* kp = reinterpret_cast<const f32x4*>(K + slice + (size_t)(ok ? key_j : 0) * D + (ok ? d0 : 0));
-    const f32x4* vp = reinterpret_cast<const f32x4*>(V + slice + (size_t)(ok ? key_j : 0) * D + (ok ? d0 : 0));
+    const int krow = ok ? key_j : 0;
+    const E* kp = view_slice<const E>(Kv, bh, H) + (long long)krow * Kv.rstride + (ok ? d0 : 0);
+    const E* vp = view_slice<const E>(Vv, bh, H) + (long long)krow * Vv.rstride + (ok ? d0 : 0);
 #pragma unroll
     for (int h2 = 0; h2 < 2; ++h2) {
       const bool ok2 = ok && d0 + 4 * h2 < D;
-      const f32x4 a = ok2 ? kp[h2] * cl2 : f32x4{0.f, 0.f, 0.f, 0.f};
-      const f32x4 b = ok2 ? vp[h2] : f32x4{0.f, 0.f, 0.f, 0.f};
+      f32x4 a = ok2 ? ld4(kp + 4 * h2) : f32x4{0.f, 0.f, 0.f, 0.f};
+      if (rope && ok2) a = rope4(a, rope_entry(rope, krow, D, d0 + 4 * h2), false);
+      a *= cl2;
+      const f32x4 b = ok2 ? ld4(vp + 4 * h2) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         xk[4 * h2 + e] = a[e];
@@ -189,6 +192,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
         sacc[rb] = f32x4{-s01[0], -s01[2], -s23[0], -s23[2]};
         pacc[rb] = f32x4{-s01[1], -s01[3], -s23[1], -s23[3]};
       }
+      prio_mfma_begin();
 #pragma unroll
       for (int kb = 0; kb < P::KB; ++kb) {
         const int col = 32 * kb + 8 * g;
@@ -215,6 +219,8 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
           pacc[1] = mfma16_step(st, ya[1], vl[kb], pacc[1]);
         }
       }
+      prio_mfma_end();
+      prio_valu_begin();
 
       // ---- segments along the slots (adjacent lanes of each DPP row) ----
       // Tiles where every slot key is visible to every query, with no key 0
@@ -289,6 +295,8 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
         xd[e] = dout_s[e >> 2][e & 3];
       }
       const Limbs wb = split8(xw), db = split8(xd);
+      prio_valu_end();
+      prio_mfma_begin();
       const int src_row = 4 * g + (j >> 2), src_col = 4 * (j & 3);
 #pragma unroll
       for (int mb = 0; mb < P::NMB; ++mb) {
@@ -307,6 +315,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
           acck[mb] = mfma16_step(st, qa, db, acck[mb]);
         }
       }
+      prio_mfma_end();
     }
     ds_blk += ds_kb_count(qt);
     if (qt + 1 < qt_end) store_tile(buf ^ 1);
@@ -318,39 +327,54 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
   // partials [key of the group][dV, dK][D] that ca_bwd_gain_merge sums.
   if (j >= 1 && j <= kBwdKeys && key_j < T && kb16 < nkb) {
     const float ck = cl2 * kLn2;
-    float* pv = nch == 1 ? dV + slice + (size_t)key_j * D
-                         : kv_part + (((size_t)bh * n_part + item) * kDkdvKeys + (key_j - w0)) * 2 * D;
-    float* pk = nch == 1 ? dK + slice + (size_t)key_j * D : pv + D;
+    if (nch == 1) {
+      // dK rotated back by the transposed RoPE (the gradient of the un-rotated k)
+      E* pv = view_slice<E>(dVv, bh, H) + (long long)key_j * dVv.rstride;
+      E* pk = view_slice<E>(dKv, bh, H) + (long long)key_j * dKv.rstride;
 #pragma unroll
-    for (int mb = 0; mb < P::NMB; ++mb) {
-      const int d0 = 16 * mb + 4 * g;
-      if (d0 < D) {
-        *reinterpret_cast<f32x4*>(pv + d0) = accv[mb];
-        *reinterpret_cast<f32x4*>(pk + d0) = acck[mb] * ck;
+      for (int mb = 0; mb < P::NMB; ++mb) {
+        const int d0 = 16 * mb + 4 * g;
+        if (d0 < D) {
+          st4(pv + d0, accv[mb]);
+          f32x4 gk = acck[mb] * ck;
+          if (rope) gk = rope4(gk, rope_entry(rope, key_j, D, d0), true);
+          st4(pk + d0, gk);
+        }
+      }
+    } else {
+      float* pv = kv_part + (((size_t)bh * n_part + item) * kDkdvKeys + (key_j - w0)) * 2 * D;
+      float* pk = pv + D;
+#pragma unroll
+      for (int mb = 0; mb < P::NMB; ++mb) {
+        const int d0 = 16 * mb + 4 * g;
+        if (d0 < D) {
+          *reinterpret_cast<f32x4*>(pv + d0) = accv[mb];
+          *reinterpret_cast<f32x4*>(pk + d0) = acck[mb] * ck;
+        }
       }
     }
   }
 }
 
-template <int D>
-hipError_t launch_bwd_dkdv(const float* k, const float* v, const BwdWork& ws, const float* log_gain,
-                           float* dk, float* dv, const DkdvSplit& kvs, int BH, int H, int T,
-                           hipStream_t stream) {
-  hipLaunchKernelGGL(ca_bwd_dkdv_kernel<D>, dim3(kvs.items * BH), dim3(256), 0, stream, k, v,
-                     ws.limbs, ws.qstat, log_gain, dk, dv, ws.dsbuf, ws.kv_part, BH, H, T,
-                     kvs.chunk, kvs.part_items);
+template <int D, class E>
+hipError_t launch_bwd_dkdv(const BwdIO& io, const BwdWork& ws, const DkdvSplit& kvs, int BH, int H,
+                           int T, hipStream_t stream) {
+  hipLaunchKernelGGL((ca_bwd_dkdv_kernel<D, E>), dim3(kvs.items * BH), dim3(256), 0, stream, io.k,
+                     io.v, io.rope, ws.limbs, ws.qstat, io.log_gain, io.dk, io.dv, ws.dsbuf,
+                     ws.kv_part, BH, H, T, kvs.chunk, kvs.part_items);
   return hipGetLastError();
 }
 
-#define CA_INSTANTIATE_DKDV(DD)                                                                   \
-  template hipError_t launch_bwd_dkdv<DD>(const float*, const float*, const BwdWork&,           \
-                                          const float*, float*, float*, const DkdvSplit&, int,   \
-                                          int, int, hipStream_t);
-CA_INSTANTIATE_DKDV(8)
-CA_INSTANTIATE_DKDV(16)
-CA_INSTANTIATE_DKDV(32)
-CA_INSTANTIATE_DKDV(64)
-CA_INSTANTIATE_DKDV(128)
+#define CA_INSTANTIATE_DKDV(DD, EE)                                                         \
+  template hipError_t launch_bwd_dkdv<DD, EE>(const BwdIO&, const BwdWork&, const DkdvSplit&, \
+                                              int, int, int, hipStream_t);
+#define CA_INSTANTIATE_DKDV_ALL(EE)                                                          \
+  CA_INSTANTIATE_DKDV(8, EE) CA_INSTANTIATE_DKDV(16, EE) CA_INSTANTIATE_DKDV(32, EE)         \
+  CA_INSTANTIATE_DKDV(64, EE) CA_INSTANTIATE_DKDV(128, EE)
+CA_INSTANTIATE_DKDV_ALL(float)
+CA_INSTANTIATE_DKDV_ALL(__bf16)
+CA_INSTANTIATE_DKDV_ALL(_Float16)
 #undef CA_INSTANTIATE_DKDV
+#undef CA_INSTANTIATE_DKDV_ALL
 
 }  // namespace ca

@@ -165,8 +165,96 @@ __device__ __forceinline__ Limbs split8(const float* x) {
                __builtin_bit_cast(bf16x8, L)};
 }
 
+// Wave priority around the matrix-product phases (experiment switch):
+// 1 raises it for MFMA blocks, 2 for the segment (VALU) blocks.
+#ifndef CA_PRIO_MFMA
+#define CA_PRIO_MFMA 0
+#endif
+__device__ __forceinline__ void prio_mfma_begin() { if (CA_PRIO_MFMA == 1) __builtin_amdgcn_s_setprio(1); }
+__device__ __forceinline__ void prio_mfma_end() { if (CA_PRIO_MFMA == 1) __builtin_amdgcn_s_setprio(0); }
+__device__ __forceinline__ void prio_valu_begin() { if (CA_PRIO_MFMA == 2) __builtin_amdgcn_s_setprio(1); }
+__device__ __forceinline__ void prio_valu_end() { if (CA_PRIO_MFMA == 2) __builtin_amdgcn_s_setprio(0); }
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// ---- operand views --------------------------------------------------------
+// Element (slice bh = b*H + h, row t, column d) of an operand of element type
+// E sits at  base + b*bstride + h*hstride + t*rstride + d.  The operator's own
+// tensors [B,H,T,D] (fp32) use (H*T*D, T*D, D); inside the decoder the
+// qkv projection output [B,T,3,H,D] serves q, k and v directly (bases H*D
+// apart, strides (3*T*H*D, D, 3*H*D)), and the attention output / its
+// gradient [B,T,H,D] uses (T*H*D, D, H*D).  Rows of D elements are
+// contiguous and start 16-byte (fp32) or 8-byte (16-bit types) aligned.
+struct View {
+  void* base;
+  long long bstride, hstride, rstride;
+};
+template <class E>
+__device__ __forceinline__ E* view_slice(const View& v, int bh, int H) {
+  return static_cast<E*>(v.base) + (long long)(bh / H) * v.bstride + (long long)(bh % H) * v.hstride;
+}
+
+// Four consecutive elements as loaded (raw) and converted to fp32.  16-bit
+// types are stored as bf16 or IEEE half; conversions round to nearest even.
+template <class E> struct Raw4;
+template <> struct Raw4<float> { typedef f32x4 type; };
+template <> struct Raw4<__bf16> { typedef u32x2 type; };
+template <> struct Raw4<_Float16> { typedef u32x2 type; };
+
+template <class E>
+__device__ __forceinline__ typename Raw4<E>::type ld_raw4(const E* p) {
+  return *reinterpret_cast<const typename Raw4<E>::type*>(p);
+}
+__device__ __forceinline__ f32x4 raw_to_f32(f32x4 r, const float*) { return r; }
+__device__ __forceinline__ f32x4 raw_to_f32(u32x2 r, const __bf16*) {
+  return f32x4{__uint_as_float(r[0] << 16), __uint_as_float(r[0] & 0xffff0000u),
+               __uint_as_float(r[1] << 16), __uint_as_float(r[1] & 0xffff0000u)};
+}
+__device__ __forceinline__ f32x4 raw_to_f32(u32x2 r, const _Float16*) {
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  const h4 a = __builtin_bit_cast(h4, r);  // whole-vector cast (see bf16x8 below)
+  return f32x4{(float)a[0], (float)a[1], (float)a[2], (float)a[3]};
+}
+template <class E>
+__device__ __forceinline__ f32x4 ld4(const E* p) {
+  return raw_to_f32(ld_raw4(p), p);
+}
+template <class E>
+__device__ __forceinline__ float ld1(const E* p) {
+  return (float)*p;
+}
+__device__ __forceinline__ float ld1(const __bf16* p) {
+  return __uint_as_float((unsigned)*reinterpret_cast<const unsigned short*>(p) << 16);
+}
+
+__device__ __forceinline__ void st4(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
+__device__ __forceinline__ void st4(__bf16* p, f32x4 v) {
+  *reinterpret_cast<u32x2*>(p) = u32x2{cvt_pk_bf16(v[0], v[1]), cvt_pk_bf16(v[2], v[3])};
+}
+__device__ __forceinline__ void st4(_Float16* p, f32x4 v) {
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  *reinterpret_cast<h4*>(p) = h4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+}
+__device__ __forceinline__ void st1(float* p, float v) { *p = v; }
+__device__ __forceinline__ void st1(__bf16* p, float v) {
+  *reinterpret_cast<unsigned short*>(p) = (unsigned short)(cvt_pk_bf16(v, 0.f) & 0xffffu);
+}
+__device__ __forceinline__ void st1(_Float16* p, float v) { *p = (_Float16)v; }
+
+// RoPE of four consecutive head-dim entries d0..d0+3 (two interleaved pairs)
+// of row t: cs is the fp32 table [T][D/2][2] = (cos, sin), whose row t holds D
+// floats, so the two pairs' entries are cs[t*D + d0 .. d0+3].  Forward
+// rotation x0' = x0 c - x1 s, x1' = x1 c + x0 s; `inverse` applies the
+// transpose (the gradient's rotation back).
+__device__ __forceinline__ f32x4 rope4(f32x4 x, f32x4 t, bool inverse) {
+  const float s0 = inverse ? -t[1] : t[1], s1 = inverse ? -t[3] : t[3];
+  return f32x4{x[0] * t[0] - x[1] * s0, x[1] * t[0] + x[0] * s0, x[2] * t[2] - x[3] * s1,
+               x[3] * t[2] + x[2] * s1};
+}
+__device__ __forceinline__ f32x4 rope_entry(const float* cs, long long t, int D, int d0) {
+  return *reinterpret_cast<const f32x4*>(cs + t * D + d0);
+}
 
 // Per-head score scale in log2 units: exp(log_gain[h]) / sqrt(D) * log2(e)
 // (the reference's scale, cuda/continuum_attention.py:656-657, times log2 e).

@@ -80,15 +80,20 @@ __device__ __forceinline__ void fwd_decode_item(int item, int G, int T, int C, i
   g = -1; s = 0; nsplit = 0;
 }
 
-template <int D>
-__device__ __forceinline__ float halo_dot(const float* qreg, const float* __restrict__ krow) {
+// q . k of key `key` (RoPE applied to the key when `rope`), reduced over the
+// two lane halves that hold the query's halves.
+template <int D, class E>
+__device__ __forceinline__ float halo_dot(const float* qreg, const E* __restrict__ Ks,
+                                          long long rstride, const float* __restrict__ rope,
+                                          int key) {
   constexpr int DH = D / 2;
   const int h = (threadIdx.x >> 5) & 1;
-  const f32x4* kp = reinterpret_cast<const f32x4*>(krow + h * DH);
+  const E* kp = Ks + (long long)key * rstride + h * DH;
   float acc = 0.0f;
 #pragma unroll
   for (int c = 0; c < DH / 4; ++c) {
-    f32x4 kv = kp[c];
+    f32x4 kv = ld4(kp + 4 * c);
+    if (rope) kv = rope4(kv, rope_entry(rope, key, D, h * DH + 4 * c), false);
     acc = fmaf(qreg[4 * c + 0], kv[0], acc);
     acc = fmaf(qreg[4 * c + 1], kv[1], acc);
     acc = fmaf(qreg[4 * c + 2], kv[2], acc);
@@ -97,11 +102,11 @@ __device__ __forceinline__ float halo_dot(const float* qreg, const float* __rest
   return acc + xhalf(acc);
 }
 
-template <int D>
+template <int D, class E, bool ROPE>
 __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
-    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-    const float* __restrict__ log_gain, float* __restrict__ O, float* __restrict__ stats,
-    float* __restrict__ part, int BH, int H, int T, int C, int G, int smax) {
+    View Qv, View Kv, View Vv, const float* __restrict__ rope, const float* __restrict__ log_gain,
+    float* __restrict__ O, View Ov, float* __restrict__ stats, float* __restrict__ part, int BH,
+    int H, int T, int C, int G, int smax) {
   using P = Fwd<D>;
   // [buffer][limb][plane]
   __shared__ __attribute__((aligned(16))) __bf16 lds_k[2][3][P::KPLANE];
@@ -129,19 +134,22 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
   const bool wave_active = (128 * g + 32 * w < T) && (t_b <= wave_tmax);
 
   const size_t slice = (size_t)bh * T * D;
-  const float* Qs = Q + slice;
-  const float* Ks = K + slice;
-  const float* Vs = V + slice;
+  const E* __restrict__ Qs = view_slice<const E>(Qv, bh, H);
+  const E* __restrict__ Ks = view_slice<const E>(Kv, bh, H);
+  const E* __restrict__ Vs = view_slice<const E>(Vv, bh, H);
+  const long long krs = Kv.rstride, vrs = Vv.rstride;
+  if (!ROPE) rope = nullptr;  // lets the compiler drop every rotation
   const int head = bh % H;
   const float cl2 = head_scale_log2(log_gain, head, D);
 
   // lane (q,h) holds Q[i][h*DH + k] * c*log2e
   float qreg[P::DH];
   {
-    const f32x4* qp = reinterpret_cast<const f32x4*>(Qs + (size_t)(qvalid ? i : 0) * D + h * P::DH);
+    const E* qp = Qs + (long long)(qvalid ? i : 0) * Qv.rstride + h * P::DH;
 #pragma unroll
     for (int c = 0; c < P::CH; ++c) {
-      f32x4 v4 = qvalid ? qp[c] : f32x4{0.f, 0.f, 0.f, 0.f};
+      f32x4 v4 = qvalid ? ld4(qp + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
+      if (rope && qvalid) v4 = rope4(v4, rope_entry(rope, i, D, h * P::DH + 4 * c), false);
       qreg[4 * c + 0] = v4[0] * cl2;
       qreg[4 * c + 1] = v4[1] * cl2;
       qreg[4 * c + 2] = v4[2] * cl2;
@@ -153,12 +161,12 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
   float m_ref = 0.f, s_carry = 0.f, r_carry = 0.f, zsum = 0.f;
   if (wave_active) {
     if (t_b == 0) {
-      m_ref = halo_dot<D>(qreg, Ks);
+      m_ref = halo_dot<D>(qreg, Ks, krs, rope, 0);
       s_carry = 0.0f;  // score of key 0 relative to m_ref
     } else {
       const int k0 = 32 * t_b;  // <= first query of this wave, so both halo keys are visible
-      s_carry = halo_dot<D>(qreg, Ks + (size_t)k0 * D);
-      const float s_prev = halo_dot<D>(qreg, Ks + (size_t)(k0 - 1) * D);
+      s_carry = halo_dot<D>(qreg, Ks, krs, rope, k0);
+      const float s_prev = halo_dot<D>(qreg, Ks, krs, rope, k0 - 1);
       m_ref = fmaxf(s_carry, s_prev);
       float l_unused;
       seg_shares(s_prev, s_carry, fast_exp2(s_prev - m_ref), fast_exp2(s_carry - m_ref), l_unused,
@@ -198,28 +206,37 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
   // lanes of one c write 16 consecutive words of each V^T row, and the four c
   // of a wave rows 80 words apart, so the stores of a wave hit 64 distinct
   // banks (the loads still read whole 64-byte row segments).
-  f32x4 pre_k[P::LD_PER_THREAD], pre_v[P::VLD][2];
+  // The loads of the next tile stay raw (input element type, RoPE entries
+  // beside them) until store_tile, so the tile in flight is not waited for.
+  typedef typename Raw4<E>::type R4;
+  R4 pre_k[P::LD_PER_THREAD], pre_v[P::VLD][2];
+  f32x4 pre_cs[ROPE ? P::LD_PER_THREAD : 1];
   auto load_tile = [&](int t) {
 #pragma unroll
     for (int j = 0; j < P::LD_PER_THREAD; ++j) {
       const int e = tid + 256 * j;
-      f32x4 kv = {0.f, 0.f, 0.f, 0.f};
+      R4 kv = {};
+      f32x4 cs = {1.f, 0.f, 1.f, 0.f};
       if (e < P::TILE_F4) {
         const int row = e / P::C4, c = e % P::C4;
         const int kk = 32 * t + 1 + row;  // score key
-        if (kk < T) kv = reinterpret_cast<const f32x4*>(Ks + (size_t)kk * D)[c];
+        if (kk < T) {
+          kv = ld_raw4(Ks + (long long)kk * krs + 4 * c);
+          if (ROPE) cs = rope_entry(rope, kk, D, 4 * c);
+        }
       }
       pre_k[j] = kv;
+      if constexpr (ROPE) pre_cs[j] = cs;
     }
 #pragma unroll
     for (int j = 0; j < P::VLD; ++j) {
       const int u = tid + 256 * j;
-      f32x4 v0 = {0.f, 0.f, 0.f, 0.f}, v1 = {0.f, 0.f, 0.f, 0.f};
+      R4 v0 = {}, v1 = {};
       if (u < P::VUNITS) {
         const int pp = u % 16, c = u / 16;
         const int vk = 32 * t + 2 * pp;  // weight key
-        if (vk < T) v0 = reinterpret_cast<const f32x4*>(Vs + (size_t)vk * D)[c];
-        if (vk + 1 < T) v1 = reinterpret_cast<const f32x4*>(Vs + (size_t)(vk + 1) * D)[c];
+        if (vk < T) v0 = ld_raw4(Vs + (long long)vk * vrs + 4 * c);
+        if (vk + 1 < T) v1 = ld_raw4(Vs + (long long)(vk + 1) * vrs + 4 * c);
       }
       pre_v[j][0] = v0;
       pre_v[j][1] = v1;
@@ -233,9 +250,11 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
         const int row = e / P::C4, c = e % P::C4;
         const int d = 4 * c, half = d / P::DH;
         const int off = arow_of_key(row) * P::KROW + half * 8 * P::KB + (d - half * P::DH);
+        f32x4 kv = raw_to_f32(pre_k[j], Ks);
+        if constexpr (ROPE) kv = rope4(kv, pre_cs[j], false);
         unsigned h0, m0, l0, h1, m1, l1;
-        split_pair(pre_k[j][0], pre_k[j][1], h0, m0, l0);
-        split_pair(pre_k[j][2], pre_k[j][3], h1, m1, l1);
+        split_pair(kv[0], kv[1], h0, m0, l0);
+        split_pair(kv[2], kv[3], h1, m1, l1);
         *reinterpret_cast<u32x2*>(&lds_k[buf][0][off]) = u32x2{h0, h1};
         *reinterpret_cast<u32x2*>(&lds_k[buf][1][off]) = u32x2{m0, m1};
         *reinterpret_cast<u32x2*>(&lds_k[buf][2][off]) = u32x2{l0, l1};
@@ -246,10 +265,11 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
       const int u = tid + 256 * j;
       if (u < P::VUNITS) {
         const int pp = u % 16, c = u / 16;
+        const f32x4 va = raw_to_f32(pre_v[j][0], Vs), vb = raw_to_f32(pre_v[j][1], Vs);
 #pragma unroll
         for (int x = 0; x < 4; ++x) {
           unsigned hv, mv, lv;
-          split_pair(pre_v[j][0][x], pre_v[j][1][x], hv, mv, lv);
+          split_pair(va[x], vb[x], hv, mv, lv);
           const int off = (4 * c + x) * P::VROW + 2 * pp;
           *reinterpret_cast<unsigned*>(&lds_vt[buf][0][off]) = hv;
           *reinterpret_cast<unsigned*>(&lds_vt[buf][1][off]) = mv;
@@ -279,6 +299,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
       f32x16 sacc;
 #pragma unroll
       for (int r = 0; r < 16; ++r) sacc[r] = -m_ref;
+      prio_mfma_begin();
       {
         const __bf16* krow = &lds_k[buf][0][q * P::KROW + h * 8 * P::KB];
 #pragma unroll
@@ -290,6 +311,8 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
           sacc = mfma_x6(ka, qb[kb], sacc);
         }
       }
+      prio_mfma_end();
+      prio_valu_begin();
       const int kbase = 32 * t + 1 + 16 * h;  // score key of register 0
       // ---- row max of the tile (visible keys only), relative to m_ref ----
       float mt = kNegBig;
@@ -359,6 +382,8 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
       r_carry = xr15;
       sacc[0] += r_in;
       zsum += zt + r_in;
+      prio_valu_end();
+      prio_mfma_begin();
 
       // ---- O^T += V^T W^T: k block kb, element e = weight key 16h + 8kb + e ----
 #pragma unroll
@@ -378,6 +403,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
           acc_o[mb] = mfma_x6(va, wb, acc_o[mb]);
         }
       }
+      prio_mfma_end();
     };
     if (wave_active && t <= wave_tmax) {
       if (t == 0 || t == wave_tmax)
@@ -417,6 +443,8 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
     return;
   }
   if (!qvalid) return;
+  // a single-split row is final: also written token-major in the input type
+  E* otok = (single && Ov.base) ? view_slice<E>(Ov, bh, H) + (long long)i * Ov.rstride : nullptr;
 #pragma unroll
   for (int mb = 0; mb < P::NMB; ++mb) {
 #pragma unroll
@@ -426,6 +454,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
         f32x4 v4 = {acc_o[mb][4 * r4 + 0] * scl, acc_o[mb][4 * r4 + 1] * scl,
                     acc_o[mb][4 * r4 + 2] * scl, acc_o[mb][4 * r4 + 3] * scl};
         *reinterpret_cast<f32x4*>(dst + d0) = v4;
+        if (otok) st4(otok + d0, v4);
       }
     }
   }
@@ -443,11 +472,11 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
 
 // Merges split partials of rows whose group spans more than one split: one
 // float4 chunk of one row per thread, splits summed in index order.
-template <int D>
+template <int D, class E>
 __global__ __launch_bounds__(256) void ca_fwd_combine_kernel(const float* __restrict__ part,
-                                                             float* __restrict__ O,
+                                                             float* __restrict__ O, View Ov,
                                                              float* __restrict__ stats, int BH,
-                                                             int T, int C, int smax) {
+                                                             int H, int T, int C, int smax) {
   constexpr int C4 = D / 4;
   const int tix = blockIdx.x * 256 + threadIdx.x;
   const int row = tix / C4, c = tix % C4;
@@ -471,46 +500,49 @@ __global__ __launch_bounds__(256) void ca_fwd_combine_kernel(const float* __rest
   }
   const float invz = 1.0f / Z;
   reinterpret_cast<f32x4*>(O + (size_t)row * D)[c] = acc * invz;
+  if (Ov.base) st4(view_slice<E>(Ov, bh, H) + (long long)i * Ov.rstride + 4 * c, acc * invz);
   if (c == 0) {
     stats[(size_t)row * 2 + 0] = M;
     stats[(size_t)row * 2 + 1] = invz;
   }
 }
 
-template <int D>
-hipError_t launch_fwd(const float* q, const float* k, const float* v, const float* log_gain,
-                      float* o, float* stats, float* part, int B, int H, int T, int C,
+template <int D, class E>
+hipError_t launch_fwd(const FwdIO& io, float* part, int B, int H, int T, int C,
                       hipStream_t stream) {
   const int BH = B * H;
   const int G = (T + 127) / 128;
   const int smax = fwd_max_splits(T, C);
   const int items = fwd_num_items(T, C);
   timer_begin(kFwd, stream);
-  hipLaunchKernelGGL(ca_fwd_kernel<D>, dim3(items * BH), dim3(256), 0, stream, q, k, v, log_gain,
-                     o, stats, part, BH, H, T, C, G, smax);
+  if (io.rope)
+    hipLaunchKernelGGL((ca_fwd_kernel<D, E, true>), dim3(items * BH), dim3(256), 0, stream, io.q,
+                       io.k, io.v, io.rope, io.log_gain, io.y, io.out, io.stats, part, BH, H, T, C,
+                       G, smax);
+  else
+    hipLaunchKernelGGL((ca_fwd_kernel<D, E, false>), dim3(items * BH), dim3(256), 0, stream, io.q,
+                       io.k, io.v, io.rope, io.log_gain, io.y, io.out, io.stats, part, BH, H, T, C,
+                       G, smax);
   timer_end(kFwd, stream);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (smax > 1) {
     const int rows = BH * T;
     timer_begin(kFwdCombine, stream);
-    hipLaunchKernelGGL(ca_fwd_combine_kernel<D>, dim3((rows * (D / 4) + 255) / 256), dim3(256), 0,
-                       stream, part, o, stats, BH, T, C, smax);
+    hipLaunchKernelGGL((ca_fwd_combine_kernel<D, E>), dim3((rows * (D / 4) + 255) / 256), dim3(256),
+                       0, stream, part, io.y, io.out, io.stats, BH, H, T, C, smax);
     timer_end(kFwdCombine, stream);
     e = hipGetLastError();
   }
   return e;
 }
 
-template hipError_t launch_fwd<8>(const float*, const float*, const float*, const float*, float*,
-                                  float*, float*, int, int, int, int, hipStream_t);
-template hipError_t launch_fwd<16>(const float*, const float*, const float*, const float*, float*,
-                                   float*, float*, int, int, int, int, hipStream_t);
-template hipError_t launch_fwd<32>(const float*, const float*, const float*, const float*, float*,
-                                   float*, float*, int, int, int, int, hipStream_t);
-template hipError_t launch_fwd<128>(const float*, const float*, const float*, const float*, float*,
-                                    float*, float*, int, int, int, int, hipStream_t);
-template hipError_t launch_fwd<64>(const float*, const float*, const float*, const float*, float*,
-                                   float*, float*, int, int, int, int, hipStream_t);
+#define CA_INST_FWD(DD, EE) \
+  template hipError_t launch_fwd<DD, EE>(const FwdIO&, float*, int, int, int, int, hipStream_t);
+#define CA_INST_FWD_ALL(EE) \
+  CA_INST_FWD(8, EE) CA_INST_FWD(16, EE) CA_INST_FWD(32, EE) CA_INST_FWD(64, EE) CA_INST_FWD(128, EE)
+CA_INST_FWD_ALL(float)
+CA_INST_FWD_ALL(__bf16)
+CA_INST_FWD_ALL(_Float16)
 
 }  // namespace ca

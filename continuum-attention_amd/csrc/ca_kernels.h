@@ -4,6 +4,7 @@
 #include <stddef.h>
 
 #include "../../include/continuum_attention_amd.h"
+#include "ca_common.h"
 
 namespace ca {
 
@@ -212,8 +213,8 @@ inline DkdvSplit dkdv_split(int BH, int T, int resident_groups) {
 
 // Per-kernel HIP-event timing (diagnostics; off unless ca_timing_enable(1)).
 enum KernelId {
-  kFwd = 0, kFwdCombine, kBwdPrep, kBwdDkdv, kBwdDq, kBwdGain, kWeights, kWeightsBwd, kQkvIn,
-  kQkvGrad, kRelayout, kRmsFwd, kRmsBwd, kSwigluFwd, kSwigluBwd, kNumKernels
+  kFwd = 0, kFwdCombine, kBwdPrep, kBwdDkdv, kBwdDq, kBwdGain, kWeights, kWeightsBwd, kRmsFwd,
+  kRmsBwd, kSwigluFwd, kSwigluBwd, kNumKernels
 };
 
 // Element types of the prologue / epilogue buffers (CA_DTYPE_* in the ABI).
@@ -272,17 +273,32 @@ hipError_t launch_weights_bwd(const float* scores, const float* grad_weights, fl
                               float* grad_scores, int BH, int Q, int K, int start,
                               hipStream_t stream);
 
-// Prologue / epilogue of the decoder caller (ca_rope.hip).
-hipError_t launch_qkv_in(const void* qkv, int dtype, const float* cs, float* q, float* k, float* v,
-                         int B, int T, int H, int D, hipStream_t s);
-hipError_t launch_qkv_grad(const float* dq, const float* dk, const float* dv, const float* cs,
-                           void* dqkv, int dtype, int B, int T, int H, int D, hipStream_t s);
-hipError_t launch_relayout(const void* src, void* dst, int dtype, bool to_tokens, int B, int H,
-                           int T, int D, hipStream_t s);
+// Operands of the forward and backward as strided views (View, ca_common.h)
+// of element type E (float, __bf16 or _Float16, a launch template
+// parameter): the operator's own fp32 [B,H,T,D] tensors, or inside the
+// decoder the token-major qkv projection output [B,T,3,H,D] with RoPE applied
+// to q and k as they are read.
+struct FwdIO {
+  View q, k, v;            // inputs
+  const float* rope;       // [T][D/2][2] (cos, sin) for q and k, or nullptr
+  const float* log_gain;   // [H]
+  float* y;                // fp32 [B,H,T,D] output (read by the backward)
+  View out;                // optional copy of the output in E (base nullptr: none)
+  float* stats;            // [B*H*T][2]
+};
+struct BwdIO {
+  View q, k, v;            // the forward's inputs
+  const float* rope;       // as in FwdIO; the gradients of q and k are rotated back
+  const float* log_gain;
+  const float* y;          // fp32 [B,H,T,D] forward output
+  const float* stats;
+  View dout;               // dL/d(output), element type E
+  View dq, dk, dv;         // gradients, element type E
+  float* dlog_gain;        // [H]
+};
 
-template <int D>
-hipError_t launch_fwd(const float* q, const float* k, const float* v, const float* log_gain,
-                      float* o, float* stats, float* part, int B, int H, int T, int C,
+template <int D, class E>
+hipError_t launch_fwd(const FwdIO& io, float* part, int B, int H, int T, int C,
                       hipStream_t stream);
 
 // Backward workspace buffers (sizes: bwd_ds_floats, bwd_limb_elems, BH*T*2
@@ -297,16 +313,13 @@ struct BwdWork {
 };
 
 // dK/dV kernel of the backward (ca_bwd_dkdv.hip, its own translation unit).
-template <int D>
-hipError_t launch_bwd_dkdv(const float* k, const float* v, const BwdWork& ws, const float* log_gain,
-                           float* dk, float* dv, const DkdvSplit& kvs, int BH, int H, int T,
-                           hipStream_t stream);
+template <int D, class E>
+hipError_t launch_bwd_dkdv(const BwdIO& io, const BwdWork& ws, const DkdvSplit& kvs, int BH, int H,
+                           int T, hipStream_t stream);
 inline size_t bwd_limb_elems(int BH, int T, int D) { return (size_t)6 * BH * T * D; }
 
-template <int D>
-hipError_t launch_bwd(const float* q, const float* k, const float* v, const float* log_gain,
-                      const float* o, const float* stats, const float* dout, float* dq, float* dk,
-                      float* dv, float* dlog_gain, const BwdWork& ws, const DqSplit& sp,
-                      const DkdvSplit& kvs, int B, int H, int T, hipStream_t stream);
+template <int D, class E>
+hipError_t launch_bwd(const BwdIO& io, const BwdWork& ws, const DqSplit& sp, const DkdvSplit& kvs,
+                      int B, int H, int T, hipStream_t stream);
 
 }  // namespace ca

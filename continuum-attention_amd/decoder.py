@@ -26,7 +26,8 @@ from torch import nn
 from torch.nn import functional as F
 
 from . import _native
-from .ops import SUPPORTED_HEAD_DIMS, _mode, ca_backward, ca_forward, continuum_attention
+from .ops import (SUPPORTED_HEAD_DIMS, _bwd_workspace_bytes, _fwd_workspace_bytes, _mode,
+                  continuum_attention)
 
 _DTYPE_CODE = {torch.float32: _native.CA_DTYPE_F32, torch.bfloat16: _native.CA_DTYPE_BF16,
                torch.float16: _native.CA_DTYPE_F16}
@@ -269,10 +270,12 @@ def _aligned(x, nbytes):
 
 class _RopeContinuumAttention(torch.autograd.Function):
     """qkv projection output -> RoPE -> CA operator -> token-major output, with
-    the prologue and epilogue as single HIP passes (ca_qkv_rope_in /
-    ca_heads_to_tokens and their gradients) around the operator's kernels.
-    Same result as ``apply_rope`` + ``continuum_attention`` + transpose, with
-    the rotation done in fp32."""
+    the operator's kernels reading the projection output [B, T, 3, H, D]
+    directly (q and k rotated as they are read, in fp32) and writing the
+    output token-major in the projection's dtype (ca_fwd_qkv); the backward
+    (ca_bwd_qkv) reads the output gradient token-major and writes the qkv
+    gradient, the q and k parts rotated back.  Same result as ``apply_rope``
+    + ``continuum_attention`` + transpose, with the rotation done in fp32."""
 
     @staticmethod
     def forward(ctx, qkv, log_gain, theta, heads, query_tile):
@@ -290,43 +293,45 @@ class _RopeContinuumAttention(torch.autograd.Function):
         D = C // heads
         dev, dt = qkv.device, _DTYPE_CODE[qkv.dtype]
         x = _aligned(qkv.detach(), 16)
-        cs = rope_cos_sin(T, D, theta, dev)
-        q, k, v = (torch.empty(Bsz, heads, T, D, device=dev, dtype=torch.float32) for _ in range(3))
-        stream = _native.stream_handle(dev)
+        cs = rope_cos_sin(T, D, theta, dev) if theta is not None else None
+        gain = log_gain.detach().float().contiguous()
+        y = torch.empty(Bsz, heads, T, D, device=dev, dtype=torch.float32)
+        out = torch.empty(Bsz, T, C, device=dev, dtype=qkv.dtype)
+        stats = torch.empty(Bsz * heads * T, 2, device=dev, dtype=torch.float32)
+        nbytes = _fwd_workspace_bytes(Bsz, heads, T, D)
+        ws = torch.empty(max(nbytes, 1), device=dev, dtype=torch.uint8)
         with _native.on_device(dev):
-            _native.check(lib.ca_qkv_rope_in(x.data_ptr(), dt, cs.data_ptr(), q.data_ptr(),
-                                             k.data_ptr(), v.data_ptr(), Bsz, T, heads, D, stream))
-            y, stats = ca_forward(q, k, v, log_gain)
-            out = torch.empty(Bsz, T, C, device=dev, dtype=qkv.dtype)
-            _native.check(lib.ca_heads_to_tokens(y.data_ptr(), out.data_ptr(), dt, Bsz, heads, T, D,
-                                                 stream))
-        ctx.save_for_backward(q, k, v, log_gain, y, stats, cs)
+            _native.check(lib.ca_fwd_qkv(x.data_ptr(), dt, cs.data_ptr() if cs is not None else None,
+                                         gain.data_ptr(), y.data_ptr(), out.data_ptr(),
+                                         stats.data_ptr(), ws.data_ptr(), nbytes, Bsz, T, heads, D,
+                                         _native.stream_handle(dev)))
+        ctx.save_for_backward(x, gain, y, stats)
+        ctx.cs = cs
         ctx.shape = (Bsz, T, heads, D)
-        ctx.qkv_dtype = qkv.dtype
+        ctx.gain_dtype = log_gain.dtype
         return out
 
     @staticmethod
     def backward(ctx, gout):
         if torch.is_grad_enabled():
             raise RuntimeError("CA Volta analytic kernel supports first-order gradients only")
-        q, k, v, log_gain, y, stats, cs = ctx.saved_tensors
+        x, gain, y, stats = ctx.saved_tensors
+        cs = ctx.cs
         Bsz, T, heads, D = ctx.shape
         lib = _native.load()
-        dev = q.device
-        g = _aligned(gout, 16)
-        if g.dtype not in _DTYPE_CODE:
-            g = g.float()
-        dyf = torch.empty(Bsz, heads, T, D, device=dev, dtype=torch.float32)
-        stream = _native.stream_handle(dev)
+        dev = x.device
+        g = _aligned(gout.to(x.dtype), 16)
+        dqkv = torch.empty(Bsz, T, 3 * heads * D, device=dev, dtype=x.dtype)
+        dg = torch.empty(heads, device=dev, dtype=torch.float32)
+        nbytes = _bwd_workspace_bytes(Bsz, heads, T, D)
+        ws = torch.empty(nbytes, device=dev, dtype=torch.uint8)
         with _native.on_device(dev):
-            _native.check(lib.ca_tokens_to_heads(g.data_ptr(), _DTYPE_CODE[g.dtype], dyf.data_ptr(),
-                                                 Bsz, heads, T, D, stream))
-            dq, dk, dv, dg = ca_backward(q, k, v, log_gain, y, stats, dyf)
-            dqkv = torch.empty(Bsz, T, 3 * heads * D, device=dev, dtype=ctx.qkv_dtype)
-            _native.check(lib.ca_qkv_rope_grad(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-                                               cs.data_ptr(), dqkv.data_ptr(),
-                                               _DTYPE_CODE[ctx.qkv_dtype], Bsz, T, heads, D, stream))
-        return dqkv, dg.to(log_gain.dtype), None, None, None
+            _native.check(lib.ca_bwd_qkv(x.data_ptr(), _DTYPE_CODE[x.dtype],
+                                         cs.data_ptr() if cs is not None else None, gain.data_ptr(),
+                                         y.data_ptr(), stats.data_ptr(), g.data_ptr(),
+                                         dqkv.data_ptr(), dg.data_ptr(), ws.data_ptr(), nbytes, Bsz,
+                                         T, heads, D, _native.stream_handle(dev)))
+        return dqkv, dg.to(ctx.gain_dtype), None, None, None
 
 
 def rope_continuum_attention(qkv, log_gain, theta, heads, query_tile=64):

@@ -110,36 +110,36 @@ int ca_weights_f32(const float* scores, float* weights, float* stats, int BH, in
 int ca_weights_bwd_f32(const float* scores, const float* grad_weights, float* weights,
                        float* grad_scores, int BH, int Q, int K, int start, void* stream);
 
-/* ---- Decoder prologue / epilogue -------------------------------------------
- * Layout and RoPE steps around the operator in the decoder caller
- * (ContinuumSelfAttention.forward, cuda/continuum_attention.py:848-854), each
- * one pass.  Token-major buffers hold elements of type `dtype` (CA_DTYPE_*);
- * head-major buffers are fp32 [B, H, T, D].  D must be a multiple of 4.
+/* ---- The operator inside the decoder ---------------------------------------
+ * The same forward and backward reading the decoder's qkv projection output
+ * directly: qkv is [B, T, 3, H, D] (the projection's [B, T, 3*H*D] output,
+ * token-major) of element type `dtype` (CA_DTYPE_*), q and k are rotated by
+ * RoPE as the kernels read them, and the attention output is written
+ * token-major [B, T, H*D] in the same type, ready for the output projection.
  * rope_cs is the fp32 table [T][D/2][2] = (cos, sin) of t * theta^(-2i/D)
- * for interleaved pairs (cuda/continuum_attention.py:826-835); NULL skips the
- * rotation.  No native counterpart in the reference: these replace torch op
- * chains. */
+ * for interleaved pairs (cuda/continuum_attention.py:826-835); NULL means no
+ * rotation.  The rotation is computed in fp32.  y is the fp32 [B, H, T, D]
+ * output the backward needs (as ca_fwd_f32's `out`); stats as in ca_fwd_f32.
+ * Workspaces are ca_fwd_workspace_bytes / ca_bwd_workspace_bytes of
+ * (B, H, T, D).  D in {8, 16, 32, 64, 128}; qkv, out, dout and dqkv 8-byte
+ * (16-bit types) or 16-byte (fp32) aligned, y 16-byte aligned.
+ * Replaces: the reshape/permute/unbind of the projection, apply_rope, the
+ * operator, and the transpose/reshape of its output in
+ * ContinuumSelfAttention.forward (cuda/continuum_attention.py:848-854), and
+ * their autograd. */
 enum { CA_DTYPE_F32 = 0, CA_DTYPE_BF16 = 1, CA_DTYPE_F16 = 2 };
 
-/* qkv [B, T, 3, H, D] (the qkv projection's output viewed per head) ->
- * q, k, v fp32 [B, H, T, D], RoPE applied to q and k in fp32.  Replaces the
- * reshape/permute/unbind and apply_rope of cuda/continuum_attention.py:
- * 849-852 and the operator's float upcast. */
-int ca_qkv_rope_in(const void* qkv, int dtype, const float* rope_cs, float* q, float* k, float* v,
-                   int B, int T, int H, int D, void* stream);
+int ca_fwd_qkv(const void* qkv, int dtype, const float* rope_cs, const float* log_gain, float* y,
+               void* out, float* stats, void* workspace, size_t workspace_bytes, int B, int T,
+               int H, int D, void* stream);
 
-/* dqkv [B, T, 3, H, D] = (R^T dq, R^T dk, dv): the backward of ca_qkv_rope_in
- * (autograd of the same torch chain). */
-int ca_qkv_rope_grad(const float* dq, const float* dk, const float* dv, const float* rope_cs,
-                     void* dqkv, int dtype, int B, int T, int H, int D, void* stream);
-
-/* y fp32 [B, H, T, D] -> out [B, T, H*D] (dtype), and back: the operator
- * output's transpose/reshape/cast into the output projection
- * (cuda/continuum_attention.py:854) and its gradient. */
-int ca_heads_to_tokens(const float* y, void* out, int dtype, int B, int H, int T, int D,
-                       void* stream);
-int ca_tokens_to_heads(const void* x, int dtype, float* out, int B, int H, int T, int D,
-                       void* stream);
+/* Backward of ca_fwd_qkv: dout [B, T, H*D] (dtype) -> dqkv [B, T, 3, H, D]
+ * (dtype; the gradients of q and k rotated back by the transposed RoPE) and
+ * dlog_gain[H]. */
+int ca_bwd_qkv(const void* qkv, int dtype, const float* rope_cs, const float* log_gain,
+               const float* y, const float* stats, const void* dout, void* dqkv,
+               float* dlog_gain, void* workspace, size_t workspace_bytes, int B, int T, int H,
+               int D, void* stream);
 
 /* ---- SwiGLU gate of the TinyLM MLP ----------------------------------------
  * No reference counterpart: F.silu(gate) * value of SwiGLU.forward
@@ -225,8 +225,8 @@ int ca_bf16_shadow(const ca_opt_tensor* tensors, int ntensors, const int* chunks
  * Per-kernel timing with HIP events recorded on the launch stream around each
  * kernel launch of the calls above.  Kernel ids: 0 forward, 1 forward split
  * combine, 2 backward prep, 3 backward dK/dV, 4 backward dQ, 5 backward
- * gain / partial merge, 6 weights, 7 weights backward, 8 qkv prologue, 9 qkv
- * gradient, 10 relayout, 11 RMSNorm forward, 12 RMSNorm backward.
+ * gain / partial merge, 6 weights, 7 weights backward, 8 RMSNorm forward,
+ * 9 RMSNorm backward, 10 SwiGLU forward, 11 SwiGLU backward.
  * ca_timing_enable(on) turns recording on/off and discards
  * unread records; ca_timing_read waits for the recorded events and returns the
  * summed milliseconds and launch counts per id (n entries), then clears them.

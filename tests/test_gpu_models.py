@@ -240,29 +240,86 @@ def _unfused_attention(Dm, qkv, log_gain, theta, heads):
     return y.transpose(1, 2).reshape(Bsz, T, C3 // 3)
 
 
-def test_prologue_relayout_bit_exact(gpu_ca):
-    """Without rotation the prologue is a pure permute and the epilogue a
-    transpose + cast: bit-identical to torch, including bf16/fp16 rounding."""
-    say("[case] prologue relayout")
-    lib = gpu_ca.native.load()
-    Bsz, T, H, D = 2, 37, 3, 16
-    g = torch.Generator().manual_seed(3)
-    for dt, code in ((torch.float32, 0), (torch.bfloat16, 1), (torch.float16, 2)):
-        qkv = (torch.randn(Bsz, T, 3 * H * D, generator=g) * 3).to(dt).cuda()
-        q, k, v = (torch.empty(Bsz, H, T, D, device="cuda") for _ in range(3))
-        s = torch.cuda.current_stream().cuda_stream
-        assert lib.ca_qkv_rope_in(qkv.data_ptr(), code, None, q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                  Bsz, T, H, D, s) == 0
-        ref = qkv.float().view(Bsz, T, 3, H, D).permute(2, 0, 3, 1, 4)
-        for got, r in zip((q, k, v), ref):
-            assert torch.equal(got, r)
-        y = torch.randn(Bsz, H, T, D, generator=g).cuda() * 7
-        out = torch.empty(Bsz, T, H * D, device="cuda", dtype=dt)
-        assert lib.ca_heads_to_tokens(y.data_ptr(), out.data_ptr(), code, Bsz, H, T, D, s) == 0
-        assert torch.equal(out, y.transpose(1, 2).reshape(Bsz, T, H * D).to(dt))
-        back = torch.empty(Bsz, H, T, D, device="cuda")
-        assert lib.ca_tokens_to_heads(out.data_ptr(), code, back.data_ptr(), Bsz, H, T, D, s) == 0
-        assert torch.equal(back, out.float().view(Bsz, T, H, D).transpose(1, 2))
+def _qkv_call(ca, qkv, gain, cs, H, dout):
+    """ca_fwd_qkv + ca_bwd_qkv through the C ABI: (y fp32 heads, out, dqkv, dgain)."""
+    lib = ca.native.load()
+    Bsz, T, C3 = qkv.shape
+    D = C3 // 3 // H
+    code = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[qkv.dtype]
+    y = torch.empty(Bsz, H, T, D, device="cuda")
+    out = torch.empty(Bsz, T, H * D, device="cuda", dtype=qkv.dtype)
+    st = torch.empty(Bsz * H * T, 2, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    nf = lib.ca_fwd_workspace_bytes(Bsz, H, T, D)
+    wf = torch.empty(max(nf, 1), device="cuda", dtype=torch.uint8)
+    csp = cs.data_ptr() if cs is not None else None
+    ca.native.check(lib.ca_fwd_qkv(qkv.data_ptr(), code, csp, gain.data_ptr(), y.data_ptr(),
+                                   out.data_ptr(), st.data_ptr(), wf.data_ptr(), nf, Bsz, T, H, D, s))
+    nb = lib.ca_bwd_workspace_bytes(Bsz, H, T, D)
+    wb = torch.empty(nb, device="cuda", dtype=torch.uint8)
+    dqkv = torch.empty_like(qkv)
+    dg = torch.empty(H, device="cuda")
+    ca.native.check(lib.ca_bwd_qkv(qkv.data_ptr(), code, csp, gain.data_ptr(), y.data_ptr(),
+                                   st.data_ptr(), dout.data_ptr(), dqkv.data_ptr(), dg.data_ptr(),
+                                   wb.data_ptr(), nb, Bsz, T, H, D, s))
+    torch.cuda.synchronize()
+    return y, out, dqkv, dg
+
+
+@pytest.mark.parametrize("D,T,splits", [(64, 130, (0, 0, 0)), (16, 77, (0, 0, 0)),
+                                        (128, 300, (0, 0, 0)), (64, 700, (1, 1, 1)),
+                                        (32, 520, (4, 16, 6))])
+def test_qkv_entry_points_match_the_operator(gpu_ca, D, T, splits):
+    """ca_fwd_qkv / ca_bwd_qkv read the token-major qkv [B,T,3,H,D] and write
+    the output and dqkv token-major.  Without rotation they are the
+    operator's kernels on the same values, so for fp32, bf16 and fp16 qkv:
+    y is bitwise the operator's output on the upcast q, k, v; the token-major
+    output is y rounded to the dtype; dqkv is the operator's gradients
+    rounded to the dtype.  With RoPE, against the operator on q, k rotated in
+    fp32 beforehand (rounding-level differences only).  Forced splits run the
+    combine and merge kernels' token-major writes."""
+    say(f"[case] qkv entry points D={D} T={T} splits {splits}")
+    Dm = gpu_ca.decoder
+    gpu_ca.ops.set_split_override(*splits)
+    try:
+        Bsz, H = 2, 3
+        g = torch.Generator().manual_seed(D + T)
+        gain = torch.tensor([0.0, 0.3, -0.25], device="cuda")
+        for dt in (torch.float32, torch.bfloat16, torch.float16):
+            qkv = (torch.randn(Bsz, T, 3 * H * D, generator=g) * 1.3).to(dt).cuda()
+            dout = torch.randn(Bsz, T, H * D, generator=g).to(dt).cuda()
+            y, out, dqkv, dg = _qkv_call(gpu_ca, qkv, gain, None, H, dout)
+            q, k, v = (t.contiguous() for t in qkv.float().view(Bsz, T, 3, H, D).permute(2, 0, 3, 1, 4))
+            dyh = dout.float().view(Bsz, T, H, D).transpose(1, 2).contiguous()
+            yr, st = gpu_ca.ca_forward(q, k, v, gain)
+            dq, dk, dv, dgr = gpu_ca.ca_backward(q, k, v, gain, yr, st, dyh)
+            assert torch.equal(y, yr), dt
+            assert torch.equal(out, yr.transpose(1, 2).reshape(Bsz, T, H * D).to(dt)), dt
+            ref = torch.stack((dq, dk, dv), 2).transpose(1, 3).reshape(Bsz, T, 3 * H * D).to(dt)
+            assert torch.equal(dqkv, ref), dt
+            assert torch.equal(dg, dgr), dt
+        # RoPE in the kernels vs rotating first
+        qkv = (torch.randn(Bsz, T, 3 * H * D, generator=g) * 1.3).cuda()
+        dout = torch.randn(Bsz, T, H * D, generator=g).cuda()
+        cs = Dm.rope_cos_sin(T, D, 10000.0, qkv.device)
+        y, out, dqkv, dg = _qkv_call(gpu_ca, qkv, gain, cs, H, dout)
+        q, k, v = qkv.view(Bsz, T, 3, H, D).permute(2, 0, 3, 1, 4)
+
+        def rot(x, inverse=False):
+            x0, x1 = x[..., 0::2], x[..., 1::2]
+            c, s_ = cs[..., 0], (-cs[..., 1] if inverse else cs[..., 1])
+            return torch.stack((x0 * c - x1 * s_, x1 * c + x0 * s_), -1).flatten(-2).contiguous()
+        qr, kr = rot(q), rot(k)
+        dyh = dout.view(Bsz, T, H, D).transpose(1, 2).contiguous()
+        yr, st = gpu_ca.ca_forward(qr, kr, v.contiguous(), gain)
+        dq, dk, dv, dgr = gpu_ca.ca_backward(qr, kr, v.contiguous(), gain, yr, st, dyh)
+        ref = torch.stack((rot(dq, True), rot(dk, True), dv), 2).transpose(1, 3).reshape(Bsz, T, 3 * H * D)
+        e = [rel(a.cpu().numpy(), b.cpu().numpy()) for a, b in
+             ((y, yr), (out, yr.transpose(1, 2).reshape(Bsz, T, H * D)), (dqkv, ref), (dg, dgr))]
+        say("   rope: y %.1e out %.1e dqkv %.1e dgain %.1e" % tuple(e))
+        assert e[0] <= 1e-6 and e[1] <= 1e-6 and e[2] <= 1e-5 and e[3] <= 1e-5
+    finally:
+        gpu_ca.ops.set_split_override(0, 0, 0)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
