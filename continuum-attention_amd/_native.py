@@ -32,7 +32,10 @@ _sz = ctypes.c_size_t
 SIGNATURES = {
     "ca_abi_version": (_i, []),
     "ca_last_error": (ctypes.c_char_p, []),
+    "ca_set_workspace_cap": (_i, [_sz]),
+    "ca_workspace_cap": (_sz, []),
     "ca_fwd_workspace_bytes": (_sz, [_i, _i, _i, _i]),
+    "ca_bwd_qkv_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "ca_fwd_f32": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp]),
     "ca_bwd_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "ca_bwd_f32": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
@@ -113,6 +116,10 @@ def load() -> ctypes.CDLL:
     ver = lib.ca_abi_version()
     if ver != ABI_VERSION:
         raise RuntimeError(f"libca_hip.so ABI version {ver}, expected {ABI_VERSION}")
+    cap_mb = os.environ.get("CA_WORKSPACE_CAP_MB")
+    if cap_mb is not None:
+        # the workspace bound (MiB, 0 = none) in place of the library's 1 GiB
+        lib.ca_set_workspace_cap(int(float(cap_mb) * (1 << 20)))
     _lib = lib
     return lib
 

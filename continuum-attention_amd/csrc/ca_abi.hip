@@ -105,41 +105,98 @@ struct SplitOverride {
 };
 SplitOverride g_split;
 
-// Forward split length: for_sizing picks the shortest split any device can
-// choose (the workspace bound), otherwise the current device's choice.
-int fwd_split(int BH, int T, int D, bool for_sizing) {
+// Workspace cap (ca_set_workspace_cap): the size the workspace-size functions
+// report when the full (single-pass, shortest-split) workspace is larger;
+// 0 means no cap.
+size_t g_workspace_cap = size_t(1) << 30;
+
+// Forward split length for a workspace of `bytes`: the device's own choice
+// (for_sizing: the shortest any device can pick), lengthened until the split
+// partials fit; a split as long as the longest row needs no partials.
+int fwd_split(int BH, int T, int D, bool for_sizing, size_t bytes = SIZE_MAX) {
   if (g_split.fwd_tiles > 0) return g_split.fwd_tiles;
-  return ca::fwd_split_tiles(BH, T, for_sizing ? kFwdSplitBound : fwd_resident_groups(D));
+  const int C = ca::fwd_split_tiles(BH, T, for_sizing ? kFwdSplitBound : fwd_resident_groups(D));
+  if (ca::fwd_part_floats(BH, T, C, D) * sizeof(float) <= bytes) return C;
+  const int G = (T + 127) / 128;
+  const int max_tiles = ca::fwd_group_tiles(G - 1, T);
+  const size_t per_split = (size_t)BH * T * (D + 2) * sizeof(float);
+  const size_t fit = bytes / per_split;  // splits the partials can hold
+  if (fit < 2) return max_tiles;
+  const int cf = (int)((max_tiles + fit - 1) / fit);
+  return cf > C ? cf : C;
 }
-ca::DqSplit dq_split_for(int BH, int T, int D, bool for_sizing) {
-  if (g_split.dq_blocks > 0) return ca::dq_split_chunk(T, g_split.dq_blocks);
+ca::DqSplit dq_split_for(int BH, int T, int D, const ca::BwdPass& p, bool for_sizing) {
+  if (g_split.dq_blocks > 0) return ca::dq_split_chunk(T, p, g_split.dq_blocks);
   // D = 128 kernels hold fewer dQ work groups per CU (two instead of three)
   const int res = for_sizing ? kDqSplitBound : (D > 64 ? dq_resident_groups() * 2 / 3 : dq_resident_groups());
-  return ca::dq_split(BH, T, res);
+  return ca::dq_split(BH, T, p, res);
 }
-ca::DkdvSplit dkdv_split_for(int BH, int T, int D, bool for_sizing) {
-  if (g_split.dkdv_tiles > 0) return ca::dkdv_split_chunk(T, g_split.dkdv_tiles);
+ca::DkdvSplit dkdv_split_for(int BH, int D, const ca::BwdPass& p, bool for_sizing) {
+  if (g_split.dkdv_tiles > 0) return ca::dkdv_split_chunk(p, g_split.dkdv_tiles);
   // D = 128: one dK/dV work group per CU instead of two (registers and LDS)
   const int res = for_sizing ? kDqSplitBound : (D > 64 ? dkdv_resident_groups() / 2 : dkdv_resident_groups());
-  return ca::dkdv_split(BH, T, res);
+  return ca::dkdv_split(BH, p, res);
 }
 
+// Workspace layout of one backward pass (every pass lays its buffers out from
+// the start of the workspace; nothing in it outlives the pass).
 struct BwdLayout {
   size_t ds, limbs, qstat, gain, dqpart, kvpart, total;
 };
-BwdLayout bwd_layout(int B, int H, int T, int D) {
+BwdLayout bwd_layout(int B, int H, int T, int D, const ca::BwdPass& p) {
   const int BH = B * H;
-  const ca::DqSplit sp = dq_split_for(BH, T, D, true);  // the largest split
+  const ca::DqSplit sp = dq_split_for(BH, T, D, p, true);  // the largest split
+  const ca::DkdvSplit kvs = dkdv_split_for(BH, D, p, true);
   BwdLayout L;
   L.ds = 0;
-  L.limbs = align256(ca::bwd_ds_floats(BH, T) * sizeof(float));
-  L.qstat = L.limbs + align256(ca::bwd_limb_elems(BH, T, D) * sizeof(uint16_t));
-  L.gain = L.qstat + align256((size_t)BH * T * 2 * sizeof(float));
+  L.limbs = align256((size_t)BH * p.ds_slice * ca::kDsBlockFloats * sizeof(float));
+  L.qstat = L.limbs + align256(ca::bwd_limb_elems(BH, p.rows, D) * sizeof(uint16_t));
+  L.gain = L.qstat + align256((size_t)BH * p.rows * 2 * sizeof(float));
   L.dqpart = L.gain + align256((size_t)BH * sp.items * sizeof(float));
   L.kvpart = L.dqpart + align256((size_t)BH * sp.part_items * ca::kDqRows * D * sizeof(float));
-  const ca::DkdvSplit kvs = dkdv_split_for(BH, T, D, true);  // the largest split
   L.total = L.kvpart + align256((size_t)BH * kvs.part_items * ca::kDkdvKeys * 2 * D * sizeof(float));
   return L;
+}
+size_t bwd_full_bytes(int B, int H, int T, int D) {
+  return bwd_layout(B, H, T, D, ca::bwd_pass(T, 0, ca::dq_num_groups(T))).total;
+}
+
+// Backward passes for a workspace of `bytes`: ranges of dQ groups from the
+// first on, each as long as its layout fits (a layout only grows when its
+// range does).  False when a single group does not fit.
+bool plan_passes(int B, int H, int T, int D, size_t bytes, std::vector<ca::BwdPass>* passes) {
+  const int G = ca::dq_num_groups(T);
+  passes->clear();
+  int g0 = 0;
+  while (g0 < G) {
+    if (bwd_layout(B, H, T, D, ca::bwd_pass(T, g0, g0 + 1)).total > bytes) return false;
+    int lo = g0 + 1, hi = G;  // largest g1 in [lo, hi] that fits
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) / 2;
+      if (bwd_layout(B, H, T, D, ca::bwd_pass(T, g0, mid)).total <= bytes) lo = mid;
+      else hi = mid - 1;
+    }
+    passes->push_back(ca::bwd_pass(T, g0, lo));
+    g0 = lo;
+  }
+  return true;
+}
+
+// Workspace the backward asks for under the cap: the full one when it fits,
+// else the largest pass of the plan for the cap, or (when not even one dQ
+// group fits under the cap) the one-group pass that needs the most.
+size_t bwd_capped_bytes(int B, int H, int T, int D) {
+  const size_t full = bwd_full_bytes(B, H, T, D);
+  if (g_workspace_cap == 0 || full <= g_workspace_cap) return full;
+  std::vector<ca::BwdPass> passes;
+  size_t need = 0;
+  if (plan_passes(B, H, T, D, g_workspace_cap, &passes)) {
+    for (const auto& p : passes) need = std::max(need, bwd_layout(B, H, T, D, p).total);
+  } else {
+    for (int g = 0; g < ca::dq_num_groups(T); ++g)
+      need = std::max(need, bwd_layout(B, H, T, D, ca::bwd_pass(T, g, g + 1)).total);
+  }
+  return need;
 }
 
 // ---- per-kernel event timing ------------------------------------------------
@@ -167,6 +224,11 @@ hipEvent_t pool_event() {
 }  // namespace
 
 namespace ca {
+bool bwd_fits(int B, int H, int T, int D, size_t bytes) {
+  std::vector<BwdPass> passes;
+  return bwd_full_bytes(B, H, T, D) <= bytes || plan_passes(B, H, T, D, bytes, &passes);
+}
+
 int set_error(int code, const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
@@ -240,14 +302,27 @@ int ca_abi_version(void) { return CA_ABI_VERSION; }
 
 const char* ca_last_error(void) { return g_err; }
 
+int ca_set_workspace_cap(size_t bytes) {
+  g_workspace_cap = bytes;
+  return CA_OK;
+}
+
+size_t ca_workspace_cap(void) { return g_workspace_cap; }
+
 size_t ca_fwd_workspace_bytes(int B, int H, int T, int D) {
   if (B <= 0 || H <= 0 || T <= 0) return 0;
-  return ca::fwd_part_floats(B * H, T, fwd_split(B * H, T, D, true), D) * sizeof(float);
+  const size_t cap = g_workspace_cap ? g_workspace_cap : SIZE_MAX;
+  return ca::fwd_part_floats(B * H, T, fwd_split(B * H, T, D, true, cap), D) * sizeof(float);
 }
 
 size_t ca_bwd_workspace_bytes(int B, int H, int T, int D) {
   if (B <= 0 || H <= 0 || T <= 0 || D <= 0) return 0;
-  return bwd_layout(B, H, T, D).total;
+  return bwd_capped_bytes(B, H, T, D);
+}
+
+size_t ca_bwd_qkv_workspace_bytes(int B, int H, int T, int D) {
+  if (B <= 0 || H <= 0 || T <= 0 || D <= 0) return 0;
+  return bwd_full_bytes(B, H, T, D);
 }
 
 }  // extern "C"
@@ -267,28 +342,30 @@ hipError_t fwd_launch(int D, const ca::FwdIO& io, float* part, int B, int H, int
 }
 
 template <class E>
-hipError_t bwd_launch(int D, const ca::BwdIO& io, const ca::BwdWork& w, const ca::DqSplit& sp,
-                      const ca::DkdvSplit& kvs, int B, int H, int T, hipStream_t s) {
+hipError_t bwd_launch(int D, const ca::BwdIO& io, const ca::BwdWork& w, const ca::BwdPass& p,
+                      const ca::DqSplit& sp, const ca::DkdvSplit& kvs, int B, int H, int T,
+                      hipStream_t s) {
   switch (D) {
-    case 8: return ca::launch_bwd<8, E>(io, w, sp, kvs, B, H, T, s);
-    case 16: return ca::launch_bwd<16, E>(io, w, sp, kvs, B, H, T, s);
-    case 32: return ca::launch_bwd<32, E>(io, w, sp, kvs, B, H, T, s);
-    case 64: return ca::launch_bwd<64, E>(io, w, sp, kvs, B, H, T, s);
-    default: return ca::launch_bwd<128, E>(io, w, sp, kvs, B, H, T, s);
+    case 8: return ca::launch_bwd<8, E>(io, w, p, sp, kvs, B, H, T, s);
+    case 16: return ca::launch_bwd<16, E>(io, w, p, sp, kvs, B, H, T, s);
+    case 32: return ca::launch_bwd<32, E>(io, w, p, sp, kvs, B, H, T, s);
+    case 64: return ca::launch_bwd<64, E>(io, w, p, sp, kvs, B, H, T, s);
+    default: return ca::launch_bwd<128, E>(io, w, p, sp, kvs, B, H, T, s);
   }
 }
 
 // Shape, workspace and launch of the forward, once the operands are views.
 int fwd_common(const ca::FwdIO& io, int dtype, void* workspace, size_t workspace_bytes, int B,
                int H, int T, int D, void* stream) {
-  const size_t need = ca_fwd_workspace_bytes(B, H, T, D);
-  if (workspace_bytes < need || (need && !workspace))
+  // the device's own split, lengthened until its partials fit the workspace
+  const size_t bytes = workspace ? workspace_bytes : 0;
+  const int C = fwd_split(B * H, T, D, false, bytes);
+  const size_t need = ca::fwd_part_floats(B * H, T, C, D) * sizeof(float);
+  if (bytes < need)
     return fail(CA_ERR_WORKSPACE, "forward workspace of %zu bytes required, %zu given", need,
                 workspace_bytes);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   float* part = static_cast<float*>(workspace);
-  // the device's own residency: a split no shorter than the workspace's
-  const int C = fwd_split(B * H, T, D, false);
   hipError_t e;
   if (dtype == CA_DTYPE_BF16) e = fwd_launch<__bf16>(D, io, part, B, H, T, C, s);
   else if (dtype == CA_DTYPE_F16) e = fwd_launch<_Float16>(D, io, part, B, H, T, C, s);
@@ -298,27 +375,37 @@ int fwd_common(const ca::FwdIO& io, int dtype, void* workspace, size_t workspace
 }
 
 int bwd_common(const ca::BwdIO& io, int dtype, void* workspace, size_t workspace_bytes, int B,
-               int H, int T, int D, void* stream) {
-  const BwdLayout L = bwd_layout(B, H, T, D);
-  if (!workspace || workspace_bytes < L.total)
-    return fail(CA_ERR_WORKSPACE, "backward workspace of %zu bytes required, %zu given", L.total,
-                workspace_bytes);
-  char* ws = static_cast<char*>(workspace);
-  ca::BwdWork work;
-  work.dsbuf = reinterpret_cast<float*>(ws + L.ds);
-  work.limbs = reinterpret_cast<__bf16*>(ws + L.limbs);
-  work.qstat = reinterpret_cast<float*>(ws + L.qstat);
-  work.gain_part = reinterpret_cast<float*>(ws + L.gain);
-  work.dq_part = reinterpret_cast<float*>(ws + L.dqpart);
-  work.kv_part = reinterpret_cast<float*>(ws + L.kvpart);
-  const ca::DqSplit sp = dq_split_for(B * H, T, D, false);
-  const ca::DkdvSplit kvs = dkdv_split_for(B * H, T, D, false);
+               int H, int T, int D, void* stream, bool single_pass) {
+  // one pass when the whole backward fits the workspace, else passes over
+  // ranges of dQ groups (dK, dV and dlog_gain accumulate in pass order)
+  std::vector<ca::BwdPass> passes;
+  const size_t full = bwd_full_bytes(B, H, T, D);
+  if (workspace && workspace_bytes >= full) {
+    passes.push_back(ca::bwd_pass(T, 0, ca::dq_num_groups(T)));
+  } else if (single_pass || !workspace ||
+             !plan_passes(B, H, T, D, workspace_bytes, &passes)) {
+    return fail(CA_ERR_WORKSPACE, "backward workspace of %zu bytes required, %zu given",
+                single_pass ? full : bwd_capped_bytes(B, H, T, D), workspace_bytes);
+  }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  hipError_t e;
-  if (dtype == CA_DTYPE_BF16) e = bwd_launch<__bf16>(D, io, work, sp, kvs, B, H, T, s);
-  else if (dtype == CA_DTYPE_F16) e = bwd_launch<_Float16>(D, io, work, sp, kvs, B, H, T, s);
-  else e = bwd_launch<float>(D, io, work, sp, kvs, B, H, T, s);
-  if (e != hipSuccess) return fail(CA_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
+  char* ws = static_cast<char*>(workspace);
+  for (const ca::BwdPass& pass : passes) {
+    const BwdLayout L = bwd_layout(B, H, T, D, pass);
+    ca::BwdWork work;
+    work.dsbuf = reinterpret_cast<float*>(ws + L.ds);
+    work.limbs = reinterpret_cast<__bf16*>(ws + L.limbs);
+    work.qstat = reinterpret_cast<float*>(ws + L.qstat);
+    work.gain_part = reinterpret_cast<float*>(ws + L.gain);
+    work.dq_part = reinterpret_cast<float*>(ws + L.dqpart);
+    work.kv_part = reinterpret_cast<float*>(ws + L.kvpart);
+    const ca::DqSplit sp = dq_split_for(B * H, T, D, pass, false);
+    const ca::DkdvSplit kvs = dkdv_split_for(B * H, D, pass, false);
+    hipError_t e;
+    if (dtype == CA_DTYPE_BF16) e = bwd_launch<__bf16>(D, io, work, pass, sp, kvs, B, H, T, s);
+    else if (dtype == CA_DTYPE_F16) e = bwd_launch<_Float16>(D, io, work, pass, sp, kvs, B, H, T, s);
+    else e = bwd_launch<float>(D, io, work, pass, sp, kvs, B, H, T, s);
+    if (e != hipSuccess) return fail(CA_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
+  }
   return CA_OK;
 }
 
@@ -366,7 +453,7 @@ int ca_bwd_f32(const float* q, const float* k, const float* v, const float* log_
   ca::BwdIO io{heads_view(q, H, T, D), heads_view(k, H, T, D), heads_view(v, H, T, D), nullptr,
                log_gain, out, stats, heads_view(dout, H, T, D), heads_view(dq, H, T, D),
                heads_view(dk, H, T, D), heads_view(dv, H, T, D), dlog_gain};
-  return bwd_common(io, CA_DTYPE_F32, workspace, workspace_bytes, B, H, T, D, stream);
+  return bwd_common(io, CA_DTYPE_F32, workspace, workspace_bytes, B, H, T, D, stream, false);
 }
 
 static int check_qkv(const char* fn, int dtype, const void* qkv, const float* rope_cs,
@@ -413,7 +500,9 @@ int ca_bwd_qkv(const void* qkv, int dtype, const float* rope_cs, const float* lo
                tokens_view(dout, dtype, 0, 1, T, H, D), tokens_view(dqkv, dtype, 0, 3, T, H, D),
                tokens_view(dqkv, dtype, 1, 3, T, H, D), tokens_view(dqkv, dtype, 2, 3, T, H, D),
                dlog_gain};
-  return bwd_common(io, dtype, workspace, workspace_bytes, B, H, T, D, stream);
+  // token-major gradients cannot be summed over passes without rounding them
+  // to the element type in between: one pass, ca_bwd_qkv_workspace_bytes
+  return bwd_common(io, dtype, workspace, workspace_bytes, B, H, T, D, stream, true);
 }
 
 static int check_rows(const char* fn, int BH, int Q, int K, int start) {

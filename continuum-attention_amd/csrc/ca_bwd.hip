@@ -43,9 +43,10 @@
 namespace ca {
 
 
-// One thread per (row, 8 elements): Dl = dY . y, then the Q and dY/Z limbs of
-// the 8 elements (one 16-byte store per plane) and, per row, (m, Dl/Z).
-// `rows` = B*H*T; plane p of `limbs` starts at p * rows * D.
+// One thread per (row of the pass, 8 elements): Dl = dY . y, then the Q and
+// dY/Z limbs of the 8 elements (one 16-byte store per plane) and, per row,
+// (m, Dl/Z).  The pass holds `prows` rows per slice from row0 on; `rows` =
+// B*H*prows, plane p of `limbs` starts at p * rows * D.
 template <int D, class E>
 __global__ __launch_bounds__(256) void ca_bwd_prep_kernel(View Qv, const float* __restrict__ rope,
                                                           View dYv,
@@ -53,12 +54,13 @@ __global__ __launch_bounds__(256) void ca_bwd_prep_kernel(View Qv, const float* 
                                                           const float* __restrict__ stats,
                                                           __bf16* __restrict__ limbs,
                                                           float* __restrict__ qstat, int H, int T,
-                                                          int rows) {
+                                                          int row0, int prows, int rows) {
   constexpr int C8 = D / 8;
   const int tix = blockIdx.x * 256 + threadIdx.x;
-  const int row = tix / C8, c = tix % C8;
+  const int row = tix / C8, c = tix % C8;  // row = bh * prows + (t - row0)
   const bool ok = row < rows;
-  const int bh = ok ? row / T : 0, t = ok ? row % T : 0;
+  const int bh = ok ? row / prows : 0, t = ok ? row0 + row % prows : 0;
+  const size_t grow = (size_t)bh * T + t;  // row of y and stats
   const E* qp = view_slice<const E>(Qv, bh, H) + (long long)t * Qv.rstride + 8 * c;
   const E* dp = view_slice<const E>(dYv, bh, H) + (long long)t * dYv.rstride + 8 * c;
   f32x4 dy[2], y[2], qq[2];
@@ -68,14 +70,14 @@ __global__ __launch_bounds__(256) void ca_bwd_prep_kernel(View Qv, const float* 
     dy[u] = y[u] = qq[u] = f32x4{0.f, 0.f, 0.f, 0.f};
     if (ok) {
       dy[u] = ld4(dp + 4 * u);
-      y[u] = reinterpret_cast<const f32x4*>(out + (size_t)row * D + 8 * c)[u];
+      y[u] = reinterpret_cast<const f32x4*>(out + grow * D + 8 * c)[u];
       qq[u] = ld4(qp + 4 * u);
       if (rope) qq[u] = rope4(qq[u], rope_entry(rope, t, D, 8 * c + 4 * u), false);
     }
   }
   if (ok) {
-    m = stats[(size_t)row * 2 + 0];
-    invz = stats[(size_t)row * 2 + 1];
+    m = stats[grow * 2 + 0];
+    invz = stats[grow * 2 + 1];
   }
   float x = 0.f;
 #pragma unroll
@@ -133,9 +135,9 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
                                                         View Kv, const float* __restrict__ rope,
                                                         const float* __restrict__ log_gain,
                                                         View dQv, float* __restrict__ dq_part,
-                                                        float* __restrict__ gain_part, int BH,
-                                                        int H, int T, int chunk, int n_items,
-                                                        int n_part) {
+                                                        float* __restrict__ gain_part, BwdPass pass,
+                                                        int BH, int H, int T, int chunk,
+                                                        int n_items, int n_part) {
   using P = DqP<D>;
   __shared__ __attribute__((aligned(16))) __bf16 kst[2 * P::STAGE];
   __shared__ float gred[kDqTiles];
@@ -143,9 +145,9 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   const int nkb = bwd_num_key_blocks(T);
   const int bh = blockIdx.x % BH;
   const int item = blockIdx.x / BH;
-  // item -> (group, chunk), heaviest groups first
-  int qg = dq_num_groups(T) - 1, ch = item, nch = dq_group_chunks(qg, T, chunk);
-  while (ch >= nch && qg > 0) {
+  // item -> (group, chunk), heaviest groups of the pass first
+  int qg = pass.g1 - 1, ch = item, nch = dq_group_chunks(qg, T, chunk);
+  while (ch >= nch && qg > pass.g0) {
     ch -= nch;
     --qg;
     nch = dq_group_chunks(qg, T, chunk);
@@ -163,7 +165,8 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   const int iters = kb_hi > kb_lo ? (kb_hi - kb_lo + 1) / 2 : 0;
   // dS of this lane: rows 16rb + l16 of the wave's tile, slots 8(g&1)..+7 of block g>>1 of a pair
   const float* arow = dsbuf +
-                      ((size_t)bh * ds_blocks_before(nqt) + ds_blocks_before(wave_on ? qt : 0)) * kDsBlockFloats +
+                      ((size_t)bh * pass.ds_slice + (ds_blocks_before(wave_on ? qt : pass.qa) - pass.ds0)) *
+                          kDsBlockFloats +
                       l16 * kBwdSlots + 8 * (g & 1);
 
   f32x4 acc[2][P::NB];
@@ -359,8 +362,8 @@ template <int D, class E>
 __global__ __launch_bounds__(256) void ca_bwd_gain_merge_kernel(
     const float* __restrict__ gain_part, const float* __restrict__ dq_part,
     const float* __restrict__ kv_part, const float* __restrict__ rope,
-    float* __restrict__ dlog_gain, View dQv, View dKv, View dVv, int B, int H, int T, int chunk,
-    int n_items, int n_part, int dq_multi, int kv_chunk, int kv_part_items) {
+    float* __restrict__ dlog_gain, View dQv, View dKv, View dVv, BwdPass pass, int B, int H, int T,
+    int chunk, int n_items, int n_part, int dq_multi, int kv_chunk, int kv_part_items) {
   const int tid = threadIdx.x;
   const int BHt = B * H;
   if (blockIdx.x >= H + BHt * dq_multi) {
@@ -368,8 +371,10 @@ __global__ __launch_bounds__(256) void ca_bwd_gain_merge_kernel(
     const int m = blockIdx.x - H - BHt * dq_multi;
     const int bh = m % BHt, wg = m / BHt;
     int first = 0;  // item index of the group's chunk 0 (multi-chunk groups come first)
-    for (int gg = 0; gg < wg; ++gg) first += dkdv_group_chunks(gg, T, kv_chunk);
-    const int nch = dkdv_group_chunks(wg, T, kv_chunk);
+    for (int gg = 0; gg < wg; ++gg) first += dkdv_group_chunks(gg, pass, kv_chunk);
+    const int nch = dkdv_group_chunks(wg, pass, kv_chunk);
+    // earlier passes already wrote this key group's dK, dV
+    const bool accumulate = dkdv_qt0(wg) < pass.qa;
     const f32x4* part =
         reinterpret_cast<const f32x4*>(kv_part + ((size_t)bh * kv_part_items + first) * kDkdvKeys * 2 * D);
     const int w0 = kDkdvKeys * wg;
@@ -381,7 +386,9 @@ __global__ __launch_bounds__(256) void ca_bwd_gain_merge_kernel(
       for (int cc = 1; cc < nch; ++cc) s += part[(size_t)cc * kDkdvKeys * 2 * C4 + e];
       const View& ov = which ? dKv : dVv;
       if (which && rope) s = rope4(s, rope_entry(rope, key, D, 4 * c4), true);
-      st4(view_slice<E>(ov, bh, H) + (long long)key * ov.rstride + 4 * c4, s);
+      E* dst = view_slice<E>(ov, bh, H) + (long long)key * ov.rstride + 4 * c4;
+      if (accumulate) s += ld4(dst);
+      st4(dst, s);
     }
     return;
   }
@@ -394,16 +401,19 @@ __global__ __launch_bounds__(256) void ca_bwd_gain_merge_kernel(
     acc = wave_sum(acc);
     if ((tid & 63) == 0) wsum[tid >> 6] = acc;
     __syncthreads();
-    if (tid == 0) dlog_gain[h] = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+    if (tid == 0) {
+      const float part_sum = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+      dlog_gain[h] = pass.first ? part_sum : dlog_gain[h] + part_sum;
+    }
     return;
   }
   constexpr int C4 = D / 4;
   const int BH = B * H;
   const int m = blockIdx.x - H;
   const int bh = m % BH, gi = m / BH;
-  const int qg = dq_num_groups(T) - 1 - gi;
+  const int qg = pass.g1 - 1 - gi;
   int first = 0;  // item index of the group's chunk 0
-  for (int gg = dq_num_groups(T) - 1; gg > qg; --gg) first += dq_group_chunks(gg, T, chunk);
+  for (int gg = pass.g1 - 1; gg > qg; --gg) first += dq_group_chunks(gg, T, chunk);
   const int nch = dq_group_chunks(qg, T, chunk);
   const f32x4* part = reinterpret_cast<const f32x4*>(dq_part + ((size_t)bh * n_part + first) * kDqRows * D);
   E* dQs = view_slice<E>(dQv, bh, H);
@@ -418,29 +428,30 @@ __global__ __launch_bounds__(256) void ca_bwd_gain_merge_kernel(
 }
 
 template <int D, class E>
-hipError_t launch_bwd(const BwdIO& io, const BwdWork& ws, const DqSplit& sp, const DkdvSplit& kvs,
-                      int B, int H, int T, hipStream_t stream) {
+hipError_t launch_bwd(const BwdIO& io, const BwdWork& ws, const BwdPass& pass, const DqSplit& sp,
+                      const DkdvSplit& kvs, int B, int H, int T, hipStream_t stream) {
   const int BH = B * H;
-  const int rows = BH * T;
+  const int rows = BH * pass.rows;
   timer_begin(kBwdPrep, stream);
   hipLaunchKernelGGL((ca_bwd_prep_kernel<D, E>), dim3((rows * (D / 8) + 255) / 256), dim3(256), 0,
-                     stream, io.q, io.rope, io.dout, io.y, io.stats, ws.limbs, ws.qstat, H, T, rows);
+                     stream, io.q, io.rope, io.dout, io.y, io.stats, ws.limbs, ws.qstat, H, T,
+                     pass.row0, pass.rows, rows);
   timer_end(kBwdPrep, stream);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   timer_begin(kBwdDkdv, stream);
-  e = launch_bwd_dkdv<D, E>(io, ws, kvs, BH, H, T, stream);
+  e = launch_bwd_dkdv<D, E>(io, ws, pass, kvs, BH, H, T, stream);
   timer_end(kBwdDkdv, stream);
   if (e != hipSuccess) return e;
   timer_begin(kBwdDq, stream);
   if (io.rope)
     hipLaunchKernelGGL((ca_bwd_dq_kernel<D, E, true>), dim3(sp.items * BH), dim3(256), 0, stream,
                        ws.dsbuf, io.q, io.k, io.rope, io.log_gain, io.dq, ws.dq_part, ws.gain_part,
-                       BH, H, T, sp.chunk, sp.items, sp.part_items);
+                       pass, BH, H, T, sp.chunk, sp.items, sp.part_items);
   else
     hipLaunchKernelGGL((ca_bwd_dq_kernel<D, E, false>), dim3(sp.items * BH), dim3(256), 0, stream,
                        ws.dsbuf, io.q, io.k, io.rope, io.log_gain, io.dq, ws.dq_part, ws.gain_part,
-                       BH, H, T, sp.chunk, sp.items, sp.part_items);
+                       pass, BH, H, T, sp.chunk, sp.items, sp.part_items);
   timer_end(kBwdDq, stream);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -448,15 +459,16 @@ hipError_t launch_bwd(const BwdIO& io, const BwdWork& ws, const DqSplit& sp, con
   hipLaunchKernelGGL((ca_bwd_gain_merge_kernel<D, E>),
                      dim3(H + BH * sp.multi_groups + BH * kvs.multi_groups), dim3(256), 0, stream,
                      ws.gain_part, ws.dq_part, ws.kv_part, io.rope, io.dlog_gain, io.dq, io.dk, io.dv,
-                     B, H, T, sp.chunk, sp.items, sp.part_items, sp.multi_groups, kvs.chunk,
+                     pass, B, H, T, sp.chunk, sp.items, sp.part_items, sp.multi_groups, kvs.chunk,
                      kvs.part_items);
   timer_end(kBwdGain, stream);
   return hipGetLastError();
 }
 
 #define CA_INST_BWD(DD, EE)                                                                     \
-  template hipError_t launch_bwd<DD, EE>(const BwdIO&, const BwdWork&, const DqSplit&,          \
-                                         const DkdvSplit&, int, int, int, hipStream_t);
+  template hipError_t launch_bwd<DD, EE>(const BwdIO&, const BwdWork&, const BwdPass&,          \
+                                         const DqSplit&, const DkdvSplit&, int, int, int,       \
+                                         hipStream_t);
 #define CA_INST_BWD_ALL(EE) \
   CA_INST_BWD(8, EE) CA_INST_BWD(16, EE) CA_INST_BWD(32, EE) CA_INST_BWD(64, EE) CA_INST_BWD(128, EE)
 CA_INST_BWD_ALL(float)

@@ -37,27 +37,26 @@ template <int D, class E>
 __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
     View Kv, View Vv, const float* __restrict__ rope, const __bf16* __restrict__ limbs,
     const float* __restrict__ qstat, const float* __restrict__ log_gain, View dKv, View dVv,
-    float* __restrict__ dsbuf, float* __restrict__ kv_part, int BH, int H, int T, int chunk,
-    int n_part) {
+    float* __restrict__ dsbuf, float* __restrict__ kv_part, BwdPass pass, int BH, int H, int T,
+    int chunk, int n_part) {
   using P = Bwd<D>;
   __shared__ __attribute__((aligned(16))) __bf16 tiles[2][P::TILE];
   __shared__ f32x4 tstat[2][16];  // rows 2u, 2u+1: (m, Dl/Z, m, Dl/Z)
 
-  const int nqt = num_q_tiles(T);
   const int nkb = bwd_num_key_blocks(T);
   const int bh = blockIdx.x % BH;
   const int item = blockIdx.x / BH;  // ascending: heaviest first
-  // item -> (key-block group, chunk of its query tiles)
+  // item -> (key-block group, chunk of its query tiles in this pass)
   int wg = item, ch = 0, nch = 1;
-  if (chunk < nqt) {
-    const int G = dkdv_num_groups(T);
+  if (chunk < pass.qb - pass.qa) {
+    const int G = pass.kv_groups;
     wg = 0;
     ch = item;
-    nch = dkdv_group_chunks(0, T, chunk);
+    nch = dkdv_group_chunks(0, pass, chunk);
     while (ch >= nch && wg < G - 1) {
       ch -= nch;
       ++wg;
-      nch = dkdv_group_chunks(wg, T, chunk);
+      nch = dkdv_group_chunks(wg, pass, chunk);
     }
   }
   const int w0 = kDkdvKeys * wg;
@@ -71,7 +70,6 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
   const int key_j = kBwdKeys * kb16 - 1 + j;  // key of this lane's slot
   const int kmin = kBwdKeys * kb16 - 1;        // key of slot 0
 
-  const size_t slice = (size_t)bh * T * D;
   const float cl2 = head_scale_log2(log_gain, bh % H, D);
 
   // Stale LDS bits must not reach an MFMA as NaN through padding columns.
@@ -116,7 +114,9 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
   }
 
   // ---- query-tile staging (all waves), one tile ahead ----
-  const size_t plane = (size_t)BH * T * D;
+  // limb planes and row statistics hold the pass's rows only
+  const size_t plane = (size_t)BH * pass.rows * D;
+  const size_t lslice = (size_t)bh * pass.rows * D;
   u32x4 pre[P::CPT];
   f32x4 pre_st = {0.f, 0.f, 0.f, 0.f};
   auto load_tile = [&](int qt) {
@@ -129,14 +129,15 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
         const int row = rem / P::RCH, ch = rem % P::RCH;
         const int i = 32 * qt + row;
         if (i < T)
-          v = *reinterpret_cast<const u32x4*>(limbs + (size_t)pl * plane + slice + (size_t)i * D + 8 * ch);
+          v = *reinterpret_cast<const u32x4*>(limbs + (size_t)pl * plane + lslice +
+                                              (size_t)(i - pass.row0) * D + 8 * ch);
       }
       pre[u] = v;
     }
     if (tid < 16) {
       const int i = 32 * qt + 2 * tid;
       f32x4 v = {0.f, 0.f, 0.f, 0.f};
-      const float* sp = qstat + ((size_t)bh * T + (i < T ? i : 0)) * 2;
+      const float* sp = qstat + ((size_t)bh * pass.rows + (i < T ? i - pass.row0 : 0)) * 2;
       if (i + 1 < T) {
         v = *reinterpret_cast<const f32x4*>(sp);
       } else if (i < T) {
@@ -159,14 +160,15 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
     if (tid < 16) tstat[buf][tid] = pre_st;
   };
 
-  // query tiles of this item: a chunk of qt0 .. nqt-1, where qt0 is the first
-  // tile that sees an owned key of the work group
-  const int ntl = dkdv_group_tiles(wg, T);
+  // query tiles of this item: a chunk of the pass's tiles that see an owned
+  // key of the work group
+  const int ntl = dkdv_group_tiles(wg, pass);
   const int clen = (ntl + nch - 1) / nch;
-  const int qt0 = w0 / 32 + ch * clen;
-  const int qt_end = min(qt0 + clen, nqt);
-  // dS block of (tile qt, this wave's block); advanced by ds_kb_count(qt) per tile
-  size_t ds_blk = (size_t)bh * ds_blocks_before(nqt) + ds_blocks_before(qt0) + kb16;
+  const int qt0 = dkdv_group_first_tile(wg, pass) + ch * clen;
+  const int qt_end = min(qt0 + clen, pass.qb);
+  // dS block of (tile qt, this wave's block) in the pass's spill; advanced by
+  // ds_kb_count(qt) per tile
+  size_t ds_blk = (size_t)bh * pass.ds_slice + (ds_blocks_before(qt0) - pass.ds0) + kb16;
   __syncthreads();          // LDS clear before the first store
   if (qt0 < qt_end) {
     load_tile(qt0);
@@ -328,16 +330,23 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
   if (j >= 1 && j <= kBwdKeys && key_j < T && kb16 < nkb) {
     const float ck = cl2 * kLn2;
     if (nch == 1) {
-      // dK rotated back by the transposed RoPE (the gradient of the un-rotated k)
+      // dK rotated back by the transposed RoPE (the gradient of the un-rotated
+      // k); added to what earlier passes wrote for this key group
+      const bool accumulate = dkdv_qt0(wg) < pass.qa;
       E* pv = view_slice<E>(dVv, bh, H) + (long long)key_j * dVv.rstride;
       E* pk = view_slice<E>(dKv, bh, H) + (long long)key_j * dKv.rstride;
 #pragma unroll
       for (int mb = 0; mb < P::NMB; ++mb) {
         const int d0 = 16 * mb + 4 * g;
         if (d0 < D) {
-          st4(pv + d0, accv[mb]);
+          f32x4 gv = accv[mb];
           f32x4 gk = acck[mb] * ck;
           if (rope) gk = rope4(gk, rope_entry(rope, key_j, D, d0), true);
+          if (accumulate) {
+            gv += ld4(pv + d0);
+            gk += ld4(pk + d0);
+          }
+          st4(pv + d0, gv);
           st4(pk + d0, gk);
         }
       }
@@ -357,17 +366,17 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
 }
 
 template <int D, class E>
-hipError_t launch_bwd_dkdv(const BwdIO& io, const BwdWork& ws, const DkdvSplit& kvs, int BH, int H,
-                           int T, hipStream_t stream) {
+hipError_t launch_bwd_dkdv(const BwdIO& io, const BwdWork& ws, const BwdPass& pass,
+                           const DkdvSplit& kvs, int BH, int H, int T, hipStream_t stream) {
   hipLaunchKernelGGL((ca_bwd_dkdv_kernel<D, E>), dim3(kvs.items * BH), dim3(256), 0, stream, io.k,
                      io.v, io.rope, ws.limbs, ws.qstat, io.log_gain, io.dk, io.dv, ws.dsbuf,
-                     ws.kv_part, BH, H, T, kvs.chunk, kvs.part_items);
+                     ws.kv_part, pass, BH, H, T, kvs.chunk, kvs.part_items);
   return hipGetLastError();
 }
 
-#define CA_INSTANTIATE_DKDV(DD, EE)                                                         \
-  template hipError_t launch_bwd_dkdv<DD, EE>(const BwdIO&, const BwdWork&, const DkdvSplit&, \
-                                              int, int, int, hipStream_t);
+#define CA_INSTANTIATE_DKDV(DD, EE)                                                          \
+  template hipError_t launch_bwd_dkdv<DD, EE>(const BwdIO&, const BwdWork&, const BwdPass&,   \
+                                              const DkdvSplit&, int, int, int, hipStream_t);
 #define CA_INSTANTIATE_DKDV_ALL(EE)                                                          \
   CA_INSTANTIATE_DKDV(8, EE) CA_INSTANTIATE_DKDV(16, EE) CA_INSTANTIATE_DKDV(32, EE)         \
   CA_INSTANTIATE_DKDV(64, EE) CA_INSTANTIATE_DKDV(128, EE)

@@ -93,8 +93,47 @@ __host__ __device__ inline int ds_kb_count(int qt) { return (32 * qt + 31) / kBw
 __host__ __device__ inline long long ds_blocks_before(int qt) {
   return qt <= 0 ? 0 : qt + floor_sum(qt, kBwdKeys, 32, 31);
 }
-inline size_t bwd_ds_floats(int BH, int T) {
-  return (size_t)BH * (size_t)ds_blocks_before(num_q_tiles(T)) * kDsBlockFloats;
+
+
+// Backward passes.  The backward's workspace (dS spill, limb planes, row
+// statistics, partials) grows with the query rows it holds, the dS spill as
+// O(T^2); so that a bounded workspace serves any T, the backward can run in
+// passes over ranges of 128-query (dQ) groups.  A pass handles dQ groups
+// [g0, g1) = query tiles [qa, qb) = rows [row0, row0 + rows): its prep,
+// dK/dV, dQ and merge launches see only those queries.  dQ rows and their dS
+// are complete within a pass; dK and dV receive every pass's contribution in
+// pass order (the first pass that reaches a key group writes, later ones
+// add), and dlog_gain likewise.  One pass covering everything is the
+// ordinary backward.
+struct BwdPass {
+  int g0, g1;         // dQ groups of the pass
+  int qa, qb;         // query tiles
+  int row0, rows;     // first query row, and rows per slice held in the limb planes
+  long long ds0;      // dS blocks per slice before tile qa
+  long long ds_slice; // dS blocks per slice in this pass
+  int kv_groups;      // dK/dV key groups that meet the pass's tiles (wg < kv_groups)
+  int first;          // 1 for the first pass (dlog_gain written, not added)
+};
+__host__ __device__ inline BwdPass bwd_pass(int T, int g0, int g1) {
+  const int nqt = num_q_tiles(T);
+  BwdPass p;
+  p.g0 = g0;
+  p.g1 = g1;
+  p.qa = kDqTiles * g0;
+  p.qb = kDqTiles * g1 < nqt ? kDqTiles * g1 : nqt;
+  p.row0 = 32 * p.qa;
+  const int row1 = 32 * p.qb < T ? 32 * p.qb : T;
+  p.rows = row1 - p.row0;
+  p.ds0 = ds_blocks_before(p.qa);
+  p.ds_slice = ds_blocks_before(p.qb) - p.ds0;
+  const int nkb = bwd_num_key_blocks(T);
+  const int ngroups = (nkb + 3) / 4;
+  // key group wg (keys 56 wg ..) first meets tile 56 wg / 32; it meets this
+  // pass's tiles when that is below qb
+  const int need = (32 * p.qb + 55) / 56;
+  p.kv_groups = need < ngroups ? need : ngroups;
+  p.first = g0 == 0;
+  return p;
 }
 
 // dQ work items: a 128-query group of one slice and one chunk of its key
@@ -102,9 +141,9 @@ inline size_t bwd_ds_floats(int BH, int T) {
 // (split-K) when the unsplit grid would not fill the GPU for one round, so
 // that the longest rows do not leave it waiting on a few work groups; with a
 // full grid every group is one item (chunk >= bwd_num_key_blocks).  Items are
-// numbered per slice from the last (heaviest) group down, so the chunks of
-// multi-chunk groups come first; those items write partial dQ tiles that a
-// second kernel sums in chunk order.
+// numbered per slice from the last (heaviest) group of the pass down, so the
+// chunks of multi-chunk groups come first; those items write partial dQ tiles
+// that a second kernel sums in chunk order.
 constexpr int kDqChunkBlocks = 64;       // split chunk length in key blocks (about 900 keys)
 constexpr int kDqChunkBlocksShort = 48;  // when 64-block chunks still leave the GPU short of a round
 // key blocks met by the last query tile of group qg (the group's key range)
@@ -123,9 +162,9 @@ struct DqSplit {
   int part_items;    // of which write partial tiles (chunks of multi-chunk groups)
   int multi_groups;  // groups with more than one chunk (the last ones)
 };
-inline DqSplit dq_split_chunk(int T, int chunk) {
+inline DqSplit dq_split_chunk(int T, const BwdPass& p, int chunk) {
   DqSplit s{chunk, 0, 0, 0};
-  for (int g = 0; g < dq_num_groups(T); ++g) {
+  for (int g = p.g0; g < p.g1; ++g) {
     const int n = dq_group_chunks(g, T, s.chunk);
     s.items += n;
     if (n > 1) {
@@ -142,14 +181,15 @@ inline DqSplit dq_split_chunk(int T, int chunk) {
 // slices, short rows): more dQ work groups, at the price of more partials to
 // merge, which outweighs the gain once half a round is filled.
 constexpr int kDqChunkSmall[] = {32, 24, 16};
-inline DqSplit dq_split(int BH, int T, int resident_groups) {
-  if ((long long)dq_num_groups(T) * BH >= resident_groups) return dq_split_chunk(T, bwd_num_key_blocks(T));
-  DqSplit s = dq_split_chunk(T, kDqChunkBlocks);
+inline DqSplit dq_split(int BH, int T, const BwdPass& p, int resident_groups) {
+  if ((long long)(p.g1 - p.g0) * BH >= resident_groups)
+    return dq_split_chunk(T, p, bwd_num_key_blocks(T));
+  DqSplit s = dq_split_chunk(T, p, kDqChunkBlocks);
   if ((long long)s.items * BH >= resident_groups) return s;
-  s = dq_split_chunk(T, kDqChunkBlocksShort);
+  s = dq_split_chunk(T, p, kDqChunkBlocksShort);
   for (int c : kDqChunkSmall) {
     if (2LL * s.items * BH >= resident_groups) break;
-    s = dq_split_chunk(T, c);
+    s = dq_split_chunk(T, p, c);
   }
   return s;
 }
@@ -159,23 +199,31 @@ inline DqSplit dq_split(int BH, int T, int resident_groups) {
 constexpr int kDqGroupsPerCu = 3;
 
 // dK/dV work items: key-block group wg (kDkdvWaves blocks, kDkdvKeys keys) of
-// one slice and a chunk of the query tiles that see its keys.  When the grid
-// of whole groups would not fill the GPU for two rounds (small B*H), a group's
-// query range is cut into chunks of at most kDkdvChunkTiles tiles, so the
-// groups with the longest ranges do not set the launch time alone; the chunks
-// write partial dK/dV that a merge sums in chunk order.  Items are numbered
-// per slice from group 0 (the longest range) up, chunks of a group together.
+// one slice and a chunk of the pass's query tiles that see its keys.  When
+// the grid of whole groups would not fill the GPU for two rounds (small B*H),
+// a group's query range is cut into chunks of at most kDkdvChunkTiles tiles,
+// so the groups with the longest ranges do not set the launch time alone; the
+// chunks write partial dK/dV that a merge sums in chunk order.  Items are
+// numbered per slice from group 0 (the longest range) up, chunks of a group
+// together.
 constexpr int kDkdvKeys = kDkdvWaves * kBwdKeys;
 constexpr int kDkdvChunkTiles = 24;
 constexpr int kDkdvGroupsPerCu = 2;
 __host__ __device__ inline int dkdv_num_groups(int T) {
   return (bwd_num_key_blocks(T) + kDkdvWaves - 1) / kDkdvWaves;
 }
-__host__ __device__ inline int dkdv_group_tiles(int wg, int T) {
-  return num_q_tiles(T) - kDkdvKeys * wg / 32;  // tiles qt0 .. nqt-1
+// first query tile that sees key group wg
+__host__ __device__ inline int dkdv_qt0(int wg) { return kDkdvKeys * wg / 32; }
+// the pass's tiles of group wg (wg < p.kv_groups): max(qt0, qa) .. qb-1
+__host__ __device__ inline int dkdv_group_first_tile(int wg, const BwdPass& p) {
+  const int a = dkdv_qt0(wg);
+  return a > p.qa ? a : p.qa;
 }
-__host__ __device__ inline int dkdv_group_chunks(int wg, int T, int chunk) {
-  return (dkdv_group_tiles(wg, T) + chunk - 1) / chunk;
+__host__ __device__ inline int dkdv_group_tiles(int wg, const BwdPass& p) {
+  return p.qb - dkdv_group_first_tile(wg, p);
+}
+__host__ __device__ inline int dkdv_group_chunks(int wg, const BwdPass& p, int chunk) {
+  return (dkdv_group_tiles(wg, p) + chunk - 1) / chunk;
 }
 struct DkdvSplit {
   int chunk;         // query tiles per chunk (upper bound)
@@ -183,11 +231,10 @@ struct DkdvSplit {
   int part_items;    // of which write partial dK/dV (chunks of multi-chunk groups)
   int multi_groups;  // groups with more than one chunk (the first ones)
 };
-// resident_groups: dK/dV work groups the GPU holds at once (0: never split)
-inline DkdvSplit dkdv_split_chunk(int T, int chunk) {
+inline DkdvSplit dkdv_split_chunk(const BwdPass& p, int chunk) {
   DkdvSplit s{chunk, 0, 0, 0};
-  for (int g = 0; g < dkdv_num_groups(T); ++g) {
-    const int n = dkdv_group_chunks(g, T, chunk);
+  for (int g = 0; g < p.kv_groups; ++g) {
+    const int n = dkdv_group_chunks(g, p, chunk);
     s.items += n;
     if (n > 1) {
       s.part_items += n;
@@ -198,15 +245,16 @@ inline DkdvSplit dkdv_split_chunk(int T, int chunk) {
 }
 // Shorter chunks while kDkdvChunkTiles leaves less than one round (fewer
 // would only add partials and merge work): the first length whose items fill
-// a round is taken, else the last.
+// a round is taken, else the last.  resident_groups: dK/dV work groups the
+// GPU holds at once (0: never split).
 constexpr int kDkdvChunkSmall[] = {16, 12, 8, 6};
-inline DkdvSplit dkdv_split(int BH, int T, int resident_groups) {
+inline DkdvSplit dkdv_split(int BH, const BwdPass& p, int resident_groups) {
   const long long want = 2LL * resident_groups;
-  if ((long long)dkdv_num_groups(T) * BH >= want) return dkdv_split_chunk(T, num_q_tiles(T));
-  DkdvSplit s = dkdv_split_chunk(T, kDkdvChunkTiles);
+  if ((long long)p.kv_groups * BH >= want) return dkdv_split_chunk(p, p.qb - p.qa);
+  DkdvSplit s = dkdv_split_chunk(p, kDkdvChunkTiles);
   for (int c : kDkdvChunkSmall) {
     if ((long long)s.items * BH >= resident_groups) break;
-    s = dkdv_split_chunk(T, c);
+    s = dkdv_split_chunk(p, c);
   }
   return s;
 }
@@ -221,6 +269,9 @@ enum KernelId {
 constexpr int kDtypeF32 = 0, kDtypeBF16 = 1, kDtypeF16 = 2;
 void timer_begin(int id, hipStream_t s);
 void timer_end(int id, hipStream_t s);
+// Whether the backward of this shape can run in a workspace of `bytes`
+// (in one pass or in passes over query-group ranges).
+bool bwd_fits(int B, int H, int T, int D, size_t bytes);
 // Sets the calling thread's ca_last_error() text; returns `code`.
 int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 
@@ -301,12 +352,13 @@ template <int D, class E>
 hipError_t launch_fwd(const FwdIO& io, float* part, int B, int H, int T, int C,
                       hipStream_t stream);
 
-// Backward workspace buffers (sizes: bwd_ds_floats, bwd_limb_elems, BH*T*2
-// qstat floats, gain partials per dQ item, dQ chunk partials).
+// Backward workspace buffers of one pass (sizes: the pass's dS blocks, limb
+// planes and qstat rows, gain partials per dQ item, dQ and dK/dV chunk
+// partials).
 struct BwdWork {
   float* dsbuf;       // dS spill, 32x16 blocks
-  __bf16* limbs;      // six bf16 planes [BH][T][D]: Q limbs h, m, l; dY/Z limbs h, m, l
-  float* qstat;       // per query row: (m, D/Z)
+  __bf16* limbs;      // six bf16 planes [BH][pass rows][D]: Q limbs h, m, l; dY/Z limbs h, m, l
+  float* qstat;       // per query row of the pass: (m, D/Z)
   float* gain_part;   // per dQ item
   float* dq_part;     // dQ chunk partials
   float* kv_part;     // dK/dV chunk partials: [BH][part item][kDkdvKeys][2][D]
@@ -314,12 +366,12 @@ struct BwdWork {
 
 // dK/dV kernel of the backward (ca_bwd_dkdv.hip, its own translation unit).
 template <int D, class E>
-hipError_t launch_bwd_dkdv(const BwdIO& io, const BwdWork& ws, const DkdvSplit& kvs, int BH, int H,
-                           int T, hipStream_t stream);
-inline size_t bwd_limb_elems(int BH, int T, int D) { return (size_t)6 * BH * T * D; }
+hipError_t launch_bwd_dkdv(const BwdIO& io, const BwdWork& ws, const BwdPass& pass,
+                           const DkdvSplit& kvs, int BH, int H, int T, hipStream_t stream);
+inline size_t bwd_limb_elems(int BH, int rows, int D) { return (size_t)6 * BH * rows * D; }
 
 template <int D, class E>
-hipError_t launch_bwd(const BwdIO& io, const BwdWork& ws, const DqSplit& sp, const DkdvSplit& kvs,
-                      int B, int H, int T, hipStream_t stream);
+hipError_t launch_bwd(const BwdIO& io, const BwdWork& ws, const BwdPass& pass, const DqSplit& sp,
+                      const DkdvSplit& kvs, int B, int H, int T, hipStream_t stream);
 
 }  // namespace ca

@@ -63,12 +63,13 @@ extern "C" int ca_bwd_f32_noalloc(const float* q, const float* k, const float* v
                                   float* dlog_gain, int B, int H, int T, int D, void* stream) {
   if (B <= 0 || H <= 0 || T <= 0)
     return ca::set_error(CA_ERR_INVALID, "invalid shape B=%d H=%d T=%d (all must be positive)", B, H, T);
-  const size_t need = ca_bwd_workspace_bytes(B, H, T, D);
-  if (need > kScratchBytes)
+  // the backward runs in passes over query-group ranges sized to the array;
+  // a shape whose single 128-query group needs more is refused
+  if (!ca::bwd_fits(B, H, T, D, kScratchBytes))
     return ca::set_error(CA_ERR_WORKSPACE,
-                         "ca_bwd_f32_noalloc: this shape needs %zu bytes of scratch, beyond the "
-                         "static %zu (B=%d H=%d T=%d D=%d); use ca_bwd_f32 with a workspace",
-                         need, kScratchBytes, B, H, T, D);
+                         "ca_bwd_f32_noalloc: one 128-query pass of this shape needs more than the "
+                         "static %zu bytes of scratch (B=%d H=%d T=%d D=%d); use ca_bwd_f32 with "
+                         "a workspace", kScratchBytes, B, H, T, D);
   // Every kernel of the backward writes each scratch element before it reads
   // it, so nothing needs clearing between calls.
   int rc = CA_OK;

@@ -26,7 +26,7 @@ from torch import nn
 from torch.nn import functional as F
 
 from . import _native
-from .ops import (SUPPORTED_HEAD_DIMS, _bwd_workspace_bytes, _fwd_workspace_bytes, _mode,
+from .ops import (SUPPORTED_HEAD_DIMS, _bwd_qkv_workspace_bytes, _fwd_workspace_bytes, _mode,
                   continuum_attention)
 
 _DTYPE_CODE = {torch.float32: _native.CA_DTYPE_F32, torch.bfloat16: _native.CA_DTYPE_BF16,
@@ -323,7 +323,7 @@ class _RopeContinuumAttention(torch.autograd.Function):
         g = _aligned(gout.to(x.dtype), 16)
         dqkv = torch.empty(Bsz, T, 3 * heads * D, device=dev, dtype=x.dtype)
         dg = torch.empty(heads, device=dev, dtype=torch.float32)
-        nbytes = _bwd_workspace_bytes(Bsz, heads, T, D)
+        nbytes = _bwd_qkv_workspace_bytes(Bsz, heads, T, D)
         ws = torch.empty(nbytes, device=dev, dtype=torch.uint8)
         with _native.on_device(dev):
             _native.check(lib.ca_bwd_qkv(x.data_ptr(), _DTYPE_CODE[x.dtype],

@@ -72,6 +72,26 @@ def _bwd_workspace_bytes(B: int, H: int, T: int, D: int) -> int:
     return int(_native.load().ca_bwd_workspace_bytes(B, H, T, D))
 
 
+@functools.lru_cache(maxsize=256)
+def _bwd_qkv_workspace_bytes(B: int, H: int, T: int, D: int) -> int:
+    return int(_native.load().ca_bwd_qkv_workspace_bytes(B, H, T, D))
+
+
+def set_workspace_cap(nbytes: int) -> None:
+    """Bounds the operator's device workspace (bytes; 0 = no bound; default
+    1 GiB, or the environment's ``CA_WORKSPACE_CAP_MB``), the role
+    ``query_tile`` plays for the reference's materialised weights: beyond it
+    the forward uses longer work splits and the backward runs in passes over
+    query ranges.  Process-wide."""
+    _native.check(_native.load().ca_set_workspace_cap(int(nbytes)))
+    _fwd_workspace_bytes.cache_clear()
+    _bwd_workspace_bytes.cache_clear()
+
+
+def workspace_cap() -> int:
+    return int(_native.load().ca_workspace_cap())
+
+
 def set_split_override(fwd_split_tiles: int = 0, dq_chunk_blocks: int = 0,
                        dkdv_chunk_tiles: int = 0) -> None:
     """Forces the kernels' work-split lengths (0 = automatic; see

@@ -44,7 +44,21 @@ int ca_abi_version(void);
 /* Text of the last error raised on the calling thread ("" if none). */
 const char* ca_last_error(void);
 
-/* Bytes of device workspace ca_fwd_f32 needs for this shape (may be 0). */
+/* Workspace bound.  The reference's query_tile bounds the memory of its
+ * materialised [B*H, query_tile, T] weights (cuda/continuum_attention.py:957);
+ * here the workspaces are bounded instead: ca_fwd_f32 lengthens its work
+ * splits until their partials fit the workspace it is given (none at all
+ * needs no workspace), and ca_bwd_f32 runs in passes over ranges of
+ * 128-query groups sized to the workspace it is given (dK, dV and dlog_gain
+ * are summed over the passes in a fixed order).  The size functions below
+ * report the full-speed size, or, when that exceeds the cap, the size of the
+ * plan that fits under it.  The cap is process-wide; default 1 GiB, 0 = no
+ * cap.  Results are deterministic for a given workspace size; different
+ * sizes sum in different orders and may differ by rounding. */
+int ca_set_workspace_cap(size_t bytes);
+size_t ca_workspace_cap(void);
+
+/* Bytes of device workspace ca_fwd_f32 asks for (may be 0; see above). */
 size_t ca_fwd_workspace_bytes(int B, int H, int T, int D);
 
 /* Forward: out = W(S) v with S = exp(log_gain[h]) / sqrt(D) * q k^T, exact CA
@@ -58,7 +72,8 @@ int ca_fwd_f32(const float* q, const float* k, const float* v, const float* log_
                float* stats, void* workspace, size_t workspace_bytes, int B, int H, int T, int D,
                void* stream);
 
-/* Bytes of device workspace ca_bwd_f32 needs for this shape. */
+/* Bytes of device workspace ca_bwd_f32 asks for (see above); the minimum is
+ * what one 128-query group of every slice needs. */
 size_t ca_bwd_workspace_bytes(int B, int H, int T, int D);
 
 /* Backward (first order): given dout = dL/dout, writes dq, dk, dv ([B,H,T,D])
@@ -135,7 +150,10 @@ int ca_fwd_qkv(const void* qkv, int dtype, const float* rope_cs, const float* lo
 
 /* Backward of ca_fwd_qkv: dout [B, T, H*D] (dtype) -> dqkv [B, T, 3, H, D]
  * (dtype; the gradients of q and k rotated back by the transposed RoPE) and
- * dlog_gain[H]. */
+ * dlog_gain[H].  It runs in one pass (gradients in the element type are not
+ * summed over passes), so its workspace is ca_bwd_qkv_workspace_bytes,
+ * regardless of the cap. */
+size_t ca_bwd_qkv_workspace_bytes(int B, int H, int T, int D);
 int ca_bwd_qkv(const void* qkv, int dtype, const float* rope_cs, const float* log_gain,
                const float* y, const float* stats, const void* dout, void* dqkv,
                float* dlog_gain, void* workspace, size_t workspace_bytes, int B, int T, int H,

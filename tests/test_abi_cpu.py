@@ -71,10 +71,17 @@ def test_null_misaligned_and_workspace_errors(ca):
     odd = ctypes.c_void_p(4100)
     assert lib.ca_fwd_f32(odd, p, p, p, p, p, None, 0, 1, 1, 8, 64, None) == 1
     assert b"aligned" in lib.ca_last_error()
-    need = lib.ca_fwd_workspace_bytes(1, 1, 4096, 64)
-    assert need > 0
-    assert lib.ca_fwd_f32(p, p, p, p, p, p, p, need - 1, 1, 1, 4096, 64, None) == 3
-    assert b"workspace" in lib.ca_last_error()
+    # a smaller workspace lengthens the forward's splits instead of failing;
+    # with a forced split the partials cannot shrink, so too little is refused
+    # before any launch
+    assert lib.ca_debug_set_splits(1, 0, 0) == 0
+    try:
+        need = lib.ca_fwd_workspace_bytes(1, 1, 4096, 64)
+        assert need > 0
+        assert lib.ca_fwd_f32(p, p, p, p, p, p, p, need - 1, 1, 1, 4096, 64, None) == 3
+        assert b"workspace" in lib.ca_last_error()
+    finally:
+        assert lib.ca_debug_set_splits(0, 0, 0) == 0
     assert lib.ca_bwd_f32(p, p, p, p, p, p, p, p, p, p, p, p, 16, 1, 1, 64, 64, None) == 3
 
 
@@ -175,11 +182,40 @@ def test_swiglu_null_and_misaligned_pointers(ca):
 
 
 def test_noalloc_backward_checks_before_any_launch(ca):
-    """ca_bwd_f32_noalloc refuses, with no HIP call, shapes whose workspace
-    exceeds its static array and invalid shapes."""
+    """ca_bwd_f32_noalloc refuses, with no HIP call, shapes whose single
+    128-query pass exceeds its static array, and invalid shapes."""
     lib = ca.native.load()
     p = ctypes.c_void_p(16)
-    assert lib.ca_bwd_workspace_bytes(4, 16, 4096, 64) > 512 << 20
-    assert lib.ca_bwd_f32_noalloc(p, p, p, p, p, p, p, p, p, p, p, 4, 16, 4096, 64, None) == 3
+    assert lib.ca_bwd_f32_noalloc(p, p, p, p, p, p, p, p, p, p, p, 8, 16, 65536, 64, None) == 3
     assert b"scratch" in lib.ca_last_error()
     assert lib.ca_bwd_f32_noalloc(p, p, p, p, p, p, p, p, p, p, p, 0, 16, 64, 64, None) == 1
+
+
+def test_workspace_cap_bounds_the_sizes(ca):
+    """The workspace bound: under the default 1 GiB cap the backward of a
+    long sequence asks for at most the cap (it runs in passes) and the
+    forward for at most the cap (longer splits); without a cap, the full
+    sizes; the token-major backward always asks for its one-pass size."""
+    lib = ca.native.load()
+    prev = lib.ca_workspace_cap()
+    try:
+        assert prev == 1 << 30
+        full = lib.ca_bwd_qkv_workspace_bytes(1, 16, 32768, 64)
+        assert full > 30 << 30
+        assert lib.ca_bwd_workspace_bytes(1, 16, 32768, 64) <= 1 << 30
+        assert lib.ca_fwd_workspace_bytes(1, 16, 32768, 64) <= 1 << 30
+        small = lib.ca_bwd_workspace_bytes(2, 16, 2048, 64)
+        assert small == lib.ca_bwd_qkv_workspace_bytes(2, 16, 2048, 64)  # fits: one pass
+        ca.ops.set_workspace_cap(0)
+        assert lib.ca_bwd_workspace_bytes(1, 16, 32768, 64) == full
+        assert lib.ca_fwd_workspace_bytes(1, 16, 32768, 64) > 1 << 30
+        ca.ops.set_workspace_cap(32 << 20)
+        assert lib.ca_bwd_workspace_bytes(1, 2, 8192, 64) <= 32 << 20
+        assert lib.ca_fwd_workspace_bytes(1, 2, 8192, 64) <= 32 << 20
+        # below what one 128-query group needs, the minimum is reported
+        ca.ops.set_workspace_cap(1 << 20)
+        least = lib.ca_bwd_workspace_bytes(1, 2, 8192, 64)
+        assert 1 << 20 < least < 32 << 20
+        assert lib.ca_fwd_workspace_bytes(1, 2, 8192, 64) == 0  # unsplit forward
+    finally:
+        ca.ops.set_workspace_cap(prev)

@@ -198,3 +198,83 @@ def test_nan_inputs_propagate_like_the_reference(gpu_ca):
     bad[0, 1, j:] = True
     assert np.isnan(y2[bad]).all()
     assert np.array_equal(y2[~bad], y0[~bad])
+
+
+@pytest.fixture
+def workspace_cap(gpu_ca):
+    prev = gpu_ca.ops.workspace_cap()
+    yield gpu_ca.ops.set_workspace_cap
+    gpu_ca.ops.set_workspace_cap(prev)
+
+
+def _row_and_suffix_checks(q, k, v, rho, dy, y, grads, rows, label):
+    """Forward and dQ on sampled rows; dK, dV, dQ of the last 256 keys exactly
+    (only queries i >= j see key j); the invariants."""
+    dq, dk, dv, dr = grads
+    qn, kn, vn, rn, dyn = q.numpy(), k.numpy(), v.numpy(), rho.numpy(), dy.numpy()
+    T = q.shape[2]
+    suffix = np.arange(T - 256, T)
+    for h in range(q.shape[1]):
+        yr = O.ca_forward_rows(qn, kn, vn, rn, 0, h, rows)
+        dqr = O.ca_backward_rows(qn, kn, vn, rn, dyn, 0, h, rows)[0]
+        dq_s, dk_s, dv_s, _ = O.ca_backward_rows(qn, kn, vn, rn, dyn, 0, h, suffix)
+        e = (rel(y[0, h][rows], yr), rel(dq[0, h][rows], dqr), rel(dk[0, h, suffix], dk_s[suffix]),
+             rel(dv[0, h, suffix], dv_s[suffix]), rel(dq[0, h, suffix], dq_s))
+        say(f"   {label} head {h}: rows out {e[0]:.2e} dq {e[1]:.2e}; last 256 keys dk {e[2]:.2e} "
+            f"dv {e[3]:.2e} dq {e[4]:.2e}")
+        assert e[0] <= OUT_TOL and all(x <= GRAD_TOL for x in e[1:])
+    check_invariants(q, k, dy, dq, dk, dv, dr)
+
+
+@pytest.mark.parametrize("T,H,cap_mb", [(16384, 2, 256), (32768, 1, 512), (16384, 1, 96)])
+def test_bounded_workspace_long_context(gpu_ca, workspace_cap, T, H, cap_mb):
+    """The workspace bound that stands in for the reference's query_tile
+    (cuda/continuum_attention.py:957): with a cap far below the full
+    backward workspace (4.2 GB for [1,2,16384,64], 8.3 GB for [1,1,32768,64])
+    the size functions report at most the cap, the backward runs in passes
+    over query ranges and the forward with longer splits, and the results
+    match the oracle: sampled rows, the last 256 keys exactly, invariants."""
+    say(f"[case] workspace cap {cap_mb} MiB, [1,{H},{T},64]")
+    lib = gpu_ca.native.load()
+    full = lib.ca_bwd_qkv_workspace_bytes(1, H, T, 64)
+    workspace_cap(cap_mb << 20)
+    wb, wf = lib.ca_bwd_workspace_bytes(1, H, T, 64), lib.ca_fwd_workspace_bytes(1, H, T, 64)
+    say(f"   backward workspace {wb / 2**20:.0f} MiB (full {full / 2**20:.0f} MiB), "
+        f"forward {wf / 2**20:.0f} MiB")
+    assert wb <= cap_mb << 20 and wf <= cap_mb << 20 and full > 4 * (cap_mb << 20)
+    q, k, v, rho, dy = config5_like(T, H)
+    y, grads = run_hip(gpu_ca, q, k, v, rho, dy)
+    assert np.all(np.isfinite(y)) and all(np.all(np.isfinite(x)) for x in grads)
+    rows = np.array([0, 1, 31, 32, 127, 128, 2047, 2048, 8191, 8192, T // 2 + 5, T - 129, T - 2, T - 1])
+    _row_and_suffix_checks(q, k, v, rho, dy, y, grads, rows, f"cap {cap_mb} MiB")
+
+
+def config5_like(T, H):
+    """Config 5's two head kinds: near-duplicate keys (delta ~ 1e-4, the Taylor
+    branch) in head 0 and keys x4 (large delta) in head 1."""
+    g = torch.Generator().manual_seed(T + H)
+    q = torch.randn(1, H, T, 64, generator=g)
+    k0 = torch.randn(1, 64, generator=g)
+    heads = [torch.cat([k0, k0 + torch.cumsum(torch.randn(T - 1, 64, generator=g) * 1e-4, 0)])]
+    if H > 1:
+        heads.append(4.0 * torch.randn(T, 64, generator=g))
+    k = torch.stack(heads)[None].contiguous()
+    v = torch.randn(1, H, T, 64, generator=g)
+    dy = torch.randn(1, H, T, 64, generator=g)
+    return q, k, v, torch.zeros(H), dy
+
+
+@pytest.mark.parametrize("cap_mb,shape", [(3, (2, 3, 3000, 64)), (1, (1, 2, 1500, 32))])
+def test_backward_passes_in_full(gpu_ca, workspace_cap, cap_mb, shape):
+    """A cap that forces many passes at a size the oracle checks in full:
+    outputs and all four gradients, and two calls bitwise equal."""
+    say(f"[case] backward passes, cap {cap_mb} MiB, {shape}")
+    workspace_cap(cap_mb << 20)
+    lib = gpu_ca.native.load()
+    B, H, T, D = shape
+    assert lib.ca_bwd_workspace_bytes(B, H, T, D) < lib.ca_bwd_qkv_workspace_bytes(B, H, T, D) // 4
+    q, k, v, rho, dy = inputs(shape, 30, [0.2, -0.3, 0.1][:H])
+    y, grads = run_hip(gpu_ca, q, k, v, rho, dy)
+    y2, grads2 = run_hip(gpu_ca, q, k, v, rho, dy)
+    assert np.array_equal(y, y2) and all(np.array_equal(a, b) for a, b in zip(grads, grads2))
+    check_full(q, k, v, rho, dy, y, grads, f"cap {cap_mb} MiB")

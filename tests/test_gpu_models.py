@@ -255,7 +255,7 @@ def _qkv_call(ca, qkv, gain, cs, H, dout):
     csp = cs.data_ptr() if cs is not None else None
     ca.native.check(lib.ca_fwd_qkv(qkv.data_ptr(), code, csp, gain.data_ptr(), y.data_ptr(),
                                    out.data_ptr(), st.data_ptr(), wf.data_ptr(), nf, Bsz, T, H, D, s))
-    nb = lib.ca_bwd_workspace_bytes(Bsz, H, T, D)
+    nb = lib.ca_bwd_qkv_workspace_bytes(Bsz, H, T, D)
     wb = torch.empty(nb, device="cuda", dtype=torch.uint8)
     dqkv = torch.empty_like(qkv)
     dg = torch.empty(H, device="cuda")
