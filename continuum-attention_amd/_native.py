@@ -65,7 +65,7 @@ SIGNATURES = {
 }
 
 KERNEL_NAMES = ("ca_fwd", "ca_fwd_combine", "ca_bwd_prep", "ca_bwd_dkdv", "ca_bwd_dq",
-                "ca_bwd_gain_merge", "ca_weights", "ca_weights_bwd", "ca_rmsnorm_fwd",
+                "ca_bwd_merge", "ca_weights", "ca_weights_bwd", "ca_rmsnorm_fwd",
                 "ca_rmsnorm_bwd", "ca_swiglu_fwd", "ca_swiglu_bwd")
 
 _lib = None

@@ -152,7 +152,7 @@ BwdLayout bwd_layout(int B, int H, int T, int D, const ca::BwdPass& p) {
   L.limbs = align256((size_t)BH * p.ds_slice * ca::kDsBlockFloats * sizeof(float));
   L.qstat = L.limbs + align256(ca::bwd_limb_elems(BH, p.rows, D) * sizeof(uint16_t));
   L.gain = L.qstat + align256((size_t)BH * p.rows * 2 * sizeof(float));
-  L.dqpart = L.gain + align256((size_t)BH * sp.items * sizeof(float));
+  L.dqpart = L.gain + align256((size_t)BH * kvs.items * sizeof(float));
   L.kvpart = L.dqpart + align256((size_t)BH * sp.part_items * ca::kDqRows * D * sizeof(float));
   L.total = L.kvpart + align256((size_t)BH * kvs.part_items * ca::kDkdvKeys * 2 * D * sizeof(float));
   return L;

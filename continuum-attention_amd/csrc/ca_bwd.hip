@@ -21,12 +21,14 @@
 //                   registers as bf16 limbs for the whole launch.  All four
 //                   products are bf16x6 on v_mfma_f32_16x16x32_bf16.  dS is
 //                   also spilled as 32x16 row blocks for the dQ pass.
+//                   Each item also forms its gain partial
+//                   sum_j (k_j - k_0) . dK_j (= sum_ij dS_ij s_ij, since
+//                   s_ij = c q_i . k_j and every row of dS sums to zero).
 //   ca_bwd_dq       dQ = c dS (K - k_ref) over the spilled blocks, one work
-//                   item per (slice, 128 queries, chunk of key blocks); each
-//                   item also forms its gain partial sum_i q_i . dQ_i
-//                   (= sum_ij dS_ij s_ij, since s_ij = c q_i . k_j).
-//   ca_bwd_gain_merge  dRho_h = sum of the gain partials; sums the dQ chunk
-//                   partials of split query groups.
+//                   item per (slice, 128 queries, chunk of key blocks); H
+//                   extra work groups sum the gain partials into dRho_h.
+//   ca_bwd_merge    sums the dQ and dK/dV chunk partials of split groups
+//                   (launched only when a split leaves some).
 //
 // Score-tile layout in ca_bwd_dkdv: the 16x16 result of S / dP' puts slot j
 // (key 14*kb - 1 + j) in lane j of each 16-lane row and queries 4*(l/16) + r
@@ -116,9 +118,27 @@ __global__ __launch_bounds__(256) void ca_bwd_prep_kernel(View Qv, const float* 
 // limbs in registers; B operand: lane (d = 16nb + l%16, g) gets the same 8
 // slots of column d through two transposed reads.  Halo slots and invisible
 // keys carry dS = 0, so no masks are needed.  A single-chunk group writes dQ;
-// the chunks of a longer group write partial tiles that ca_bwd_gain_merge
-// sums.  Every item writes its gain partial sum_i q_i . dQ_i(chunk) (linear in
-// dQ, so the partials add up).
+// the chunks of a longer group write partial tiles that ca_bwd_merge sums.
+// Gain gradient: dlog_gain[h] = the fixed-order sum over batch and dK/dV
+// items of the partials the dK/dV kernel wrote (added to the earlier passes'
+// sum after the first pass).  Launched as H extra work groups of the dQ grid.
+__device__ __forceinline__ void gain_sum(const float* __restrict__ gain_part,
+                                         float* __restrict__ dlog_gain, int h, int B, int H,
+                                         int n_kv_items, bool first) {
+  __shared__ float wsum[4];
+  const int tid = threadIdx.x;
+  float acc = 0.f;
+  for (int b = 0; b < B; ++b)
+    for (int k = tid; k < n_kv_items; k += 256) acc += gain_part[((size_t)b * H + h) * n_kv_items + k];
+  acc = wave_sum(acc);
+  if ((tid & 63) == 0) wsum[tid >> 6] = acc;
+  __syncthreads();
+  if (tid == 0) {
+    const float part_sum = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+    dlog_gain[h] = first ? part_sum : dlog_gain[h] + part_sum;
+  }
+}
+
 template <int D>
 struct DqP {
   static constexpr int NB = (D + 15) / 16;            // 16-column d blocks of dQ
@@ -131,16 +151,21 @@ struct DqP {
 };
 
 template <int D, class E, bool ROPE>
-__global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict__ dsbuf, View Qv,
+__global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict__ dsbuf,
                                                         View Kv, const float* __restrict__ rope,
                                                         const float* __restrict__ log_gain,
                                                         View dQv, float* __restrict__ dq_part,
-                                                        float* __restrict__ gain_part, BwdPass pass,
-                                                        int BH, int H, int T, int chunk,
-                                                        int n_items, int n_part) {
+                                                        const float* __restrict__ gain_part,
+                                                        float* __restrict__ dlog_gain, BwdPass pass,
+                                                        int B, int H, int T, int chunk,
+                                                        int n_items, int n_part, int n_kv_items) {
   using P = DqP<D>;
+  const int BH = B * H;
+  if ((int)blockIdx.x >= n_items * BH) {  // the H gain work groups
+    gain_sum(gain_part, dlog_gain, blockIdx.x - n_items * BH, B, H, n_kv_items, pass.first);
+    return;
+  }
   __shared__ __attribute__((aligned(16))) __bf16 kst[2 * P::STAGE];
-  __shared__ float gred[kDqTiles];
   const int nqt = num_q_tiles(T);
   const int nkb = bwd_num_key_blocks(T);
   const int bh = blockIdx.x % BH;
@@ -302,14 +327,12 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   }
   // lane (d = 16nb + l16, group g) holds rows 16rb + 4g + r of the wave's
   // tile; the other column of d's RoPE pair (d ^ 1) is in lane l16 ^ 1
-  float gsum = 0.f;
   if (wave_on) {
     // single-chunk groups write dQ; chunk partials are item-indexed tiles
     // [kDqRows queries][D] (items of multi-chunk groups are numbered first),
     // summed and rotated back by the merge
     const bool single = nch == 1;
     float* part = dq_part + ((size_t)bh * n_part + item) * kDqRows * D;
-    const E* Qs = view_slice<const E>(Qv, bh, H);
     E* dQs = view_slice<E>(dQv, bh, H);
     const bool odd = l16 & 1;
 #pragma unroll
@@ -322,24 +345,15 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
           const int row = kDqRows * qg + rloc;
           const int d = 16 * nb + l16;
           const float val = acc[rb][nb][r] * c;
-          const float val_pair = __shfl_xor(val, 1);
+          const float val_pair = ROPE ? __shfl_xor(val, 1) : 0.f;
           if (row < T && d < D) {
-            const E* qrow = Qs + (long long)row * Qv.rstride;
-            float qd = ld1(qrow + d);
-            float cs_c = 1.f, cs_s = 0.f;
-            if (rope) {
-              const float* e = rope + (long long)row * D + (d & ~1);
-              cs_c = e[0];
-              cs_s = e[1];
-              const float qp = ld1(qrow + (d ^ 1));
-              qd = odd ? fmaf(qd, cs_c, qp * cs_s) : fmaf(qd, cs_c, -qp * cs_s);
-            }
-            gsum = fmaf(qd, val, gsum);
             if (single) {
-              // transposed rotation back to the un-rotated q
-              const float o = rope ? (odd ? fmaf(val, cs_c, -val_pair * cs_s)
-                                          : fmaf(val, cs_c, val_pair * cs_s))
-                                   : val;
+              float o = val;
+              if (ROPE) {
+                // transposed rotation back to the un-rotated q
+                const float* e = rope + (long long)row * D + (d & ~1);
+                o = odd ? fmaf(val, e[0], -val_pair * e[1]) : fmaf(val, e[0], val_pair * e[1]);
+              }
               st1(dQs + (long long)row * dQv.rstride + d, o);
             } else {
               part[(size_t)rloc * D + d] = val;
@@ -347,28 +361,22 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
           }
         }
   }
-  gsum = wave_sum(gsum);
-  if (lane == 0) gred[w] = gsum;
-  __syncthreads();
-  if (tid == 0) gain_part[(size_t)bh * n_items + item] = (gred[0] + gred[1]) + (gred[2] + gred[3]);
 }
 
-// Work groups [0, H): dRho_h = sum over batch and dQ items of the gain
-// partials (fixed order).  Work groups H + BH*gi + bh: dQ of multi-chunk
-// group nqg-1-gi of slice bh, the sum of its chunk partials in chunk order.
-// Work groups after those: dK, dV of multi-chunk dK/dV group gi of slice bh,
-// the sum of its chunk partials in chunk order.
+// Merges of chunk partials, in chunk order.  Work groups BH*gi + bh: dQ of
+// multi-chunk group g1-1-gi of slice bh (rotated back when RoPE is on).  Work
+// groups after those: dK, dV of multi-chunk dK/dV group gi of slice bh, added
+// to what earlier passes wrote for that key group.
 template <int D, class E>
-__global__ __launch_bounds__(256) void ca_bwd_gain_merge_kernel(
-    const float* __restrict__ gain_part, const float* __restrict__ dq_part,
-    const float* __restrict__ kv_part, const float* __restrict__ rope,
-    float* __restrict__ dlog_gain, View dQv, View dKv, View dVv, BwdPass pass, int B, int H, int T,
-    int chunk, int n_items, int n_part, int dq_multi, int kv_chunk, int kv_part_items) {
+__global__ __launch_bounds__(256) void ca_bwd_merge_kernel(
+    const float* __restrict__ dq_part, const float* __restrict__ kv_part,
+    const float* __restrict__ rope, View dQv, View dKv, View dVv, BwdPass pass, int B, int H, int T,
+    int chunk, int n_part, int dq_multi, int kv_chunk, int kv_part_items) {
   const int tid = threadIdx.x;
   const int BHt = B * H;
-  if (blockIdx.x >= H + BHt * dq_multi) {
+  if (blockIdx.x >= BHt * dq_multi) {
     constexpr int C4 = D / 4;
-    const int m = blockIdx.x - H - BHt * dq_multi;
+    const int m = blockIdx.x - BHt * dq_multi;
     const int bh = m % BHt, wg = m / BHt;
     int first = 0;  // item index of the group's chunk 0 (multi-chunk groups come first)
     for (int gg = 0; gg < wg; ++gg) first += dkdv_group_chunks(gg, pass, kv_chunk);
@@ -392,24 +400,9 @@ __global__ __launch_bounds__(256) void ca_bwd_gain_merge_kernel(
     }
     return;
   }
-  if (blockIdx.x < H) {
-    __shared__ float wsum[4];
-    const int h = blockIdx.x;
-    float acc = 0.f;
-    for (int b = 0; b < B; ++b)
-      for (int k = tid; k < n_items; k += 256) acc += gain_part[((size_t)b * H + h) * n_items + k];
-    acc = wave_sum(acc);
-    if ((tid & 63) == 0) wsum[tid >> 6] = acc;
-    __syncthreads();
-    if (tid == 0) {
-      const float part_sum = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
-      dlog_gain[h] = pass.first ? part_sum : dlog_gain[h] + part_sum;
-    }
-    return;
-  }
   constexpr int C4 = D / 4;
   const int BH = B * H;
-  const int m = blockIdx.x - H;
+  const int m = blockIdx.x;
   const int bh = m % BH, gi = m / BH;
   const int qg = pass.g1 - 1 - gi;
   int first = 0;  // item index of the group's chunk 0
@@ -444,23 +437,26 @@ hipError_t launch_bwd(const BwdIO& io, const BwdWork& ws, const BwdPass& pass, c
   timer_end(kBwdDkdv, stream);
   if (e != hipSuccess) return e;
   timer_begin(kBwdDq, stream);
+  // the dQ grid's H extra work groups sum the gain partials of the dK/dV items
+  const dim3 dq_grid(sp.items * BH + H);
   if (io.rope)
-    hipLaunchKernelGGL((ca_bwd_dq_kernel<D, E, true>), dim3(sp.items * BH), dim3(256), 0, stream,
-                       ws.dsbuf, io.q, io.k, io.rope, io.log_gain, io.dq, ws.dq_part, ws.gain_part,
-                       pass, BH, H, T, sp.chunk, sp.items, sp.part_items);
+    hipLaunchKernelGGL((ca_bwd_dq_kernel<D, E, true>), dq_grid, dim3(256), 0, stream, ws.dsbuf,
+                       io.k, io.rope, io.log_gain, io.dq, ws.dq_part, ws.gain_part, io.dlog_gain,
+                       pass, B, H, T, sp.chunk, sp.items, sp.part_items, kvs.items);
   else
-    hipLaunchKernelGGL((ca_bwd_dq_kernel<D, E, false>), dim3(sp.items * BH), dim3(256), 0, stream,
-                       ws.dsbuf, io.q, io.k, io.rope, io.log_gain, io.dq, ws.dq_part, ws.gain_part,
-                       pass, BH, H, T, sp.chunk, sp.items, sp.part_items);
+    hipLaunchKernelGGL((ca_bwd_dq_kernel<D, E, false>), dq_grid, dim3(256), 0, stream, ws.dsbuf,
+                       io.k, io.rope, io.log_gain, io.dq, ws.dq_part, ws.gain_part, io.dlog_gain,
+                       pass, B, H, T, sp.chunk, sp.items, sp.part_items, kvs.items);
   timer_end(kBwdDq, stream);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
+  // chunk partials (small grids only) are merged by a launch of their own
+  const int merges = BH * sp.multi_groups + BH * kvs.multi_groups;
+  if (merges == 0) return hipSuccess;
   timer_begin(kBwdGain, stream);
-  hipLaunchKernelGGL((ca_bwd_gain_merge_kernel<D, E>),
-                     dim3(H + BH * sp.multi_groups + BH * kvs.multi_groups), dim3(256), 0, stream,
-                     ws.gain_part, ws.dq_part, ws.kv_part, io.rope, io.dlog_gain, io.dq, io.dk, io.dv,
-                     pass, B, H, T, sp.chunk, sp.items, sp.part_items, sp.multi_groups, kvs.chunk,
-                     kvs.part_items);
+  hipLaunchKernelGGL((ca_bwd_merge_kernel<D, E>), dim3(merges), dim3(256), 0, stream, ws.dq_part,
+                     ws.kv_part, io.rope, io.dq, io.dk, io.dv, pass, B, H, T, sp.chunk,
+                     sp.part_items, sp.multi_groups, kvs.chunk, kvs.part_items);
   timer_end(kBwdGain, stream);
   return hipGetLastError();
 }

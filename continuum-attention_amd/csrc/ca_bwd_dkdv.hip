@@ -37,8 +37,8 @@ template <int D, class E>
 __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
     View Kv, View Vv, const float* __restrict__ rope, const __bf16* __restrict__ limbs,
     const float* __restrict__ qstat, const float* __restrict__ log_gain, View dKv, View dVv,
-    float* __restrict__ dsbuf, float* __restrict__ kv_part, BwdPass pass, int BH, int H, int T,
-    int chunk, int n_part) {
+    float* __restrict__ dsbuf, float* __restrict__ kv_part, float* __restrict__ gain_part,
+    BwdPass pass, int BH, int H, int T, int chunk, int n_items, int n_part) {
   using P = Bwd<D>;
   __shared__ __attribute__((aligned(16))) __bf16 tiles[2][P::TILE];
   __shared__ f32x4 tstat[2][16];  // rows 2u, 2u+1: (m, Dl/Z, m, Dl/Z)
@@ -326,8 +326,41 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
 
   // ---- epilogue: lane (slot j, group g) holds d = 16mb + 4g + r of its key ----
   // A single-chunk group writes dK/dV; the chunks of a longer group write
-  // partials [key of the group][dV, dK][D] that ca_bwd_gain_merge sums.
-  if (j >= 1 && j <= kBwdKeys && key_j < T && kb16 < nkb) {
+  // partials [key of the group][dV, dK][D] that ca_bwd_merge sums.
+  // Each item also writes its part of the gain gradient
+  //   dlog_gain = sum_ij dS_ij s_ij = sum_j k_j . dK_j = sum_j (k_j - k_0) . dK_j
+  // (the last because sum_j dK_j = c sum_i q_i sum_j dS_ij = 0: every row of
+  // dS sums to zero), with k_0 the slice's first key: near-duplicate keys
+  // then contribute small differences instead of cancelling terms.
+  float gsum = 0.f;
+  const bool owned_key = j >= 1 && j <= kBwdKeys && key_j < T && kb16 < nkb;
+  if (owned_key) {
+    const float ck = cl2 * kLn2;
+    const E* k0 = view_slice<const E>(Kv, bh, H);
+    const E* kj = k0 + (long long)key_j * Kv.rstride;
+#pragma unroll
+    for (int mb = 0; mb < P::NMB; ++mb) {
+      const int d0 = 16 * mb + 4 * g;
+      if (d0 < D) {
+        f32x4 a = ld4(kj + d0), b = ld4(k0 + d0);
+        if (rope) {
+          a = rope4(a, rope_entry(rope, key_j, D, d0), false);
+          b = rope4(b, rope_entry(rope, 0, D, d0), false);
+        }
+        const f32x4 dk = acck[mb] * ck;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) gsum = fmaf(a[r] - b[r], dk[r], gsum);
+      }
+    }
+  }
+  {
+    __shared__ float gred[kDkdvWaves];
+    gsum = wave_sum(gsum);
+    if (lane == 0) gred[wv] = gsum;
+    __syncthreads();
+    if (tid == 0) gain_part[(size_t)bh * n_items + item] = (gred[0] + gred[1]) + (gred[2] + gred[3]);
+  }
+  if (owned_key) {
     const float ck = cl2 * kLn2;
     if (nch == 1) {
       // dK rotated back by the transposed RoPE (the gradient of the un-rotated
@@ -370,7 +403,8 @@ hipError_t launch_bwd_dkdv(const BwdIO& io, const BwdWork& ws, const BwdPass& pa
                            const DkdvSplit& kvs, int BH, int H, int T, hipStream_t stream) {
   hipLaunchKernelGGL((ca_bwd_dkdv_kernel<D, E>), dim3(kvs.items * BH), dim3(256), 0, stream, io.k,
                      io.v, io.rope, ws.limbs, ws.qstat, io.log_gain, io.dk, io.dv, ws.dsbuf,
-                     ws.kv_part, pass, BH, H, T, kvs.chunk, kvs.part_items);
+                     ws.kv_part, ws.gain_part, pass, BH, H, T, kvs.chunk, kvs.items,
+                     kvs.part_items);
   return hipGetLastError();
 }
 

@@ -242,8 +242,8 @@ int ca_bf16_shadow(const ca_opt_tensor* tensors, int ntensors, const int* chunks
 /* ---- Diagnostics (no counterpart in the reference; used by bench.py) -------
  * Per-kernel timing with HIP events recorded on the launch stream around each
  * kernel launch of the calls above.  Kernel ids: 0 forward, 1 forward split
- * combine, 2 backward prep, 3 backward dK/dV, 4 backward dQ, 5 backward
- * gain / partial merge, 6 weights, 7 weights backward, 8 RMSNorm forward,
+ * combine, 2 backward prep, 3 backward dK/dV, 4 backward dQ (with the gain
+ * sum), 5 backward chunk-partial merge, 6 weights, 7 weights backward, 8 RMSNorm forward,
  * 9 RMSNorm backward, 10 SwiGLU forward, 11 SwiGLU backward.
  * ca_timing_enable(on) turns recording on/off and discards
  * unread records; ca_timing_read waits for the recorded events and returns the
