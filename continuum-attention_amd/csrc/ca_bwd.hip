@@ -10,7 +10,7 @@
 //   ca_bwd_prep     per query row: Dl_i = dY_i . y_i (the reference forms the
 //                   same row mean at cuda/continuum_attention.py:268-269),
 //                   Q_i and dY_i / Z_i split into bf16 limb planes, and
-//                   (m_i, Dl_i / Z_i).
+//                   (-m_i, -Dl_i / Z_i).
 //   ca_bwd_dkdv     (ca_bwd_dkdv.hip) one work group per (slice, 56 keys); wave w owns 14 keys
 //                   (16 MFMA slots).  The 4 waves walk the query tiles
 //                   together: each 32-query tile of Q and dY/Z limbs is staged
@@ -102,8 +102,9 @@ __global__ __launch_bounds__(256) void ca_bwd_prep_kernel(View Qv, const float* 
   put(0, qq, 1.0f);
   put(3, dy, invz);
   if (c == 0) {
-    qstat[(size_t)row * 2 + 0] = m;
-    qstat[(size_t)row * 2 + 1] = x * invz;
+    // negated: the dK/dV kernel starts its S and dP' accumulators from them
+    qstat[(size_t)row * 2 + 0] = -m;
+    qstat[(size_t)row * 2 + 1] = -(x * invz);
   }
 }
 

@@ -41,7 +41,9 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
     BwdPass pass, int BH, int H, int T, int chunk, int n_items, int n_part) {
   using P = Bwd<D>;
   __shared__ __attribute__((aligned(16))) __bf16 tiles[2][P::TILE];
-  __shared__ f32x4 tstat[2][16];  // rows 2u, 2u+1: (m, Dl/Z, m, Dl/Z)
+  // per staged row: -m (tstat[b][0][row]) and -Dl/Z (tstat[b][1][row]), in
+  // the order of the S / dP' accumulator registers
+  __shared__ __attribute__((aligned(16))) float tstat[2][2][32];
 
   const int nkb = bwd_num_key_blocks(T);
   const int bh = blockIdx.x % BH;
@@ -157,7 +159,10 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
         *reinterpret_cast<u32x4*>(&tiles[buf][pl * P::LIMB + row * P::LDR + 8 * ch]) = pre[u];
       }
     }
-    if (tid < 16) tstat[buf][tid] = pre_st;
+    if (tid < 16) {
+      *reinterpret_cast<f32x2*>(&tstat[buf][0][2 * tid]) = f32x2{pre_st[0], pre_st[2]};
+      *reinterpret_cast<f32x2*>(&tstat[buf][1][2 * tid]) = f32x2{pre_st[1], pre_st[3]};
+    }
   };
 
   // query tiles of this item: a chunk of the pass's tiles that see an owned
@@ -190,9 +195,8 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
       f32x4 sacc[2], pacc[2];
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb) {
-        const f32x4 s01 = tstat[buf][8 * rb + 2 * g], s23 = tstat[buf][8 * rb + 2 * g + 1];
-        sacc[rb] = f32x4{-s01[0], -s01[2], -s23[0], -s23[2]};
-        pacc[rb] = f32x4{-s01[1], -s01[3], -s23[1], -s23[3]};
+        sacc[rb] = *reinterpret_cast<const f32x4*>(&tstat[buf][0][16 * rb + 4 * g]);
+        pacc[rb] = *reinterpret_cast<const f32x4*>(&tstat[buf][1][16 * rb + 4 * g]);
       }
       prio_mfma_begin();
 #pragma unroll

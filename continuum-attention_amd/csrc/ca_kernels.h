@@ -358,7 +358,7 @@ hipError_t launch_fwd(const FwdIO& io, float* part, int B, int H, int T, int C,
 struct BwdWork {
   float* dsbuf;       // dS spill, 32x16 blocks
   __bf16* limbs;      // six bf16 planes [BH][pass rows][D]: Q limbs h, m, l; dY/Z limbs h, m, l
-  float* qstat;       // per query row of the pass: (m, D/Z)
+  float* qstat;       // per query row of the pass: (-m, -D/Z)
   float* gain_part;   // per dQ item
   float* dq_part;     // dQ chunk partials
   float* kv_part;     // dK/dV chunk partials: [BH][part item][kDkdvKeys][2][D]
