@@ -149,7 +149,7 @@ BwdLayout bwd_layout(int B, int H, int T, int D, const ca::BwdPass& p) {
   const ca::DkdvSplit kvs = dkdv_split_for(BH, D, p, true);
   BwdLayout L;
   L.ds = 0;
-  L.limbs = align256((size_t)BH * p.ds_slice * ca::kDsBlockFloats * sizeof(float));
+  L.limbs = align256((size_t)BH * p.ds_slice * sizeof(float));
   L.qstat = L.limbs + align256(ca::bwd_limb_elems(BH, p.rows, D) * sizeof(uint16_t));
   L.gain = L.qstat + align256((size_t)BH * p.rows * 2 * sizeof(float));
   L.dqpart = L.gain + align256((size_t)BH * kvs.items * sizeof(float));

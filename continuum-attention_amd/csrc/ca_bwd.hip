@@ -19,13 +19,14 @@
 //                   (dV^T += (dY/Z)^T W, dK^T += Q^T dS) with
 //                   ds_read_b64_tr_b16.  K and V of the wave's slots stay in
 //                   registers as bf16 limbs for the whole launch.  All four
-//                   products are bf16x6 on v_mfma_f32_16x16x32_bf16.  dS is
-//                   also spilled as 32x16 row blocks for the dQ pass.
+//                   products are bf16x6 on v_mfma_f32_16x16x32_bf16.  dS of
+//                   the owned keys is also spilled, one 32-query column per
+//                   (query tile, key), for the dQ pass.
 //                   Each item also forms its gain partial
 //                   sum_j (k_j - k_0) . dK_j (= sum_ij dS_ij s_ij, since
 //                   s_ij = c q_i . k_j and every row of dS sums to zero).
-//   ca_bwd_dq       dQ = c dS (K - k_ref) over the spilled blocks, one work
-//                   item per (slice, 128 queries, chunk of key blocks); H
+//   ca_bwd_dq       dQ = c dS (K - k_ref) over the spilled rows, one work
+//                   item per (slice, 128 queries, chunk of 32-key stages); H
 //                   extra work groups sum the gain partials into dRho_h.
 //   ca_bwd_merge    sums the dQ and dK/dV chunk partials of split groups
 //                   (launched only when a split leaves some).
@@ -108,18 +109,20 @@ __global__ __launch_bounds__(256) void ca_bwd_prep_kernel(View Qv, const float* 
   }
 }
 
-// dQ = c dS (K - k_ref) over the 32x16 dS blocks written by ca_bwd_dkdv, as
-// bf16x6 products on v_mfma_f32_16x16x32_bf16 (k = 32 slots = a pair of key
-// blocks).  Work item: one chunk of the key blocks of a 128-query group (four
-// 32-query tiles, one per wave) of one slice.  Per stage the K rows of one
-// block pair (slots 14kb-1 .. 14kb+14 of each block) are staged in LDS
-// (double-buffered) as row-major bf16 limb planes [slot][d], relative to
+// dQ = c dS (K - k_ref) over the dS columns spilled by ca_bwd_dkdv, as bf16x6
+// products on v_mfma_f32_16x16x32_bf16 (k = one stage of 32 consecutive
+// keys).  Work item: one chunk of the key stages of a 128-query group (four
+// 32-query tiles, one per wave) of one slice; the wave of tile qt takes the
+// chunk's stages up to qt.  Per stage the 32 K rows are staged in LDS
+// (double-buffered) as row-major bf16 limb planes [key][d], relative to
 // k_ref, and shared by the four waves.  A operand: lane (query 16rb + l%16,
-// group g) holds dS of block g/2 of the pair, slots 8(g%2) .. +7, split into
-// limbs in registers; B operand: lane (d = 16nb + l%16, g) gets the same 8
-// slots of column d through two transposed reads.  Halo slots and invisible
-// keys carry dS = 0, so no masks are needed.  A single-chunk group writes dQ;
-// the chunks of a longer group write partial tiles that ca_bwd_merge sums.
+// group g) holds dS of keys 8g .. 8g+7 of the stage (gathered from their
+// spilled key columns), split into limbs in registers;
+// B operand: lane (d = 16nb + l%16, g) gets the same 8 keys of column d
+// through two transposed reads.  Invisible keys carry dS = 0 in the spill and keys past T
+// are zeroed at load, so no other masks are needed.  A single-chunk group
+// writes dQ; the chunks of a longer group write partial tiles that
+// ca_bwd_merge sums.
 // Gain gradient: dlog_gain[h] = the fixed-order sum over batch and dK/dV
 // items of the partials the dK/dV kernel wrote (added to the earlier passes'
 // sum after the first pass).  Launched as H extra work groups of the dQ grid.
@@ -144,10 +147,10 @@ template <int D>
 struct DqP {
   static constexpr int NB = (D + 15) / 16;            // 16-column d blocks of dQ
   static constexpr int C4 = D / 4;
-  static constexpr int UNITS = 2 * kBwdSlots * C4;    // (slot of the pair, float4) per stage
+  static constexpr int UNITS = 32 * C4;               // (key of the stage, float4) per stage
   static constexpr int UPT = (UNITS + 255) / 256;
   static constexpr int LDK = NB * 16 + 16;            // bf16 row stride (160 bytes for D = 64)
-  static constexpr int PLANE = 2 * kBwdSlots * LDK;   // bf16 per limb plane of a stage
+  static constexpr int PLANE = 32 * LDK;              // bf16 per limb plane of a stage
   static constexpr int STAGE = 3 * PLANE;
 };
 
@@ -168,7 +171,6 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   }
   __shared__ __attribute__((aligned(16))) __bf16 kst[2 * P::STAGE];
   const int nqt = num_q_tiles(T);
-  const int nkb = bwd_num_key_blocks(T);
   const int bh = blockIdx.x % BH;
   const int item = blockIdx.x / BH;
   // item -> (group, chunk), heaviest groups of the pass first
@@ -178,22 +180,21 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
     --qg;
     nch = dq_group_chunks(qg, T, chunk);
   }
-  const int gblocks = dq_group_blocks(qg, T);
-  const int clen = (gblocks + nch - 1) / nch;
-  const int kb_lo = ch * clen;
-  const int kb_hi = min(kb_lo + clen, gblocks);
+  const int gstages = dq_group_stages(qg, T);
+  const int clen = (gstages + nch - 1) / nch;
+  const int st_lo = ch * clen;
+  const int st_hi = min(st_lo + clen, gstages);
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
   const int qt = kDqTiles * qg + w;
   const bool wave_on = qt < nqt;
   const float c = head_scale_log2(log_gain, bh % H, D) * kLn2;
-  // key blocks of this chunk met by the wave's tile
-  const int my_end = wave_on ? min(min(ds_kb_count(qt), nkb), kb_hi) : 0;
-  const int iters = kb_hi > kb_lo ? (kb_hi - kb_lo + 1) / 2 : 0;
-  // dS of this lane: rows 16rb + l16 of the wave's tile, slots 8(g&1)..+7 of block g>>1 of a pair
-  const float* arow = dsbuf +
-                      ((size_t)bh * pass.ds_slice + (ds_blocks_before(wave_on ? qt : pass.qa) - pass.ds0)) *
-                          kDsBlockFloats +
-                      l16 * kBwdSlots + 8 * (g & 1);
+  // stages of this chunk met by the wave's tile (stage s holds keys 32s .. 32s+31)
+  const int my_end = wave_on ? min(qt + 1, st_hi) : 0;
+  const int iters = st_hi > st_lo ? st_hi - st_lo : 0;
+  // dS of this lane: rows 16rb + l16 of the wave's tile, keys 32s + 8g .. +7
+  // (one dword of each key's column)
+  const float* arow = dsbuf + (size_t)bh * pass.ds_slice +
+                      (ds_floats_before(wave_on ? qt : pass.qa) - pass.ds0) + l16;
 
   f32x4 acc[2][P::NB];
 #pragma unroll
@@ -206,11 +207,10 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   // keys are taken relative to the key at the group's first query: when
   // neighbouring keys nearly coincide the products stay small instead of
   // cancelling (|k| ~ 1 against |k_j - k_ref| ~ 1e-2 in the near-duplicate-key
-  // case), and the gain partial sum_i q_i . dQ_i inherits the same accuracy.
-  // All chunks of a group use the same k_ref, so the k_ref terms cancel in the
-  // sum of the chunk partials.
-  // Staging unit u: slot u / C4 of the pair (block = slot / 16), d = 4(u % C4)..+3;
-  // a thread's units all have d chunk tid % C4, since 256 % C4 == 0.
+  // case).  All chunks of a group use the same k_ref, so the k_ref terms
+  // cancel in the sum of the chunk partials.
+  // Staging unit u: slot (key of the stage) u / C4, d = 4(u % C4)..+3; a
+  // thread's units all have d chunk tid % C4, since 256 % C4 == 0.
   // rows of K (RoPE applied when `rope`): loaded raw a stage ahead and
   // converted, rotated and shifted when stored
   if (!ROPE) rope = nullptr;  // lets the compiler drop every rotation
@@ -224,10 +224,7 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   R4 pre[P::UPT];
   f32x4 pre_cs[ROPE ? P::UPT : 1];
   const f32x4 kref = k_row4(kDqRows * qg, 4 * (tid % P::C4));
-  auto unit_key = [&](int u, int it) {
-    const int s = u / P::C4;
-    return kBwdKeys * (kb_lo + 2 * it + s / kBwdSlots) - 1 + s % kBwdSlots;
-  };
+  auto unit_key = [&](int u, int it) { return 32 * (st_lo + it) + u / P::C4; };
   auto load_k = [&](int it) {
 #pragma unroll
     for (int uu = 0; uu < P::UPT; ++uu) {
@@ -246,8 +243,8 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
     }
   };
   // The shift is applied when the prefetched rows are stored, so the loads
-  // issued a stage ahead are not waited for inside the MFMA loop.  Slots of
-  // keys outside [0, T) stay 0 (their dS is 0 too).
+  // issued a stage ahead are not waited for inside the MFMA loop.  Rows of
+  // keys at or past T stay 0.
   auto store_k = [&](int buf, int it) {
 #pragma unroll
     for (int uu = 0; uu < P::UPT; ++uu) {
@@ -267,19 +264,23 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
       }
     }
   };
-  // dS of the lane for stage it (blocks kb_lo + 2it, +1), both row blocks
+  // dS of the lane for stage st_lo + it (called only for stages below
+  // my_end), both row blocks: for each of its 8 keys one dword per row block,
+  // where the 16 lanes of a group read 64 contiguous bytes of the key's
+  // column.  Keys at or past T (in the stage that holds T) have no spill
+  // entry: they read as 0.
   auto load_a = [&](int it, float (&a)[2][8]) {
-    const int kbm = kb_lo + 2 * it + (g >> 1);
-    const bool ok = kbm < my_end;
+    const int k0 = 32 * (st_lo + it) + 8 * g;
+    const float* src = arow + (size_t)k0 * kDsColFloats;
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      const f32x4* src = reinterpret_cast<const f32x4*>(arow + (size_t)(ok ? kbm : 0) * kDsBlockFloats + 16 * rb * kBwdSlots);
+    for (int e = 0; e < 8; ++e)
 #pragma unroll
-      for (int c4 = 0; c4 < 2; ++c4) {
-        const f32x4 v4 = ok ? src[c4] : f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int rb = 0; rb < 2; ++rb) a[rb][e] = src[e * kDsColFloats + 16 * rb];
+    if (k0 + 8 > T) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) a[rb][4 * c4 + e] = v4[e];
-      }
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[rb][e] = k0 + e < T ? a[rb][e] : 0.f;
     }
   };
 
@@ -289,23 +290,23 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
     __syncthreads();
   }
   float a_next[2][8];
-  if (kb_lo < my_end) load_a(0, a_next);
+  if (st_lo < my_end) load_a(0, a_next);
   load_k(0);
   store_k(0, 0);
   __syncthreads();
-  // transposed reads: source lane 4j + m of group g points at slot
-  // 16(g/2) + 8(g%2) + j (+4 for the second read) of the pair, column 16nb + 4m
+  // transposed reads: source lane 4j + m of group g points at key 8g + j
+  // (+4 for the second read) of the stage, column 16nb + 4m
   const int srow = 8 * g + (l16 >> 2);
   for (int it = 0; it < iters; ++it) {
     const int buf = it & 1;
     if (it + 1 < iters) load_k(it + 1);
-    if (kb_lo + 2 * it < my_end) {
+    if (st_lo + it < my_end) {
       float a[2][8];
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
         for (int e = 0; e < 8; ++e) a[rb][e] = a_next[rb][e];
-      if (kb_lo + 2 * (it + 1) < my_end) load_a(it + 1, a_next);
+      if (st_lo + it + 1 < my_end) load_a(it + 1, a_next);
       const Limbs al0 = split8(a[0]), al1 = split8(a[1]);
       const __bf16* kb_base = kst + buf * P::STAGE;
 #pragma unroll

@@ -171,9 +171,11 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
   const int clen = (ntl + nch - 1) / nch;
   const int qt0 = dkdv_group_first_tile(wg, pass) + ch * clen;
   const int qt_end = min(qt0 + clen, pass.qb);
-  // dS block of (tile qt, this wave's block) in the pass's spill; advanced by
-  // ds_kb_count(qt) per tile
-  size_t ds_blk = (size_t)bh * pass.ds_slice + (ds_blocks_before(qt0) - pass.ds0) + kb16;
+  // this lane's spilled dS column in tile qt: owned slots 1 .. 14 hold keys
+  // 14 kb16 .. +13; tile qt's columns start at ds_tile, advanced per tile
+  size_t ds_tile = (size_t)bh * pass.ds_slice + (ds_floats_before(qt0) - pass.ds0);
+  const int ds_key = kBwdKeys * kb16 + j - 1;
+  const bool ds_lane = j >= 1 && j <= kBwdKeys;
   __syncthreads();          // LDS clear before the first store
   if (qt0 < qt_end) {
     load_tile(qt0);
@@ -268,12 +270,10 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
               w += cap;
               ds = fmaf(cap, gg, ds);
             }
-            // Slots 0 and 15 are not owned: their w only reaches output
-            // columns that are never stored, but their dS must be 0 in the
-            // spill that the dQ pass reads.
-            const bool owned = j >= 1 && j <= kBwdKeys;
+            // Slots 0 and 15 are not owned: their w and dS only reach dV / dK
+            // columns that are never stored, and they are not spilled.
             wout[rb][r] = w;
-            dout_s[rb][r] = owned ? ds : 0.f;
+            dout_s[rb][r] = ds;
           }
         }
       };
@@ -282,13 +282,13 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
       else
         segments(std::false_type{});
 
-      // ---- dS block (query tile qt, key block kb16) for the dQ pass ----
-      {
-        float* dst = dsbuf + ds_blk * kDsBlockFloats;
+      // ---- dS of (query tile qt, the block's keys) for the dQ pass ----
+      if (ds_lane) {
+        float* col = dsbuf + ds_tile + (size_t)ds_key * kDsColFloats + 4 * g;
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) dst[(16 * rb + 4 * g + r) * kBwdSlots + j] = dout_s[rb][r];
+          *reinterpret_cast<f32x4*>(col + 16 * rb) =
+              f32x4{dout_s[rb][0], dout_s[rb][1], dout_s[rb][2], dout_s[rb][3]};
       }
 
       // ---- dV^T += (dY/Z)^T w and dK^T += Q^T dS ----
@@ -323,7 +323,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
       }
       prio_mfma_end();
     }
-    ds_blk += ds_kb_count(qt);
+    ds_tile += (size_t)kDsColFloats * kBwdKeys * ds_kb_count(qt);
     if (qt + 1 < qt_end) store_tile(buf ^ 1);
     __syncthreads();
   }

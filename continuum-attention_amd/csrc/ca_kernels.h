@@ -84,16 +84,20 @@ __host__ __device__ inline long long floor_sum(long long n, long long m, long lo
   return ans;
 }
 
-// dS blocks for the dQ pass: one 32-query x 16-slot block (row-major) for
-// every query tile qt and key block kb that meets it (14*kb <= 32*qt + 31).
-// Blocks are stored qt-major, kb ascending, so a dQ work group reads its rows
-// contiguously.  Blocks past the last key block are counted but never touched.
-constexpr int kDsBlockFloats = 32 * kBwdSlots;
+// dS spill for the dQ pass, key-major: for every query tile qt the keys of
+// the dK/dV key blocks that meet it (keys 0 .. 14 ds_kb_count(qt) - 1), each
+// as one column of 32 floats (dS of the tile's 32 queries, 128 bytes), tiles
+// in order.  Invisible keys hold 0; keys past T are never written.  Each key
+// column is written by the four lanes of one dK/dV wave that own the key, as
+// two 16-byte stores each, so every 128-byte line is written whole by one
+// wave; no key is stored twice (the halo slots are not spilled).  The dQ pass
+// gathers 8-key runs of one query from 8 columns (one dword per key).
+constexpr int kDsColFloats = 32;
 __host__ __device__ inline int ds_kb_count(int qt) { return (32 * qt + 31) / kBwdKeys + 1; }
-__host__ __device__ inline long long ds_blocks_before(int qt) {
-  return qt <= 0 ? 0 : qt + floor_sum(qt, kBwdKeys, 32, 31);
+// floats of the columns of tiles 0 .. qt-1: 32 * 14 * sum of ds_kb_count(t)
+__host__ __device__ inline long long ds_floats_before(int qt) {
+  return qt <= 0 ? 0 : (long long)kDsColFloats * kBwdKeys * (qt + floor_sum(qt, kBwdKeys, 32, 31));
 }
-
 
 // Backward passes.  The backward's workspace (dS spill, limb planes, row
 // statistics, partials) grows with the query rows it holds, the dS spill as
@@ -109,8 +113,8 @@ struct BwdPass {
   int g0, g1;         // dQ groups of the pass
   int qa, qb;         // query tiles
   int row0, rows;     // first query row, and rows per slice held in the limb planes
-  long long ds0;      // dS blocks per slice before tile qa
-  long long ds_slice; // dS blocks per slice in this pass
+  long long ds0;      // dS floats per slice before tile qa
+  long long ds_slice; // dS floats per slice in this pass
   int kv_groups;      // dK/dV key groups that meet the pass's tiles (wg < kv_groups)
   int first;          // 1 for the first pass (dlog_gain written, not added)
 };
@@ -124,8 +128,8 @@ __host__ __device__ inline BwdPass bwd_pass(int T, int g0, int g1) {
   p.row0 = 32 * p.qa;
   const int row1 = 32 * p.qb < T ? 32 * p.qb : T;
   p.rows = row1 - p.row0;
-  p.ds0 = ds_blocks_before(p.qa);
-  p.ds_slice = ds_blocks_before(p.qb) - p.ds0;
+  p.ds0 = ds_floats_before(p.qa);
+  p.ds_slice = ds_floats_before(p.qb) - p.ds0;
   const int nkb = bwd_num_key_blocks(T);
   const int ngroups = (nkb + 3) / 4;
   // key group wg (keys 56 wg ..) first meets tile 56 wg / 32; it meets this
@@ -137,27 +141,27 @@ __host__ __device__ inline BwdPass bwd_pass(int T, int g0, int g1) {
 }
 
 // dQ work items: a 128-query group of one slice and one chunk of its key
-// blocks.  A group of n blocks is cut into ceil(n / chunk) near-equal chunks
-// (split-K) when the unsplit grid would not fill the GPU for one round, so
-// that the longest rows do not leave it waiting on a few work groups; with a
-// full grid every group is one item (chunk >= bwd_num_key_blocks).  Items are
-// numbered per slice from the last (heaviest) group of the pass down, so the
-// chunks of multi-chunk groups come first; those items write partial dQ tiles
-// that a second kernel sums in chunk order.
-constexpr int kDqChunkBlocks = 64;       // split chunk length in key blocks (about 900 keys)
-constexpr int kDqChunkBlocksShort = 48;  // when 64-block chunks still leave the GPU short of a round
-// key blocks met by the last query tile of group qg (the group's key range)
-__host__ __device__ inline int dq_group_blocks(int qg, int T) {
+// stages (32 keys each; the group's last tile qt needs stages 0 .. qt).  A
+// group of n stages is cut into ceil(n / chunk) near-equal chunks (split-K)
+// when the unsplit grid would not fill the GPU for one round, so that the
+// longest rows do not leave it waiting on a few work groups; with a full grid
+// every group is one item (chunk >= num_q_tiles).  Items are numbered per
+// slice from the last (heaviest) group of the pass down, so the chunks of
+// multi-chunk groups come first; those items write partial dQ tiles that a
+// second kernel sums in chunk order.
+constexpr int kDqChunkStages = 28;       // split chunk length in 32-key stages (896 keys)
+constexpr int kDqChunkStagesShort = 21;  // when 28-stage chunks still leave the GPU short of a round
+// key stages of group qg (those met by its last query tile)
+__host__ __device__ inline int dq_group_stages(int qg, int T) {
   const int nqt = num_q_tiles(T);
   const int last = kDqTiles * qg + kDqTiles - 1 < nqt ? kDqTiles * qg + kDqTiles - 1 : nqt - 1;
-  const int c = ds_kb_count(last), nkb = bwd_num_key_blocks(T);
-  return c < nkb ? c : nkb;
+  return last + 1;
 }
 __host__ __device__ inline int dq_group_chunks(int qg, int T, int chunk) {
-  return (dq_group_blocks(qg, T) + chunk - 1) / chunk;
+  return (dq_group_stages(qg, T) + chunk - 1) / chunk;
 }
 struct DqSplit {
-  int chunk;         // key blocks per chunk (upper bound)
+  int chunk;         // key stages per chunk (upper bound)
   int items;         // work items per slice
   int part_items;    // of which write partial tiles (chunks of multi-chunk groups)
   int multi_groups;  // groups with more than one chunk (the last ones)
@@ -180,13 +184,13 @@ inline DqSplit dq_split_chunk(int T, const BwdPass& p, int chunk) {
 // Shorter chunks while the grid would fill less than half a round (few
 // slices, short rows): more dQ work groups, at the price of more partials to
 // merge, which outweighs the gain once half a round is filled.
-constexpr int kDqChunkSmall[] = {32, 24, 16};
+constexpr int kDqChunkSmall[] = {14, 10, 7};
 inline DqSplit dq_split(int BH, int T, const BwdPass& p, int resident_groups) {
   if ((long long)(p.g1 - p.g0) * BH >= resident_groups)
-    return dq_split_chunk(T, p, bwd_num_key_blocks(T));
-  DqSplit s = dq_split_chunk(T, p, kDqChunkBlocks);
+    return dq_split_chunk(T, p, num_q_tiles(T));
+  DqSplit s = dq_split_chunk(T, p, kDqChunkStages);
   if ((long long)s.items * BH >= resident_groups) return s;
-  s = dq_split_chunk(T, p, kDqChunkBlocksShort);
+  s = dq_split_chunk(T, p, kDqChunkStagesShort);
   for (int c : kDqChunkSmall) {
     if (2LL * s.items * BH >= resident_groups) break;
     s = dq_split_chunk(T, p, c);
@@ -194,8 +198,8 @@ inline DqSplit dq_split(int BH, int T, const BwdPass& p, int resident_groups) {
   return s;
 }
 // dQ work groups per CU the split heuristic counts as resident: 3, although
-// the D = 64 kernel's 126 VGPRs allow 4 (counting 4 picks 48-block chunks at
-// [2,16,2048,64] and measured 4% slower)
+// the D = 64 kernel's 124 VGPRs allow 4 (counting 4 picks shorter chunks at
+// [2,16,2048,64], measured 4% slower)
 constexpr int kDqGroupsPerCu = 3;
 
 // dK/dV work items: key-block group wg (kDkdvWaves blocks, kDkdvKeys keys) of
