@@ -527,38 +527,49 @@ def train_step(model, optimizer, batch, amp_dtype=torch.bfloat16, grad_clip=1.0)
     return loss.detach()
 
 
-# torch's embedding backward sums rows without sorting for at most this many
-# indices; above it (and always with scale_grad_by_freq) it sorts and runs
-# rocprim's partition, which records a hipMemsetAsync of its selected counters
-# into a captured graph.  Replays do not reliably redo such memset nodes; with
-# stale counters the partition writes past its output buffer.
-_GRAPH_SAFE_EMBEDDING_INDICES = 3072
+# HIP graph node type of a memset (hipGraphNodeTypeMemset) and of a child
+# graph (hipGraphNodeTypeGraph), hip_runtime_api.h.
+_HIP_NODE_MEMSET, _HIP_NODE_GRAPH = 2, 4
 
 
-@contextlib.contextmanager
-def _embedding_graph_guard(model):
-    """Raises ValueError from the forward of any trainable nn.Embedding of
-    ``model`` whose backward would take torch's sorting path."""
+def _hip_graph_memset_nodes(graph: "torch.cuda.CUDAGraph") -> int:
+    """Memset nodes of a captured HIP graph kept by torch (keep_graph=True),
+    child graphs included.  Queried through the HIP runtime torch loaded
+    (soname libamdhip64.so.7, so dlopen returns that same library)."""
+    import ctypes
 
-    def check(name):
-        def hook(mod, args):
-            ids = args[0]
-            if mod.weight.requires_grad and not mod.sparse and (
-                    ids.numel() > _GRAPH_SAFE_EMBEDDING_INDICES or mod.scale_grad_by_freq):
-                raise ValueError(
-                    f"GraphedTrainStep: embedding '{name}' looks up {ids.numel()} indices; the "
-                    f"backward of more than {_GRAPH_SAFE_EMBEDDING_INDICES} (or with "
-                    "scale_grad_by_freq) records a memset node that graph replays do not "
-                    "reliably redo; train this model with the eager step")
-        return hook
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    get_nodes, get_type = hip.hipGraphGetNodes, hip.hipGraphNodeGetType
+    get_child = hip.hipGraphChildGraphNodeGetGraph
+    get_nodes.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p),
+                          ctypes.POINTER(ctypes.c_size_t)]
+    get_type.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int)]
+    get_child.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]
+    for f in (get_nodes, get_type, get_child):
+        f.restype = ctypes.c_int
 
-    handles = [m.register_forward_pre_hook(check(n)) for n, m in model.named_modules()
-               if isinstance(m, nn.Embedding)]
-    try:
-        yield
-    finally:
-        for h in handles:
-            h.remove()
+    def check(err, what):
+        if err != 0:
+            raise RuntimeError(f"GraphedTrainStep: {what} failed (hipError {err})")
+
+    def walk(g):
+        n = ctypes.c_size_t(0)
+        check(get_nodes(g, None, ctypes.byref(n)), "hipGraphGetNodes")
+        nodes = (ctypes.c_void_p * max(n.value, 1))()
+        check(get_nodes(g, nodes, ctypes.byref(n)), "hipGraphGetNodes")
+        count = 0
+        for k in range(n.value):
+            t = ctypes.c_int(-1)
+            check(get_type(nodes[k], ctypes.byref(t)), "hipGraphNodeGetType")
+            if t.value == _HIP_NODE_MEMSET:
+                count += 1
+            elif t.value == _HIP_NODE_GRAPH:
+                child = ctypes.c_void_p()
+                check(get_child(nodes[k], ctypes.byref(child)), "hipGraphChildGraphNodeGetGraph")
+                count += walk(child)
+        return count
+
+    return walk(ctypes.c_void_p(graph.raw_cuda_graph()))
 
 
 class GraphedTrainStep:
@@ -579,10 +590,12 @@ class GraphedTrainStep:
     are in memory, so in-place changes to them between steps are seen;
     hyper-parameters of the eager optimizer step can change freely.
 
-    Models whose nn.Embedding backward takes torch's sorting path (more than
-    3072 indices per lookup, or scale_grad_by_freq) are refused with
-    ValueError before capture: that path records a memset node that graph
-    replays do not reliably redo."""
+    A capture that recorded any memset node is refused with ValueError before
+    it is instantiated (nothing of it runs): graph replays on this platform do
+    not reliably redo memset nodes.  Library code records them by itself
+    (torch's sorting embedding backward, used above 3072 indices per lookup,
+    through rocprim's partition; reductions over many blocks), so the check
+    walks the captured graph rather than guessing which ops do."""
 
     def __init__(self, model, optimizer, batch, amp_dtype=torch.bfloat16, grad_clip=1.0, warmup=2,
                  loss_fn=None):
@@ -598,18 +611,22 @@ class GraphedTrainStep:
         side = torch.cuda.Stream(device=dev)
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side):
-            for i in range(max(warmup, 1)):
+            for _ in range(max(warmup, 1)):
                 optimizer.zero_grad(set_to_none=True)
-                if i == 0:
-                    with _embedding_graph_guard(model):
-                        self._forward_backward()
-                else:
-                    self._forward_backward()
+                self._forward_backward()
         torch.cuda.current_stream(dev).wait_stream(side)
         optimizer.zero_grad(set_to_none=True)
-        self.graph = torch.cuda.CUDAGraph()
+        self.graph = torch.cuda.CUDAGraph(keep_graph=True)
         with torch.cuda.graph(self.graph):
             self.static_loss = self._forward_backward()
+        memsets = _hip_graph_memset_nodes(self.graph)
+        if memsets:
+            self.graph.reset()
+            raise ValueError(
+                f"GraphedTrainStep: the captured forward/backward holds {memsets} memset "
+                "node(s), which graph replays do not reliably redo (e.g. torch's embedding "
+                "backward above 3072 indices per lookup); train this model with the eager step")
+        self.graph.instantiate()
 
     def _forward_backward(self):
         amp = (torch.autocast(device_type="cuda", dtype=self.amp_dtype, cache_enabled=False)
