@@ -101,7 +101,7 @@ int dq_resident_groups() {
 // Forced split lengths (ca_debug_set_splits; 0 = automatic).  When one is
 // set, the workspace sizes and the launches both use it, so the two agree.
 struct SplitOverride {
-  int fwd_tiles = 0, dq_blocks = 0, dkdv_tiles = 0;
+  int fwd_tiles = 0, dq_stages = 0, dkdv_tiles = 0;
 };
 SplitOverride g_split;
 
@@ -126,7 +126,7 @@ int fwd_split(int BH, int T, int D, bool for_sizing, size_t bytes = SIZE_MAX) {
   return cf > C ? cf : C;
 }
 ca::DqSplit dq_split_for(int BH, int T, int D, const ca::BwdPass& p, bool for_sizing) {
-  if (g_split.dq_blocks > 0) return ca::dq_split_chunk(T, p, g_split.dq_blocks);
+  if (g_split.dq_stages > 0) return ca::dq_split_chunk(T, p, g_split.dq_stages);
   // D = 128 kernels hold fewer dQ work groups per CU (two instead of three)
   const int res = for_sizing ? kDqSplitBound : (D > 64 ? dq_resident_groups() * 2 / 3 : dq_resident_groups());
   return ca::dq_split(BH, T, p, res);
@@ -289,11 +289,11 @@ int ca_timing_read(double* total_ms, int* launches, int n) {
 }
 
 
-int ca_debug_set_splits(int fwd_split_tiles, int dq_chunk_blocks, int dkdv_chunk_tiles) {
-  if (fwd_split_tiles < 0 || dq_chunk_blocks < 0 || dkdv_chunk_tiles < 0)
+int ca_debug_set_splits(int fwd_split_tiles, int dq_chunk_stages, int dkdv_chunk_tiles) {
+  if (fwd_split_tiles < 0 || dq_chunk_stages < 0 || dkdv_chunk_tiles < 0)
     return fail(CA_ERR_INVALID, "ca_debug_set_splits: lengths must be >= 0 (0 = automatic)");
   g_split.fwd_tiles = fwd_split_tiles;
-  g_split.dq_blocks = dq_chunk_blocks;
+  g_split.dq_stages = dq_chunk_stages;
   g_split.dkdv_tiles = dkdv_chunk_tiles;
   return CA_OK;
 }

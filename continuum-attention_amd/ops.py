@@ -92,13 +92,13 @@ def workspace_cap() -> int:
     return int(_native.load().ca_workspace_cap())
 
 
-def set_split_override(fwd_split_tiles: int = 0, dq_chunk_blocks: int = 0,
+def set_split_override(fwd_split_tiles: int = 0, dq_chunk_stages: int = 0,
                        dkdv_chunk_tiles: int = 0) -> None:
     """Forces the kernels' work-split lengths (0 = automatic; see
     ``ca_debug_set_splits`` in the C header).  For tests: the automatic
     choice depends on the device's CU count, so a forced length runs each one
     at a small shape.  Clears the cached workspace sizes, which follow it."""
-    _native.check(_native.load().ca_debug_set_splits(int(fwd_split_tiles), int(dq_chunk_blocks),
+    _native.check(_native.load().ca_debug_set_splits(int(fwd_split_tiles), int(dq_chunk_stages),
                                                      int(dkdv_chunk_tiles)))
     _fwd_workspace_bytes.cache_clear()
     _bwd_workspace_bytes.cache_clear()

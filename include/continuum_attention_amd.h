@@ -254,13 +254,13 @@ int ca_timing_read(double* total_ms, int* launches, int n);
 
 /* Forces the work-split lengths of ca_fwd_f32 / ca_bwd_f32 (0 = automatic,
  * the default): forward split length in 32-key tiles, dQ chunk length in
- * 14-key blocks, dK/dV chunk length in 32-query tiles.  While set, the
+ * 32-key stages, dK/dV chunk length in 32-query tiles.  While set, the
  * workspace-size functions return the sizes for the forced lengths, so size
  * queries and calls must see the same setting.  Process-wide, not
  * thread-safe; no counterpart in the reference: it lets tests run every
  * split length the automatic choice can pick (which depends on the device's
  * CU count) at small shapes. */
-int ca_debug_set_splits(int fwd_split_tiles, int dq_chunk_blocks, int dkdv_chunk_tiles);
+int ca_debug_set_splits(int fwd_split_tiles, int dq_chunk_stages, int dkdv_chunk_tiles);
 
 #ifdef __cplusplus
 }

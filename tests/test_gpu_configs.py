@@ -129,8 +129,10 @@ def test_config4_layer_shape(gpu_ca):
     check_invariants(q, k, dy, dq, dk, dv, dr)
 
 
-# (forward split tiles, dQ chunk blocks, dK/dV chunk tiles); 0 = automatic
-SPLITS = [(4, 16, 6), (6, 24, 8), (8, 32, 12), (12, 48, 16), (12, 64, 24), (5, 7, 5), (1, 1, 1),
+# (forward split tiles, dQ chunk stages of 32 keys, dK/dV chunk tiles); 0 =
+# automatic.  The automatic choices are forward 12/8/6/4, dQ 28/21/14/10/7 and
+# dK/dV 24/16/12/8/6; each appears below, at a shape where it cuts some group.
+SPLITS = [(4, 7, 6), (6, 10, 8), (8, 14, 12), (12, 21, 16), (12, 28, 24), (5, 5, 5), (1, 1, 1),
           (3, 2, 2)]
 
 
@@ -142,9 +144,9 @@ def split_override(gpu_ca):
 
 @pytest.mark.parametrize("splits", SPLITS, ids=lambda s: "fwd%d-dq%d-kv%d" % s)
 def test_every_split_length(gpu_ca, split_override, splits):
-    """Each forced split length at [1,2,1100,64] (35 query tiles, 79 key
-    blocks: every length cuts some ranges unevenly) in full against the
-    oracle, and two calls bitwise equal (fixed merge order)."""
+    """Each forced split length at [1,2,1100,64] (35 query tiles and key
+    stages, 79 key blocks: every length cuts some ranges unevenly) in full
+    against the oracle, and two calls bitwise equal (fixed merge order)."""
     say(f"[case] forced splits {splits} [1,2,1100,64]")
     split_override(*splits)
     q, k, v, rho, dy = inputs((1, 2, 1100, 64), 21, [0.3, -0.4])
@@ -154,7 +156,7 @@ def test_every_split_length(gpu_ca, split_override, splits):
     check_full(q, k, v, rho, dy, y, grads, f"splits {splits}")
 
 
-@pytest.mark.parametrize("D,splits", [(128, (4, 16, 6)), (32, (6, 24, 8)), (16, (1, 3, 1))])
+@pytest.mark.parametrize("D,splits", [(128, (4, 16, 6)), (32, (6, 10, 8)), (16, (1, 3, 1))])
 def test_forced_splits_other_head_dims(gpu_ca, split_override, D, splits):
     say(f"[case] forced splits {splits} [1,2,700,{D}]")
     split_override(*splits)

@@ -181,12 +181,13 @@ def test_forward_splits_and_combine(gpu_ca):
 
 
 def test_dq_split_k(gpu_ca):
-    """Grids smaller than one resident round split the dQ pass over chunks of
-    at most 32 key blocks, merged in chunk order.  T=2049, one slice: the last
-    query group spans 69 key blocks (3 chunks), checked in full against the
-    oracle.  T=4000, two D=32 slices with different gains: up to 5 chunks,
-    checked on the last 200 queries (every chunk of the last groups) and on
-    sampled rows.  Two calls agree bit for bit (fixed merge order)."""
+    """Grids far below one resident round split the dQ pass into chunks of
+    7 key stages (224 keys, the shortest automatic length), merged in chunk
+    order.  T=2049, one slice: the last query group's 65 stages make 10
+    chunks, checked in full against the oracle.  T=4000, two D=32 slices with
+    different gains: up to 18 chunks, checked on the last 200 queries (every
+    chunk of the last groups) and on sampled rows.  Two calls agree bit for
+    bit (fixed merge order)."""
     check_case(gpu_ca, (1, 1, 2049, 64), 12, 1.0, [0.25], "dq split T=2049")
     say("[case] dq split T=4000 D=32")
     T = 4000
