@@ -95,8 +95,10 @@ int ca_bwd_f32(const float* q, const float* k, const float* v, const float* log_
  * runs on until the process ends.  No counterpart in the reference: for
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc).  It allocates
- * nothing; shapes whose ca_bwd_workspace_bytes exceeds the array fail with
- * CA_ERR_WORKSPACE before any launch.  All calls on one device share its
+ * nothing; a shape whose full backward workspace exceeds the array runs in
+ * passes over 128-query groups sized to it, and a shape whose single group
+ * needs more fails with CA_ERR_WORKSPACE before any launch.  All calls on one
+ * device share its
  * array, so calls that overlap in time on one device (other streams, other
  * threads) race and must be serialised by the caller. */
 int ca_bwd_f32_noalloc(const float* q, const float* k, const float* v, const float* log_gain,
