@@ -150,8 +150,8 @@ BwdLayout bwd_layout(int B, int H, int T, int D, const ca::BwdPass& p) {
   BwdLayout L;
   L.ds = 0;
   L.limbs = align256((size_t)BH * p.ds_slice * sizeof(float));
-  L.qstat = L.limbs + align256(ca::bwd_limb_elems(BH, p.rows, D) * sizeof(uint16_t));
-  L.gain = L.qstat + align256((size_t)BH * p.rows * 2 * sizeof(float));
+  L.qstat = L.limbs + align256(ca::bwd_limb_elems(BH, p, D) * sizeof(uint16_t));
+  L.gain = L.qstat + align256(ca::bwd_qstat_floats(BH, p) * sizeof(float));
   L.dqpart = L.gain + align256((size_t)BH * kvs.items * sizeof(float));
   L.kvpart = L.dqpart + align256((size_t)BH * sp.part_items * ca::kDqRows * D * sizeof(float));
   L.total = L.kvpart + align256((size_t)BH * kvs.part_items * ca::kDkdvKeys * 2 * D * sizeof(float));
@@ -457,9 +457,15 @@ int ca_bwd_f32(const float* q, const float* k, const float* v, const float* log_
 }
 
 static int check_qkv(const char* fn, int dtype, const void* qkv, const float* rope_cs,
-                     const float* y, const void* tok) {
+                     const float* y, const void* tok, int T, int H, int D) {
   if (dtype != CA_DTYPE_F32 && dtype != CA_DTYPE_BF16 && dtype != CA_DTYPE_F16)
     return fail(CA_ERR_INVALID, "%s: unknown dtype code %d", fn, dtype);
+  // the forward reads one head's key and value rows of qkv (and 32 rows past
+  // T) through 32-bit byte offsets
+  if (ca::view_rows_bytes(T + 32, 3LL * H * D, D, (int)dtype_size(dtype)) >= (1ULL << 32))
+    return fail(CA_ERR_UNSUPPORTED,
+                "%s: one head's rows of qkv span 4 GiB or more (T=%d, H*D=%d); the kernels "
+                "address them with 32-bit offsets", fn, T, H * D);
   const size_t a = dtype == CA_DTYPE_F32 ? 16 : 8;
   if (!aligned_to(qkv, a) || !aligned_to(tok, a) || !aligned16(y) ||
       (rope_cs && !aligned16(rope_cs)))
@@ -475,7 +481,7 @@ int ca_fwd_qkv(const void* qkv, int dtype, const float* rope_cs, const float* lo
   if (rc) return rc;
   if (!qkv || !log_gain || !y || !out || !stats)
     return fail(CA_ERR_INVALID, "ca_fwd_qkv: null pointer");
-  rc = check_qkv("ca_fwd_qkv", dtype, qkv, rope_cs, y, out);
+  rc = check_qkv("ca_fwd_qkv", dtype, qkv, rope_cs, y, out, T, H, D);
   if (rc) return rc;
   ca::FwdIO io{tokens_view(qkv, dtype, 0, 3, T, H, D), tokens_view(qkv, dtype, 1, 3, T, H, D),
                tokens_view(qkv, dtype, 2, 3, T, H, D), rope_cs, log_gain, y,
@@ -491,7 +497,7 @@ int ca_bwd_qkv(const void* qkv, int dtype, const float* rope_cs, const float* lo
   if (rc) return rc;
   if (!qkv || !log_gain || !y || !stats || !dout || !dqkv || !dlog_gain)
     return fail(CA_ERR_INVALID, "ca_bwd_qkv: null pointer");
-  rc = check_qkv("ca_bwd_qkv", dtype, qkv, rope_cs, y, dout);
+  rc = check_qkv("ca_bwd_qkv", dtype, qkv, rope_cs, y, dout, T, H, D);
   if (rc) return rc;
   if (!aligned_to(dqkv, dtype == CA_DTYPE_F32 ? 16 : 8))
     return fail(CA_ERR_INVALID, "ca_bwd_qkv: misaligned dqkv");

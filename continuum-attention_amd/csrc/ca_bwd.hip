@@ -46,10 +46,12 @@
 namespace ca {
 
 
-// One thread per (row of the pass, 8 elements): Dl = dY . y, then the Q and
-// dY/Z limbs of the 8 elements (one 16-byte store per plane) and, per row,
-// (m, Dl/Z).  The pass holds `prows` rows per slice from row0 on; `rows` =
-// B*H*prows, plane p of `limbs` starts at p * rows * D.
+// One thread per (row of the pass's query tiles, 8 elements): Dl = dY . y,
+// then the Q and dY/Z limbs of the 8 elements (one 16-byte store per plane)
+// and, per row, (-m, -Dl/Z).  The limb planes are tile-major: tile j of the
+// pass in slice bh is the block limbs[(bh * ntiles + j) * 6 * 32 * D ..] of
+// six planes [32 rows][D].  Rows past T (in the last tile) are written as
+// zeros, so the dK/dV kernel stages whole tiles without bounds tests.
 template <int D, class E>
 __global__ __launch_bounds__(256) void ca_bwd_prep_kernel(View Qv, const float* __restrict__ rope,
                                                           View dYv,
@@ -57,15 +59,17 @@ __global__ __launch_bounds__(256) void ca_bwd_prep_kernel(View Qv, const float* 
                                                           const float* __restrict__ stats,
                                                           __bf16* __restrict__ limbs,
                                                           float* __restrict__ qstat, int H, int T,
-                                                          int row0, int prows, int rows) {
+                                                          int row0, int ntiles, int rows) {
   constexpr int C8 = D / 8;
   const int tix = blockIdx.x * 256 + threadIdx.x;
-  const int row = tix / C8, c = tix % C8;  // row = bh * prows + (t - row0)
-  const bool ok = row < rows;
-  const int bh = ok ? row / prows : 0, t = ok ? row0 + row % prows : 0;
-  const size_t grow = (size_t)bh * T + t;  // row of y and stats
-  const E* qp = view_slice<const E>(Qv, bh, H) + (long long)t * Qv.rstride + 8 * c;
-  const E* dp = view_slice<const E>(dYv, bh, H) + (long long)t * dYv.rstride + 8 * c;
+  const int row = tix / C8, c = tix % C8;  // row = bh * 32 ntiles + (t - row0)
+  if (row >= rows) return;
+  const int prows = 32 * ntiles;
+  const int bh = row / prows, r = row % prows, t = row0 + r;
+  const bool ok = t < T;
+  const size_t grow = (size_t)bh * T + (ok ? t : 0);  // row of y and stats
+  const E* qp = view_slice<const E>(Qv, bh, H) + (long long)(ok ? t : 0) * Qv.rstride + 8 * c;
+  const E* dp = view_slice<const E>(dYv, bh, H) + (long long)(ok ? t : 0) * dYv.rstride + 8 * c;
   f32x4 dy[2], y[2], qq[2];
   float m = 0.f, invz = 0.f;
 #pragma unroll
@@ -88,17 +92,15 @@ __global__ __launch_bounds__(256) void ca_bwd_prep_kernel(View Qv, const float* 
     x += dy[u][0] * y[u][0] + dy[u][1] * y[u][1] + dy[u][2] * y[u][2] + dy[u][3] * y[u][3];
 #pragma unroll
   for (int o = C8 / 2; o >= 1; o >>= 1) x += __shfl_xor(x, o);
-  if (!ok) return;
-  const size_t plane = (size_t)rows * D;
-  const size_t off = (size_t)row * D + 8 * c;
+  __bf16* tile = limbs + ((size_t)bh * ntiles + r / 32) * limb_tile_elems(D) + (r % 32) * D + 8 * c;
   auto put = [&](int p0, const f32x4* v, float scale) {
     float e[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) e[u] = v[u >> 2][u & 3] * scale;
     const Limbs lb = split8(e);
-    *reinterpret_cast<bf16x8*>(limbs + (size_t)(p0 + 0) * plane + off) = lb.h;
-    *reinterpret_cast<bf16x8*>(limbs + (size_t)(p0 + 1) * plane + off) = lb.m;
-    *reinterpret_cast<bf16x8*>(limbs + (size_t)(p0 + 2) * plane + off) = lb.l;
+    *reinterpret_cast<bf16x8*>(tile + (p0 + 0) * 32 * D) = lb.h;
+    *reinterpret_cast<bf16x8*>(tile + (p0 + 1) * 32 * D) = lb.m;
+    *reinterpret_cast<bf16x8*>(tile + (p0 + 2) * 32 * D) = lb.l;
   };
   put(0, qq, 1.0f);
   put(3, dy, invz);
@@ -426,11 +428,12 @@ template <int D, class E>
 hipError_t launch_bwd(const BwdIO& io, const BwdWork& ws, const BwdPass& pass, const DqSplit& sp,
                       const DkdvSplit& kvs, int B, int H, int T, hipStream_t stream) {
   const int BH = B * H;
-  const int rows = BH * pass.rows;
+  const int ntiles = bwd_pass_tiles(pass);
+  const int rows = BH * 32 * ntiles;
   timer_begin(kBwdPrep, stream);
   hipLaunchKernelGGL((ca_bwd_prep_kernel<D, E>), dim3((rows * (D / 8) + 255) / 256), dim3(256), 0,
                      stream, io.q, io.rope, io.dout, io.y, io.stats, ws.limbs, ws.qstat, H, T,
-                     pass.row0, pass.rows, rows);
+                     pass.row0, ntiles, rows);
   timer_end(kBwdPrep, stream);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;

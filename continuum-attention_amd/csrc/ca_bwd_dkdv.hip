@@ -116,52 +116,40 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
   }
 
   // ---- query-tile staging (all waves), one tile ahead ----
-  // limb planes and row statistics hold the pass's rows only
-  const size_t plane = (size_t)BH * pass.rows * D;
-  const size_t lslice = (size_t)bh * pass.rows * D;
+  // Tile qt of the pass is one contiguous block of six limb planes [32][D]
+  // (rows past T are zero) and 32 row statistics: thread tid copies 16-byte
+  // chunks tid + 256u of the block, so the only per-tile address work is the
+  // uniform block base.
+  const int ntiles = bwd_pass_tiles(pass);
+  constexpr unsigned kTileBytes = limb_tile_elems(D) * sizeof(__bf16);
+  const __amdgpu_buffer_rsrc_t lrs =
+      buffer_rsrc(limbs + (size_t)bh * ntiles * limb_tile_elems(D), ntiles * kTileBytes);
+  const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(qstat + (size_t)bh * ntiles * 64, ntiles * 256u);
   u32x4 pre[P::CPT];
-  f32x4 pre_st = {0.f, 0.f, 0.f, 0.f};
+  u32x4 pre_st = {0u, 0u, 0u, 0u};
   auto load_tile = [&](int qt) {
+    const unsigned t = qt - pass.qa;
 #pragma unroll
     for (int u = 0; u < P::CPT; ++u) {
       const int e = tid + 256 * u;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (e < P::CHUNKS) {
-        const int pl = e / (32 * P::RCH), rem = e % (32 * P::RCH);
-        const int row = rem / P::RCH, ch = rem % P::RCH;
-        const int i = 32 * qt + row;
-        if (i < T)
-          v = *reinterpret_cast<const u32x4*>(limbs + (size_t)pl * plane + lslice +
-                                              (size_t)(i - pass.row0) * D + 8 * ch);
-      }
-      pre[u] = v;
+      if (P::CHUNKS % 256 == 0 || e < P::CHUNKS)
+        pre[u] = buffer_ld16(lrs, 16u * tid, t * kTileBytes + 4096u * u);
     }
-    if (tid < 16) {
-      const int i = 32 * qt + 2 * tid;
-      f32x4 v = {0.f, 0.f, 0.f, 0.f};
-      const float* sp = qstat + ((size_t)bh * pass.rows + (i < T ? i - pass.row0 : 0)) * 2;
-      if (i + 1 < T) {
-        v = *reinterpret_cast<const f32x4*>(sp);
-      } else if (i < T) {
-        v[0] = sp[0];
-        v[1] = sp[1];
-      }
-      pre_st = v;
-    }
+    if (tid < 16) pre_st = buffer_ld16(srs, 16u * tid, t * 256u);
   };
   auto store_tile = [&](int buf) {
 #pragma unroll
     for (int u = 0; u < P::CPT; ++u) {
       const int e = tid + 256 * u;
-      if (e < P::CHUNKS) {
+      if (P::CHUNKS % 256 == 0 || e < P::CHUNKS) {
         const int pl = e / (32 * P::RCH), rem = e % (32 * P::RCH);
         const int row = rem / P::RCH, ch = rem % P::RCH;
         *reinterpret_cast<u32x4*>(&tiles[buf][pl * P::LIMB + row * P::LDR + 8 * ch]) = pre[u];
       }
     }
     if (tid < 16) {
-      *reinterpret_cast<f32x2*>(&tstat[buf][0][2 * tid]) = f32x2{pre_st[0], pre_st[2]};
-      *reinterpret_cast<f32x2*>(&tstat[buf][1][2 * tid]) = f32x2{pre_st[1], pre_st[3]};
+      *reinterpret_cast<u32x2*>(&tstat[buf][0][2 * tid]) = u32x2{pre_st[0], pre_st[2]};
+      *reinterpret_cast<u32x2*>(&tstat[buf][1][2 * tid]) = u32x2{pre_st[1], pre_st[3]};
     }
   };
 

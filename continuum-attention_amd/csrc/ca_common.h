@@ -179,6 +179,25 @@ __device__ __forceinline__ void prio_valu_end() { if (CA_PRIO_MFMA == 2) __built
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 
+// ---- buffer loads -----------------------------------------------------------
+// A raw buffer resource over `bytes` bytes at `base`: a load's address is
+// base + voffset + soffset, with a per-lane 32-bit voffset and a uniform
+// soffset (an SGPR), so loop-invariant per-lane offsets cost no address
+// arithmetic; loads whose voffset lies at or past `bytes` return zeros.  The
+// range must stay below 4 GiB.  0x00020000 is the gfx9 descriptor word 3 for
+// untyped 32-bit data.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ u32x4 buffer_ld16(__amdgpu_buffer_rsrc_t r, unsigned voff,
+                                             unsigned soff) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+__device__ __forceinline__ u32x2 buffer_ld8(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+}
+
 // ---- operand views --------------------------------------------------------
 // Element (slice bh = b*H + h, row t, column d) of an operand of element type
 // E sits at  base + b*bstride + h*hstride + t*rstride + d.  The operator's own
@@ -217,6 +236,23 @@ __device__ __forceinline__ f32x4 raw_to_f32(u32x2 r, const _Float16*) {
   const h4 a = __builtin_bit_cast(h4, r);  // whole-vector cast (see bf16x8 below)
   return f32x4{(float)a[0], (float)a[1], (float)a[2], (float)a[3]};
 }
+// Four consecutive elements through a buffer resource (zeros past its range).
+__device__ __forceinline__ f32x4 buffer_ld_raw4(__amdgpu_buffer_rsrc_t r, unsigned voff,
+                                                const float*) {
+  return __builtin_bit_cast(f32x4, buffer_ld16(r, voff, 0));
+}
+template <class E>
+__device__ __forceinline__ u32x2 buffer_ld_raw4(__amdgpu_buffer_rsrc_t r, unsigned voff, const E*) {
+  return buffer_ld8(r, voff, 0);
+}
+// Bytes a buffer resource over rows 0 .. T-1 (row stride rstride, D elements
+// of `esize` bytes each) must cover; loads of rows T .. T+31 read zeros.  The
+// host refuses views for which this (with 32 rows of slack) reaches 4 GiB.
+__host__ __device__ inline unsigned long long view_rows_bytes(int T, long long rstride, int D,
+                                                              int esize) {
+  return ((unsigned long long)(T - 1) * rstride + D) * esize;
+}
+
 template <class E>
 __device__ __forceinline__ f32x4 ld4(const E* p) {
   return raw_to_f32(ld_raw4(p), p);

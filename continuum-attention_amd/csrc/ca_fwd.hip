@@ -211,35 +211,47 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
   typedef typename Raw4<E>::type R4;
   R4 pre_k[P::LD_PER_THREAD], pre_v[P::VLD][2];
   f32x4 pre_cs[ROPE ? P::LD_PER_THREAD : 1];
+  // K, V (and RoPE table) rows through buffer resources: rows at or past T
+  // read as zeros (the hardware range check), and a tile's offsets are the
+  // thread's fixed offsets plus one uniform step per tile.
+  constexpr unsigned kEsz = sizeof(E);
+  const __amdgpu_buffer_rsrc_t kres = buffer_rsrc(Ks, (unsigned)view_rows_bytes(T, krs, D, kEsz));
+  const __amdgpu_buffer_rsrc_t vres = buffer_rsrc(Vs, (unsigned)view_rows_bytes(T, vrs, D, kEsz));
+  const __amdgpu_buffer_rsrc_t cres =
+      buffer_rsrc(ROPE ? rope : log_gain, ROPE ? (unsigned)(T * D * sizeof(float)) : 0u);
+  const unsigned kstep = 32u * (unsigned)krs * kEsz, vstep = 32u * (unsigned)vrs * kEsz;
+  const unsigned vrow = (unsigned)vrs * kEsz;
+  unsigned koff[P::LD_PER_THREAD], csoff[P::LD_PER_THREAD], voff[P::VLD];
+#pragma unroll
+  for (int j = 0; j < P::LD_PER_THREAD; ++j) {
+    const int e = tid + 256 * j;
+    const int row = e / P::C4, c = e % P::C4;  // score key 32t + 1 + row
+    koff[j] = ((unsigned)(1 + row) * (unsigned)krs + 4 * c) * kEsz;
+    csoff[j] = ((unsigned)(1 + row) * D + 4 * c) * (unsigned)sizeof(float);
+  }
+#pragma unroll
+  for (int j = 0; j < P::VLD; ++j) {
+    const int u = tid + 256 * j;
+    const int pp = u % 16, c = u / 16;  // weight keys 32t + 2pp, +1
+    voff[j] = ((unsigned)(2 * pp) * (unsigned)vrs + 4 * c) * kEsz;
+  }
   auto load_tile = [&](int t) {
 #pragma unroll
     for (int j = 0; j < P::LD_PER_THREAD; ++j) {
       const int e = tid + 256 * j;
-      R4 kv = {};
-      f32x4 cs = {1.f, 0.f, 1.f, 0.f};
-      if (e < P::TILE_F4) {
-        const int row = e / P::C4, c = e % P::C4;
-        const int kk = 32 * t + 1 + row;  // score key
-        if (kk < T) {
-          kv = ld_raw4(Ks + (long long)kk * krs + 4 * c);
-          if (ROPE) cs = rope_entry(rope, kk, D, 4 * c);
-        }
+      if (P::TILE_F4 % 256 == 0 || e < P::TILE_F4) {
+        pre_k[j] = buffer_ld_raw4(kres, koff[j] + t * kstep, Ks);
+        if constexpr (ROPE)
+          pre_cs[j] = __builtin_bit_cast(f32x4, buffer_ld16(cres, csoff[j] + t * (32u * D * 4u), 0));
       }
-      pre_k[j] = kv;
-      if constexpr (ROPE) pre_cs[j] = cs;
     }
 #pragma unroll
     for (int j = 0; j < P::VLD; ++j) {
       const int u = tid + 256 * j;
-      R4 v0 = {}, v1 = {};
-      if (u < P::VUNITS) {
-        const int pp = u % 16, c = u / 16;
-        const int vk = 32 * t + 2 * pp;  // weight key
-        if (vk < T) v0 = ld_raw4(Vs + (long long)vk * vrs + 4 * c);
-        if (vk + 1 < T) v1 = ld_raw4(Vs + (long long)(vk + 1) * vrs + 4 * c);
+      if (P::VUNITS % 256 == 0 || u < P::VUNITS) {
+        pre_v[j][0] = buffer_ld_raw4(vres, voff[j] + t * vstep, Vs);
+        pre_v[j][1] = buffer_ld_raw4(vres, voff[j] + t * vstep + vrow, Vs);
       }
-      pre_v[j][0] = v0;
-      pre_v[j][1] = v1;
     }
   };
   auto store_tile = [&](int buf) {

@@ -361,8 +361,9 @@ hipError_t launch_fwd(const FwdIO& io, float* part, int B, int H, int T, int C,
 // partials).
 struct BwdWork {
   float* dsbuf;       // dS spill, 32x16 blocks
-  __bf16* limbs;      // six bf16 planes [BH][pass rows][D]: Q limbs h, m, l; dY/Z limbs h, m, l
-  float* qstat;       // per query row of the pass: (-m, -D/Z)
+  __bf16* limbs;      // per slice and query tile of the pass, six bf16 planes [32 rows][D]:
+                      // Q limbs h, m, l; dY/Z limbs h, m, l ([BH][tile][plane][32][D])
+  float* qstat;       // per slice and padded row of the pass's tiles: (-m, -D/Z)
   float* gain_part;   // per dQ item
   float* dq_part;     // dQ chunk partials
   float* kv_part;     // dK/dV chunk partials: [BH][part item][kDkdvKeys][2][D]
@@ -372,7 +373,15 @@ struct BwdWork {
 template <int D, class E>
 hipError_t launch_bwd_dkdv(const BwdIO& io, const BwdWork& ws, const BwdPass& pass,
                            const DkdvSplit& kvs, int BH, int H, int T, hipStream_t stream);
-inline size_t bwd_limb_elems(int BH, int rows, int D) { return (size_t)6 * BH * rows * D; }
+// The limb planes and row statistics are kept per whole 32-query tile (tile-
+// major, rows past T zero) so that the dK/dV kernel stages a tile as one
+// contiguous block with no bounds tests.
+__host__ __device__ inline int bwd_pass_tiles(const BwdPass& p) { return p.qb - p.qa; }
+__host__ __device__ constexpr int limb_tile_elems(int D) { return 6 * 32 * D; }
+inline size_t bwd_limb_elems(int BH, const BwdPass& p, int D) {
+  return (size_t)BH * bwd_pass_tiles(p) * limb_tile_elems(D);
+}
+inline size_t bwd_qstat_floats(int BH, const BwdPass& p) { return (size_t)BH * bwd_pass_tiles(p) * 32 * 2; }
 
 template <int D, class E>
 hipError_t launch_bwd(const BwdIO& io, const BwdWork& ws, const BwdPass& pass, const DqSplit& sp,
