@@ -27,9 +27,10 @@
 //                   s_ij = c q_i . k_j and every row of dS sums to zero).
 //   ca_bwd_dq       dQ = c dS (K - k_ref) over the spilled rows, one work
 //                   item per (slice, 128 queries, chunk of 32-key stages); H
-//                   extra work groups sum the gain partials into dRho_h.
-//   ca_bwd_merge    sums the dQ and dK/dV chunk partials of split groups
-//                   (launched only when a split leaves some).
+//                   extra work groups sum the gain partials into dRho_h, and
+//                   one more per split dK/dV key group sums its chunk partials.
+//   ca_bwd_merge    sums the dQ chunk partials of split groups (launched only
+//                   when a split leaves some).
 //
 // Score-tile layout in ca_bwd_dkdv: the 16x16 result of S / dP' puts slot j
 // (key 14*kb - 1 + j) in lane j of each 16-lane row and queries 4*(l/16) + r
@@ -127,7 +128,8 @@ __global__ __launch_bounds__(256) void ca_bwd_prep_kernel(View Qv, const float* 
 // ca_bwd_merge sums.
 // Gain gradient: dlog_gain[h] = the fixed-order sum over batch and dK/dV
 // items of the partials the dK/dV kernel wrote (added to the earlier passes'
-// sum after the first pass).  Launched as H extra work groups of the dQ grid.
+// sum after the first pass).  Launched as H extra work groups of the dQ grid
+// (after the dQ items, followed by the dK/dV partial merges).
 __device__ __forceinline__ void gain_sum(const float* __restrict__ gain_part,
                                          float* __restrict__ dlog_gain, int h, int B, int H,
                                          int n_kv_items, bool first) {
@@ -142,6 +144,40 @@ __device__ __forceinline__ void gain_sum(const float* __restrict__ gain_part,
   if (tid == 0) {
     const float part_sum = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
     dlog_gain[h] = first ? part_sum : dlog_gain[h] + part_sum;
+  }
+}
+
+// Sum of the dK/dV chunk partials of multi-chunk key group wg of slice bh,
+// in chunk order (dK rotated back when RoPE is on), written to dK and dV or,
+// when an earlier pass already wrote this key group, added to them.  Run by
+// extra work groups of the dQ launch, which follows the dK/dV launch that
+// wrote the partials.
+template <int D, class E>
+__device__ __forceinline__ void merge_kv_group(const float* __restrict__ kv_part,
+                                               const float* __restrict__ rope, const View& dKv,
+                                               const View& dVv, const BwdPass& pass, int bh,
+                                               int wg, int H, int T, int kv_chunk,
+                                               int kv_part_items) {
+  constexpr int C4 = D / 4;
+  const int tid = threadIdx.x;
+  int first = 0;  // item index of the group's chunk 0 (multi-chunk groups come first)
+  for (int gg = 0; gg < wg; ++gg) first += dkdv_group_chunks(gg, pass, kv_chunk);
+  const int nch = dkdv_group_chunks(wg, pass, kv_chunk);
+  const bool accumulate = dkdv_qt0(wg) < pass.qa;
+  const f32x4* part = reinterpret_cast<const f32x4*>(
+      kv_part + ((size_t)bh * kv_part_items + first) * kDkdvKeys * 2 * D);
+  const int w0 = kDkdvKeys * wg;
+  for (int e = tid; e < kDkdvKeys * 2 * C4; e += 256) {
+    const int kl = e / (2 * C4), which = (e / C4) % 2, c4 = e % C4;
+    const int key = w0 + kl;
+    if (key >= T) break;
+    f32x4 s = part[e];
+    for (int cc = 1; cc < nch; ++cc) s += part[(size_t)cc * kDkdvKeys * 2 * C4 + e];
+    const View& ov = which ? dKv : dVv;
+    if (which && rope) s = rope4(s, rope_entry(rope, key, D, 4 * c4), true);
+    E* dst = view_slice<E>(ov, bh, H) + (long long)key * ov.rstride + 4 * c4;
+    if (accumulate) s += ld4(dst);
+    st4(dst, s);
   }
 }
 
@@ -164,11 +200,19 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
                                                         const float* __restrict__ gain_part,
                                                         float* __restrict__ dlog_gain, BwdPass pass,
                                                         int B, int H, int T, int chunk,
-                                                        int n_items, int n_part, int n_kv_items) {
+                                                        int n_items, int n_part, int n_kv_items,
+                                                        const float* __restrict__ kv_part,
+                                                        View dKv, View dVv, int kv_chunk,
+                                                        int kv_part_items) {
   using P = DqP<D>;
   const int BH = B * H;
-  if ((int)blockIdx.x >= n_items * BH) {  // the H gain work groups
-    gain_sum(gain_part, dlog_gain, blockIdx.x - n_items * BH, B, H, n_kv_items, pass.first);
+  if ((int)blockIdx.x >= n_items * BH) {
+    const int x = blockIdx.x - n_items * BH;
+    if (x < H)  // the H gain work groups
+      gain_sum(gain_part, dlog_gain, x, B, H, n_kv_items, pass.first);
+    else        // then one per (multi-chunk dK/dV key group, slice)
+      merge_kv_group<D, E>(kv_part, rope, dKv, dVv, pass, (x - H) % BH, (x - H) / BH, H, T,
+                           kv_chunk, kv_part_items);
     return;
   }
   __shared__ __attribute__((aligned(16))) __bf16 kst[2 * P::STAGE];
@@ -367,43 +411,16 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   }
 }
 
-// Merges of chunk partials, in chunk order.  Work groups BH*gi + bh: dQ of
-// multi-chunk group g1-1-gi of slice bh (rotated back when RoPE is on).  Work
-// groups after those: dK, dV of multi-chunk dK/dV group gi of slice bh, added
-// to what earlier passes wrote for that key group.
+// Merge of dQ chunk partials, in chunk order: work group BH*gi + bh sums the
+// chunks of multi-chunk dQ group g1-1-gi of slice bh (rotated back when RoPE
+// is on).  (The dK/dV chunk partials are summed by extra work groups of the
+// dQ launch.)
 template <int D, class E>
-__global__ __launch_bounds__(256) void ca_bwd_merge_kernel(
-    const float* __restrict__ dq_part, const float* __restrict__ kv_part,
-    const float* __restrict__ rope, View dQv, View dKv, View dVv, BwdPass pass, int B, int H, int T,
-    int chunk, int n_part, int dq_multi, int kv_chunk, int kv_part_items) {
+__global__ __launch_bounds__(256) void ca_bwd_merge_kernel(const float* __restrict__ dq_part,
+                                                           const float* __restrict__ rope,
+                                                           View dQv, BwdPass pass, int B, int H,
+                                                           int T, int chunk, int n_part) {
   const int tid = threadIdx.x;
-  const int BHt = B * H;
-  if (blockIdx.x >= BHt * dq_multi) {
-    constexpr int C4 = D / 4;
-    const int m = blockIdx.x - BHt * dq_multi;
-    const int bh = m % BHt, wg = m / BHt;
-    int first = 0;  // item index of the group's chunk 0 (multi-chunk groups come first)
-    for (int gg = 0; gg < wg; ++gg) first += dkdv_group_chunks(gg, pass, kv_chunk);
-    const int nch = dkdv_group_chunks(wg, pass, kv_chunk);
-    // earlier passes already wrote this key group's dK, dV
-    const bool accumulate = dkdv_qt0(wg) < pass.qa;
-    const f32x4* part =
-        reinterpret_cast<const f32x4*>(kv_part + ((size_t)bh * kv_part_items + first) * kDkdvKeys * 2 * D);
-    const int w0 = kDkdvKeys * wg;
-    for (int e = tid; e < kDkdvKeys * 2 * C4; e += 256) {
-      const int kl = e / (2 * C4), which = (e / C4) % 2, c4 = e % C4;
-      const int key = w0 + kl;
-      if (key >= T) break;
-      f32x4 s = part[e];
-      for (int cc = 1; cc < nch; ++cc) s += part[(size_t)cc * kDkdvKeys * 2 * C4 + e];
-      const View& ov = which ? dKv : dVv;
-      if (which && rope) s = rope4(s, rope_entry(rope, key, D, 4 * c4), true);
-      E* dst = view_slice<E>(ov, bh, H) + (long long)key * ov.rstride + 4 * c4;
-      if (accumulate) s += ld4(dst);
-      st4(dst, s);
-    }
-    return;
-  }
   constexpr int C4 = D / 4;
   const int BH = B * H;
   const int m = blockIdx.x;
@@ -442,26 +459,28 @@ hipError_t launch_bwd(const BwdIO& io, const BwdWork& ws, const BwdPass& pass, c
   timer_end(kBwdDkdv, stream);
   if (e != hipSuccess) return e;
   timer_begin(kBwdDq, stream);
-  // the dQ grid's H extra work groups sum the gain partials of the dK/dV items
-  const dim3 dq_grid(sp.items * BH + H);
+  // the dQ grid's extra work groups: H that sum the gain partials of the dK/dV
+  // items, then one per (multi-chunk dK/dV key group, slice) that sums its
+  // chunk partials
+  const dim3 dq_grid(sp.items * BH + H + kvs.multi_groups * BH);
   if (io.rope)
     hipLaunchKernelGGL((ca_bwd_dq_kernel<D, E, true>), dq_grid, dim3(256), 0, stream, ws.dsbuf,
                        io.k, io.rope, io.log_gain, io.dq, ws.dq_part, ws.gain_part, io.dlog_gain,
-                       pass, B, H, T, sp.chunk, sp.items, sp.part_items, kvs.items);
+                       pass, B, H, T, sp.chunk, sp.items, sp.part_items, kvs.items, ws.kv_part,
+                       io.dk, io.dv, kvs.chunk, kvs.part_items);
   else
     hipLaunchKernelGGL((ca_bwd_dq_kernel<D, E, false>), dq_grid, dim3(256), 0, stream, ws.dsbuf,
                        io.k, io.rope, io.log_gain, io.dq, ws.dq_part, ws.gain_part, io.dlog_gain,
-                       pass, B, H, T, sp.chunk, sp.items, sp.part_items, kvs.items);
+                       pass, B, H, T, sp.chunk, sp.items, sp.part_items, kvs.items, ws.kv_part,
+                       io.dk, io.dv, kvs.chunk, kvs.part_items);
   timer_end(kBwdDq, stream);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  // chunk partials (small grids only) are merged by a launch of their own
-  const int merges = BH * sp.multi_groups + BH * kvs.multi_groups;
-  if (merges == 0) return hipSuccess;
+  // dQ chunk partials (small grids only) are merged by a launch of their own
+  if (sp.multi_groups == 0) return hipSuccess;
   timer_begin(kBwdGain, stream);
-  hipLaunchKernelGGL((ca_bwd_merge_kernel<D, E>), dim3(merges), dim3(256), 0, stream, ws.dq_part,
-                     ws.kv_part, io.rope, io.dq, io.dk, io.dv, pass, B, H, T, sp.chunk,
-                     sp.part_items, sp.multi_groups, kvs.chunk, kvs.part_items);
+  hipLaunchKernelGGL((ca_bwd_merge_kernel<D, E>), dim3(BH * sp.multi_groups), dim3(256), 0, stream,
+                     ws.dq_part, io.rope, io.dq, pass, B, H, T, sp.chunk, sp.part_items);
   timer_end(kBwdGain, stream);
   return hipGetLastError();
 }
