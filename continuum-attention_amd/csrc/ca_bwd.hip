@@ -270,36 +270,44 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   R4 pre[P::UPT];
   f32x4 pre_cs[ROPE ? P::UPT : 1];
   const f32x4 kref = k_row4(kDqRows * qg, 4 * (tid % P::C4));
-  auto unit_key = [&](int u, int it) { return 32 * (st_lo + it) + u / P::C4; };
+  // K rows (and RoPE table rows) through buffer resources: a stage's offsets
+  // are the thread's fixed offsets plus one uniform step per stage, and rows
+  // at or past T read as zeros.  Those rows become -k_ref after the shift and
+  // meet dS = 0 (keys past T carry no dS), so they add exactly nothing.
+  constexpr unsigned kEsz = sizeof(E);
+  const __amdgpu_buffer_rsrc_t kres = buffer_rsrc(Ks, (unsigned)view_rows_bytes(T, krs, D, kEsz));
+  const __amdgpu_buffer_rsrc_t cres =
+      buffer_rsrc(ROPE ? rope : log_gain, ROPE ? (unsigned)(T * D * sizeof(float)) : 0u);
+  const unsigned kstep = 32u * (unsigned)krs * kEsz;
+  unsigned koff[P::UPT], csoff[P::UPT];
+#pragma unroll
+  for (int uu = 0; uu < P::UPT; ++uu) {
+    const int u = tid + 256 * uu;
+    const unsigned row = 32u * st_lo + u / P::C4, c = u % P::C4;  // key of stage 0
+    koff[uu] = (row * (unsigned)krs + 4 * c) * kEsz;
+    csoff[uu] = (row * D + 4 * c) * (unsigned)sizeof(float);
+  }
   auto load_k = [&](int it) {
 #pragma unroll
     for (int uu = 0; uu < P::UPT; ++uu) {
       const int u = tid + 256 * uu;
-      R4 v = {};
-      f32x4 cs = {1.f, 0.f, 1.f, 0.f};
-      if (u < P::UNITS) {
-        const int key = unit_key(u, it);
-        if (key >= 0 && key < T) {
-          v = ld_raw4(Ks + (long long)key * krs + 4 * (u % P::C4));
-          if (ROPE) cs = rope_entry(rope, key, D, 4 * (u % P::C4));
-        }
+      if (P::UNITS % 256 == 0 || u < P::UNITS) {
+        pre[uu] = buffer_ld_raw4(kres, koff[uu] + it * kstep, Ks);
+        if constexpr (ROPE)
+          pre_cs[uu] = __builtin_bit_cast(f32x4, buffer_ld16(cres, csoff[uu] + it * (32u * D * 4u), 0));
       }
-      pre[uu] = v;
-      if constexpr (ROPE) pre_cs[uu] = cs;
     }
   };
   // The shift is applied when the prefetched rows are stored, so the loads
-  // issued a stage ahead are not waited for inside the MFMA loop.  Rows of
-  // keys at or past T stay 0.
-  auto store_k = [&](int buf, int it) {
+  // issued a stage ahead are not waited for inside the MFMA loop.
+  auto store_k = [&](int buf) {
 #pragma unroll
     for (int uu = 0; uu < P::UPT; ++uu) {
       const int u = tid + 256 * uu;
-      if (u < P::UNITS) {
-        const int key = unit_key(u, it);
+      if (P::UNITS % 256 == 0 || u < P::UNITS) {
         f32x4 kx = raw_to_f32(pre[uu], Ks);
         if constexpr (ROPE) kx = rope4(kx, pre_cs[uu], false);
-        const f32x4 kv = (key >= 0 && key < T) ? kx - kref : f32x4{0.f, 0.f, 0.f, 0.f};
+        const f32x4 kv = kx - kref;
         unsigned h0, m0, l0, h1, m1, l1;
         split_pair(kv[0], kv[1], h0, m0, l0);
         split_pair(kv[2], kv[3], h1, m1, l1);
@@ -338,7 +346,7 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   float a_next[2][8];
   if (st_lo < my_end) load_a(0, a_next);
   load_k(0);
-  store_k(0, 0);
+  store_k(0);
   __syncthreads();
   // transposed reads: source lane 4j + m of group g points at key 8g + j
   // (+4 for the second read) of the stage, column 16nb + 4m
@@ -370,7 +378,7 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
         }
       }
     }
-    if (it + 1 < iters) store_k(buf ^ 1, it + 1);
+    if (it + 1 < iters) store_k(buf ^ 1);
     __syncthreads();
   }
   // lane (d = 16nb + l16, group g) holds rows 16rb + 4g + r of the wave's
