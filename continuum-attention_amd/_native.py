@@ -36,6 +36,7 @@ SIGNATURES = {
     "ca_workspace_cap": (_sz, []),
     "ca_fwd_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "ca_bwd_qkv_workspace_bytes": (_sz, [_i, _i, _i, _i]),
+    "ca_fwd_qkv_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "ca_fwd_f32": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp]),
     "ca_bwd_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "ca_bwd_f32": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,

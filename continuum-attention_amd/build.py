@@ -42,13 +42,21 @@ HIPCC_FLAGS = [
 # other sources (norms, optimizer, SwiGLU, weight rows) keep IEEE semantics:
 # a diverging run's non-finite values must behave there as in torch.
 _FINITE_MATH = ["-fno-honor-nans", "-fno-honor-infinities"]
+# The attention kernels contract multiply-adds only within one source
+# expression (their fused multiply-adds are written as fmaf): every template
+# instantiation (fp32, bf16, fp16 operands; each head dim) then rounds the same
+# arithmetic the same way, so the bf16 kernels, which skip the zero limb
+# products of bf16-valued operands, return the fp32 kernels' results on the
+# same values bit for bit.  Measured: the same instruction counts in the tile
+# loops as contraction across statements.
+_ATTN = _FINITE_MATH + ["-ffp-contract=on"]
 
 # Per-source flags: the dK/dV kernel schedules better with LLVM's max-ILP
 # machine-scheduler strategy (about 2% faster); the other kernels are slower
 # with it, so it applies to that translation unit only.
-SOURCE_FLAGS = {"ca_fwd.hip": _FINITE_MATH,
-                "ca_bwd.hip": _FINITE_MATH,
-                "ca_bwd_dkdv.hip": _FINITE_MATH + ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]}
+SOURCE_FLAGS = {"ca_fwd.hip": _ATTN,
+                "ca_bwd.hip": _ATTN,
+                "ca_bwd_dkdv.hip": _ATTN + ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]}
 
 
 def hipcc() -> str:

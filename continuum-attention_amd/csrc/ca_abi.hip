@@ -160,6 +160,11 @@ BwdLayout bwd_layout(int B, int H, int T, int D, const ca::BwdPass& p) {
 size_t bwd_full_bytes(int B, int H, int T, int D) {
   return bwd_layout(B, H, T, D, ca::bwd_pass(T, 0, ca::dq_num_groups(T))).total;
 }
+// Room for the rotated keys of the token-major entry points ([B*H][T][D],
+// 4-byte elements: enough for every operand type).
+size_t rotated_keys_bytes(int B, int H, int T, int D) {
+  return align256((size_t)B * H * T * D * sizeof(float));
+}
 
 // Backward passes for a workspace of `bytes`: ranges of dQ groups from the
 // first on, each as long as its layout fits (a layout only grows when its
@@ -320,9 +325,14 @@ size_t ca_bwd_workspace_bytes(int B, int H, int T, int D) {
   return bwd_capped_bytes(B, H, T, D);
 }
 
+size_t ca_fwd_qkv_workspace_bytes(int B, int H, int T, int D) {
+  if (B <= 0 || H <= 0 || T <= 0 || D <= 0) return 0;
+  return rotated_keys_bytes(B, H, T, D) + ca_fwd_workspace_bytes(B, H, T, D);
+}
+
 size_t ca_bwd_qkv_workspace_bytes(int B, int H, int T, int D) {
   if (B <= 0 || H <= 0 || T <= 0 || D <= 0) return 0;
-  return bwd_full_bytes(B, H, T, D);
+  return rotated_keys_bytes(B, H, T, D) + bwd_full_bytes(B, H, T, D);
 }
 
 }  // extern "C"
@@ -352,6 +362,48 @@ hipError_t bwd_launch(int D, const ca::BwdIO& io, const ca::BwdWork& w, const ca
     case 64: return ca::launch_bwd<64, E>(io, w, p, sp, kvs, B, H, T, s);
     default: return ca::launch_bwd<128, E>(io, w, p, sp, kvs, B, H, T, s);
   }
+}
+
+// [B,H,T,D] tensor (element units, any element type) as a view
+ca::View heads_view(const void* p, int H, int T, int D) {
+  return ca::View{const_cast<void*>(p), (long long)H * T * D, (long long)T * D, (long long)D};
+}
+size_t dtype_size(int dtype) { return dtype == CA_DTYPE_F32 ? 4 : 2; }
+
+template <class E>
+hipError_t rope_keys_launch(int D, const ca::View& k, const float* rope, void* out, int BH, int H,
+                            int T, hipStream_t s) {
+  switch (D) {
+    case 8: return ca::launch_rope_keys<8, E>(k, rope, out, BH, H, T, s);
+    case 16: return ca::launch_rope_keys<16, E>(k, rope, out, BH, H, T, s);
+    case 32: return ca::launch_rope_keys<32, E>(k, rope, out, BH, H, T, s);
+    case 64: return ca::launch_rope_keys<64, E>(k, rope, out, BH, H, T, s);
+    default: return ca::launch_rope_keys<128, E>(k, rope, out, BH, H, T, s);
+  }
+}
+
+// The token-major entry points with RoPE rotate the keys once, into the
+// start of their workspace ([B*H][T][D] in the operand type, room for 4-byte
+// elements), when it has that room besides what the operator needs (the
+// callers check): their kernels then read the keys unrotated instead of
+// rotating every staged key tile (the forward and the dQ pass stage each
+// tile for many query groups).  Advances *ws / *bytes past the rotated keys.
+// Without RoPE: nothing.
+int rotate_keys_first(ca::View* k, bool* k_rotated, const float* rope, int dtype, char** ws,
+                      size_t* bytes, int B, int H, int T, int D, void* stream) {
+  const size_t need = rotated_keys_bytes(B, H, T, D);
+  if (!rope || !*ws || *bytes < need) return CA_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e;
+  if (dtype == CA_DTYPE_BF16) e = rope_keys_launch<__bf16>(D, *k, rope, *ws, B * H, H, T, s);
+  else if (dtype == CA_DTYPE_F16) e = rope_keys_launch<_Float16>(D, *k, rope, *ws, B * H, H, T, s);
+  else e = rope_keys_launch<float>(D, *k, rope, *ws, B * H, H, T, s);
+  if (e != hipSuccess) return fail(CA_ERR_HIP, "key rotation launch: %s", hipGetErrorString(e));
+  *k = heads_view(*ws, H, T, D);
+  *k_rotated = true;
+  *ws += need;
+  *bytes -= need;
+  return CA_OK;
 }
 
 // Shape, workspace and launch of the forward, once the operands are views.
@@ -409,11 +461,6 @@ int bwd_common(const ca::BwdIO& io, int dtype, void* workspace, size_t workspace
   return CA_OK;
 }
 
-// fp32 [B,H,T,D] tensor as a view
-ca::View heads_view(const void* p, int H, int T, int D) {
-  return ca::View{const_cast<void*>(p), (long long)H * T * D, (long long)T * D, (long long)D};
-}
-size_t dtype_size(int dtype) { return dtype == CA_DTYPE_F32 ? 4 : 2; }
 // part `part` (of `parts`) of a token-major [B,T,parts,H,D] tensor as a view
 ca::View tokens_view(const void* p, int dtype, int part, int parts, int T, int H, int D) {
   char* base = static_cast<char*>(const_cast<void*>(p)) + (size_t)part * H * D * dtype_size(dtype);
@@ -435,7 +482,7 @@ int ca_fwd_f32(const float* q, const float* k, const float* v, const float* log_
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
     return fail(CA_ERR_INVALID, "q, k, v and out must be 16-byte aligned");
   ca::FwdIO io{heads_view(q, H, T, D), heads_view(k, H, T, D), heads_view(v, H, T, D), nullptr,
-               log_gain, out, ca::View{nullptr, 0, 0, 0}, stats};
+               false, log_gain, out, ca::View{nullptr, 0, 0, 0}, stats};
   return fwd_common(io, CA_DTYPE_F32, workspace, workspace_bytes, B, H, T, D, stream);
 }
 
@@ -451,7 +498,7 @@ int ca_bwd_f32(const float* q, const float* k, const float* v, const float* log_
       !aligned16(dq) || !aligned16(dk) || !aligned16(dv))
     return fail(CA_ERR_INVALID, "q, k, v, out, dout, dq, dk and dv must be 16-byte aligned");
   ca::BwdIO io{heads_view(q, H, T, D), heads_view(k, H, T, D), heads_view(v, H, T, D), nullptr,
-               log_gain, out, stats, heads_view(dout, H, T, D), heads_view(dq, H, T, D),
+               false, log_gain, out, stats, heads_view(dout, H, T, D), heads_view(dq, H, T, D),
                heads_view(dk, H, T, D), heads_view(dv, H, T, D), dlog_gain};
   return bwd_common(io, CA_DTYPE_F32, workspace, workspace_bytes, B, H, T, D, stream, false);
 }
@@ -484,9 +531,15 @@ int ca_fwd_qkv(const void* qkv, int dtype, const float* rope_cs, const float* lo
   rc = check_qkv("ca_fwd_qkv", dtype, qkv, rope_cs, y, out, T, H, D);
   if (rc) return rc;
   ca::FwdIO io{tokens_view(qkv, dtype, 0, 3, T, H, D), tokens_view(qkv, dtype, 1, 3, T, H, D),
-               tokens_view(qkv, dtype, 2, 3, T, H, D), rope_cs, log_gain, y,
+               tokens_view(qkv, dtype, 2, 3, T, H, D), rope_cs, false, log_gain, y,
                tokens_view(out, dtype, 0, 1, T, H, D), stats};
-  return fwd_common(io, dtype, workspace, workspace_bytes, B, H, T, D, stream);
+  char* ws = static_cast<char*>(workspace);
+  size_t bytes = workspace_bytes;
+  if (workspace && workspace_bytes >= ca_fwd_qkv_workspace_bytes(B, H, T, D)) {
+    rc = rotate_keys_first(&io.k, &io.k_rotated, rope_cs, dtype, &ws, &bytes, B, H, T, D, stream);
+    if (rc) return rc;
+  }
+  return fwd_common(io, dtype, ws, bytes, B, H, T, D, stream);
 }
 
 int ca_bwd_qkv(const void* qkv, int dtype, const float* rope_cs, const float* log_gain,
@@ -502,13 +555,19 @@ int ca_bwd_qkv(const void* qkv, int dtype, const float* rope_cs, const float* lo
   if (!aligned_to(dqkv, dtype == CA_DTYPE_F32 ? 16 : 8))
     return fail(CA_ERR_INVALID, "ca_bwd_qkv: misaligned dqkv");
   ca::BwdIO io{tokens_view(qkv, dtype, 0, 3, T, H, D), tokens_view(qkv, dtype, 1, 3, T, H, D),
-               tokens_view(qkv, dtype, 2, 3, T, H, D), rope_cs, log_gain, y, stats,
+               tokens_view(qkv, dtype, 2, 3, T, H, D), rope_cs, false, log_gain, y, stats,
                tokens_view(dout, dtype, 0, 1, T, H, D), tokens_view(dqkv, dtype, 0, 3, T, H, D),
                tokens_view(dqkv, dtype, 1, 3, T, H, D), tokens_view(dqkv, dtype, 2, 3, T, H, D),
                dlog_gain};
+  char* ws = static_cast<char*>(workspace);
+  size_t bytes = workspace_bytes;
+  if (workspace && workspace_bytes >= rotated_keys_bytes(B, H, T, D) + bwd_full_bytes(B, H, T, D)) {
+    rc = rotate_keys_first(&io.k, &io.k_rotated, rope_cs, dtype, &ws, &bytes, B, H, T, D, stream);
+    if (rc) return rc;
+  }
   // token-major gradients cannot be summed over passes without rounding them
   // to the element type in between: one pass, ca_bwd_qkv_workspace_bytes
-  return bwd_common(io, dtype, workspace, workspace_bytes, B, H, T, D, stream, true);
+  return bwd_common(io, dtype, ws, bytes, B, H, T, D, stream, true);
 }
 
 static int check_rows(const char* fn, int BH, int Q, int K, int start) {

@@ -50,9 +50,10 @@ namespace ca {
 // One thread per (row of the pass's query tiles, 8 elements): Dl = dY . y,
 // then the Q and dY/Z limbs of the 8 elements (one 16-byte store per plane)
 // and, per row, (-m, -Dl/Z).  The limb planes are tile-major: tile j of the
-// pass in slice bh is the block limbs[(bh * ntiles + j) * 6 * 32 * D ..] of
-// six planes [32 rows][D].  Rows past T (in the last tile) are written as
-// zeros, so the dK/dV kernel stages whole tiles without bounds tests.
+// pass in slice bh is the block limbs[(bh * ntiles + j) * P * 32 * D ..] of
+// P planes [32 rows][D] (P = q_limb_planes<E>() + 3).  Rows past T (in the
+// last tile) are written as zeros, so the dK/dV kernel stages whole tiles
+// without bounds tests.
 template <int D, class E>
 __global__ __launch_bounds__(256) void ca_bwd_prep_kernel(View Qv, const float* __restrict__ rope,
                                                           View dYv,
@@ -80,7 +81,7 @@ __global__ __launch_bounds__(256) void ca_bwd_prep_kernel(View Qv, const float* 
       dy[u] = ld4(dp + 4 * u);
       y[u] = reinterpret_cast<const f32x4*>(out + grow * D + 8 * c)[u];
       qq[u] = ld4(qp + 4 * u);
-      if (rope) qq[u] = rope4(qq[u], rope_entry(rope, t, D, 8 * c + 4 * u), false);
+      if (rope) qq[u] = rope4_in<E>(qq[u], rope_entry(rope, t, D, 8 * c + 4 * u));
     }
   }
   if (ok) {
@@ -93,18 +94,22 @@ __global__ __launch_bounds__(256) void ca_bwd_prep_kernel(View Qv, const float* 
     x += dy[u][0] * y[u][0] + dy[u][1] * y[u][1] + dy[u][2] * y[u][2] + dy[u][3] * y[u][3];
 #pragma unroll
   for (int o = C8 / 2; o >= 1; o >>= 1) x += __shfl_xor(x, o);
-  __bf16* tile = limbs + ((size_t)bh * ntiles + r / 32) * limb_tile_elems(D) + (r % 32) * D + 8 * c;
-  auto put = [&](int p0, const f32x4* v, float scale) {
+  constexpr int QL = q_limb_planes<E>();
+  __bf16* tile = limbs + ((size_t)bh * ntiles + r / 32) * limb_tile_elems(D, QL + 3) +
+                 (r % 32) * D + 8 * c;
+  auto put = [&](int p0, int nl, const f32x4* v, float scale) {
     float e[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) e[u] = v[u >> 2][u & 3] * scale;
     const Limbs lb = split8(e);
     *reinterpret_cast<bf16x8*>(tile + (p0 + 0) * 32 * D) = lb.h;
-    *reinterpret_cast<bf16x8*>(tile + (p0 + 1) * 32 * D) = lb.m;
-    *reinterpret_cast<bf16x8*>(tile + (p0 + 2) * 32 * D) = lb.l;
+    if (nl > 1) {
+      *reinterpret_cast<bf16x8*>(tile + (p0 + 1) * 32 * D) = lb.m;
+      *reinterpret_cast<bf16x8*>(tile + (p0 + 2) * 32 * D) = lb.l;
+    }
   };
-  put(0, qq, 1.0f);
-  put(3, dy, invz);
+  put(0, QL, qq, 1.0f);  // bf16 operands: Q is bf16-valued, its h limb is exact
+  put(QL, 3, dy, invz);
   if (c == 0) {
     // negated: the dK/dV kernel starts its S and dP' accumulators from them
     qstat[(size_t)row * 2 + 0] = -m;
@@ -257,14 +262,15 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   // cancel in the sum of the chunk partials.
   // Staging unit u: slot (key of the stage) u / C4, d = 4(u % C4)..+3; a
   // thread's units all have d chunk tid % C4, since 256 % C4 == 0.
-  // rows of K (RoPE applied when `rope`): loaded raw a stage ahead and
-  // converted, rotated and shifted when stored
-  if (!ROPE) rope = nullptr;  // lets the compiler drop every rotation
+  // rows of K (rotated here when ROPE; otherwise they arrive rotated, or
+  // without RoPE): loaded raw a stage ahead and converted, rotated and
+  // shifted when stored.  dQ is rotated back whenever `rope` is given.
+  const float* __restrict__ rope_k = ROPE ? rope : nullptr;  // drops every key rotation
   const E* __restrict__ Ks = view_slice<const E>(Kv, bh, H);
   const long long krs = Kv.rstride;
   auto k_row4 = [&](int key, int d0) {
     f32x4 x = ld4(Ks + (long long)key * krs + d0);
-    return rope ? rope4(x, rope_entry(rope, key, D, d0), false) : x;
+    return rope_k ? rope4_in<E>(x, rope_entry(rope_k, key, D, d0)) : x;
   };
   typedef typename Raw4<E>::type R4;
   R4 pre[P::UPT];
@@ -277,7 +283,7 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   constexpr unsigned kEsz = sizeof(E);
   const __amdgpu_buffer_rsrc_t kres = buffer_rsrc(Ks, (unsigned)view_rows_bytes(T, krs, D, kEsz));
   const __amdgpu_buffer_rsrc_t cres =
-      buffer_rsrc(ROPE ? rope : log_gain, ROPE ? (unsigned)(T * D * sizeof(float)) : 0u);
+      buffer_rsrc(ROPE ? rope_k : log_gain, ROPE ? (unsigned)(T * D * sizeof(float)) : 0u);
   const unsigned kstep = 32u * (unsigned)krs * kEsz;
   unsigned koff[P::UPT], csoff[P::UPT];
 #pragma unroll
@@ -306,7 +312,7 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
       const int u = tid + 256 * uu;
       if (P::UNITS % 256 == 0 || u < P::UNITS) {
         f32x4 kx = raw_to_f32(pre[uu], Ks);
-        if constexpr (ROPE) kx = rope4(kx, pre_cs[uu], false);
+        if constexpr (ROPE) kx = rope4_in<E>(kx, pre_cs[uu]);
         const f32x4 kv = kx - kref;
         unsigned h0, m0, l0, h1, m1, l1;
         split_pair(kv[0], kv[1], h0, m0, l0);
@@ -386,36 +392,44 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   if (wave_on) {
     // single-chunk groups write dQ; chunk partials are item-indexed tiles
     // [kDqRows queries][D] (items of multi-chunk groups are numbered first),
-    // summed and rotated back by the merge
+    // summed and rotated back by the merge.  The rotation test is taken once,
+    // outside the unrolled stores, so each version issues its loads together.
     const bool single = nch == 1;
     float* part = dq_part + ((size_t)bh * n_part + item) * kDqRows * D;
     E* dQs = view_slice<E>(dQv, bh, H);
     const bool odd = l16 & 1;
+    auto store = [&](auto rotate_tag) {
+      constexpr bool kRot = decltype(rotate_tag)::value;
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+      for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-      for (int nb = 0; nb < P::NB; ++nb)
+        for (int nb = 0; nb < P::NB; ++nb)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int rloc = 32 * w + 16 * rb + 4 * g + r;
-          const int row = kDqRows * qg + rloc;
-          const int d = 16 * nb + l16;
-          const float val = acc[rb][nb][r] * c;
-          const float val_pair = ROPE ? __shfl_xor(val, 1) : 0.f;
-          if (row < T && d < D) {
-            if (single) {
-              float o = val;
-              if (ROPE) {
-                // transposed rotation back to the un-rotated q
-                const float* e = rope + (long long)row * D + (d & ~1);
-                o = odd ? fmaf(val, e[0], -val_pair * e[1]) : fmaf(val, e[0], val_pair * e[1]);
+          for (int r = 0; r < 4; ++r) {
+            const int rloc = 32 * w + 16 * rb + 4 * g + r;
+            const int row = kDqRows * qg + rloc;
+            const int d = 16 * nb + l16;
+            const float val = acc[rb][nb][r] * c;
+            const float val_pair = kRot ? __shfl_xor(val, 1) : 0.f;
+            if (row < T && d < D) {
+              if (single) {
+                float o = val;
+                if (kRot) {
+                  // transposed rotation back to the un-rotated q
+                  const float* e = rope + (long long)row * D + (d & ~1);
+                  o = odd ? fmaf(val, e[0], -val_pair * e[1]) : fmaf(val, e[0], val_pair * e[1]);
+                }
+                st1(dQs + (long long)row * dQv.rstride + d, o);
+              } else {
+                part[(size_t)rloc * D + d] = val;
               }
-              st1(dQs + (long long)row * dQv.rstride + d, o);
-            } else {
-              part[(size_t)rloc * D + d] = val;
             }
           }
-        }
+    };
+    if (rope)
+      store(std::true_type{});
+    else
+      store(std::false_type{});
   }
 }
 
@@ -471,7 +485,7 @@ hipError_t launch_bwd(const BwdIO& io, const BwdWork& ws, const BwdPass& pass, c
   // items, then one per (multi-chunk dK/dV key group, slice) that sums its
   // chunk partials
   const dim3 dq_grid(sp.items * BH + H + kvs.multi_groups * BH);
-  if (io.rope)
+  if (io.rope && !io.k_rotated)
     hipLaunchKernelGGL((ca_bwd_dq_kernel<D, E, true>), dq_grid, dim3(256), 0, stream, ws.dsbuf,
                        io.k, io.rope, io.log_gain, io.dq, ws.dq_part, ws.gain_part, io.dlog_gain,
                        pass, B, H, T, sp.chunk, sp.items, sp.part_items, kvs.items, ws.kv_part,

@@ -18,7 +18,7 @@
 
 namespace ca {
 
-template <int D>
+template <int D, int QL>
 struct Bwd {
   static constexpr int C4 = D / 4;             // float4 chunks per row
   static constexpr int KB = (D + 31) / 32;     // 32-wide k blocks of S / dP'
@@ -27,19 +27,26 @@ struct Bwd {
   // 16-row row-wise reads and the transposed reads free of bank conflicts
   static constexpr int LDR = D + 16;
   static constexpr int LIMB = 32 * LDR;        // bf16 per limb plane of a tile
-  static constexpr int TILE = 6 * LIMB;        // Q limbs h, m, l then dY/Z limbs h, m, l
+  static constexpr int PLANES = QL + 3;        // QL Q limbs (h[, m, l]), then dY/Z limbs h, m, l
+  static constexpr int TILE = PLANES * LIMB;
   static constexpr int RCH = D / 8;            // 16-byte chunks per row and plane
-  static constexpr int CHUNKS = 6 * 32 * RCH;  // chunks staged per tile
+  static constexpr int CHUNKS = PLANES * 32 * RCH;  // chunks staged per tile
   static constexpr int CPT = (CHUNKS + 255) / 256;
 };
 
 template <int D, class E>
 __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
-    View Kv, View Vv, const float* __restrict__ rope, const __bf16* __restrict__ limbs,
+    View Kv, View Vv, const float* __restrict__ rope, const float* __restrict__ rope_k,
+    const __bf16* __restrict__ limbs,
     const float* __restrict__ qstat, const float* __restrict__ log_gain, View dKv, View dVv,
     float* __restrict__ dsbuf, float* __restrict__ kv_part, float* __restrict__ gain_part,
     BwdPass pass, int BH, int H, int T, int chunk, int n_items, int n_part) {
-  using P = Bwd<D>;
+  // bf16 operands: Q (rotated and rounded as the reference rounds it) and V
+  // are bf16-valued, so the tile carries Q's h limb alone and the products
+  // with Q or V skip their zero limb products (limb_step_used), with the same
+  // sums bit for bit.  K enters S scaled by the head's gain, in three limbs.
+  constexpr bool BF = q_limb_planes<E>() == 1;
+  using P = Bwd<D, q_limb_planes<E>()>;
   __shared__ __attribute__((aligned(16))) __bf16 tiles[2][P::TILE];
   // per staged row: -m (tstat[b][0][row]) and -Dl/Z (tstat[b][1][row]), in
   // the order of the S / dP' accumulator registers
@@ -80,7 +87,8 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
     for (int e = tid; e < 2 * P::TILE / 2; e += 256) z[e] = 0u;
   }
 
-  // K (RoPE applied when `rope`, then scaled by c log2e) and V of this lane's
+  // K (rotated here when `rope_k`; otherwise it arrives rotated, or without
+  // RoPE; then scaled by c log2e) and V of this lane's
   // slot: B operands of S / dP', k block kb, element e = d 32kb + 8g + e.
   Limbs kl[P::KB], vl[P::KB];
 #pragma unroll
@@ -95,7 +103,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
     for (int h2 = 0; h2 < 2; ++h2) {
       const bool ok2 = ok && d0 + 4 * h2 < D;
       f32x4 a = ok2 ? ld4(kp + 4 * h2) : f32x4{0.f, 0.f, 0.f, 0.f};
-      if (rope && ok2) a = rope4(a, rope_entry(rope, krow, D, d0 + 4 * h2), false);
+      if (rope_k && ok2) a = rope4_in<E>(a, rope_entry(rope_k, krow, D, d0 + 4 * h2));
       a *= cl2;
       const f32x4 b = ok2 ? ld4(vp + 4 * h2) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -121,9 +129,9 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
   // chunks tid + 256u of the block, so the only per-tile address work is the
   // uniform block base.
   const int ntiles = bwd_pass_tiles(pass);
-  constexpr unsigned kTileBytes = limb_tile_elems(D) * sizeof(__bf16);
+  constexpr unsigned kTileBytes = limb_tile_elems(D, P::PLANES) * sizeof(__bf16);
   const __amdgpu_buffer_rsrc_t lrs =
-      buffer_rsrc(limbs + (size_t)bh * ntiles * limb_tile_elems(D), ntiles * kTileBytes);
+      buffer_rsrc(limbs + (size_t)bh * ntiles * limb_tile_elems(D, P::PLANES), ntiles * kTileBytes);
   const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(qstat + (size_t)bh * ntiles * 64, ntiles * 256u);
   u32x4 pre[P::CPT];
   u32x4 pre_st = {0u, 0u, 0u, 0u};
@@ -179,7 +187,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
     const bool work = kb16 < nkb && kBwdKeys * kb16 <= i0 + 31;
     if (work) {
       const __bf16* Tq = &tiles[buf][0];
-      const __bf16* Ty = &tiles[buf][3 * P::LIMB];
+      const __bf16* Ty = &tiles[buf][(P::PLANES - 3) * P::LIMB];
 
       // ---- S - m and dP' - Dl/Z (row blocks rb: queries i0 + 16rb + 4g + r) ----
       f32x4 sacc[2], pacc[2];
@@ -199,8 +207,10 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
           if (col < D) {
             const int o = (16 * rb + j) * P::LDR + col;
             qa[rb].h = *reinterpret_cast<const bf16x8*>(Tq + o);
-            qa[rb].m = *reinterpret_cast<const bf16x8*>(Tq + P::LIMB + o);
-            qa[rb].l = *reinterpret_cast<const bf16x8*>(Tq + 2 * P::LIMB + o);
+            if (!BF) {
+              qa[rb].m = *reinterpret_cast<const bf16x8*>(Tq + P::LIMB + o);
+              qa[rb].l = *reinterpret_cast<const bf16x8*>(Tq + 2 * P::LIMB + o);
+            }
             ya[rb].h = *reinterpret_cast<const bf16x8*>(Ty + o);
             ya[rb].m = *reinterpret_cast<const bf16x8*>(Ty + P::LIMB + o);
             ya[rb].l = *reinterpret_cast<const bf16x8*>(Ty + 2 * P::LIMB + o);
@@ -209,10 +219,10 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
         // four independent accumulators per limb product
 #pragma unroll
         for (int st = 0; st < 6; ++st) {
-          sacc[0] = mfma16_step(st, qa[0], kl[kb], sacc[0]);
-          pacc[0] = mfma16_step(st, ya[0], vl[kb], pacc[0]);
-          sacc[1] = mfma16_step(st, qa[1], kl[kb], sacc[1]);
-          pacc[1] = mfma16_step(st, ya[1], vl[kb], pacc[1]);
+          if (limb_step_used<BF, false>(st)) sacc[0] = mfma16_step(st, qa[0], kl[kb], sacc[0]);
+          if (limb_step_used<false, BF>(st)) pacc[0] = mfma16_step(st, ya[0], vl[kb], pacc[0]);
+          if (limb_step_used<BF, false>(st)) sacc[1] = mfma16_step(st, qa[1], kl[kb], sacc[1]);
+          if (limb_step_used<false, BF>(st)) pacc[1] = mfma16_step(st, ya[1], vl[kb], pacc[1]);
         }
       }
       prio_mfma_end();
@@ -301,12 +311,16 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
         ya.m = lds_read_tr8(Ty + P::LIMB + o0, Ty + P::LIMB + o1);
         ya.l = lds_read_tr8(Ty + 2 * P::LIMB + o0, Ty + 2 * P::LIMB + o1);
         qa.h = lds_read_tr8(Tq + o0, Tq + o1);
-        qa.m = lds_read_tr8(Tq + P::LIMB + o0, Tq + P::LIMB + o1);
-        qa.l = lds_read_tr8(Tq + 2 * P::LIMB + o0, Tq + 2 * P::LIMB + o1);
+        if (BF) {
+          qa.m = qa.l = bf16x8{};
+        } else {
+          qa.m = lds_read_tr8(Tq + P::LIMB + o0, Tq + P::LIMB + o1);
+          qa.l = lds_read_tr8(Tq + 2 * P::LIMB + o0, Tq + 2 * P::LIMB + o1);
+        }
 #pragma unroll
         for (int st = 0; st < 6; ++st) {
           accv[mb] = mfma16_step(st, ya, wb, accv[mb]);
-          acck[mb] = mfma16_step(st, qa, db, acck[mb]);
+          if (limb_step_used<BF, false>(st)) acck[mb] = mfma16_step(st, qa, db, acck[mb]);
         }
       }
       prio_mfma_end();
@@ -335,9 +349,9 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
       const int d0 = 16 * mb + 4 * g;
       if (d0 < D) {
         f32x4 a = ld4(kj + d0), b = ld4(k0 + d0);
-        if (rope) {
-          a = rope4(a, rope_entry(rope, key_j, D, d0), false);
-          b = rope4(b, rope_entry(rope, 0, D, d0), false);
+        if (rope_k) {
+          a = rope4_in<E>(a, rope_entry(rope_k, key_j, D, d0));
+          b = rope4_in<E>(b, rope_entry(rope_k, 0, D, d0));
         }
         const f32x4 dk = acck[mb] * ck;
 #pragma unroll
@@ -394,7 +408,8 @@ template <int D, class E>
 hipError_t launch_bwd_dkdv(const BwdIO& io, const BwdWork& ws, const BwdPass& pass,
                            const DkdvSplit& kvs, int BH, int H, int T, hipStream_t stream) {
   hipLaunchKernelGGL((ca_bwd_dkdv_kernel<D, E>), dim3(kvs.items * BH), dim3(256), 0, stream, io.k,
-                     io.v, io.rope, ws.limbs, ws.qstat, io.log_gain, io.dk, io.dv, ws.dsbuf,
+                     io.v, io.rope, io.k_rotated ? nullptr : io.rope, ws.limbs, ws.qstat,
+                     io.log_gain, io.dk, io.dv, ws.dsbuf,
                      ws.kv_part, ws.gain_part, pass, BH, H, T, kvs.chunk, kvs.items,
                      kvs.part_items);
   return hipGetLastError();

@@ -112,6 +112,27 @@ __device__ __forceinline__ f32x4 mfma16_step(int step, const Limbs& a, const Lim
   }
 }
 
+// bf16-valued operands: an fp32 value that is exactly a bf16 number splits
+// into h = the value and m = l = 0, so the limb products that use its m or l
+// limb are exactly zero and are skipped (an MFMA adding zero products leaves
+// the accumulator unchanged, so the result is the same bit for bit).
+// limb_step_used<ABF, BBF>(st): step st of mfma16_step (a.l b.h, a.m b.m,
+// a.h b.l, a.m b.h, a.h b.m, a.h b.h) is nonzero when operand a (ABF) / b
+// (BBF) is bf16-valued.
+template <bool ABF, bool BBF>
+__host__ __device__ constexpr bool limb_step_used(int st) {
+  const bool a_low = st == 0 || st == 1 || st == 3;  // uses a.m or a.l
+  const bool b_low = st == 1 || st == 2 || st == 4;  // uses b.m or b.l
+  return !(ABF && a_low) && !(BBF && b_low);
+}
+// c += a * b over 16 k values (32x32x16 tiles) with bf16-valued a: the three
+// products of a.h, small terms first (the nonzero steps of mfma_x6)
+__device__ __forceinline__ f32x16 mfma_x3_abf(bf16x8 ah, const Limbs& b, f32x16 c) {
+  c = mfma_bf16(ah, b.l, c);
+  c = mfma_bf16(ah, b.m, c);
+  return mfma_bf16(ah, b.h, c);
+}
+
 // Transposed LDS read (ds_read_b64_tr_b16): within each 16-lane group, lane
 // i receives element (i & 3) of the 4 bf16 that lanes 4j + (i >> 2) address,
 // for j = 0..3.  With lane i' = 4j + m pointing at row r0 + j, column c0 + 4m
@@ -293,6 +314,34 @@ __device__ __forceinline__ f32x4 rope_entry(const float* cs, long long t, int D,
   return *reinterpret_cast<const f32x4*>(cs + t * D + d0);
 }
 
+// fp32 value rounded to the element type E (round to nearest even) and back;
+// the identity for fp32.
+template <class E> __device__ __forceinline__ float round_to(float x) { return x; }
+template <> __device__ __forceinline__ float round_to<__bf16>(float x) {
+  return __uint_as_float(cvt_pk_bf16(x, 0.f) << 16);
+}
+template <> __device__ __forceinline__ float round_to<_Float16>(float x) {
+  return (float)(_Float16)x;
+}
+// RoPE of an operand of element type E the way the reference computes it in
+// that type (cuda/continuum_attention.py:826-835, q * cos + rotate(q) * sin
+// with cos and sin cast to q's dtype): for 16-bit E each product and the sum
+// are rounded to E, so the rotated values are E-valued (with t, the (cos,
+// sin) pairs, given already rounded to E, every step is the reference's own
+// rounding: products of two E values and their sums are formed in fp32 as
+// torch's 16-bit arithmetic forms them).  fp32 operands rotate in fp32.
+template <class E> __device__ __forceinline__ f32x4 rope4_in(f32x4 x, f32x4 t) {
+  if constexpr (sizeof(E) == sizeof(float)) {
+    return rope4(x, t, false);
+  } else {
+    const float c0 = t[0], s0 = t[1], c1 = t[2], s1 = t[3];
+    return f32x4{round_to<E>(round_to<E>(x[0] * c0) - round_to<E>(x[1] * s0)),
+                 round_to<E>(round_to<E>(x[1] * c0) + round_to<E>(x[0] * s0)),
+                 round_to<E>(round_to<E>(x[2] * c1) - round_to<E>(x[3] * s1)),
+                 round_to<E>(round_to<E>(x[3] * c1) + round_to<E>(x[2] * s1))};
+  }
+}
+
 // Per-head score scale in log2 units: exp(log_gain[h]) / sqrt(D) * log2(e)
 // (the reference's scale, cuda/continuum_attention.py:656-657, times log2 e).
 __device__ __forceinline__ float head_scale_log2(const float* log_gain, int head, int D) {
@@ -350,9 +399,9 @@ __device__ __forceinline__ float j2_odd(float y) {
 __device__ __forceinline__ void seg_shares_x(float x, float pl, float pr, float& L, float& R) {
   const float dp = pr - pl;
   const float inv_x = fast_rcp(x);
-  const float a = dp * inv_x;           // p_l J0
-  const float rc = (pr - a) * inv_x;    // p_l J1
-  const float lc = a - rc;              // p_l (J0 - J1)
+  // a = dp/x = p_l J0 enters both shares through fused multiply-adds
+  const float rc = fmaf(-dp, inv_x, pr) * inv_x;  // (p_r - a) / x = p_l J1
+  const float lc = fmaf(dp, inv_x, -rc);          // a - R = p_l (J0 - J1)
   const float y = x * x;
   const float e1 = j1_even(y), o1 = j1_odd(y);
   const float rs = pl * fmaf(x, o1, e1);   // p_l J1(x)
@@ -372,9 +421,8 @@ __device__ __forceinline__ void seg_shares_grad_x(float x, float pl, float pr, f
                                                   float& L, float& R, float& dL, float& dR) {
   const float dp = pr - pl;
   const float inv_x = fast_rcp(x);
-  const float a = dp * inv_x;
-  const float rc = (pr - a) * inv_x;
-  const float lc = a - rc;
+  const float rc = fmaf(-dp, inv_x, pr) * inv_x;
+  const float lc = fmaf(dp, inv_x, -rc);
   const float j2c = fmaf(-2.0f, rc, pr) * inv_x;  // p_l J2
   const float y = x * x;
   const float e1 = j1_even(y), o1 = j1_odd(y);

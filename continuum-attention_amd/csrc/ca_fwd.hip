@@ -93,7 +93,7 @@ __device__ __forceinline__ float halo_dot(const float* qreg, const E* __restrict
 #pragma unroll
   for (int c = 0; c < DH / 4; ++c) {
     f32x4 kv = ld4(kp + 4 * c);
-    if (rope) kv = rope4(kv, rope_entry(rope, key, D, h * DH + 4 * c), false);
+    if (rope) kv = rope4_in<E>(kv, rope_entry(rope, key, D, h * DH + 4 * c));
     acc = fmaf(qreg[4 * c + 0], kv[0], acc);
     acc = fmaf(qreg[4 * c + 1], kv[1], acc);
     acc = fmaf(qreg[4 * c + 2], kv[2], acc);
@@ -108,9 +108,15 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
     float* __restrict__ O, View Ov, float* __restrict__ stats, float* __restrict__ part, int BH,
     int H, int T, int C, int G, int smax) {
   using P = Fwd<D>;
+  // bf16 operands (with RoPE rounded to bf16 as the reference does) are
+  // bf16-valued: their limb split is h = the value, m = l = 0, so a K or V
+  // tile is staged as its h plane alone and every product with it takes the
+  // three nonzero limb products (mfma_x3_abf), bit for bit the same sums.
+  constexpr bool BF = std::is_same<E, __bf16>::value;
+  constexpr int NL = BF ? 1 : 3;  // limb planes staged per K and V tile
   // [buffer][limb][plane]
-  __shared__ __attribute__((aligned(16))) __bf16 lds_k[2][3][P::KPLANE];
-  __shared__ __attribute__((aligned(16))) __bf16 lds_vt[2][3][P::VPLANE];
+  __shared__ __attribute__((aligned(16))) __bf16 lds_k[2][NL][P::KPLANE];
+  __shared__ __attribute__((aligned(16))) __bf16 lds_vt[2][NL][P::VPLANE];
 
   const int bh = blockIdx.x % BH;
   const int item = blockIdx.x / BH;
@@ -138,7 +144,10 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
   const E* __restrict__ Ks = view_slice<const E>(Kv, bh, H);
   const E* __restrict__ Vs = view_slice<const E>(Vv, bh, H);
   const long long krs = Kv.rstride, vrs = Vv.rstride;
-  if (!ROPE) rope = nullptr;  // lets the compiler drop every rotation
+  // RoPE: q is rotated (once per lane) whenever `rope` is given; the keys are
+  // rotated as they are read only when ROPE (otherwise they arrive rotated,
+  // or unrotated without RoPE), so the compiler drops every key rotation
+  const float* __restrict__ rope_k = ROPE ? rope : nullptr;
   const int head = bh % H;
   const float cl2 = head_scale_log2(log_gain, head, D);
 
@@ -149,7 +158,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
 #pragma unroll
     for (int c = 0; c < P::CH; ++c) {
       f32x4 v4 = qvalid ? ld4(qp + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
-      if (rope && qvalid) v4 = rope4(v4, rope_entry(rope, i, D, h * P::DH + 4 * c), false);
+      if (rope && qvalid) v4 = rope4_in<E>(v4, rope_entry(rope, i, D, h * P::DH + 4 * c));
       qreg[4 * c + 0] = v4[0] * cl2;
       qreg[4 * c + 1] = v4[1] * cl2;
       qreg[4 * c + 2] = v4[2] * cl2;
@@ -161,12 +170,12 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
   float m_ref = 0.f, s_carry = 0.f, r_carry = 0.f, zsum = 0.f;
   if (wave_active) {
     if (t_b == 0) {
-      m_ref = halo_dot<D>(qreg, Ks, krs, rope, 0);
+      m_ref = halo_dot<D>(qreg, Ks, krs, rope_k, 0);
       s_carry = 0.0f;  // score of key 0 relative to m_ref
     } else {
       const int k0 = 32 * t_b;  // <= first query of this wave, so both halo keys are visible
-      s_carry = halo_dot<D>(qreg, Ks, krs, rope, k0);
-      const float s_prev = halo_dot<D>(qreg, Ks, krs, rope, k0 - 1);
+      s_carry = halo_dot<D>(qreg, Ks, krs, rope_k, k0);
+      const float s_prev = halo_dot<D>(qreg, Ks, krs, rope_k, k0 - 1);
       m_ref = fmaxf(s_carry, s_prev);
       float l_unused;
       seg_shares(s_prev, s_carry, fast_exp2(s_prev - m_ref), fast_exp2(s_carry - m_ref), l_unused,
@@ -195,7 +204,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
   // buffers once; the tile stores never write the pads.
   if (P::DH < 8) {
     unsigned* z = reinterpret_cast<unsigned*>(&lds_k[0][0][0]);
-    for (int e = tid; e < 2 * 3 * P::KPLANE / 2; e += 256) z[e] = 0u;
+    for (int e = tid; e < 2 * NL * P::KPLANE / 2; e += 256) z[e] = 0u;
     __syncthreads();
   }
 
@@ -218,7 +227,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
   const __amdgpu_buffer_rsrc_t kres = buffer_rsrc(Ks, (unsigned)view_rows_bytes(T, krs, D, kEsz));
   const __amdgpu_buffer_rsrc_t vres = buffer_rsrc(Vs, (unsigned)view_rows_bytes(T, vrs, D, kEsz));
   const __amdgpu_buffer_rsrc_t cres =
-      buffer_rsrc(ROPE ? rope : log_gain, ROPE ? (unsigned)(T * D * sizeof(float)) : 0u);
+      buffer_rsrc(ROPE ? rope_k : log_gain, ROPE ? (unsigned)(T * D * sizeof(float)) : 0u);
   const unsigned kstep = 32u * (unsigned)krs * kEsz, vstep = 32u * (unsigned)vrs * kEsz;
   const unsigned vrow = (unsigned)vrs * kEsz;
   unsigned koff[P::LD_PER_THREAD], csoff[P::LD_PER_THREAD], voff[P::VLD];
@@ -262,14 +271,25 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
         const int row = e / P::C4, c = e % P::C4;
         const int d = 4 * c, half = d / P::DH;
         const int off = arow_of_key(row) * P::KROW + half * 8 * P::KB + (d - half * P::DH);
-        f32x4 kv = raw_to_f32(pre_k[j], Ks);
-        if constexpr (ROPE) kv = rope4(kv, pre_cs[j], false);
-        unsigned h0, m0, l0, h1, m1, l1;
-        split_pair(kv[0], kv[1], h0, m0, l0);
-        split_pair(kv[2], kv[3], h1, m1, l1);
-        *reinterpret_cast<u32x2*>(&lds_k[buf][0][off]) = u32x2{h0, h1};
-        *reinterpret_cast<u32x2*>(&lds_k[buf][1][off]) = u32x2{m0, m1};
-        *reinterpret_cast<u32x2*>(&lds_k[buf][2][off]) = u32x2{l0, l1};
+        if constexpr (BF && !ROPE) {
+          // the raw bf16 row chunk is its own h limb
+          *reinterpret_cast<u32x2*>(&lds_k[buf][0][off]) = pre_k[j];
+        } else {
+          f32x4 kv = raw_to_f32(pre_k[j], Ks);
+          if constexpr (ROPE) kv = rope4_in<E>(kv, pre_cs[j]);
+          if constexpr (BF) {
+            // rotated and rounded to bf16: exact in one limb
+            *reinterpret_cast<u32x2*>(&lds_k[buf][0][off]) =
+                u32x2{cvt_pk_bf16(kv[0], kv[1]), cvt_pk_bf16(kv[2], kv[3])};
+          } else {
+            unsigned h0, m0, l0, h1, m1, l1;
+            split_pair(kv[0], kv[1], h0, m0, l0);
+            split_pair(kv[2], kv[3], h1, m1, l1);
+            *reinterpret_cast<u32x2*>(&lds_k[buf][0][off]) = u32x2{h0, h1};
+            *reinterpret_cast<u32x2*>(&lds_k[buf][1][off]) = u32x2{m0, m1};
+            *reinterpret_cast<u32x2*>(&lds_k[buf][2][off]) = u32x2{l0, l1};
+          }
+        }
       }
     }
 #pragma unroll
@@ -277,15 +297,26 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
       const int u = tid + 256 * j;
       if (u < P::VUNITS) {
         const int pp = u % 16, c = u / 16;
-        const f32x4 va = raw_to_f32(pre_v[j][0], Vs), vb = raw_to_f32(pre_v[j][1], Vs);
+        if constexpr (BF) {
+          // V^T row 4c + x, keys 2pp, 2pp + 1: the bf16 halves of the two rows
 #pragma unroll
-        for (int x = 0; x < 4; ++x) {
-          unsigned hv, mv, lv;
-          split_pair(va[x], vb[x], hv, mv, lv);
-          const int off = (4 * c + x) * P::VROW + 2 * pp;
-          *reinterpret_cast<unsigned*>(&lds_vt[buf][0][off]) = hv;
-          *reinterpret_cast<unsigned*>(&lds_vt[buf][1][off]) = mv;
-          *reinterpret_cast<unsigned*>(&lds_vt[buf][2][off]) = lv;
+          for (int x = 0; x < 4; ++x) {
+            const unsigned wa = pre_v[j][0][x >> 1], wb = pre_v[j][1][x >> 1];
+            const unsigned pair = (x & 1) ? ((wa >> 16) | (wb & 0xffff0000u))
+                                          : ((wa & 0xffffu) | (wb << 16));
+            *reinterpret_cast<unsigned*>(&lds_vt[buf][0][(4 * c + x) * P::VROW + 2 * pp]) = pair;
+          }
+        } else {
+          const f32x4 va = raw_to_f32(pre_v[j][0], Vs), vb = raw_to_f32(pre_v[j][1], Vs);
+#pragma unroll
+          for (int x = 0; x < 4; ++x) {
+            unsigned hv, mv, lv;
+            split_pair(va[x], vb[x], hv, mv, lv);
+            const int off = (4 * c + x) * P::VROW + 2 * pp;
+            *reinterpret_cast<unsigned*>(&lds_vt[buf][0][off]) = hv;
+            *reinterpret_cast<unsigned*>(&lds_vt[buf][1][off]) = mv;
+            *reinterpret_cast<unsigned*>(&lds_vt[buf][2][off]) = lv;
+          }
         }
       }
     }
@@ -316,11 +347,15 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
         const __bf16* krow = &lds_k[buf][0][q * P::KROW + h * 8 * P::KB];
 #pragma unroll
         for (int kb = 0; kb < P::KB; ++kb) {
-          Limbs ka;
-          ka.h = *reinterpret_cast<const bf16x8*>(krow + 8 * kb);
-          ka.m = *reinterpret_cast<const bf16x8*>(krow + P::KPLANE + 8 * kb);
-          ka.l = *reinterpret_cast<const bf16x8*>(krow + 2 * P::KPLANE + 8 * kb);
-          sacc = mfma_x6(ka, qb[kb], sacc);
+          if constexpr (BF) {
+            sacc = mfma_x3_abf(*reinterpret_cast<const bf16x8*>(krow + 8 * kb), qb[kb], sacc);
+          } else {
+            Limbs ka;
+            ka.h = *reinterpret_cast<const bf16x8*>(krow + 8 * kb);
+            ka.m = *reinterpret_cast<const bf16x8*>(krow + P::KPLANE + 8 * kb);
+            ka.l = *reinterpret_cast<const bf16x8*>(krow + 2 * P::KPLANE + 8 * kb);
+            sacc = mfma_x6(ka, qb[kb], sacc);
+          }
         }
       }
       prio_mfma_end();
@@ -407,12 +442,17 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
 #pragma unroll
         for (int mb = 0; mb < P::NMB; ++mb) {
           const __bf16* vrow = &lds_vt[buf][0][(dok ? 32 * mb + q : 0) * P::VROW + 16 * h + 8 * kb];
-          Limbs va;
-          va.h = *reinterpret_cast<const bf16x8*>(vrow);
-          va.m = *reinterpret_cast<const bf16x8*>(vrow + P::VPLANE);
-          va.l = *reinterpret_cast<const bf16x8*>(vrow + 2 * P::VPLANE);
-          if (!dok) va = Limbs{bf16x8{}, bf16x8{}, bf16x8{}};
-          acc_o[mb] = mfma_x6(va, wb, acc_o[mb]);
+          if constexpr (BF) {
+            const bf16x8 vh = dok ? *reinterpret_cast<const bf16x8*>(vrow) : bf16x8{};
+            acc_o[mb] = mfma_x3_abf(vh, wb, acc_o[mb]);
+          } else {
+            Limbs va;
+            va.h = *reinterpret_cast<const bf16x8*>(vrow);
+            va.m = *reinterpret_cast<const bf16x8*>(vrow + P::VPLANE);
+            va.l = *reinterpret_cast<const bf16x8*>(vrow + 2 * P::VPLANE);
+            if (!dok) va = Limbs{bf16x8{}, bf16x8{}, bf16x8{}};
+            acc_o[mb] = mfma_x6(va, wb, acc_o[mb]);
+          }
         }
       }
       prio_mfma_end();
@@ -527,7 +567,7 @@ hipError_t launch_fwd(const FwdIO& io, float* part, int B, int H, int T, int C,
   const int smax = fwd_max_splits(T, C);
   const int items = fwd_num_items(T, C);
   timer_begin(kFwd, stream);
-  if (io.rope)
+  if (io.rope && !io.k_rotated)
     hipLaunchKernelGGL((ca_fwd_kernel<D, E, true>), dim3(items * BH), dim3(256), 0, stream, io.q,
                        io.k, io.v, io.rope, io.log_gain, io.y, io.out, io.stats, part, BH, H, T, C,
                        G, smax);
@@ -549,8 +589,35 @@ hipError_t launch_fwd(const FwdIO& io, float* part, int B, int H, int T, int C,
   return e;
 }
 
-#define CA_INST_FWD(DD, EE) \
-  template hipError_t launch_fwd<DD, EE>(const FwdIO&, float*, int, int, int, int, hipStream_t);
+// Keys rotated once for the kernels that read them many times: row t of
+// slice bh of the key view, RoPE applied as the reference computes it in E
+// (rope4_in), written to out[bh][t][D] in E.  One thread per 4 elements.
+template <int D, class E>
+__global__ __launch_bounds__(256) void ca_rope_keys_kernel(View Kv, const float* __restrict__ rope,
+                                                           E* __restrict__ out, int BH, int H,
+                                                           int T) {
+  constexpr int C4 = D / 4;
+  const long long tix = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (tix >= (long long)BH * T * C4) return;
+  const int c = (int)(tix % C4);
+  const long long row = tix / C4;
+  const int bh = (int)(row / T), t = (int)(row % T);
+  const E* src = view_slice<const E>(Kv, bh, H) + (long long)t * Kv.rstride + 4 * c;
+  st4(out + row * D + 4 * c, rope4_in<E>(ld4(src), rope_entry(rope, t, D, 4 * c)));
+}
+
+template <int D, class E>
+hipError_t launch_rope_keys(View k, const float* rope, void* out, int BH, int H, int T,
+                            hipStream_t stream) {
+  const long long n = (long long)BH * T * (D / 4);
+  hipLaunchKernelGGL((ca_rope_keys_kernel<D, E>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     stream, k, rope, static_cast<E*>(out), BH, H, T);
+  return hipGetLastError();
+}
+
+#define CA_INST_FWD(DD, EE)                                                                       \
+  template hipError_t launch_fwd<DD, EE>(const FwdIO&, float*, int, int, int, int, hipStream_t);   \
+  template hipError_t launch_rope_keys<DD, EE>(View, const float*, void*, int, int, int, hipStream_t);
 #define CA_INST_FWD_ALL(EE) \
   CA_INST_FWD(8, EE) CA_INST_FWD(16, EE) CA_INST_FWD(32, EE) CA_INST_FWD(64, EE) CA_INST_FWD(128, EE)
 CA_INST_FWD_ALL(float)

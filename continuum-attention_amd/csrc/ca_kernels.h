@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 
+#include <type_traits>
+
 #include "../../include/continuum_attention_amd.h"
 #include "ca_common.h"
 
@@ -336,6 +338,7 @@ hipError_t launch_weights_bwd(const float* scores, const float* grad_weights, fl
 struct FwdIO {
   View q, k, v;            // inputs
   const float* rope;       // [T][D/2][2] (cos, sin) for q and k, or nullptr
+  bool k_rotated;          // k is already rotated (launch_rope_keys): rope applies to q only
   const float* log_gain;   // [H]
   float* y;                // fp32 [B,H,T,D] output (read by the backward)
   View out;                // optional copy of the output in E (base nullptr: none)
@@ -344,6 +347,7 @@ struct FwdIO {
 struct BwdIO {
   View q, k, v;            // the forward's inputs
   const float* rope;       // as in FwdIO; the gradients of q and k are rotated back
+  bool k_rotated;          // k is already rotated: rope applies to q and the gradients only
   const float* log_gain;
   const float* y;          // fp32 [B,H,T,D] forward output
   const float* stats;
@@ -355,6 +359,11 @@ struct BwdIO {
 template <int D, class E>
 hipError_t launch_fwd(const FwdIO& io, float* part, int B, int H, int T, int C,
                       hipStream_t stream);
+// Rotated keys [B*H][T][D] in E (out) from the key view k, for a forward or
+// backward that then reads them with k_rotated set.
+template <int D, class E>
+hipError_t launch_rope_keys(View k, const float* rope, void* out, int BH, int H, int T,
+                            hipStream_t stream);
 
 // Backward workspace buffers of one pass (sizes: the pass's dS blocks, limb
 // planes and qstat rows, gain partials per dQ item, dQ and dK/dV chunk
@@ -377,7 +386,14 @@ hipError_t launch_bwd_dkdv(const BwdIO& io, const BwdWork& ws, const BwdPass& pa
 // major, rows past T zero) so that the dK/dV kernel stages a tile as one
 // contiguous block with no bounds tests.
 __host__ __device__ inline int bwd_pass_tiles(const BwdPass& p) { return p.qb - p.qa; }
-__host__ __device__ constexpr int limb_tile_elems(int D) { return 6 * 32 * D; }
+// Limb planes per staged query tile: the Q limbs, then the three dY/Z limbs.
+// bf16 operands have a bf16-valued Q (RoPE included, rounded as the
+// reference rounds it), whose m and l limbs are zero: its tiles carry the h
+// plane alone.  Workspaces are sized for six planes.
+template <class E> __host__ __device__ constexpr int q_limb_planes() {
+  return std::is_same<E, __bf16>::value ? 1 : 3;
+}
+__host__ __device__ constexpr int limb_tile_elems(int D, int planes = 6) { return planes * 32 * D; }
 inline size_t bwd_limb_elems(int BH, const BwdPass& p, int D) {
   return (size_t)BH * bwd_pass_tiles(p) * limb_tile_elems(D);
 }

@@ -26,7 +26,7 @@ from torch import nn
 from torch.nn import functional as F
 
 from . import _native
-from .ops import (SUPPORTED_HEAD_DIMS, _bwd_qkv_workspace_bytes, _fwd_workspace_bytes, _mode,
+from .ops import (SUPPORTED_HEAD_DIMS, _bwd_qkv_workspace_bytes, _fwd_qkv_workspace_bytes, _mode,
                   continuum_attention)
 
 _DTYPE_CODE = {torch.float32: _native.CA_DTYPE_F32, torch.bfloat16: _native.CA_DTYPE_BF16,
@@ -242,12 +242,13 @@ def apply_rope(q, k, theta):
 _CS_CACHE: dict = {}
 
 
-def rope_cos_sin(T, D, theta, device):
-    """fp32 table ``[T, D/2, 2]`` of (cos, sin) of ``t * theta^(-2i/D)``: the
-    reference's angles before their cast to the autocast dtype
-    (cuda/continuum_attention.py:828-830); ``theta=None`` gives the identity
-    rotation (cos 1, sin 0, exact in the prologue); cached per shape."""
-    key = (T, D, None if theta is None else float(theta), device)
+def rope_cos_sin(T, D, theta, device, dtype=torch.float32):
+    """fp32 table ``[T, D/2, 2]`` of (cos, sin) of ``t * theta^(-2i/D)``, the
+    reference's angles, rounded to ``dtype`` as the reference casts them to
+    the operands' dtype (cuda/continuum_attention.py:828-830) and stored as
+    fp32; ``theta=None`` gives the identity rotation (cos 1, sin 0, exact in
+    every dtype); cached per shape and dtype."""
+    key = (T, D, None if theta is None else float(theta), device, dtype)
     cs = _CS_CACHE.get(key)
     if cs is None:
         if theta is None:
@@ -256,7 +257,8 @@ def rope_cos_sin(T, D, theta, device):
         else:
             freq = 1.0 / (theta ** (torch.arange(0, D, 2, device=device, dtype=torch.float32) / D))
             phase = torch.outer(torch.arange(T, device=device, dtype=torch.float32), freq)
-            cs = torch.stack((phase.cos(), phase.sin()), -1).contiguous()
+            cs = torch.stack((phase.cos(), phase.sin()), -1)
+            cs = cs.to(dtype).float().contiguous()
         if len(_CS_CACHE) > 64:
             _CS_CACHE.clear()
         _CS_CACHE[key] = cs
@@ -271,11 +273,14 @@ def _aligned(x, nbytes):
 class _RopeContinuumAttention(torch.autograd.Function):
     """qkv projection output -> RoPE -> CA operator -> token-major output, with
     the operator's kernels reading the projection output [B, T, 3, H, D]
-    directly (q and k rotated as they are read, in fp32) and writing the
-    output token-major in the projection's dtype (ca_fwd_qkv); the backward
-    (ca_bwd_qkv) reads the output gradient token-major and writes the qkv
-    gradient, the q and k parts rotated back.  Same result as ``apply_rope``
-    + ``continuum_attention`` + transpose, with the rotation done in fp32."""
+    directly (q and k rotated as they are read, with the reference's
+    rounding to the projection's dtype) and writing the output token-major in
+    that dtype (ca_fwd_qkv); the backward (ca_bwd_qkv) reads the output
+    gradient token-major and writes the qkv gradient, the q and k parts
+    rotated back (in fp32, rounded once).  The forward is ``apply_rope`` +
+    ``continuum_attention`` + transpose; the gradients differ from that
+    composition's only in rounding (it rounds each step of the rotation's
+    backward to the dtype)."""
 
     @staticmethod
     def forward(ctx, qkv, log_gain, theta, heads, query_tile):
@@ -293,12 +298,12 @@ class _RopeContinuumAttention(torch.autograd.Function):
         D = C // heads
         dev, dt = qkv.device, _DTYPE_CODE[qkv.dtype]
         x = _aligned(qkv.detach(), 16)
-        cs = rope_cos_sin(T, D, theta, dev) if theta is not None else None
+        cs = rope_cos_sin(T, D, theta, dev, qkv.dtype) if theta is not None else None
         gain = log_gain.detach().float().contiguous()
         y = torch.empty(Bsz, heads, T, D, device=dev, dtype=torch.float32)
         out = torch.empty(Bsz, T, C, device=dev, dtype=qkv.dtype)
         stats = torch.empty(Bsz * heads * T, 2, device=dev, dtype=torch.float32)
-        nbytes = _fwd_workspace_bytes(Bsz, heads, T, D)
+        nbytes = _fwd_qkv_workspace_bytes(Bsz, heads, T, D)
         ws = torch.empty(max(nbytes, 1), device=dev, dtype=torch.uint8)
         with _native.on_device(dev):
             _native.check(lib.ca_fwd_qkv(x.data_ptr(), dt, cs.data_ptr() if cs is not None else None,

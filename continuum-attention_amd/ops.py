@@ -77,6 +77,11 @@ def _bwd_qkv_workspace_bytes(B: int, H: int, T: int, D: int) -> int:
     return int(_native.load().ca_bwd_qkv_workspace_bytes(B, H, T, D))
 
 
+@functools.lru_cache(maxsize=256)
+def _fwd_qkv_workspace_bytes(B: int, H: int, T: int, D: int) -> int:
+    return int(_native.load().ca_fwd_qkv_workspace_bytes(B, H, T, D))
+
+
 def set_workspace_cap(nbytes: int) -> None:
     """Bounds the operator's device workspace (bytes; 0 = no bound; default
     1 GiB, or the environment's ``CA_WORKSPACE_CAP_MB``), the role
@@ -86,6 +91,7 @@ def set_workspace_cap(nbytes: int) -> None:
     _native.check(_native.load().ca_set_workspace_cap(int(nbytes)))
     _fwd_workspace_bytes.cache_clear()
     _bwd_workspace_bytes.cache_clear()
+    _fwd_qkv_workspace_bytes.cache_clear()
 
 
 def workspace_cap() -> int:

@@ -135,17 +135,26 @@ int ca_weights_bwd_f32(const float* scores, const float* grad_weights, float* we
  * token-major [B, T, H*D] in the same type, ready for the output projection.
  * rope_cs is the fp32 table [T][D/2][2] = (cos, sin) of t * theta^(-2i/D)
  * for interleaved pairs (cuda/continuum_attention.py:826-835); NULL means no
- * rotation.  The rotation is computed in fp32.  y is the fp32 [B, H, T, D]
- * output the backward needs (as ca_fwd_f32's `out`); stats as in ca_fwd_f32.
- * Workspaces are ca_fwd_workspace_bytes / ca_bwd_workspace_bytes of
- * (B, H, T, D).  D in {8, 16, 32, 64, 128}; qkv, out, dout and dqkv 8-byte
- * (16-bit types) or 16-byte (fp32) aligned, y 16-byte aligned.
+ * rotation.  The rotation is computed as the reference computes it in the
+ * operand type: for bf16 and fp16, q * cos and rotate(q) * sin each rounded
+ * to that type and then their sum (pass the table's values rounded to the
+ * type, as the reference casts cos and sin, to reproduce its rotation bit for
+ * bit); for fp32 in fp32.  The gradients' rotation back is computed in fp32
+ * and rounded once.  y is the fp32 [B, H, T, D] output the backward needs
+ * (as ca_fwd_f32's `out`); stats as in ca_fwd_f32.  The forward's workspace
+ * is ca_fwd_qkv_workspace_bytes (with RoPE it starts with the keys rotated
+ * once for the kernels; a workspace of ca_fwd_workspace_bytes also works,
+ * the kernels then rotate every staged key tile).  D in {8, 16, 32, 64,
+ * 128}; qkv, out, dout and dqkv 8-byte (16-bit types) or 16-byte (fp32)
+ * aligned, y 16-byte aligned.  One head's key and value rows of qkv must
+ * span less than 4 GiB (CA_ERR_UNSUPPORTED otherwise).
  * Replaces: the reshape/permute/unbind of the projection, apply_rope, the
  * operator, and the transpose/reshape of its output in
  * ContinuumSelfAttention.forward (cuda/continuum_attention.py:848-854), and
  * their autograd. */
 enum { CA_DTYPE_F32 = 0, CA_DTYPE_BF16 = 1, CA_DTYPE_F16 = 2 };
 
+size_t ca_fwd_qkv_workspace_bytes(int B, int H, int T, int D);
 int ca_fwd_qkv(const void* qkv, int dtype, const float* rope_cs, const float* log_gain, float* y,
                void* out, float* stats, void* workspace, size_t workspace_bytes, int B, int T,
                int H, int D, void* stream);
@@ -154,7 +163,9 @@ int ca_fwd_qkv(const void* qkv, int dtype, const float* rope_cs, const float* lo
  * (dtype; the gradients of q and k rotated back by the transposed RoPE) and
  * dlog_gain[H].  It runs in one pass (gradients in the element type are not
  * summed over passes), so its workspace is ca_bwd_qkv_workspace_bytes,
- * regardless of the cap. */
+ * regardless of the cap (with RoPE it also holds the keys rotated once; a
+ * workspace without that room, ca_bwd_qkv_workspace_bytes minus
+ * B*H*T*D*4 bytes rounded up to 256, also works). */
 size_t ca_bwd_qkv_workspace_bytes(int B, int H, int T, int D);
 int ca_bwd_qkv(const void* qkv, int dtype, const float* rope_cs, const float* log_gain,
                const float* y, const float* stats, const void* dout, void* dqkv,

@@ -205,9 +205,14 @@ def test_workspace_cap_bounds_the_sizes(ca):
         assert lib.ca_bwd_workspace_bytes(1, 16, 32768, 64) <= 1 << 30
         assert lib.ca_fwd_workspace_bytes(1, 16, 32768, 64) <= 1 << 30
         small = lib.ca_bwd_workspace_bytes(2, 16, 2048, 64)
-        assert small == lib.ca_bwd_qkv_workspace_bytes(2, 16, 2048, 64)  # fits: one pass
+        # the token-major entry points add room for the keys rotated once
+        # ([B*H][T][D], 4-byte elements, rounded up to 256 bytes)
+        rot = 2 * 16 * 2048 * 64 * 4
+        assert lib.ca_bwd_qkv_workspace_bytes(2, 16, 2048, 64) == small + rot  # fits: one pass
+        assert lib.ca_fwd_qkv_workspace_bytes(2, 16, 2048, 64) == \
+            rot + lib.ca_fwd_workspace_bytes(2, 16, 2048, 64)
         ca.ops.set_workspace_cap(0)
-        assert lib.ca_bwd_workspace_bytes(1, 16, 32768, 64) == full
+        assert lib.ca_bwd_workspace_bytes(1, 16, 32768, 64) == full - 16 * 32768 * 64 * 4
         assert lib.ca_fwd_workspace_bytes(1, 16, 32768, 64) > 1 << 30
         ca.ops.set_workspace_cap(32 << 20)
         assert lib.ca_bwd_workspace_bytes(1, 2, 8192, 64) <= 32 << 20

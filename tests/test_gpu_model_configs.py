@@ -53,13 +53,6 @@ def heads(qkv, H):
     return qkv.float().view(B, T, 3, H, C3 // (3 * H)).permute(2, 0, 3, 1, 4).unbind(0)
 
 
-def rotate_fp32(x, cs):
-    """Interleaved-pair rotation with the fp32 (cos, sin) table [T, D/2, 2]."""
-    x0, x1 = x[..., 0::2], x[..., 1::2]
-    c, s = cs[..., 0], cs[..., 1]
-    return torch.stack((x0 * c - x1 * s, x1 * c + x0 * s), -1).flatten(-2)
-
-
 def attention_vs_oracle(q, k, v, log_gain, y_tokens, rows, bar):
     """Sampled rows of every (b, h) slice of the [B, T, H*D] attention output
     against the float64 row oracle."""
@@ -174,8 +167,10 @@ def test_config4_ca_s_step(gpu_ca):
     assert all(torch.isfinite(p).all() for p in model.parameters())
     assert store["y"].dtype == torch.bfloat16
     q, k, v = heads(store["qkv"], cfg.n_heads)
-    cs = Dm.rope_cos_sin(cfg.block_size, cfg.d_model // cfg.n_heads, cfg.rope_theta, q.device)
-    q, k = rotate_fp32(q, cs), rotate_fp32(k, cs)
+    # RoPE as the reference computes it under bf16 autocast (the kernels' own
+    # rotation): in bf16, cuda/continuum_attention.py:826-835
+    qb, kb = Dm.apply_rope(q.to(torch.bfloat16), k.to(torch.bfloat16), cfg.rope_theta)
+    q, k = qb.float(), kb.float()
     rows = np.array([0, 1, 2, 63, 64, 511, 1024, 1535, 2046, 2047])
     # the output is rounded to bf16: half an ulp (2^-9 relative) per element
     attention_vs_oracle(q, k, v, torch.zeros(cfg.n_heads), store["y"], rows, 4e-3)

@@ -240,8 +240,11 @@ def _unfused_attention(Dm, qkv, log_gain, theta, heads):
     return y.transpose(1, 2).reshape(Bsz, T, C3 // 3)
 
 
-def _qkv_call(ca, qkv, gain, cs, H, dout):
-    """ca_fwd_qkv + ca_bwd_qkv through the C ABI: (y fp32 heads, out, dqkv, dgain)."""
+def _qkv_call(ca, qkv, gain, cs, H, dout, rotate_keys_first=(False, True)):
+    """ca_fwd_qkv + ca_bwd_qkv through the C ABI: (y fp32 heads, out, dqkv, dgain).
+    rotate_keys_first: (forward, backward) workspaces with room for the keys
+    rotated once (ca_fwd_qkv_workspace_bytes / ca_bwd_qkv_workspace_bytes), or
+    without it (the kernels then rotate the keys they read)."""
     lib = ca.native.load()
     Bsz, T, C3 = qkv.shape
     D = C3 // 3 // H
@@ -250,12 +253,15 @@ def _qkv_call(ca, qkv, gain, cs, H, dout):
     out = torch.empty(Bsz, T, H * D, device="cuda", dtype=qkv.dtype)
     st = torch.empty(Bsz * H * T, 2, device="cuda")
     s = torch.cuda.current_stream().cuda_stream
-    nf = lib.ca_fwd_workspace_bytes(Bsz, H, T, D)
+    nf = (lib.ca_fwd_qkv_workspace_bytes if rotate_keys_first[0] else lib.ca_fwd_workspace_bytes)(
+        Bsz, H, T, D)
     wf = torch.empty(max(nf, 1), device="cuda", dtype=torch.uint8)
     csp = cs.data_ptr() if cs is not None else None
     ca.native.check(lib.ca_fwd_qkv(qkv.data_ptr(), code, csp, gain.data_ptr(), y.data_ptr(),
                                    out.data_ptr(), st.data_ptr(), wf.data_ptr(), nf, Bsz, T, H, D, s))
     nb = lib.ca_bwd_qkv_workspace_bytes(Bsz, H, T, D)
+    if not rotate_keys_first[1]:
+        nb -= (Bsz * H * T * D * 4 + 255) // 256 * 256
     wb = torch.empty(nb, device="cuda", dtype=torch.uint8)
     dqkv = torch.empty_like(qkv)
     dg = torch.empty(H, device="cuda")
@@ -322,12 +328,36 @@ def test_qkv_entry_points_match_the_operator(gpu_ca, D, T, splits):
         gpu_ca.ops.set_split_override(0, 0, 0)
 
 
+@pytest.mark.parametrize("D,T", [(64, 300), (16, 77), (128, 130)])
+def test_qkv_keys_rotated_once_match_in_kernel_rotation(gpu_ca, D, T):
+    """With RoPE the token-major entry points rotate the keys once into their
+    workspace when it has the room, else the kernels rotate the keys they
+    read: the same arithmetic (the reference's rounding to the operand type),
+    so outputs and gradients agree bit for bit, for each operand type."""
+    say(f"[case] keys rotated once vs in-kernel, D={D} T={T}")
+    Bsz, H = 2, 3
+    g = torch.Generator().manual_seed(3 * D + T)
+    gain = torch.tensor([0.0, 0.3, -0.25], device="cuda")
+    for dt in (torch.float32, torch.bfloat16, torch.float16):
+        qkv = (torch.randn(Bsz, T, 3 * H * D, generator=g) * 1.3).to(dt).cuda()
+        dout = torch.randn(Bsz, T, H * D, generator=g).to(dt).cuda()
+        cs = gpu_ca.decoder.rope_cos_sin(T, D, 10000.0, qkv.device, dt)
+        a = _qkv_call(gpu_ca, qkv, gain, cs, H, dout, (True, True))
+        b = _qkv_call(gpu_ca, qkv, gain, cs, H, dout, (False, False))
+        for x, y in zip(a, b):
+            assert torch.equal(x, y), dt
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_fused_rope_attention_vs_unfused(gpu_ca, dtype):
     """The decoder's fused prologue/epilogue against the reference composition
     (apply_rope + operator + transpose): outputs and gradients of qkv and the
-    gains.  fp32: RoPE rounding only; bf16: the composition's RoPE rounds to
-    bf16 (cuda/continuum_attention.py:826-835), the fused one stays fp32."""
+    gains.  fp32: RoPE rounding only.  bf16: both rotate as the reference does
+    in bf16 (cuda/continuum_attention.py:826-835) and the fused kernels skip
+    the zero limb products of the bf16-valued operands, so the output and the
+    gain gradient are the composition's bit for bit; the qkv gradient differs
+    by the rotation backward's rounding (the composition rounds each of its
+    steps to bf16, the fused epilogue rotates in fp32 and rounds once)."""
     say(f"[case] fused rope attention {dtype}")
     Dm = gpu_ca.decoder
     torch.manual_seed(8)
@@ -344,10 +374,12 @@ def test_fused_rope_attention_vs_unfused(gpu_ca, dtype):
         assert y.dtype == dtype and y.shape == (Bsz, T, H * D)
         ga, gb = torch.autograd.grad(y, (a, b), dout)
         res[name] = [t.float().cpu().numpy() for t in (y.detach(), ga, gb)]
-    tol = (2e-5, 2e-4) if dtype == torch.float32 else (2e-2, 5e-2)
     errs = [rel(x, r) for x, r in zip(res["fused"], res["unfused"])]
     say(f"   out {errs[0]:.2e} dqkv {errs[1]:.2e} dgain {errs[2]:.2e}")
-    assert errs[0] <= tol[0] and errs[1] <= tol[1] and errs[2] <= tol[1]
+    if dtype == torch.float32:
+        assert errs[0] <= 2e-5 and errs[1] <= 2e-4 and errs[2] <= 2e-4
+    else:
+        assert errs[0] == 0.0 and errs[2] == 0.0 and errs[1] <= 2e-2
 
 
 def _rmsnorm_composition(x, w, eps):
