@@ -34,8 +34,17 @@ struct Bwd {
   static constexpr int CPT = (CHUNKS + 255) / 256;
 };
 
+// Waves per SIMD the register budget is set for: bf16 operands need fewer
+// limb registers and fit three (165 VGPRs at D = 64, 41 KB of LDS per work
+// group), which hides more of the segment math's latency (one CA-S layer:
+// 0.137 -> 0.132 ms); fp32 and fp16 operands keep two.
 template <int D, class E>
-__global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_bwd_dkdv_kernel(
+constexpr int dkdv_waves_per_simd() {
+  return D > 64 ? 1 : (q_limb_planes<E>() == 1 ? 3 : 2);
+}
+
+template <int D, class E>
+__global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, E>())) void ca_bwd_dkdv_kernel(
     View Kv, View Vv, const float* __restrict__ rope, const float* __restrict__ rope_k,
     const __bf16* __restrict__ limbs,
     const float* __restrict__ qstat, const float* __restrict__ log_gain, View dKv, View dVv,
