@@ -131,10 +131,19 @@ ca::DqSplit dq_split_for(int BH, int T, int D, const ca::BwdPass& p, bool for_si
   const int res = for_sizing ? kDqSplitBound : (D > 64 ? dq_resident_groups() * 2 / 3 : dq_resident_groups());
   return ca::dq_split(BH, T, p, res);
 }
-ca::DkdvSplit dkdv_split_for(int BH, int D, const ca::BwdPass& p, bool for_sizing) {
+ca::DkdvSplit dkdv_split_for(int BH, int D, int dtype, const ca::BwdPass& p, bool for_sizing) {
   if (g_split.dkdv_tiles > 0) return ca::dkdv_split_chunk(p, g_split.dkdv_tiles);
-  // D = 128: one dK/dV work group per CU instead of two (registers and LDS)
-  const int res = for_sizing ? kDqSplitBound : (D > 64 ? dkdv_resident_groups() / 2 : dkdv_resident_groups());
+  // D = 128: one dK/dV work group per CU instead of two (registers and LDS).
+  // bf16 operands at D <= 64: three per CU, and the split test asks for 1.5
+  // rounds of them (9/4 of the two-per-CU count; at [1,16,2048,64] chunks of
+  // 16 tiles took 0.277 ms per fwd+bwd against 0.283 ms for 24 and 0.281 ms
+  // for 12, while fp32 operands keep 24: 0.302 ms against 0.306 ms for 16).
+  int res = kDqSplitBound;
+  if (!for_sizing) {
+    const int two_per_cu = dkdv_resident_groups();
+    res = D > 64 ? two_per_cu / 2 : dtype == CA_DTYPE_BF16 ? std::min(two_per_cu * 9 / 4, kDqSplitBound)
+                                                           : two_per_cu;
+  }
   return ca::dkdv_split(BH, p, res);
 }
 
@@ -146,7 +155,7 @@ struct BwdLayout {
 BwdLayout bwd_layout(int B, int H, int T, int D, const ca::BwdPass& p) {
   const int BH = B * H;
   const ca::DqSplit sp = dq_split_for(BH, T, D, p, true);  // the largest split
-  const ca::DkdvSplit kvs = dkdv_split_for(BH, D, p, true);
+  const ca::DkdvSplit kvs = dkdv_split_for(BH, D, CA_DTYPE_F32, p, true);
   BwdLayout L;
   L.ds = 0;
   L.limbs = align256((size_t)BH * p.ds_slice * sizeof(float));
@@ -451,7 +460,7 @@ int bwd_common(const ca::BwdIO& io, int dtype, void* workspace, size_t workspace
     work.dq_part = reinterpret_cast<float*>(ws + L.dqpart);
     work.kv_part = reinterpret_cast<float*>(ws + L.kvpart);
     const ca::DqSplit sp = dq_split_for(B * H, T, D, pass, false);
-    const ca::DkdvSplit kvs = dkdv_split_for(B * H, D, pass, false);
+    const ca::DkdvSplit kvs = dkdv_split_for(B * H, D, dtype, pass, false);
     hipError_t e;
     if (dtype == CA_DTYPE_BF16) e = bwd_launch<__bf16>(D, io, work, pass, sp, kvs, B, H, T, s);
     else if (dtype == CA_DTYPE_F16) e = bwd_launch<_Float16>(D, io, work, pass, sp, kvs, B, H, T, s);

@@ -82,6 +82,13 @@ def _fwd_qkv_workspace_bytes(B: int, H: int, T: int, D: int) -> int:
     return int(_native.load().ca_fwd_qkv_workspace_bytes(B, H, T, D))
 
 
+def _clear_workspace_sizes() -> None:
+    # the sizes follow the workspace cap and the split override
+    for f in (_fwd_workspace_bytes, _bwd_workspace_bytes, _fwd_qkv_workspace_bytes,
+              _bwd_qkv_workspace_bytes):
+        f.cache_clear()
+
+
 def set_workspace_cap(nbytes: int) -> None:
     """Bounds the operator's device workspace (bytes; 0 = no bound; default
     1 GiB, or the environment's ``CA_WORKSPACE_CAP_MB``), the role
@@ -89,9 +96,7 @@ def set_workspace_cap(nbytes: int) -> None:
     the forward uses longer work splits and the backward runs in passes over
     query ranges.  Process-wide."""
     _native.check(_native.load().ca_set_workspace_cap(int(nbytes)))
-    _fwd_workspace_bytes.cache_clear()
-    _bwd_workspace_bytes.cache_clear()
-    _fwd_qkv_workspace_bytes.cache_clear()
+    _clear_workspace_sizes()
 
 
 def workspace_cap() -> int:
@@ -106,8 +111,7 @@ def set_split_override(fwd_split_tiles: int = 0, dq_chunk_stages: int = 0,
     at a small shape.  Clears the cached workspace sizes, which follow it."""
     _native.check(_native.load().ca_debug_set_splits(int(fwd_split_tiles), int(dq_chunk_stages),
                                                      int(dkdv_chunk_tiles)))
-    _fwd_workspace_bytes.cache_clear()
-    _bwd_workspace_bytes.cache_clear()
+    _clear_workspace_sizes()
 
 
 def _check_device(*ts: torch.Tensor) -> torch.device:

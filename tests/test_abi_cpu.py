@@ -224,3 +224,31 @@ def test_workspace_cap_bounds_the_sizes(ca):
         assert lib.ca_fwd_workspace_bytes(1, 2, 8192, 64) == 0  # unsplit forward
     finally:
         ca.ops.set_workspace_cap(prev)
+
+
+def test_workspace_size_caches_follow_the_cap_and_splits(ca):
+    # the Python side caches every workspace size; changing the cap or the
+    # split override must drop all four caches
+    ops = ca.ops
+    shape = (1, 2, 8192, 64)
+    sizes = (ops._fwd_workspace_bytes, ops._bwd_workspace_bytes, ops._fwd_qkv_workspace_bytes,
+             ops._bwd_qkv_workspace_bytes)
+    prev = ops.workspace_cap()
+    try:
+        ops.set_workspace_cap(0)
+        before = [f(*shape) for f in sizes]
+        ops.set_workspace_cap(32 << 20)
+        after = [f(*shape) for f in sizes]
+        assert after[1] < before[1]  # passes over query ranges
+        assert after[3] == before[3]  # the token-major backward runs in one pass
+        lib = ca.native.load()
+        assert after == [lib.ca_fwd_workspace_bytes(*shape), lib.ca_bwd_workspace_bytes(*shape),
+                         lib.ca_fwd_qkv_workspace_bytes(*shape), lib.ca_bwd_qkv_workspace_bytes(*shape)]
+        ops.set_split_override(4, 0, 0)
+        forced = [f(*shape) for f in sizes]
+        assert forced[0] == lib.ca_fwd_workspace_bytes(*shape) != after[0]
+        assert forced == [lib.ca_fwd_workspace_bytes(*shape), lib.ca_bwd_workspace_bytes(*shape),
+                          lib.ca_fwd_qkv_workspace_bytes(*shape), lib.ca_bwd_qkv_workspace_bytes(*shape)]
+    finally:
+        ops.set_split_override(0, 0, 0)
+        ops.set_workspace_cap(prev)
