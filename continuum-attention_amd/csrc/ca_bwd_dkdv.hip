@@ -50,10 +50,12 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, E>())) void ca_bwd_dkd
     const float* __restrict__ qstat, const float* __restrict__ log_gain, View dKv, View dVv,
     float* __restrict__ dsbuf, float* __restrict__ kv_part, float* __restrict__ gain_part,
     BwdPass pass, int BH, int H, int T, int chunk, int n_items, int n_part) {
-  // bf16 operands: Q (rotated and rounded as the reference rounds it) and V
-  // are bf16-valued, so the tile carries Q's h limb alone and the products
-  // with Q or V skip their zero limb products (limb_step_used), with the same
-  // sums bit for bit.  K enters S scaled by the head's gain, in three limbs.
+  // bf16 operands: Q, K (rotated and rounded as the reference rounds them)
+  // and V are bf16-valued, so the tile carries Q's h limb alone and the
+  // products with Q or V skip their zero limb products (limb_step_used), with
+  // the same sums bit for bit; S is q.k of the h limbs, scaled after the
+  // product.  Other operand types: K enters S scaled by the head's gain, in
+  // three limbs.
   constexpr bool BF = q_limb_planes<E>() == 1;
   using P = Bwd<D, q_limb_planes<E>()>;
   __shared__ __attribute__((aligned(16))) __bf16 tiles[2][P::TILE];
@@ -97,8 +99,9 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, E>())) void ca_bwd_dkd
   }
 
   // K (rotated here when `rope_k`; otherwise it arrives rotated, or without
-  // RoPE; then scaled by c log2e) and V of this lane's
-  // slot: B operands of S / dP', k block kb, element e = d 32kb + 8g + e.
+  // RoPE; then scaled by c log2e, except bf16 operands, whose scores are
+  // scaled after the product) and V of this lane's slot: B operands of S /
+  // dP', k block kb, element e = d 32kb + 8g + e.
   Limbs kl[P::KB], vl[P::KB];
 #pragma unroll
   for (int kb = 0; kb < P::KB; ++kb) {
@@ -113,7 +116,7 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, E>())) void ca_bwd_dkd
       const bool ok2 = ok && d0 + 4 * h2 < D;
       f32x4 a = ok2 ? ld4(kp + 4 * h2) : f32x4{0.f, 0.f, 0.f, 0.f};
       if (rope_k && ok2) a = rope4_in<E>(a, rope_entry(rope_k, krow, D, d0 + 4 * h2));
-      a *= cl2;
+      if (!BF) a *= cl2;
       const f32x4 b = ok2 ? ld4(vp + 4 * h2) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -199,10 +202,15 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, E>())) void ca_bwd_dkd
       const __bf16* Ty = &tiles[buf][(P::PLANES - 3) * P::LIMB];
 
       // ---- S - m and dP' - Dl/Z (row blocks rb: queries i0 + 16rb + 4g + r) ----
-      f32x4 sacc[2], pacc[2];
+      // bf16 operands: S accumulates q.k from zero (Q and K bf16-valued: the
+      // h limb product alone) and takes c log2e and -m in one fused
+      // multiply-add; otherwise K carries c log2e and the accumulator starts
+      // from -m.
+      f32x4 sacc[2], pacc[2], negm[2];
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb) {
-        sacc[rb] = *reinterpret_cast<const f32x4*>(&tstat[buf][0][16 * rb + 4 * g]);
+        negm[rb] = *reinterpret_cast<const f32x4*>(&tstat[buf][0][16 * rb + 4 * g]);
+        sacc[rb] = BF ? f32x4{0.f, 0.f, 0.f, 0.f} : negm[rb];
         pacc[rb] = *reinterpret_cast<const f32x4*>(&tstat[buf][1][16 * rb + 4 * g]);
       }
       prio_mfma_begin();
@@ -228,14 +236,20 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, E>())) void ca_bwd_dkd
         // four independent accumulators per limb product
 #pragma unroll
         for (int st = 0; st < 6; ++st) {
-          if (limb_step_used<BF, false>(st)) sacc[0] = mfma16_step(st, qa[0], kl[kb], sacc[0]);
+          if (limb_step_used<BF, BF>(st)) sacc[0] = mfma16_step(st, qa[0], kl[kb], sacc[0]);
           if (limb_step_used<false, BF>(st)) pacc[0] = mfma16_step(st, ya[0], vl[kb], pacc[0]);
-          if (limb_step_used<BF, false>(st)) sacc[1] = mfma16_step(st, qa[1], kl[kb], sacc[1]);
+          if (limb_step_used<BF, BF>(st)) sacc[1] = mfma16_step(st, qa[1], kl[kb], sacc[1]);
           if (limb_step_used<false, BF>(st)) pacc[1] = mfma16_step(st, ya[1], vl[kb], pacc[1]);
         }
       }
       prio_mfma_end();
       prio_valu_begin();
+      if (BF) {
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sacc[rb][r] = fmaf(sacc[rb][r], cl2, negm[rb][r]);
+      }
 
       // ---- segments along the slots (adjacent lanes of each DPP row) ----
       // Tiles where every slot key is visible to every query, with no key 0

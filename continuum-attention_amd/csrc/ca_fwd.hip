@@ -151,7 +151,10 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
   const int head = bh % H;
   const float cl2 = head_scale_log2(log_gain, head, D);
 
-  // lane (q,h) holds Q[i][h*DH + k] * c*log2e
+  // lane (q,h) holds Q[i][h*DH + k].  The scores are scaled after the
+  // product, as the reference scales q.k (s = c log2e (q.k) - m_ref, one
+  // fused multiply-add per score): bf16 operands then stay bf16-valued, and
+  // their S^T takes one limb product per k block.
   float qreg[P::DH];
   {
     const E* qp = Qs + (long long)(qvalid ? i : 0) * Qv.rstride + h * P::DH;
@@ -159,10 +162,10 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
     for (int c = 0; c < P::CH; ++c) {
       f32x4 v4 = qvalid ? ld4(qp + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
       if (rope && qvalid) v4 = rope4_in<E>(v4, rope_entry(rope, i, D, h * P::DH + 4 * c));
-      qreg[4 * c + 0] = v4[0] * cl2;
-      qreg[4 * c + 1] = v4[1] * cl2;
-      qreg[4 * c + 2] = v4[2] * cl2;
-      qreg[4 * c + 3] = v4[3] * cl2;
+      qreg[4 * c + 0] = v4[0];
+      qreg[4 * c + 1] = v4[1];
+      qreg[4 * c + 2] = v4[2];
+      qreg[4 * c + 3] = v4[3];
     }
   }
 
@@ -170,12 +173,12 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
   float m_ref = 0.f, s_carry = 0.f, r_carry = 0.f, zsum = 0.f;
   if (wave_active) {
     if (t_b == 0) {
-      m_ref = halo_dot<D>(qreg, Ks, krs, rope_k, 0);
+      m_ref = halo_dot<D>(qreg, Ks, krs, rope_k, 0) * cl2;
       s_carry = 0.0f;  // score of key 0 relative to m_ref
     } else {
       const int k0 = 32 * t_b;  // <= first query of this wave, so both halo keys are visible
-      s_carry = halo_dot<D>(qreg, Ks, krs, rope_k, k0);
-      const float s_prev = halo_dot<D>(qreg, Ks, krs, rope_k, k0 - 1);
+      s_carry = halo_dot<D>(qreg, Ks, krs, rope_k, k0) * cl2;
+      const float s_prev = halo_dot<D>(qreg, Ks, krs, rope_k, k0 - 1) * cl2;
       m_ref = fmaxf(s_carry, s_prev);
       float l_unused;
       seg_shares(s_prev, s_carry, fast_exp2(s_prev - m_ref), fast_exp2(s_carry - m_ref), l_unused,
@@ -184,7 +187,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
     }
   }
 
-  // B operand of S^T in limbs: k block kb, element e = Q[i][h*DH + 8kb + e] * c*log2e
+  // B operand of S^T in limbs: k block kb, element e = Q[i][h*DH + 8kb + e]
   Limbs qb[P::KB];
 #pragma unroll
   for (int kb = 0; kb < P::KB; ++kb) {
@@ -337,18 +340,19 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
     auto tile = [&](auto general_tag) {
       constexpr bool kGeneral = decltype(general_tag)::value;
       const bool diag = kGeneral && (t == wave_tmax);
-      // ---- S^T = K Q^T - m_ref (log2 units; the row shift rides in the
-      //      accumulator so the MFMA returns s - m directly) ----
+      // ---- S^T = c log2e (K Q^T) - m_ref (log2 units; the scale and the
+      //      row shift are one fused multiply-add per score) ----
       f32x16 sacc;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[r] = -m_ref;
+      for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
       prio_mfma_begin();
       {
         const __bf16* krow = &lds_k[buf][0][q * P::KROW + h * 8 * P::KB];
 #pragma unroll
         for (int kb = 0; kb < P::KB; ++kb) {
           if constexpr (BF) {
-            sacc = mfma_x3_abf(*reinterpret_cast<const bf16x8*>(krow + 8 * kb), qb[kb], sacc);
+            // both operands bf16-valued: the h limbs carry the whole product
+            sacc = mfma_bf16(*reinterpret_cast<const bf16x8*>(krow + 8 * kb), qb[kb].h, sacc);
           } else {
             Limbs ka;
             ka.h = *reinterpret_cast<const bf16x8*>(krow + 8 * kb);
@@ -360,6 +364,8 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
       }
       prio_mfma_end();
       prio_valu_begin();
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[r] = fmaf(sacc[r], cl2, -m_ref);
       const int kbase = 32 * t + 1 + 16 * h;  // score key of register 0
       // ---- row max of the tile (visible keys only), relative to m_ref ----
       float mt = kNegBig;

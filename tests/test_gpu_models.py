@@ -281,8 +281,12 @@ def test_qkv_entry_points_match_the_operator(gpu_ca, D, T, splits):
     operator's kernels on the same values, so for fp32, bf16 and fp16 qkv:
     y is bitwise the operator's output on the upcast q, k, v; the token-major
     output is y rounded to the dtype; dqkv is the operator's gradients
-    rounded to the dtype.  With RoPE, against the operator on q, k rotated in
-    fp32 beforehand (rounding-level differences only).  Forced splits run the
+    rounded to the dtype.  bf16 is the exception for the gradients: its dK/dV
+    kernel forms q.k of the bf16 values and scales it after the product,
+    where the fp32 kernel scales k first, so its scores differ in fp32
+    rounding and a few gradient elements round to the neighbouring bf16
+    value.  With RoPE, against the operator on q, k rotated in fp32
+    beforehand (rounding-level differences only).  Forced splits run the
     combine and merge kernels' token-major writes."""
     say(f"[case] qkv entry points D={D} T={T} splits {splits}")
     Dm = gpu_ca.decoder
@@ -302,8 +306,15 @@ def test_qkv_entry_points_match_the_operator(gpu_ca, D, T, splits):
             assert torch.equal(y, yr), dt
             assert torch.equal(out, yr.transpose(1, 2).reshape(Bsz, T, H * D).to(dt)), dt
             ref = torch.stack((dq, dk, dv), 2).transpose(1, 3).reshape(Bsz, T, 3 * H * D).to(dt)
-            assert torch.equal(dqkv, ref), dt
-            assert torch.equal(dg, dgr), dt
+            if dt == torch.bfloat16:
+                unequal = (dqkv != ref).float().mean().item()
+                e_q = rel(dqkv.float().cpu().numpy(), ref.float().cpu().numpy())
+                e_g = rel(dg.cpu().numpy(), dgr.cpu().numpy())
+                say(f"   bf16: {unequal:.2e} of dqkv differ, rel {e_q:.1e}; dgain rel {e_g:.1e}")
+                assert unequal <= 0.02 and e_q <= 2.0 ** -7 and e_g <= 1e-5
+            else:
+                assert torch.equal(dqkv, ref), dt
+                assert torch.equal(dg, dgr), dt
         # RoPE in the kernels vs rotating first
         qkv = (torch.randn(Bsz, T, 3 * H * D, generator=g) * 1.3).cuda()
         dout = torch.randn(Bsz, T, H * D, generator=g).cuda()
@@ -354,8 +365,10 @@ def test_fused_rope_attention_vs_unfused(gpu_ca, dtype):
     (apply_rope + operator + transpose): outputs and gradients of qkv and the
     gains.  fp32: RoPE rounding only.  bf16: both rotate as the reference does
     in bf16 (cuda/continuum_attention.py:826-835) and the fused kernels skip
-    the zero limb products of the bf16-valued operands, so the output and the
-    gain gradient are the composition's bit for bit; the qkv gradient differs
+    the zero limb products of the bf16-valued operands, so the output is the
+    composition's bit for bit; the gain gradient differs in fp32 rounding
+    (the fused dK/dV kernel scales q.k after the product, as bf16 operands
+    allow, the composition's fp32 kernel scales k first), and the qkv gradient
     by the rotation backward's rounding (the composition rounds each of its
     steps to bf16, the fused epilogue rotates in fp32 and rounds once)."""
     say(f"[case] fused rope attention {dtype}")
@@ -379,7 +392,7 @@ def test_fused_rope_attention_vs_unfused(gpu_ca, dtype):
     if dtype == torch.float32:
         assert errs[0] <= 2e-5 and errs[1] <= 2e-4 and errs[2] <= 2e-4
     else:
-        assert errs[0] == 0.0 and errs[2] == 0.0 and errs[1] <= 2e-2
+        assert errs[0] == 0.0 and errs[2] <= 1e-5 and errs[1] <= 2e-2
 
 
 def _rmsnorm_composition(x, w, eps):
