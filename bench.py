@@ -116,37 +116,51 @@ def cpu_baseline(reps=3):
                     "(cuda/run.sh:8) is overridden"}
 
 
-def _timed_steps(ca, step, steps, warmup):
-    """Runs `warmup` untimed and `steps` timed calls of step(i); returns
-    (ms per step from HIP events on the current stream, CA kernel ms per step).
-    The CA kernel time comes from a separate instrumented run of the same
-    number of steps, so the per-kernel events do not load the timed steps."""
+def _time_steps(step, steps, warmup, first=0):
+    """Runs `warmup` untimed and `steps` timed calls of step(i), i counting
+    from `first`; returns (ms per step from HIP events on the current stream,
+    the last step's output)."""
     import torch
     for i in range(warmup):
-        step(i)
+        step(first + i)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for i in range(steps):
-        out = step(i)
+        out = step(first + warmup + i)
     e1.record()
     torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
+    return e0.elapsed_time(e1) / steps, out
+
+
+def _ca_kernel_ms(ca, step, steps, first=0):
+    """CA kernel ms per step of an instrumented run of `steps` calls (its
+    per-kernel events do not load the timed steps)."""
+    import torch
     ca.native.timing_enable(True)
     for i in range(steps):
-        step(warmup + steps + i)
+        step(first + i)
     torch.cuda.synchronize()
     kt = ca.native.timing_read()
     ca.native.timing_enable(False)
-    ca_ms = sum(t for t, c in kt.values()) / steps
-    return ms, ca_ms, out
+    return sum(t for t, c in kt.values()) / steps
+
+
+def _timed_steps(ca, step, steps, warmup):
+    """(ms per step, CA kernel ms per step, last output) of step(i)."""
+    ms, out = _time_steps(step, steps, warmup)
+    return ms, _ca_kernel_ms(ca, step, steps, warmup + steps), out
 
 
 def bench_ca_s(ca, dev, steps=20, warmup=5):
     """one CA-S decoder training step (101,205,120 params,
     T=2048, batch 1, bf16 autocast with fp32 CA scores, AdamW + clip 1.0 as
     the library's fused HIP optimizer) on uniform-random bytes, random-init
-    weights."""
+    weights.  The timed step is decoder.GraphedTrainStep: forward and backward
+    replayed as one HIP graph, then the eager clip + AdamW (the eager step
+    issues ~270 launches from Python, and on a slow host its launch time
+    exceeds its GPU time); the eager step's time and its CA kernel time are
+    reported beside it."""
     import torch
     Dm = ca.decoder
     torch.manual_seed(0)
@@ -156,11 +170,16 @@ def bench_ca_s(ca, dev, steps=20, warmup=5):
     opt = Dm.build_fused_adamw(model)
     g = torch.Generator().manual_seed(1)
     batches = [torch.randint(0, 256, (1, cfg.block_size), generator=g).to(dev) for _ in range(4)]
-    ms, ca_ms, loss = _timed_steps(ca, lambda i: Dm.train_step(model, opt, batches[i % 4]), steps,
-                                   warmup)
+    eager_ms, ca_ms, _ = _timed_steps(ca, lambda i: Dm.train_step(model, opt, batches[i % 4]),
+                                      steps, warmup)
+    # the graph holds the gradient buffers from here on (no eager step after it)
+    graphed = Dm.GraphedTrainStep(model, opt, batches[0])
+    ms, loss = _time_steps(lambda i: graphed(batches[i % 4]), steps, warmup)
+    del graphed
     tokens = cfg.block_size
     res = {"metric": "CA-S tokens/s", "tokens_per_s": round(tokens / (ms * 1e-3), 1),
            "ms_per_step": round(ms, 3), "ca_kernels_ms_per_step": round(ca_ms, 3),
+           "eager_ms_per_step": round(eager_ms, 3), "step": "GraphedTrainStep",
            "steps": steps, "warmup": warmup, "params": nparams, "loss": round(float(loss), 4),
            "dtype": "bf16 autocast, f32 CA scores", "data": "synthetic uniform bytes",
            "config": {"workload": "CA-S decoder train step (BASELINE config 4)", "d_model": cfg.d_model,
