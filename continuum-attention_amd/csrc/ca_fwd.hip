@@ -102,8 +102,18 @@ __device__ __forceinline__ float halo_dot(const float* qreg, const E* __restrict
   return acc + xhalf(acc);
 }
 
+// Waves per SIMD the register budget is set for: bf16 operands stage one
+// limb plane and take one product per k block of S, so with keys rotated
+// beforehand (no table reads) they fit four (128 VGPRs, 20 KB of LDS per
+// work group; one CA-S layer's forward 0.0708 -> 0.0689 ms), with in-kernel
+// key rotation three; other operand types two.
 template <int D, class E, bool ROPE>
-__global__ __launch_bounds__(256, D > 64 ? 1 : 2) void ca_fwd_kernel(
+constexpr int fwd_waves_per_simd() {
+  return D > 64 ? 1 : std::is_same<E, __bf16>::value ? (ROPE ? 3 : 4) : 2;
+}
+
+template <int D, class E, bool ROPE>
+__global__ __launch_bounds__(256, (fwd_waves_per_simd<D, E, ROPE>())) void ca_fwd_kernel(
     View Qv, View Kv, View Vv, const float* __restrict__ rope, const float* __restrict__ log_gain,
     float* __restrict__ O, View Ov, float* __restrict__ stats, float* __restrict__ part, int BH,
     int H, int T, int C, int G, int smax) {
