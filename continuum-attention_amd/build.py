@@ -45,8 +45,8 @@ _FINITE_MATH = ["-fno-honor-nans", "-fno-honor-infinities"]
 # The attention kernels contract multiply-adds only within one source
 # expression (their fused multiply-adds are written as fmaf): every template
 # instantiation (fp32, bf16, fp16 operands; each head dim) then rounds the same
-# arithmetic the same way, so the bf16 kernels, which skip the zero limb
-# products of bf16-valued operands, return the fp32 kernels' results on the
+# arithmetic the same way, so the bf16 forward, which skips the zero limb
+# products of bf16-valued operands, returns the fp32 forward's results on the
 # same values bit for bit.  Measured: the same instruction counts in the tile
 # loops as contraction across statements.
 _ATTN = _FINITE_MATH + ["-ffp-contract=on"]
