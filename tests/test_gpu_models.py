@@ -339,6 +339,35 @@ def test_qkv_entry_points_match_the_operator(gpu_ca, D, T, splits):
         gpu_ca.ops.set_split_override(0, 0, 0)
 
 
+def test_qkv_bf16_at_the_ca_s_layer_shape(gpu_ca):
+    """One CA-S layer's shape, [1,16,2048,64], through the token-major entry
+    points in bf16 with the automatic work splits (bf16 dK/dV takes 16-tile
+    chunks there, the fp32 kernels 24) against the fp32 operator on the same
+    values (pinned against the oracle by the parity tests): the output equal
+    bit for bit, the gradients within bf16 rounding of the fp32 operator's
+    and the gain gradient within fp32 rounding."""
+    say("[case] bf16 qkv entry points at [1,16,2048,64]")
+    Bsz, T, H, D = 1, 2048, 16, 64
+    g = torch.Generator().manual_seed(64)
+    gain = (torch.randn(H, generator=g) * 0.3).cuda()
+    qkv = (torch.randn(Bsz, T, 3 * H * D, generator=g) * 1.3).to(torch.bfloat16).cuda()
+    dout = torch.randn(Bsz, T, H * D, generator=g).to(torch.bfloat16).cuda()
+    y, out, dqkv, dg = _qkv_call(gpu_ca, qkv, gain, None, H, dout)
+    q, k, v = (t.contiguous() for t in qkv.float().view(Bsz, T, 3, H, D).permute(2, 0, 3, 1, 4))
+    dyh = dout.float().view(Bsz, T, H, D).transpose(1, 2).contiguous()
+    yr, st = gpu_ca.ca_forward(q, k, v, gain)
+    dq, dk, dv, dgr = gpu_ca.ca_backward(q, k, v, gain, yr, st, dyh)
+    assert torch.equal(y, yr)
+    ref = torch.stack((dq, dk, dv), 2).transpose(1, 3).reshape(Bsz, T, 3 * H * D)
+    ref16 = ref.to(torch.bfloat16)
+    unequal = (dqkv != ref16).float().mean().item()
+    e_q = rel(dqkv.float().cpu().numpy(), ref.cpu().numpy())
+    e_g = rel(dg.cpu().numpy(), dgr.cpu().numpy())
+    say(f"   {unequal:.2e} of dqkv differ from the rounded fp32 gradients, rel {e_q:.1e}; "
+        f"dgain rel {e_g:.1e}")
+    assert unequal <= 0.02 and e_q <= 2.0 ** -7 and e_g <= 1e-5
+
+
 @pytest.mark.parametrize("D,T", [(64, 300), (16, 77), (128, 130)])
 def test_qkv_keys_rotated_once_match_in_kernel_rotation(gpu_ca, D, T):
     """With RoPE the token-major entry points rotate the keys once into their
