@@ -35,16 +35,27 @@ struct Bwd {
 };
 
 // Waves per SIMD the register budget is set for: bf16 operands need fewer
-// limb registers and fit three (165 VGPRs at D = 64, 41 KB of LDS per work
+// limb registers and fit three (156 VGPRs at D = 64, 41 KB of LDS per work
 // group), which hides more of the segment math's latency (one CA-S layer:
-// 0.137 -> 0.132 ms); fp32 and fp16 operands keep two.
-template <int D, class E>
+// 0.137 -> 0.132 ms); fp32 and fp16 operands keep two, except the
+// single-buffered variant (SB): one staged tile (31 KB) and no register
+// prefetch, three waves (168 VGPRs).  SB loads each tile after the previous
+// one is done, so its load latency is covered only by the other resident
+// work groups: it pays on split (small) grids, where the longer residency
+// hides more ([1,16,2048,64] fp32 dK/dV 0.161 -> 0.155 ms), and breaks even
+// at config 2, which keeps the double-buffered kernel.
+template <int D, class E, bool SB>
 constexpr int dkdv_waves_per_simd() {
-  return D > 64 ? 1 : (q_limb_planes<E>() == 1 ? 3 : 2);
+  return D > 64 ? 1 : (q_limb_planes<E>() == 1 || SB) ? 3 : 2;
+}
+// the single-buffered variant is built for fp32 operands at D = 64
+template <int D, class E>
+constexpr bool dkdv_has_single_buffer() {
+  return D == 64 && std::is_same<E, float>::value;
 }
 
-template <int D, class E>
-__global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, E>())) void ca_bwd_dkdv_kernel(
+template <int D, class E, bool SB>
+__global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, E, SB>())) void ca_bwd_dkdv_kernel(
     View Kv, View Vv, const float* __restrict__ rope, const float* __restrict__ rope_k,
     const __bf16* __restrict__ limbs,
     const float* __restrict__ qstat, const float* __restrict__ log_gain, View dKv, View dVv,
@@ -58,10 +69,11 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, E>())) void ca_bwd_dkd
   // three limbs.
   constexpr bool BF = q_limb_planes<E>() == 1;
   using P = Bwd<D, q_limb_planes<E>()>;
-  __shared__ __attribute__((aligned(16))) __bf16 tiles[2][P::TILE];
+  constexpr int NBUF = SB ? 1 : 2;
+  __shared__ __attribute__((aligned(16))) __bf16 tiles[NBUF][P::TILE];
   // per staged row: -m (tstat[b][0][row]) and -Dl/Z (tstat[b][1][row]), in
   // the order of the S / dP' accumulator registers
-  __shared__ __attribute__((aligned(16))) float tstat[2][2][32];
+  __shared__ __attribute__((aligned(16))) float tstat[NBUF][2][32];
 
   const int nkb = bwd_num_key_blocks(T);
   const int bh = blockIdx.x % BH;
@@ -95,7 +107,7 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, E>())) void ca_bwd_dkd
   // Stale LDS bits must not reach an MFMA as NaN through padding columns.
   {
     unsigned* z = reinterpret_cast<unsigned*>(&tiles[0][0]);
-    for (int e = tid; e < 2 * P::TILE / 2; e += 256) z[e] = 0u;
+    for (int e = tid; e < NBUF * P::TILE / 2; e += 256) z[e] = 0u;
   }
 
   // K (rotated here when `rope_k`; otherwise it arrives rotated, or without
@@ -192,8 +204,8 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, E>())) void ca_bwd_dkd
   __syncthreads();
 
   for (int qt = qt0; qt < qt_end; ++qt) {
-    const int buf = (qt - qt0) & 1;
-    if (qt + 1 < qt_end) load_tile(qt + 1);
+    const int buf = SB ? 0 : (qt - qt0) & 1;
+    if (!SB && qt + 1 < qt_end) load_tile(qt + 1);
     const int i0 = 32 * qt;
     // the wave's block meets this tile (and exists)
     const bool work = kb16 < nkb && kBwdKeys * kb16 <= i0 + 31;
@@ -349,7 +361,15 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, E>())) void ca_bwd_dkd
       prio_mfma_end();
     }
     ds_tile += (size_t)kDsColFloats * kBwdKeys * ds_kb_count(qt);
-    if (qt + 1 < qt_end) store_tile(buf ^ 1);
+    if (SB) {
+      if (qt + 1 < qt_end) {
+        __syncthreads();  // every wave is done with the tile
+        load_tile(qt + 1);
+        store_tile(0);
+      }
+    } else if (qt + 1 < qt_end) {
+      store_tile(buf ^ 1);
+    }
     __syncthreads();
   }
 
@@ -430,7 +450,11 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, E>())) void ca_bwd_dkd
 template <int D, class E>
 hipError_t launch_bwd_dkdv(const BwdIO& io, const BwdWork& ws, const BwdPass& pass,
                            const DkdvSplit& kvs, int BH, int H, int T, hipStream_t stream) {
-  hipLaunchKernelGGL((ca_bwd_dkdv_kernel<D, E>), dim3(kvs.items * BH), dim3(256), 0, stream, io.k,
+  // split grids take the single-buffered variant where it is built
+  const bool sb = dkdv_has_single_buffer<D, E>() && kvs.chunk < pass.qb - pass.qa;
+  auto kernel = sb ? ca_bwd_dkdv_kernel<D, E, dkdv_has_single_buffer<D, E>()>
+                   : ca_bwd_dkdv_kernel<D, E, false>;
+  hipLaunchKernelGGL(kernel, dim3(kvs.items * BH), dim3(256), 0, stream, io.k,
                      io.v, io.rope, io.k_rotated ? nullptr : io.rope, ws.limbs, ws.qstat,
                      io.log_gain, io.dk, io.dv, ws.dsbuf,
                      ws.kv_part, ws.gain_part, pass, BH, H, T, kvs.chunk, kvs.items,
