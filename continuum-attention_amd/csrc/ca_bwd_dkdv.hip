@@ -39,11 +39,12 @@ struct Bwd {
 // group), which hides more of the segment math's latency (one CA-S layer:
 // 0.137 -> 0.132 ms); fp32 and fp16 operands keep two, except the
 // single-buffered variant (SB): one staged tile (31 KB) and no register
-// prefetch, three waves (168 VGPRs).  SB loads each tile after the previous
-// one is done, so its load latency is covered only by the other resident
-// work groups: it pays on split (small) grids, where the longer residency
-// hides more ([1,16,2048,64] fp32 dK/dV 0.161 -> 0.155 ms), and breaks even
-// at config 2, which keeps the double-buffered kernel.
+// prefetch across the tile's work, three waves (168 VGPRs).  SB issues the
+// next tile's loads when its own products are issued, waits at the barrier
+// for the other waves, then stores: the load latency overlaps the barrier
+// wait and the other resident work groups' work.  fp32 at D = 64 runs it on
+// every grid (config 2 dK/dV 0.309 -> 0.291 ms, [1,16,2048,64] 0.162 ->
+// 0.161 ms against the double-buffered two-wave kernel on one box).
 template <int D, class E, bool SB>
 constexpr int dkdv_waves_per_simd() {
   return D > 64 ? 1 : (q_limb_planes<E>() == 1 || SB) ? 3 : 2;
@@ -363,8 +364,8 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, E, SB>())) void ca_bwd
     ds_tile += (size_t)kDsColFloats * kBwdKeys * ds_kb_count(qt);
     if (SB) {
       if (qt + 1 < qt_end) {
+        load_tile(qt + 1);  // issued before the barrier: its latency overlaps the wait
         __syncthreads();  // every wave is done with the tile
-        load_tile(qt + 1);
         store_tile(0);
       }
     } else if (qt + 1 < qt_end) {
@@ -450,8 +451,8 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, E, SB>())) void ca_bwd
 template <int D, class E>
 hipError_t launch_bwd_dkdv(const BwdIO& io, const BwdWork& ws, const BwdPass& pass,
                            const DkdvSplit& kvs, int BH, int H, int T, hipStream_t stream) {
-  // split grids take the single-buffered variant where it is built
-  const bool sb = dkdv_has_single_buffer<D, E>() && kvs.chunk < pass.qb - pass.qa;
+  // the single-buffered variant wherever it is built
+  const bool sb = dkdv_has_single_buffer<D, E>();
   auto kernel = sb ? ca_bwd_dkdv_kernel<D, E, dkdv_has_single_buffer<D, E>()>
                    : ca_bwd_dkdv_kernel<D, E, false>;
   hipLaunchKernelGGL(kernel, dim3(kvs.items * BH), dim3(256), 0, stream, io.k,
