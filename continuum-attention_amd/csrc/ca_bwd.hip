@@ -197,8 +197,9 @@ struct DqP {
   static constexpr int STAGE = 3 * PLANE;
 };
 
+// bf16 operands (the h plane of K alone) are held to four waves per SIMD
 template <int D, class E, bool ROPE>
-__global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict__ dsbuf,
+__global__ __launch_bounds__(256, (std::is_same<E, __bf16>::value && D <= 64 ? 4 : 1)) void ca_bwd_dq_kernel(const float* __restrict__ dsbuf,
                                                         View Kv, const float* __restrict__ rope,
                                                         const float* __restrict__ log_gain,
                                                         View dQv, float* __restrict__ dq_part,
@@ -275,7 +276,14 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
   typedef typename Raw4<E>::type R4;
   R4 pre[P::UPT];
   f32x4 pre_cs[ROPE ? P::UPT : 1];
-  const f32x4 kref = k_row4(kDqRows * qg, 4 * (tid % P::C4));
+  // bf16 operands: the keys are bf16-valued, and so are the stage's rows
+  // without the k_ref shift: they are staged as their h plane alone, each
+  // dS limb times k is exact in fp32, and the products with the zero m and l
+  // limbs are skipped (the shift, which keeps near-coinciding keys' products
+  // small, matters at fp32 key spacings; bf16 keys differ by at least 2^-8
+  // of their size, so the unshifted sum loses at most 2^-16 of it)
+  constexpr bool BF = std::is_same<E, __bf16>::value;
+  const f32x4 kref = BF ? f32x4{0.f, 0.f, 0.f, 0.f} : k_row4(kDqRows * qg, 4 * (tid % P::C4));
   // K rows (and RoPE table rows) through buffer resources: a stage's offsets
   // are the thread's fixed offsets plus one uniform step per stage, and rows
   // at or past T read as zeros.  Those rows become -k_ref after the shift and
@@ -313,14 +321,19 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
       if (P::UNITS % 256 == 0 || u < P::UNITS) {
         f32x4 kx = raw_to_f32(pre[uu], Ks);
         if constexpr (ROPE) kx = rope4_in<E>(kx, pre_cs[uu]);
-        const f32x4 kv = kx - kref;
-        unsigned h0, m0, l0, h1, m1, l1;
-        split_pair(kv[0], kv[1], h0, m0, l0);
-        split_pair(kv[2], kv[3], h1, m1, l1);
         const int off = buf * P::STAGE + (u / P::C4) * P::LDK + 4 * (u % P::C4);
-        *reinterpret_cast<u32x2*>(&kst[off]) = u32x2{h0, h1};
-        *reinterpret_cast<u32x2*>(&kst[off + P::PLANE]) = u32x2{m0, m1};
-        *reinterpret_cast<u32x2*>(&kst[off + 2 * P::PLANE]) = u32x2{l0, l1};
+        if constexpr (BF) {
+          *reinterpret_cast<u32x2*>(&kst[off]) =
+              u32x2{cvt_pk_bf16(kx[0], kx[1]), cvt_pk_bf16(kx[2], kx[3])};
+        } else {
+          const f32x4 kv = kx - kref;
+          unsigned h0, m0, l0, h1, m1, l1;
+          split_pair(kv[0], kv[1], h0, m0, l0);
+          split_pair(kv[2], kv[3], h1, m1, l1);
+          *reinterpret_cast<u32x2*>(&kst[off]) = u32x2{h0, h1};
+          *reinterpret_cast<u32x2*>(&kst[off + P::PLANE]) = u32x2{m0, m1};
+          *reinterpret_cast<u32x2*>(&kst[off + 2 * P::PLANE]) = u32x2{l0, l1};
+        }
       }
     }
   };
@@ -375,12 +388,18 @@ __global__ __launch_bounds__(256) void ca_bwd_dq_kernel(const float* __restrict_
         const int o1 = o0 + 4 * P::LDK;
         Limbs bl;
         bl.h = lds_read_tr8(kb_base + o0, kb_base + o1);
-        bl.m = lds_read_tr8(kb_base + P::PLANE + o0, kb_base + P::PLANE + o1);
-        bl.l = lds_read_tr8(kb_base + 2 * P::PLANE + o0, kb_base + 2 * P::PLANE + o1);
+        if (BF) {
+          bl.m = bl.l = bf16x8{};
+        } else {
+          bl.m = lds_read_tr8(kb_base + P::PLANE + o0, kb_base + P::PLANE + o1);
+          bl.l = lds_read_tr8(kb_base + 2 * P::PLANE + o0, kb_base + 2 * P::PLANE + o1);
+        }
 #pragma unroll
         for (int st = 0; st < 6; ++st) {
-          acc[0][nb] = mfma16_step(st, al0, bl, acc[0][nb]);
-          acc[1][nb] = mfma16_step(st, al1, bl, acc[1][nb]);
+          if (limb_step_used<false, BF>(st)) {
+            acc[0][nb] = mfma16_step(st, al0, bl, acc[0][nb]);
+            acc[1][nb] = mfma16_step(st, al1, bl, acc[1][nb]);
+          }
         }
       }
     }
