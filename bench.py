@@ -194,8 +194,11 @@ def bench_ca_s(ca, dev, steps=20, warmup=5):
 def bench_ca_p(ca, dev, steps=30, warmup=10):
     """small CA-P decoder (TinyLM backbone with 4 blocks,
     d 256, 4 heads, fixed tau 0.30, T=512, batch 16), one fp32 step on
-    uniform-random bytes, random-init weights."""
+    uniform-random bytes, random-init weights.  Timed as
+    decoder.GraphedTrainStep (forward and backward replayed as one HIP graph,
+    the clip + AdamW eager), with the eager step's time beside it."""
     import torch
+    import torch.nn.functional as F
     A = ca.architecture
     torch.manual_seed(0)
     model = A.TinyLM(variant="P", backend="hip", seq_len=512, width=256, hidden=720, heads=4,
@@ -208,15 +211,31 @@ def bench_ca_p(ca, dev, steps=30, warmup=10):
     # (3.54 against 3.77 ms/step measured)
     prev_blas = torch.backends.cuda.preferred_blas_library()
     torch.backends.cuda.preferred_blas_library("cublas")
+    step_kind = "GraphedTrainStep"
     try:
-        ms, ca_ms, loss = _timed_steps(
+        eager_ms, ca_ms, loss = _timed_steps(
             ca, lambda i: A.train_step(model, opt, data[i % 4][:, :-1], data[i % 4][:, 1:]), steps,
             warmup)
+        ms = eager_ms
+        # the same step replayed as one HIP graph (forward + backward), the
+        # clip + AdamW eager after it; a capture the graph step refuses keeps
+        # the eager time
+        loss_fn = lambda m, x, t: F.cross_entropy(m(x).reshape(-1, 256), t.reshape(-1))
+        try:
+            graphed = ca.decoder.GraphedTrainStep(model, opt, (data[0][:, :-1], data[0][:, 1:]),
+                                                  amp_dtype=None, loss_fn=loss_fn)
+        except ValueError:
+            step_kind = "eager"
+        else:
+            ms, loss = _time_steps(lambda i: graphed(data[i % 4][:, :-1], data[i % 4][:, 1:]),
+                                   steps, warmup)
+            del graphed
     finally:
         torch.backends.cuda.preferred_blas_library(prev_blas)
     tokens = 16 * 512
     res = {"metric": "CA-P tokens/s", "tokens_per_s": round(tokens / (ms * 1e-3), 1),
            "ms_per_step": round(ms, 3), "ca_kernels_ms_per_step": round(ca_ms, 3),
+           "eager_ms_per_step": round(eager_ms, 3), "step": step_kind,
            "steps": steps, "warmup": warmup, "params": A.parameters(model),
            "loss": round(float(loss), 4), "dtype": "f32", "data": "synthetic uniform bytes",
            "config": {"workload": "CA-P TinyLM train step (BASELINE config 3)", "layers": 4,

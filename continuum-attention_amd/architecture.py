@@ -246,6 +246,29 @@ class Block(nn.Module):
         return x + self.mlp(self.norm_mlp(x))
 
 
+class _TokenEmbedding(torch.autograd.Function):
+    """The token lookup ``weight[tokens]`` with its weight gradient formed as
+    ``one_hot(tokens)^T @ grad`` (a scatter of ones into a zeroed matrix, then
+    one GEMM): deterministic, and free of the sorting path torch's embedding
+    backward takes above 3072 lookups, which records memset nodes that HIP
+    graph replays do not reliably redo.  Same values as nn.Embedding's
+    gradient up to the summation order of the rows of equal tokens."""
+
+    @staticmethod
+    def forward(ctx, tokens, weight):
+        ctx.save_for_backward(tokens)
+        ctx.num = weight.shape[0]
+        return F.embedding(tokens, weight)
+
+    @staticmethod
+    def backward(ctx, grad):
+        (tokens,) = ctx.saved_tensors
+        flat = tokens.reshape(-1, 1)
+        onehot = torch.zeros(flat.shape[0], ctx.num, device=grad.device, dtype=grad.dtype)
+        onehot.scatter_(1, flat, 1.0)
+        return None, onehot.t().mm(grad.reshape(-1, grad.shape[-1]))
+
+
 class TinyLM(nn.Module):
     """Pre-norm byte LM with learned positions and a tied head
     (architecture.py:180-241).  ``layers`` defaults to the reference's six
@@ -278,7 +301,9 @@ class TinyLM(nn.Module):
         if length > self.seq_len:
             raise ValueError("Sequence exceeds model seq_len")
         pos = torch.arange(length, device=tokens.device)
-        x = self.tok_embed(tokens) + self.pos_embed(pos)[None, :, :]
+        tok = (_TokenEmbedding.apply(tokens, self.tok_embed.weight) if tokens.is_cuda
+               else self.tok_embed(tokens))
+        x = tok + self.pos_embed(pos)[None, :, :]
         blocks = [getattr(self, f"b{i}") for i in range(self.layers)]
         if self.final_norm._fusable(x):
             # the blocks' chain x = x + attn(norm_attn(x)); x = x + mlp(norm_mlp(x)),

@@ -737,14 +737,17 @@ def test_graphed_train_step_matches_eager(gpu_ca):
         assert worst <= 1e-6, worst
 
 
-def test_graphed_tinylm_step_matches_eager(gpu_ca):
+@pytest.mark.parametrize("batch", [6, 16])
+def test_graphed_tinylm_step_matches_eager(gpu_ca, batch):
     """GraphedTrainStep with a caller's loss (TinyLM's next-byte cross-entropy
     on (inputs, targets)), fp32 without autocast, a tied head and FusedAdamW's
     two parameter groups under a global clip, against the eager step over
-    three replays; 3072 token lookups per step, the most whose embedding
-    backward records no memset node (a larger batch's capture holds one and is
-    refused before it is instantiated)."""
-    say("[case] graphed TinyLM step vs eager (B 6, T 512)")
+    three replays; at batch 16 (8192 token lookups, the CA-P configuration)
+    TinyLM's one-hot token-embedding gradient keeps the capture free of the
+    memset nodes torch's sorting embedding backward records, which a direct
+    nn.Embedding lookup of that size still does (that capture is refused
+    before it is instantiated)."""
+    say(f"[case] graphed TinyLM step vs eager (B {batch}, T 512)")
     A, Dm = gpu_ca.architecture, gpu_ca.decoder
     torch.manual_seed(31)
     kw = dict(variant="P", backend="hip", seq_len=512, width=64, hidden=128, heads=4,
@@ -753,7 +756,7 @@ def test_graphed_tinylm_step_matches_eager(gpu_ca):
     mb.load_state_dict(ma.state_dict())
     oa, ob = A.build_fused_adamw(ma), A.build_fused_adamw(mb)
     g = torch.Generator().manual_seed(32)
-    data = [torch.randint(0, 256, (6, 513), generator=g).cuda() for _ in range(3)]
+    data = [torch.randint(0, 256, (batch, 513), generator=g).cuda() for _ in range(3)]
     loss_fn = lambda m, x, t: F.cross_entropy(m(x).reshape(-1, 256), t.reshape(-1))
     step = Dm.GraphedTrainStep(ma, oa, (data[0][:, :-1], data[0][:, 1:]), amp_dtype=None,
                                grad_clip=0.5, loss_fn=loss_fn)
@@ -767,10 +770,12 @@ def test_graphed_tinylm_step_matches_eager(gpu_ca):
         worst = max(((pa - pb).abs().max() / pb.abs().max()).item()
                     for pa, pb in zip(ma.parameters(), mb.parameters()))
         assert worst <= 1e-6, worst
-    say("[case] graphed TinyLM step refused at B 16 (8192 lookups)")
-    big = torch.randint(0, 256, (16, 513), generator=g).cuda()
-    with pytest.raises(ValueError, match="memset node"):
-        Dm.GraphedTrainStep(mb, ob, (big[:, :-1], big[:, 1:]), amp_dtype=None, loss_fn=loss_fn)
+    if batch == 16:
+        say("[case] graphed step with a direct nn.Embedding lookup of 8192 tokens refused")
+        lookup = lambda m, x, t: m.tok_embed(x).square().mean()
+        with pytest.raises(ValueError, match="memset node"):
+            Dm.GraphedTrainStep(mb, ob, (data[0][:, :-1], data[0][:, 1:]), amp_dtype=None,
+                                loss_fn=lookup)
 
 
 @pytest.mark.parametrize("variant", ["P", "R", "S", "H"])

@@ -218,3 +218,24 @@ def test_graph_memset_node_count(Dm, monkeypatch):
     graphs[4] = [("k", None), ("c", None)]
     nodes[401], nodes[402] = (0, None), (1, None)
     assert Dm._hip_graph_memset_nodes(FakeGraph(4)) == 0
+
+
+def test_token_embedding_gradient_matches_nn_embedding():
+    """TinyLM's GPU token lookup (architecture._TokenEmbedding: the weight
+    gradient as one_hot(tokens)^T @ grad) gives nn.Embedding's output and
+    weight gradient, repeated tokens included (run here on CPU tensors)."""
+    import importlib
+    A = importlib.import_module("continuum-attention_amd.architecture")
+    g = torch.Generator().manual_seed(5)
+    w = torch.randn(256, 24, generator=g, dtype=torch.float64)
+    tokens = torch.randint(0, 256, (7, 300), generator=g)
+    tokens[0, :50] = 3  # many repeats of one token
+    up = torch.randn(7, 300, 24, generator=g, dtype=torch.float64)
+    wa = w.clone().requires_grad_(True)
+    ya = A._TokenEmbedding.apply(tokens, wa)
+    (ga,) = torch.autograd.grad(ya, (wa,), up)
+    wb = w.clone().requires_grad_(True)
+    yb = torch.nn.functional.embedding(tokens, wb)
+    (gb,) = torch.autograd.grad(yb, (wb,), up)
+    assert torch.equal(ya, yb)
+    assert torch.allclose(ga, gb, rtol=1e-12, atol=1e-12)
