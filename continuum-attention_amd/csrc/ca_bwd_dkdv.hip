@@ -226,7 +226,7 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, E, SB>())) void ca_bwd
         sacc[rb] = BF ? f32x4{0.f, 0.f, 0.f, 0.f} : negm[rb];
         pacc[rb] = *reinterpret_cast<const f32x4*>(&tstat[buf][1][16 * rb + 4 * g]);
       }
-      prio_mfma_begin();
+      prio_mfma_begin<!BF>();
 #pragma unroll
       for (int kb = 0; kb < P::KB; ++kb) {
         const int col = 32 * kb + 8 * g;
@@ -255,8 +255,7 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, E, SB>())) void ca_bwd
           if (limb_step_used<false, BF>(st)) pacc[1] = mfma16_step(st, ya[1], vl[kb], pacc[1]);
         }
       }
-      prio_mfma_end();
-      prio_valu_begin();
+      prio_mfma_end<!BF>();
       if (BF) {
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb)
@@ -335,8 +334,7 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, E, SB>())) void ca_bwd
         xd[e] = dout_s[e >> 2][e & 3];
       }
       const Limbs wb = split8(xw), db = split8(xd);
-      prio_valu_end();
-      prio_mfma_begin();
+      prio_mfma_begin<!BF>();
       const int src_row = 4 * g + (j >> 2), src_col = 4 * (j & 3);
 #pragma unroll
       for (int mb = 0; mb < P::NMB; ++mb) {
@@ -359,7 +357,7 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, E, SB>())) void ca_bwd
           if (limb_step_used<BF, false>(st)) acck[mb] = mfma16_step(st, qa, db, acck[mb]);
         }
       }
-      prio_mfma_end();
+      prio_mfma_end<!BF>();
     }
     ds_tile += (size_t)kDsColFloats * kBwdKeys * ds_kb_count(qt);
     if (SB) {

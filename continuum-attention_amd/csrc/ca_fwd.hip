@@ -355,7 +355,7 @@ __global__ __launch_bounds__(256, (fwd_waves_per_simd<D, E, ROPE>())) void ca_fw
       f32x16 sacc;
 #pragma unroll
       for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
-      prio_mfma_begin();
+      prio_mfma_begin<!BF>();
       {
         const __bf16* krow = &lds_k[buf][0][q * P::KROW + h * 8 * P::KB];
 #pragma unroll
@@ -372,8 +372,7 @@ __global__ __launch_bounds__(256, (fwd_waves_per_simd<D, E, ROPE>())) void ca_fw
           }
         }
       }
-      prio_mfma_end();
-      prio_valu_begin();
+      prio_mfma_end<!BF>();
 #pragma unroll
       for (int r = 0; r < 16; ++r) sacc[r] = fmaf(sacc[r], cl2, -m_ref);
       const int kbase = 32 * t + 1 + 16 * h;  // score key of register 0
@@ -445,8 +444,7 @@ __global__ __launch_bounds__(256, (fwd_waves_per_simd<D, E, ROPE>())) void ca_fw
       r_carry = xr15;
       sacc[0] += r_in;
       zsum += zt + r_in;
-      prio_valu_end();
-      prio_mfma_begin();
+      prio_mfma_begin<!BF>();
 
       // ---- O^T += V^T W^T: k block kb, element e = weight key 16h + 8kb + e ----
 #pragma unroll
@@ -471,7 +469,7 @@ __global__ __launch_bounds__(256, (fwd_waves_per_simd<D, E, ROPE>())) void ca_fw
           }
         }
       }
-      prio_mfma_end();
+      prio_mfma_end<!BF>();
     };
     if (wave_active && t <= wave_tmax) {
       if (t == 0 || t == wave_tmax)
