@@ -246,13 +246,22 @@ class Block(nn.Module):
         return x + self.mlp(self.norm_mlp(x))
 
 
+# Largest vocabulary whose embedding gradient is formed as a one-hot GEMM
+# (its [tokens, vocab] one-hot matrix costs O(tokens * vocab)); the byte
+# vocabulary (256) is far below it.
+ONE_HOT_MAX_VOCAB = 4096
+
+
 class _TokenEmbedding(torch.autograd.Function):
     """The token lookup ``weight[tokens]`` with its weight gradient formed as
     ``one_hot(tokens)^T @ grad`` (a scatter of ones into a zeroed matrix, then
     one GEMM): deterministic, and free of the sorting path torch's embedding
     backward takes above 3072 lookups, which records memset nodes that HIP
     graph replays do not reliably redo.  Same values as nn.Embedding's
-    gradient up to the summation order of the rows of equal tokens."""
+    gradient up to the summation order of the rows of equal tokens, for
+    finite gradients; a non-finite gradient row reaches every vocabulary row
+    (0 * inf is NaN in the GEMM) where nn.Embedding's touches only the looked-up
+    row.  Used for vocabularies of at most ONE_HOT_MAX_VOCAB rows."""
 
     @staticmethod
     def forward(ctx, tokens, weight):
@@ -301,7 +310,8 @@ class TinyLM(nn.Module):
         if length > self.seq_len:
             raise ValueError("Sequence exceeds model seq_len")
         pos = torch.arange(length, device=tokens.device)
-        tok = (_TokenEmbedding.apply(tokens, self.tok_embed.weight) if tokens.is_cuda
+        tok = (_TokenEmbedding.apply(tokens, self.tok_embed.weight)
+               if tokens.is_cuda and self.tok_embed.num_embeddings <= ONE_HOT_MAX_VOCAB
                else self.tok_embed(tokens))
         x = tok + self.pos_embed(pos)[None, :, :]
         blocks = [getattr(self, f"b{i}") for i in range(self.layers)]

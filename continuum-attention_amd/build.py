@@ -5,6 +5,7 @@ The shared library is written next to this file and loaded by _native.py.
 """
 from __future__ import annotations
 
+import concurrent.futures
 import os
 import shutil
 import subprocess
@@ -66,24 +67,38 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC)")
 
 
+def _jobs() -> int:
+    # at most 8 compiles at once (one per source; hipcc is single-threaded)
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(8, n, len(SOURCES)))
+
+
 def build(verbose: bool = False, extra_flags=None) -> str:
-    objs = []
     build_dir = os.path.join(HERE, "_build")
     os.makedirs(build_dir, exist_ok=True)
     flags = HIPCC_FLAGS + list(extra_flags or [])
-    for src in SOURCES:
+
+    def compile_one(src):
         obj = os.path.join(build_dir, src.replace(".hip", ".o"))
         cmd = [hipcc(), *flags, *SOURCE_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
-        if verbose:
-            print(" ".join(cmd), flush=True)
         res = subprocess.run(cmd, capture_output=True, text=True)
         out = "\n".join(l for l in (res.stdout + res.stderr).splitlines()
                         if "packed-fp32-ops" not in l)
-        if res.returncode != 0:
-            raise RuntimeError(f"hipcc failed on {src}:\n{out}")
-        if verbose and out.strip():
-            print(out, flush=True)
-        objs.append(obj)
+        return src, cmd, obj, res.returncode, out
+
+    objs = []
+    with concurrent.futures.ThreadPoolExecutor(_jobs()) as pool:
+        for src, cmd, obj, rc, out in pool.map(compile_one, SOURCES):
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            if rc != 0:
+                raise RuntimeError(f"hipcc failed on {src}:\n{out}")
+            if verbose and out.strip():
+                print(out, flush=True)
+            objs.append(obj)
     tmp = LIB + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -33,9 +33,12 @@ constexpr int kFwdSplitBound = 1024;
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-int check_shape(int B, int H, int T, int D) {
-  if (B <= 0 || H <= 0 || T <= 0)
-    return fail(CA_ERR_INVALID, "invalid shape B=%d H=%d T=%d (all must be positive)", B, H, T);
+}  // namespace
+
+int ca::check_shape(int B, int H, int T, int D) {
+  if (B <= 0 || H <= 0 || T <= 0 || D <= 0)
+    return fail(CA_ERR_INVALID, "invalid shape B=%d H=%d T=%d D=%d (all must be positive)", B, H,
+                T, D);
   if (D != 8 && D != 16 && D != 32 && D != 64 && D != 128)
     return fail(CA_ERR_UNSUPPORTED, "head dim D=%d not supported (HIP kernels cover D in {8,16,32,64,128})", D);
   if ((long long)B * H * T * D > (1ll << 31) - 1)
@@ -44,6 +47,9 @@ int check_shape(int B, int H, int T, int D) {
   if (T > 65536) return fail(CA_ERR_UNSUPPORTED, "T=%d exceeds the supported 65536", T);
   return CA_OK;
 }
+
+namespace {
+using ca::check_shape;
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
@@ -196,21 +202,77 @@ bool plan_passes(int B, int H, int T, int D, size_t bytes, std::vector<ca::BwdPa
   return true;
 }
 
-// Workspace the backward asks for under the cap: the full one when it fits,
-// else the largest pass of the plan for the cap, or (when not even one dQ
-// group fits under the cap) the one-group pass that needs the most.
-size_t bwd_capped_bytes(int B, int H, int T, int D) {
-  const size_t full = bwd_full_bytes(B, H, T, D);
-  if (g_workspace_cap == 0 || full <= g_workspace_cap) return full;
-  std::vector<ca::BwdPass> passes;
+// Bytes of the fp32 dK and dV sums of `slices` slices, which the token-major
+// backward keeps at the start of its workspace when it runs in passes.
+size_t kv_sum_bytes(int slices, int T, int D) {
+  return 2 * align256((size_t)slices * T * D * sizeof(float));
+}
+
+// A backward plan.  The slices run as one set (every slice) or, when not even
+// one 128-query group of every slice fits, as sets of consecutive heads of
+// one batch: slices are independent, so a set is the backward of a
+// [1, nh, T, D] sub-problem, and its workspace grows with nh instead of B*H.
+// Each set runs in passes over ranges of 128-query groups.  With kv_sums,
+// the set's dK and dV are summed over its passes in fp32 (kv_sum_bytes at
+// the start of the workspace, the passes' buffers after them).
+struct BwdPlan {
+  int hc = 0;                            // heads per set; 0: one set of every slice
+  std::vector<ca::BwdPass> passes;       // passes of a set of hc heads (or of the one set)
+  int tail = 0;                          // heads of each batch's last set when fewer than hc
+  std::vector<ca::BwdPass> tail_passes;  // and its passes
+  size_t need = 0;                       // the most workspace any pass of the plan uses
+};
+size_t passes_need(int B, int H, int T, int D, const std::vector<ca::BwdPass>& passes) {
   size_t need = 0;
-  if (plan_passes(B, H, T, D, g_workspace_cap, &passes)) {
-    for (const auto& p : passes) need = std::max(need, bwd_layout(B, H, T, D, p).total);
-  } else {
-    for (int g = 0; g < ca::dq_num_groups(T); ++g)
-      need = std::max(need, bwd_layout(B, H, T, D, ca::bwd_pass(T, g, g + 1)).total);
-  }
+  for (const auto& p : passes) need = std::max(need, bwd_layout(B, H, T, D, p).total);
   return need;
+}
+// The plan for a workspace of `bytes`: every slice in one set if one group of
+// each fits, else the fewest head sets (of near-equal sizes) that fit.  False
+// when not even one group of one slice fits.
+bool plan_bwd(int B, int H, int T, int D, size_t bytes, bool kv_sums, BwdPlan* plan) {
+  auto extra = [&](int slices) { return kv_sums ? kv_sum_bytes(slices, T, D) : size_t(0); };
+  *plan = BwdPlan();
+  if (bytes > extra(B * H) && plan_passes(B, H, T, D, bytes - extra(B * H), &plan->passes)) {
+    plan->need = extra(B * H) + passes_need(B, H, T, D, plan->passes);
+    return true;
+  }
+  for (int hc = H; hc >= 1; --hc) {
+    if (bytes <= extra(hc)) continue;
+    const int nsets = (H + hc - 1) / hc;
+    const int hb = (H + nsets - 1) / nsets;  // <= hc
+    const int tail = H - (nsets - 1) * hb;   // <= hb
+    *plan = BwdPlan();
+    if (!plan_passes(1, hb, T, D, bytes - extra(hb), &plan->passes)) continue;
+    plan->hc = hb;
+    plan->need = extra(hb) + passes_need(1, hb, T, D, plan->passes);
+    if (tail != hb) {
+      if (!plan_passes(1, tail, T, D, bytes - extra(tail), &plan->tail_passes)) continue;
+      plan->tail = tail;
+      plan->need = std::max(plan->need, extra(tail) + passes_need(1, tail, T, D, plan->tail_passes));
+    }
+    return true;
+  }
+  *plan = BwdPlan();
+  return false;
+}
+
+// Workspace the backward asks for under the cap: the full one when it fits
+// (without kv_sums), else the need of the plan for the cap, or, when no plan
+// fits under the cap, the least any plan needs (sets of one head, one
+// 128-query group per pass).
+size_t bwd_capped_bytes(int B, int H, int T, int D, bool kv_sums) {
+  if (!kv_sums) {
+    const size_t full = bwd_full_bytes(B, H, T, D);
+    if (g_workspace_cap == 0 || full <= g_workspace_cap) return full;
+  }
+  BwdPlan plan;
+  if (plan_bwd(B, H, T, D, g_workspace_cap ? g_workspace_cap : SIZE_MAX, kv_sums, &plan))
+    return plan.need;
+  size_t need = 0;
+  for (int g = 0; g < ca::dq_num_groups(T); ++g)
+    need = std::max(need, bwd_layout(1, 1, T, D, ca::bwd_pass(T, g, g + 1)).total);
+  return need + (kv_sums ? kv_sum_bytes(1, T, D) : 0);
 }
 
 // ---- per-kernel event timing ------------------------------------------------
@@ -239,8 +301,8 @@ hipEvent_t pool_event() {
 
 namespace ca {
 bool bwd_fits(int B, int H, int T, int D, size_t bytes) {
-  std::vector<BwdPass> passes;
-  return bwd_full_bytes(B, H, T, D) <= bytes || plan_passes(B, H, T, D, bytes, &passes);
+  BwdPlan plan;
+  return plan_bwd(B, H, T, D, bytes, false, &plan);
 }
 
 int set_error(int code, const char* fmt, ...) {
@@ -331,17 +393,28 @@ size_t ca_fwd_workspace_bytes(int B, int H, int T, int D) {
 
 size_t ca_bwd_workspace_bytes(int B, int H, int T, int D) {
   if (B <= 0 || H <= 0 || T <= 0 || D <= 0) return 0;
-  return bwd_capped_bytes(B, H, T, D);
+  return bwd_capped_bytes(B, H, T, D, false);
 }
 
+// The token-major entry points add room for the keys rotated once when that
+// fits under the cap (their kernels otherwise rotate each staged key tile).
 size_t ca_fwd_qkv_workspace_bytes(int B, int H, int T, int D) {
   if (B <= 0 || H <= 0 || T <= 0 || D <= 0) return 0;
-  return rotated_keys_bytes(B, H, T, D) + ca_fwd_workspace_bytes(B, H, T, D);
+  const size_t fwd = ca_fwd_workspace_bytes(B, H, T, D);
+  const size_t with_keys = rotated_keys_bytes(B, H, T, D) + fwd;
+  return g_workspace_cap == 0 || with_keys <= g_workspace_cap ? with_keys : fwd;
 }
 
+// One pass (gradients written in the element type) when it fits under the
+// cap, with the rotated keys when they fit too; else passes, with dK and dV
+// summed over them in fp32 in the workspace.
 size_t ca_bwd_qkv_workspace_bytes(int B, int H, int T, int D) {
   if (B <= 0 || H <= 0 || T <= 0 || D <= 0) return 0;
-  return rotated_keys_bytes(B, H, T, D) + bwd_full_bytes(B, H, T, D);
+  const size_t full = bwd_full_bytes(B, H, T, D);
+  const size_t with_keys = rotated_keys_bytes(B, H, T, D) + full;
+  if (g_workspace_cap == 0 || with_keys <= g_workspace_cap) return with_keys;
+  if (full <= g_workspace_cap) return full;
+  return std::min(full, bwd_capped_bytes(B, H, T, D, true));
 }
 
 }  // extern "C"
@@ -435,22 +508,42 @@ int fwd_common(const ca::FwdIO& io, int dtype, void* workspace, size_t workspace
   return CA_OK;
 }
 
-int bwd_common(const ca::BwdIO& io, int dtype, void* workspace, size_t workspace_bytes, int B,
-               int H, int T, int D, void* stream, bool single_pass) {
-  // one pass when the whole backward fits the workspace, else passes over
-  // ranges of dQ groups (dK, dV and dlog_gain accumulate in pass order)
-  std::vector<ca::BwdPass> passes;
-  const size_t full = bwd_full_bytes(B, H, T, D);
-  if (workspace && workspace_bytes >= full) {
-    passes.push_back(ca::bwd_pass(T, 0, ca::dq_num_groups(T)));
-  } else if (single_pass || !workspace ||
-             !plan_passes(B, H, T, D, workspace_bytes, &passes)) {
-    return fail(CA_ERR_WORKSPACE, "backward workspace of %zu bytes required, %zu given",
-                single_pass ? full : bwd_capped_bytes(B, H, T, D), workspace_bytes);
+template <class E>
+hipError_t kv_cast_launch(int D, const float* dk_sum, const float* dv_sum, const ca::View& dk,
+                          const ca::View& dv, int BH, int H, int T, hipStream_t s) {
+  switch (D) {
+    case 8: return ca::launch_kv_cast<8, E>(dk_sum, dv_sum, dk, dv, BH, H, T, s);
+    case 16: return ca::launch_kv_cast<16, E>(dk_sum, dv_sum, dk, dv, BH, H, T, s);
+    case 32: return ca::launch_kv_cast<32, E>(dk_sum, dv_sum, dk, dv, BH, H, T, s);
+    case 64: return ca::launch_kv_cast<64, E>(dk_sum, dv_sum, dk, dv, BH, H, T, s);
+    default: return ca::launch_kv_cast<128, E>(dk_sum, dv_sum, dk, dv, BH, H, T, s);
   }
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  char* ws = static_cast<char*>(workspace);
-  for (const ca::BwdPass& pass : passes) {
+}
+
+// view of the slices of batch b from head h0 on (elements of esz bytes)
+ca::View sub_view(const ca::View& v, int b, int h0, size_t esz) {
+  ca::View r = v;
+  r.base = static_cast<char*>(v.base) + ((long long)b * v.bstride + (long long)h0 * v.hstride) * (long long)esz;
+  return r;
+}
+
+// One set of slices (the whole problem, or heads h0 .. h0 + H - 1 of one
+// batch as a [1, H, T, D] problem) in its passes.  With kv_sums, dK and dV
+// are summed in fp32 at the start of the workspace and rounded into io.dk /
+// io.dv at the end.
+int run_set(const ca::BwdIO& io, int dtype, char* ws, const std::vector<ca::BwdPass>& passes,
+            bool first_set, bool kv_sums, int B, int H, int T, int D, hipStream_t s) {
+  ca::BwdIO pio = io;
+  if (kv_sums) {
+    const size_t half = kv_sum_bytes(B * H, T, D) / 2;
+    pio.dk = heads_view(ws, H, T, D);
+    pio.dv = heads_view(ws + half, H, T, D);
+    pio.kv_f32 = true;
+    ws += 2 * half;
+  }
+  for (ca::BwdPass pass : passes) {
+    // dlog_gain is written by the first pass of the first set, added to after
+    pass.first = first_set && pass.g0 == 0;
     const BwdLayout L = bwd_layout(B, H, T, D, pass);
     ca::BwdWork work;
     work.dsbuf = reinterpret_cast<float*>(ws + L.ds);
@@ -462,10 +555,58 @@ int bwd_common(const ca::BwdIO& io, int dtype, void* workspace, size_t workspace
     const ca::DqSplit sp = dq_split_for(B * H, T, D, pass, false);
     const ca::DkdvSplit kvs = dkdv_split_for(B * H, D, dtype, pass, false);
     hipError_t e;
-    if (dtype == CA_DTYPE_BF16) e = bwd_launch<__bf16>(D, io, work, pass, sp, kvs, B, H, T, s);
-    else if (dtype == CA_DTYPE_F16) e = bwd_launch<_Float16>(D, io, work, pass, sp, kvs, B, H, T, s);
-    else e = bwd_launch<float>(D, io, work, pass, sp, kvs, B, H, T, s);
+    if (dtype == CA_DTYPE_BF16) e = bwd_launch<__bf16>(D, pio, work, pass, sp, kvs, B, H, T, s);
+    else if (dtype == CA_DTYPE_F16) e = bwd_launch<_Float16>(D, pio, work, pass, sp, kvs, B, H, T, s);
+    else e = bwd_launch<float>(D, pio, work, pass, sp, kvs, B, H, T, s);
     if (e != hipSuccess) return fail(CA_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
+  }
+  if (kv_sums) {
+    const float* dk_sum = static_cast<const float*>(pio.dk.base);
+    const float* dv_sum = static_cast<const float*>(pio.dv.base);
+    hipError_t e;
+    if (dtype == CA_DTYPE_BF16) e = kv_cast_launch<__bf16>(D, dk_sum, dv_sum, io.dk, io.dv, B * H, H, T, s);
+    else if (dtype == CA_DTYPE_F16) e = kv_cast_launch<_Float16>(D, dk_sum, dv_sum, io.dk, io.dv, B * H, H, T, s);
+    else e = kv_cast_launch<float>(D, dk_sum, dv_sum, io.dk, io.dv, B * H, H, T, s);
+    if (e != hipSuccess) return fail(CA_ERR_HIP, "dK/dV rounding launch: %s", hipGetErrorString(e));
+  }
+  return CA_OK;
+}
+
+// The backward in the plan for the workspace it is given: one pass when the
+// whole backward fits, else passes over ranges of dQ groups, of every slice or
+// of sets of heads (dK, dV and dlog_gain accumulate in a fixed order).
+// kv_sums: io.dk and io.dv are the element type's gradients and the passes sum
+// dK and dV in fp32 first (the token-major backward in passes).
+int bwd_common(const ca::BwdIO& io, int dtype, void* workspace, size_t workspace_bytes, int B,
+               int H, int T, int D, void* stream, bool kv_sums) {
+  BwdPlan plan;
+  if (!workspace || !plan_bwd(B, H, T, D, workspace_bytes, kv_sums, &plan))
+    return fail(CA_ERR_WORKSPACE, "backward workspace of %zu bytes required, %zu given",
+                bwd_capped_bytes(B, H, T, D, kv_sums), workspace ? workspace_bytes : 0);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  if (plan.hc == 0) return run_set(io, dtype, ws, plan.passes, true, kv_sums, B, H, T, D, s);
+  const size_t esz = dtype_size(dtype);
+  for (int b = 0; b < B; ++b) {
+    for (int h0 = 0; h0 < H; h0 += plan.hc) {
+      const int nh = std::min(plan.hc, H - h0);
+      ca::BwdIO sio = io;
+      sio.q = sub_view(io.q, b, h0, esz);
+      sio.k = sub_view(io.k, b, h0, esz);
+      sio.v = sub_view(io.v, b, h0, esz);
+      sio.dout = sub_view(io.dout, b, h0, esz);
+      sio.dq = sub_view(io.dq, b, h0, esz);
+      sio.dk = sub_view(io.dk, b, h0, io.kv_f32 ? sizeof(float) : esz);
+      sio.dv = sub_view(io.dv, b, h0, io.kv_f32 ? sizeof(float) : esz);
+      const size_t row0 = ((size_t)b * H + h0) * T;
+      sio.y = io.y + row0 * D;
+      sio.stats = io.stats + row0 * 2;
+      sio.log_gain = io.log_gain + h0;
+      sio.dlog_gain = io.dlog_gain + h0;
+      const int rc = run_set(sio, dtype, ws, nh == plan.hc ? plan.passes : plan.tail_passes,
+                             b == 0, kv_sums, 1, nh, T, D, s);
+      if (rc) return rc;
+    }
   }
   return CA_OK;
 }
@@ -544,7 +685,8 @@ int ca_fwd_qkv(const void* qkv, int dtype, const float* rope_cs, const float* lo
                tokens_view(out, dtype, 0, 1, T, H, D), stats};
   char* ws = static_cast<char*>(workspace);
   size_t bytes = workspace_bytes;
-  if (workspace && workspace_bytes >= ca_fwd_qkv_workspace_bytes(B, H, T, D)) {
+  if (workspace &&
+      workspace_bytes >= rotated_keys_bytes(B, H, T, D) + ca_fwd_workspace_bytes(B, H, T, D)) {
     rc = rotate_keys_first(&io.k, &io.k_rotated, rope_cs, dtype, &ws, &bytes, B, H, T, D, stream);
     if (rc) return rc;
   }
@@ -570,12 +712,18 @@ int ca_bwd_qkv(const void* qkv, int dtype, const float* rope_cs, const float* lo
                dlog_gain};
   char* ws = static_cast<char*>(workspace);
   size_t bytes = workspace_bytes;
-  if (workspace && workspace_bytes >= rotated_keys_bytes(B, H, T, D) + bwd_full_bytes(B, H, T, D)) {
-    rc = rotate_keys_first(&io.k, &io.k_rotated, rope_cs, dtype, &ws, &bytes, B, H, T, D, stream);
-    if (rc) return rc;
+  const size_t full = bwd_full_bytes(B, H, T, D);
+  if (workspace && workspace_bytes >= full) {
+    // one pass, gradients written in the element type (keys rotated once
+    // when the workspace also has room for them)
+    if (workspace_bytes >= rotated_keys_bytes(B, H, T, D) + full) {
+      rc = rotate_keys_first(&io.k, &io.k_rotated, rope_cs, dtype, &ws, &bytes, B, H, T, D, stream);
+      if (rc) return rc;
+    }
+    return bwd_common(io, dtype, ws, bytes, B, H, T, D, stream, false);
   }
-  // token-major gradients cannot be summed over passes without rounding them
-  // to the element type in between: one pass, ca_bwd_qkv_workspace_bytes
+  // passes: the element type cannot carry dK and dV across them without
+  // rounding each pass's sum, so they are summed in fp32 and rounded once
   return bwd_common(io, dtype, ws, bytes, B, H, T, D, stream, true);
 }
 

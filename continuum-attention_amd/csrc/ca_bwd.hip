@@ -162,7 +162,7 @@ __device__ __forceinline__ void merge_kv_group(const float* __restrict__ kv_part
                                                const float* __restrict__ rope, const View& dKv,
                                                const View& dVv, const BwdPass& pass, int bh,
                                                int wg, int H, int T, int kv_chunk,
-                                               int kv_part_items) {
+                                               int kv_part_items, bool kv_f32) {
   constexpr int C4 = D / 4;
   const int tid = threadIdx.x;
   int first = 0;  // item index of the group's chunk 0 (multi-chunk groups come first)
@@ -180,9 +180,14 @@ __device__ __forceinline__ void merge_kv_group(const float* __restrict__ kv_part
     for (int cc = 1; cc < nch; ++cc) s += part[(size_t)cc * kDkdvKeys * 2 * C4 + e];
     const View& ov = which ? dKv : dVv;
     if (which && rope) s = rope4(s, rope_entry(rope, key, D, 4 * c4), true);
-    E* dst = view_slice<E>(ov, bh, H) + (long long)key * ov.rstride + 4 * c4;
-    if (accumulate) s += ld4(dst);
-    st4(dst, s);
+    auto write = [&](auto* dst) {
+      if (accumulate) s += ld4(dst);
+      st4(dst, s);
+    };
+    if (std::is_same<E, float>::value || kv_f32)
+      write(view_slice<float>(ov, bh, H) + (long long)key * ov.rstride + 4 * c4);
+    else
+      write(view_slice<E>(ov, bh, H) + (long long)key * ov.rstride + 4 * c4);
   }
 }
 
@@ -209,7 +214,7 @@ __global__ __launch_bounds__(256, (std::is_same<E, __bf16>::value && D <= 64 ? 4
                                                         int n_items, int n_part, int n_kv_items,
                                                         const float* __restrict__ kv_part,
                                                         View dKv, View dVv, int kv_chunk,
-                                                        int kv_part_items) {
+                                                        int kv_part_items, bool kv_f32) {
   using P = DqP<D>;
   const int BH = B * H;
   if ((int)blockIdx.x >= n_items * BH) {
@@ -218,7 +223,7 @@ __global__ __launch_bounds__(256, (std::is_same<E, __bf16>::value && D <= 64 ? 4
       gain_sum(gain_part, dlog_gain, x, B, H, n_kv_items, pass.first);
     else        // then one per (multi-chunk dK/dV key group, slice)
       merge_kv_group<D, E>(kv_part, rope, dKv, dVv, pass, (x - H) % BH, (x - H) / BH, H, T,
-                           kv_chunk, kv_part_items);
+                           kv_chunk, kv_part_items, kv_f32);
     return;
   }
   __shared__ __attribute__((aligned(16))) __bf16 kst[2 * P::STAGE];
@@ -482,6 +487,35 @@ __global__ __launch_bounds__(256) void ca_bwd_merge_kernel(const float* __restri
   }
 }
 
+// dK and dV summed over the passes in fp32 ([BH][T][D] each) rounded to the
+// element type into their views: one thread per (slice row, 4 values).
+template <int D, class E>
+__global__ __launch_bounds__(256) void ca_kv_cast_kernel(const float* __restrict__ dk_sum,
+                                                         const float* __restrict__ dv_sum,
+                                                         View dKv, View dVv, int BH, int H,
+                                                         int T) {
+  constexpr int C4 = D / 4;
+  const long long tix = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (tix >= (long long)BH * T * C4) return;
+  const int c = (int)(tix % C4);
+  const long long row = tix / C4;
+  const int bh = (int)(row / T), t = (int)(row % T);
+  const long long src = row * D + 4 * c;
+  st4(view_slice<E>(dKv, bh, H) + (long long)t * dKv.rstride + 4 * c,
+      *reinterpret_cast<const f32x4*>(dk_sum + src));
+  st4(view_slice<E>(dVv, bh, H) + (long long)t * dVv.rstride + 4 * c,
+      *reinterpret_cast<const f32x4*>(dv_sum + src));
+}
+
+template <int D, class E>
+hipError_t launch_kv_cast(const float* dk_sum, const float* dv_sum, View dk, View dv, int BH,
+                          int H, int T, hipStream_t stream) {
+  const long long n = (long long)BH * T * (D / 4);
+  hipLaunchKernelGGL((ca_kv_cast_kernel<D, E>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     stream, dk_sum, dv_sum, dk, dv, BH, H, T);
+  return hipGetLastError();
+}
+
 template <int D, class E>
 hipError_t launch_bwd(const BwdIO& io, const BwdWork& ws, const BwdPass& pass, const DqSplit& sp,
                       const DkdvSplit& kvs, int B, int H, int T, hipStream_t stream) {
@@ -508,12 +542,12 @@ hipError_t launch_bwd(const BwdIO& io, const BwdWork& ws, const BwdPass& pass, c
     hipLaunchKernelGGL((ca_bwd_dq_kernel<D, E, true>), dq_grid, dim3(256), 0, stream, ws.dsbuf,
                        io.k, io.rope, io.log_gain, io.dq, ws.dq_part, ws.gain_part, io.dlog_gain,
                        pass, B, H, T, sp.chunk, sp.items, sp.part_items, kvs.items, ws.kv_part,
-                       io.dk, io.dv, kvs.chunk, kvs.part_items);
+                       io.dk, io.dv, kvs.chunk, kvs.part_items, io.kv_f32);
   else
     hipLaunchKernelGGL((ca_bwd_dq_kernel<D, E, false>), dq_grid, dim3(256), 0, stream, ws.dsbuf,
                        io.k, io.rope, io.log_gain, io.dq, ws.dq_part, ws.gain_part, io.dlog_gain,
                        pass, B, H, T, sp.chunk, sp.items, sp.part_items, kvs.items, ws.kv_part,
-                       io.dk, io.dv, kvs.chunk, kvs.part_items);
+                       io.dk, io.dv, kvs.chunk, kvs.part_items, io.kv_f32);
   timer_end(kBwdDq, stream);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -529,7 +563,9 @@ hipError_t launch_bwd(const BwdIO& io, const BwdWork& ws, const BwdPass& pass, c
 #define CA_INST_BWD(DD, EE)                                                                     \
   template hipError_t launch_bwd<DD, EE>(const BwdIO&, const BwdWork&, const BwdPass&,          \
                                          const DqSplit&, const DkdvSplit&, int, int, int,       \
-                                         hipStream_t);
+                                         hipStream_t);                                          \
+  template hipError_t launch_kv_cast<DD, EE>(const float*, const float*, View, View, int, int,  \
+                                             int, hipStream_t);
 #define CA_INST_BWD_ALL(EE) \
   CA_INST_BWD(8, EE) CA_INST_BWD(16, EE) CA_INST_BWD(32, EE) CA_INST_BWD(64, EE) CA_INST_BWD(128, EE)
 CA_INST_BWD_ALL(float)

@@ -61,7 +61,7 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, E, SB>())) void ca_bwd
     const __bf16* __restrict__ limbs,
     const float* __restrict__ qstat, const float* __restrict__ log_gain, View dKv, View dVv,
     float* __restrict__ dsbuf, float* __restrict__ kv_part, float* __restrict__ gain_part,
-    BwdPass pass, int BH, int H, int T, int chunk, int n_items, int n_part) {
+    BwdPass pass, int BH, int H, int T, int chunk, int n_items, int n_part, bool kv_f32) {
   // bf16 operands: Q, K (rotated and rounded as the reference rounds them)
   // and V are bf16-valued, so the tile carries Q's h limb alone and the
   // products with Q or V skip their zero limb products (limb_step_used), with
@@ -412,25 +412,32 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, E, SB>())) void ca_bwd
     const float ck = cl2 * kLn2;
     if (nch == 1) {
       // dK rotated back by the transposed RoPE (the gradient of the un-rotated
-      // k); added to what earlier passes wrote for this key group
+      // k); added to what earlier passes wrote for this key group (in E, or
+      // in fp32 sums when kv_f32)
       const bool accumulate = dkdv_qt0(wg) < pass.qa;
-      E* pv = view_slice<E>(dVv, bh, H) + (long long)key_j * dVv.rstride;
-      E* pk = view_slice<E>(dKv, bh, H) + (long long)key_j * dKv.rstride;
+      auto write = [&](auto* pv, auto* pk) {
 #pragma unroll
-      for (int mb = 0; mb < P::NMB; ++mb) {
-        const int d0 = 16 * mb + 4 * g;
-        if (d0 < D) {
-          f32x4 gv = accv[mb];
-          f32x4 gk = acck[mb] * ck;
-          if (rope) gk = rope4(gk, rope_entry(rope, key_j, D, d0), true);
-          if (accumulate) {
-            gv += ld4(pv + d0);
-            gk += ld4(pk + d0);
+        for (int mb = 0; mb < P::NMB; ++mb) {
+          const int d0 = 16 * mb + 4 * g;
+          if (d0 < D) {
+            f32x4 gv = accv[mb];
+            f32x4 gk = acck[mb] * ck;
+            if (rope) gk = rope4(gk, rope_entry(rope, key_j, D, d0), true);
+            if (accumulate) {
+              gv += ld4(pv + d0);
+              gk += ld4(pk + d0);
+            }
+            st4(pv + d0, gv);
+            st4(pk + d0, gk);
           }
-          st4(pv + d0, gv);
-          st4(pk + d0, gk);
         }
-      }
+      };
+      if (std::is_same<E, float>::value || kv_f32)
+        write(view_slice<float>(dVv, bh, H) + (long long)key_j * dVv.rstride,
+              view_slice<float>(dKv, bh, H) + (long long)key_j * dKv.rstride);
+      else
+        write(view_slice<E>(dVv, bh, H) + (long long)key_j * dVv.rstride,
+              view_slice<E>(dKv, bh, H) + (long long)key_j * dKv.rstride);
     } else {
       float* pv = kv_part + (((size_t)bh * n_part + item) * kDkdvKeys + (key_j - w0)) * 2 * D;
       float* pk = pv + D;
@@ -457,7 +464,7 @@ hipError_t launch_bwd_dkdv(const BwdIO& io, const BwdWork& ws, const BwdPass& pa
                      io.v, io.rope, io.k_rotated ? nullptr : io.rope, ws.limbs, ws.qstat,
                      io.log_gain, io.dk, io.dv, ws.dsbuf,
                      ws.kv_part, ws.gain_part, pass, BH, H, T, kvs.chunk, kvs.items,
-                     kvs.part_items);
+                     kvs.part_items, io.kv_f32);
   return hipGetLastError();
 }
 

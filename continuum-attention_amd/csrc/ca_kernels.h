@@ -276,8 +276,13 @@ constexpr int kDtypeF32 = 0, kDtypeBF16 = 1, kDtypeF16 = 2;
 void timer_begin(int id, hipStream_t s);
 void timer_end(int id, hipStream_t s);
 // Whether the backward of this shape can run in a workspace of `bytes`
-// (in one pass or in passes over query-group ranges).
+// (in one pass, or in passes over query-group ranges of all slices or of
+// sets of heads).
 bool bwd_fits(int B, int H, int T, int D, size_t bytes);
+// Shape check of the operator's entry points: CA_OK, or an error code
+// (CA_ERR_INVALID for non-positive sizes, CA_ERR_UNSUPPORTED for head dims
+// and sizes outside the kernels' range) with ca_last_error() set.
+int check_shape(int B, int H, int T, int D);
 // Sets the calling thread's ca_last_error() text; returns `code`.
 int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 
@@ -352,8 +357,12 @@ struct BwdIO {
   const float* y;          // fp32 [B,H,T,D] forward output
   const float* stats;
   View dout;               // dL/d(output), element type E
-  View dq, dk, dv;         // gradients, element type E
+  View dq, dk, dv;         // gradients, element type E (dk, dv: fp32 when kv_f32)
   float* dlog_gain;        // [H]
+  // dk and dv are fp32 views whatever E is: the token-major backward in
+  // passes sums dK and dV over the passes in fp32 and rounds them to E once
+  // (launch_kv_cast) instead of after every pass
+  bool kv_f32 = false;
 };
 
 template <int D, class E>
@@ -402,5 +411,10 @@ inline size_t bwd_qstat_floats(int BH, const BwdPass& p) { return (size_t)BH * b
 template <int D, class E>
 hipError_t launch_bwd(const BwdIO& io, const BwdWork& ws, const BwdPass& pass, const DqSplit& sp,
                       const DkdvSplit& kvs, int B, int H, int T, hipStream_t stream);
+// dK and dV summed in fp32 ([BH][T][D] each, dk_sum and dv_sum) rounded to
+// E into the views dk and dv (slices bh = 0 .. BH-1 of H heads per batch).
+template <int D, class E>
+hipError_t launch_kv_cast(const float* dk_sum, const float* dv_sum, View dk, View dv, int BH,
+                          int H, int T, hipStream_t stream);
 
 }  // namespace ca

@@ -61,10 +61,11 @@ extern "C" int ca_bwd_f32_noalloc(const float* q, const float* k, const float* v
                                   const float* log_gain, const float* out, const float* stats,
                                   const float* dout, float* dq, float* dk, float* dv,
                                   float* dlog_gain, int B, int H, int T, int D, void* stream) {
-  if (B <= 0 || H <= 0 || T <= 0)
-    return ca::set_error(CA_ERR_INVALID, "invalid shape B=%d H=%d T=%d (all must be positive)", B, H, T);
-  // the backward runs in passes over query-group ranges sized to the array;
-  // a shape whose single 128-query group needs more is refused
+  const int rc0 = ca::check_shape(B, H, T, D);
+  if (rc0) return rc0;
+  // the backward runs in passes over query-group ranges (of every slice, or
+  // of sets of heads) sized to the array; a shape whose single 128-query
+  // group of one slice needs more is refused
   if (!ca::bwd_fits(B, H, T, D, kScratchBytes))
     return ca::set_error(CA_ERR_WORKSPACE,
                          "ca_bwd_f32_noalloc: one 128-query pass of this shape needs more than the "

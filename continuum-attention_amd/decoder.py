@@ -537,13 +537,33 @@ def train_step(model, optimizer, batch, amp_dtype=torch.bfloat16, grad_clip=1.0)
 _HIP_NODE_MEMSET, _HIP_NODE_GRAPH = 2, 4
 
 
-def _hip_graph_memset_nodes(graph: "torch.cuda.CUDAGraph") -> int:
-    """Memset nodes of a captured HIP graph kept by torch (keep_graph=True),
-    child graphs included.  Queried through the HIP runtime torch loaded
-    (soname libamdhip64.so.7, so dlopen returns that same library)."""
+def _loaded_hip_runtime():
+    """The HIP runtime library this process already has loaded (torch's), as
+    a ctypes handle: its path is read from /proc/self/maps, so dlopen returns
+    that same library rather than loading a second runtime by a fixed name."""
     import ctypes
 
-    hip = ctypes.CDLL("libamdhip64.so.7")
+    paths = []
+    with open("/proc/self/maps") as maps:
+        for line in maps:
+            path = line.split(None, 5)[-1].strip() if line.count(" ") >= 5 else ""
+            if "/libamdhip64.so" in path and path not in paths:
+                paths.append(path)
+    if not paths:
+        raise RuntimeError("GraphedTrainStep: no HIP runtime (libamdhip64.so) is loaded in this "
+                           "process; the captured graph cannot be inspected")
+    if len(paths) > 1:
+        raise RuntimeError(f"GraphedTrainStep: several HIP runtimes are loaded ({paths}); the "
+                           "captured graph cannot be inspected reliably")
+    return ctypes.CDLL(paths[0])
+
+
+def _hip_graph_memset_nodes(graph: "torch.cuda.CUDAGraph") -> int:
+    """Memset nodes of a captured HIP graph kept by torch (keep_graph=True),
+    child graphs included.  Queried through the HIP runtime torch loaded."""
+    import ctypes
+
+    hip = _loaded_hip_runtime()
     get_nodes, get_type = hip.hipGraphGetNodes, hip.hipGraphNodeGetType
     get_child = hip.hipGraphChildGraphNodeGetGraph
     get_nodes.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p),

@@ -182,38 +182,71 @@ def test_swiglu_null_and_misaligned_pointers(ca):
 
 
 def test_noalloc_backward_checks_before_any_launch(ca):
-    """ca_bwd_f32_noalloc refuses, with no HIP call, shapes whose single
-    128-query pass exceeds its static array, and invalid shapes."""
+    """ca_bwd_f32_noalloc validates the shape (B, H, T and D) before anything
+    else, with no HIP call: non-positive sizes are CA_ERR_INVALID, head dims
+    and sizes outside the kernels' range CA_ERR_UNSUPPORTED."""
     lib = ca.native.load()
     p = ctypes.c_void_p(16)
-    assert lib.ca_bwd_f32_noalloc(p, p, p, p, p, p, p, p, p, p, p, 8, 16, 65536, 64, None) == 3
-    assert b"scratch" in lib.ca_last_error()
     assert lib.ca_bwd_f32_noalloc(p, p, p, p, p, p, p, p, p, p, p, 0, 16, 64, 64, None) == 1
+    assert lib.ca_bwd_f32_noalloc(p, p, p, p, p, p, p, p, p, p, p, 1, 16, 64, -64, None) == 1
+    assert b"positive" in lib.ca_last_error()
+    assert lib.ca_bwd_f32_noalloc(p, p, p, p, p, p, p, p, p, p, p, 1, 16, 64, 0, None) == 1
+    assert lib.ca_bwd_f32_noalloc(p, p, p, p, p, p, p, p, p, p, p, 1, 16, 64, 24, None) == 2
+    assert lib.ca_bwd_f32_noalloc(p, p, p, p, p, p, p, p, p, p, p, 64, 16, 65536, 64, None) == 2
+    assert b"2^31" in lib.ca_last_error()
+
+
+def test_no_valid_shape_exceeds_the_noalloc_array(ca):
+    """Head sets bound the backward's workspace by one head's 128-query group:
+    at the largest T the kernels take (65536) that is about 32 MiB, so every
+    shape check_shape accepts fits the static 512 MiB array."""
+    lib = ca.native.load()
+    prev = lib.ca_workspace_cap()
+    try:
+        ca.ops.set_workspace_cap(1)  # below any plan: the least workspace is reported
+        least = lib.ca_bwd_workspace_bytes(1, 1, 65536, 128)
+        assert least < 64 << 20
+        scratch_mb = int(re.search(r"#define CA_NOALLOC_SCRATCH_MB (\d+)", open(HEADER).read()).group(1))
+        assert least <= scratch_mb << 20
+    finally:
+        ca.ops.set_workspace_cap(prev)
 
 
 def test_workspace_cap_bounds_the_sizes(ca):
     """The workspace bound: under the default 1 GiB cap the backward of a
-    long sequence asks for at most the cap (it runs in passes) and the
-    forward for at most the cap (longer splits); without a cap, the full
-    sizes; the token-major backward always asks for its one-pass size."""
+    long sequence asks for at most the cap (it runs in passes), the forward
+    for at most the cap (longer splits), and so do the token-major entry
+    points (the backward then sums dK and dV over its passes in fp32 in the
+    workspace); without a cap, the full sizes."""
     lib = ca.native.load()
     prev = lib.ca_workspace_cap()
     try:
         assert prev == 1 << 30
-        full = lib.ca_bwd_qkv_workspace_bytes(1, 16, 32768, 64)
-        assert full > 30 << 30
         assert lib.ca_bwd_workspace_bytes(1, 16, 32768, 64) <= 1 << 30
         assert lib.ca_fwd_workspace_bytes(1, 16, 32768, 64) <= 1 << 30
+        assert lib.ca_bwd_qkv_workspace_bytes(1, 16, 32768, 64) <= 1 << 30
+        assert lib.ca_fwd_qkv_workspace_bytes(1, 16, 32768, 64) <= 1 << 30
         small = lib.ca_bwd_workspace_bytes(2, 16, 2048, 64)
         # the token-major entry points add room for the keys rotated once
         # ([B*H][T][D], 4-byte elements, rounded up to 256 bytes)
         rot = 2 * 16 * 2048 * 64 * 4
         assert lib.ca_bwd_qkv_workspace_bytes(2, 16, 2048, 64) == small + rot  # fits: one pass
+        # one CA-S layer (268 MiB) is one pass under the default cap
+        assert lib.ca_bwd_qkv_workspace_bytes(1, 16, 2048, 64) == \
+            lib.ca_bwd_workspace_bytes(1, 16, 2048, 64) + 16 * 2048 * 64 * 4
         assert lib.ca_fwd_qkv_workspace_bytes(2, 16, 2048, 64) == \
             rot + lib.ca_fwd_workspace_bytes(2, 16, 2048, 64)
         ca.ops.set_workspace_cap(0)
+        full = lib.ca_bwd_qkv_workspace_bytes(1, 16, 32768, 64)
+        assert full > 30 << 30
         assert lib.ca_bwd_workspace_bytes(1, 16, 32768, 64) == full - 16 * 32768 * 64 * 4
         assert lib.ca_fwd_workspace_bytes(1, 16, 32768, 64) > 1 << 30
+        # the token-major backward of one CA-S layer at T = 16384 under 256 MiB:
+        # its fp32 dK/dV sums (128 MiB for 16 heads) leave too little for one
+        # group of every head, so it runs in sets of heads
+        ca.ops.set_workspace_cap(256 << 20)
+        assert lib.ca_bwd_qkv_workspace_bytes(1, 16, 16384, 64) <= 256 << 20
+        assert lib.ca_bwd_workspace_bytes(1, 16, 16384, 64) <= 256 << 20
         ca.ops.set_workspace_cap(32 << 20)
         assert lib.ca_bwd_workspace_bytes(1, 2, 8192, 64) <= 32 << 20
         assert lib.ca_fwd_workspace_bytes(1, 2, 8192, 64) <= 32 << 20
@@ -240,7 +273,7 @@ def test_workspace_size_caches_follow_the_cap_and_splits(ca):
         ops.set_workspace_cap(32 << 20)
         after = [f(*shape) for f in sizes]
         assert after[1] < before[1]  # passes over query ranges
-        assert after[3] == before[3]  # the token-major backward runs in one pass
+        assert after[3] < before[3]  # the token-major backward too
         lib = ca.native.load()
         assert after == [lib.ca_fwd_workspace_bytes(*shape), lib.ca_bwd_workspace_bytes(*shape),
                          lib.ca_fwd_qkv_workspace_bytes(*shape), lib.ca_bwd_qkv_workspace_bytes(*shape)]

@@ -212,12 +212,23 @@ def test_graph_memset_node_count(Dm, monkeypatch):
         def raw_cuda_graph(self):
             return self.h
 
-    monkeypatch.setattr(ctypes, "CDLL", lambda name: FakeHip())
+    monkeypatch.setattr(Dm, "_loaded_hip_runtime", lambda: FakeHip())
     assert Dm._hip_graph_memset_nodes(FakeGraph(1)) == 3
     assert Dm._hip_graph_memset_nodes(FakeGraph(3)) == 1
     graphs[4] = [("k", None), ("c", None)]
     nodes[401], nodes[402] = (0, None), (1, None)
     assert Dm._hip_graph_memset_nodes(FakeGraph(4)) == 0
+
+
+def test_graph_check_uses_the_loaded_hip_runtime(Dm):
+    """The memset-node check queries the HIP runtime torch already loaded
+    (found in /proc/self/maps), not a library opened by a fixed soname."""
+    import torch  # noqa: F401  (loads the HIP runtime of this ROCm build)
+
+    maps = open("/proc/self/maps").read()
+    lib = Dm._loaded_hip_runtime()
+    assert "/libamdhip64.so" in lib._name and lib._name in maps
+    assert hasattr(lib, "hipGraphGetNodes")
 
 
 def test_token_embedding_gradient_matches_nn_embedding():
