@@ -152,6 +152,109 @@ def _timed_steps(ca, step, steps, warmup):
     return ms, _ca_kernel_ms(ca, step, steps, warmup + steps), out
 
 
+def time_operator(ca, dev, q, k, v, rho, dy, steps, warmup):
+    """Forward + backward of the operator on resident inputs: median fwd, bwd
+    and total ms of `steps` uninstrumented steps (HIP events on the current
+    stream around each half), then the same steps with HIP events around every
+    kernel launch on its stream (per-kernel times)."""
+    import torch
+    q, k, v = (x.to(dev).requires_grad_(True) for x in (q, k, v))
+    rho = rho.to(dev).requires_grad_(True)
+    dy = dy.to(dev)
+    B, H, T, D = q.shape
+
+    def step():
+        y = ca.continuum_attention(q, k, v, rho, 128)
+        torch.autograd.grad(y, (q, k, v, rho), dy)
+        return y
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = []
+    t_start = time.perf_counter()
+    for _ in range(steps):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        ev[0].record()
+        y = ca.continuum_attention(q, k, v, rho, 128)
+        ev[1].record()
+        torch.autograd.grad(y, (q, k, v, rho), dy)
+        ev[2].record()
+        evs.append(ev)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    fwd = statistics.median(ev[0].elapsed_time(ev[1]) for ev in evs)
+    bwd = statistics.median(ev[1].elapsed_time(ev[2]) for ev in evs)
+    tot = statistics.median(ev[0].elapsed_time(ev[2]) for ev in evs)
+    ca.native.timing_enable(True)
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    kt = ca.native.timing_read()
+    ca.native.timing_enable(False)
+    P = pairs(B, H, T)
+    fpp = kernel_flops_per_pair(D)
+    per_kernel = {}
+    for n, (t, c) in kt.items():
+        if c:
+            per_kernel[n] = {"avg_ms": round(t / c, 4), "launches": c}
+            if n in fpp:
+                # the kernel's algorithmic flops per step over its time per step
+                per_kernel[n]["tflops"] = round(fpp[n] * P / (t / steps * 1e-3) / 1e12, 2)
+    return {"fwd_ms": round(fwd, 4), "bwd_ms": round(bwd, 4), "total_ms": round(tot, 4),
+            "fwd_tflops": round(4 * D * P / (fwd * 1e-3) / 1e12, 2),
+            "bwd_tflops": round(10 * D * P / (bwd * 1e-3) / 1e12, 2),
+            "tflops": round(14 * D * P / (tot * 1e-3) / 1e12, 2),
+            "roofline_frac": round(14 * D * P / (tot * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
+            "wall_s": round(wall, 3), "kernels": per_kernel, "kt": kt}
+
+
+def config5_inputs(T=8192):
+    """[1,16,T,64]; heads 0-7 near-duplicate adjacent keys
+    k_j = k_{j-1} + N(0, 1e-4^2) (delta ~ 1e-4, the Taylor branch), heads 8-15
+    keys 4 N(0,1) (large delta); q, v, dY ~ N(0,1); seed 0."""
+    import torch
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(1, 16, T, 64, generator=g)
+    k0 = torch.randn(8, 1, 64, generator=g)
+    walk = torch.cumsum(torch.randn(8, T - 1, 64, generator=g) * 1e-4, 1)
+    k = torch.cat([torch.cat([k0, k0 + walk], 1), 4.0 * torch.randn(8, T, 64, generator=g)], 0)[None]
+    v = torch.randn(1, 16, T, 64, generator=g)
+    dy = torch.randn(1, 16, T, 64, generator=g)
+    return q, k.contiguous(), v, torch.zeros(16), dy
+
+
+def operator_leg(ca, dev, name, shape, steps, warmup):
+    """One more operator shape on the same line: fwd, bwd, total ms and
+    TFLOP/s (algorithmic: 4 D, 10 D, 14 D flops per causal pair)."""
+    import torch
+    B, H, T, D = shape
+    if name == "config5":
+        q, k, v, rho, dy = config5_inputs(T)
+        inputs = ("BASELINE config 5: heads 0-7 k_j = k_{j-1} + N(0,1e-4^2), heads 8-15 "
+                  "keys 4 N(0,1); q, v, dY ~ N(0,1), seed 0")
+    else:
+        g = torch.Generator().manual_seed(0)
+        q, k, v, dy = (torch.randn(shape, generator=g) for _ in range(4))
+        rho = torch.zeros(H)
+        inputs = "q, k, v, dY ~ N(0,1), seed 0 (one CA-S layer's operator shape, fp32)"
+    lib = ca.native.load()
+    ws_f, ws_b = lib.ca_fwd_workspace_bytes(*shape), lib.ca_bwd_workspace_bytes(*shape)
+    prev = ca.ops.workspace_cap()
+    ca.ops.set_workspace_cap(0)
+    full_b = lib.ca_bwd_workspace_bytes(*shape)
+    ca.ops.set_workspace_cap(prev)
+    op = time_operator(ca, dev, q, k, v, rho, dy, steps, warmup)
+    op.pop("kt")
+    op.update({"shape": list(shape), "inputs": inputs, "steps": steps, "warmup": warmup,
+               "workspace_cap_bytes": prev, "fwd_workspace_bytes": ws_f,
+               "bwd_workspace_bytes": ws_b, "bwd_workspace_unbounded_bytes": full_b,
+               "bwd_passes_note": ("the backward runs in passes under the cap"
+                                   if full_b > ws_b else "one backward pass")})
+    torch.cuda.empty_cache()
+    return op
+
+
 def bench_ca_s(ca, dev, steps=20, warmup=5):
     """one CA-S decoder training step (101,205,120 params,
     T=2048, batch 1, bf16 autocast with fp32 CA scores, AdamW + clip 1.0 as
@@ -256,6 +359,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-models", action="store_true",
                     help="skip the CA-S (config 4) and CA-P (config 3) training-step legs")
+    ap.add_argument("--no-extra-shapes", action="store_true",
+                    help="skip the config-5 [1,16,8192,64] and CA-S layer [1,16,2048,64] "
+                         "operator legs")
     ap.add_argument("--shape", default=None,
                     help="B,H,T,D of the operator leg (diagnostics; default is BASELINE config 2)")
     ap.add_argument("--only", choices=["ca_s", "ca_p"], default=None,
@@ -292,60 +398,16 @@ def main():
     shape = tuple(int(x) for x in args.shape.split(",")) if args.shape else SHAPE
     B, H, T, D = shape
     g = torch.Generator().manual_seed(0)
-    q, k, v = (torch.randn(shape, generator=g).to(dev).requires_grad_(True) for _ in range(3))
-    rho = torch.zeros(H, device=dev, requires_grad=True)
-    dy = torch.randn(shape, generator=g).to(dev)
-
-    def step():
-        y = ca.continuum_attention(q, k, v, rho, 128)
-        torch.autograd.grad(y, (q, k, v, rho), dy)
-        return y
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-
-    # Timed region 1: whole fwd+bwd steps bracketed by events on the current
-    # stream, with no per-kernel instrumentation (this is `value`).
-    fwd, bwd, tot = [], [], []
-    torch.cuda.synchronize()
-    t_start = time.perf_counter()
-    for _ in range(args.steps):
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-        ev[0].record()
-        y = ca.continuum_attention(q, k, v, rho, 128)
-        ev[1].record()
-        torch.autograd.grad(y, (q, k, v, rho), dy)
-        ev[2].record()
-        fwd.append(ev)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t_start
-    for ev in fwd:
-        tot.append(ev[0].elapsed_time(ev[2]))
-        bwd.append(ev[1].elapsed_time(ev[2]))
-    fwd = [ev[0].elapsed_time(ev[1]) for ev in fwd]
-    # Timed region 2: the same steps with HIP events recorded around every
-    # kernel launch on the launch stream (per-kernel table and roofline).
-    ca.native.timing_enable(True)
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    kt = ca.native.timing_read()
-    ca.native.timing_enable(False)
-
+    q, k, v, dy = (torch.randn(shape, generator=g) for _ in range(4))
+    op = time_operator(ca, dev, q, k, v, torch.zeros(H), dy, args.steps, args.warmup)
+    ms, kt, per_kernel = op["total_ms"], op["kt"], op["kernels"]
     P = pairs(B, H, T)
     flops_total = 14 * D * P
-    ms = statistics.median(tot)
-    per_kernel = {n: {"avg_ms": round(t / c, 4), "launches": c}
-                  for n, (t, c) in kt.items() if c}
     fpp = kernel_flops_per_pair(D)
     dom = max((n for n in per_kernel if n in fpp), key=lambda n: per_kernel[n]["avg_ms"])
     dom_ms = kt[dom][0] / kt[dom][1]
     achieved = fpp[dom] * P / (dom_ms * 1e-3) / 1e12
     op_tflops = flops_total / (ms * 1e-3) / 1e12
-    for n in per_kernel:
-        if n in fpp:
-            per_kernel[n]["tflops"] = round(fpp[n] * P / (kt[n][0] / kt[n][1] * 1e-3) / 1e12, 2)
 
     out = {
         "metric": "CA fwd+bwd ms @[2,16,2048,64] fp32; % of fp32-MFMA roofline; CA-S tokens/s",
@@ -363,12 +425,14 @@ def main():
         "config": {"workload": (f"CA operator fwd+bwd [B,H,T,D]=[{B},{H},{T},{D}] fp32, causal, "
                                 "log_gain=0" + (" (BASELINE config 2)" if shape == SHAPE else "")),
                    "B": B, "H": H, "T": T, "D": D, "query_tile": 128},
-        "fwd_ms": round(statistics.median(fwd), 4),
-        "bwd_ms": round(statistics.median(bwd), 4),
+        "fwd_ms": op["fwd_ms"],
+        "bwd_ms": op["bwd_ms"],
         "op_tflops": round(op_tflops, 2),
         "op_roofline_frac": round(op_tflops / PEAK_FP32_MFMA_TFLOPS, 4),
+        "fwd_tflops": op["fwd_tflops"],
+        "bwd_tflops": op["bwd_tflops"],
         "algorithmic_gflop": round(flops_total / 1e9, 3),
-        "wall_s_timed_region": round(wall, 3),
+        "wall_s_timed_region": op["wall_s"],
         "kernels": per_kernel,
         # achieved = algorithmic fp32 flops of the dominant kernel / its launch
         # time, against the fp32-MFMA peak the metric names.  The products run
@@ -391,6 +455,13 @@ def main():
                 out["roofline"]["traffic"] = rec["total_bytes"]
                 out["roofline"]["traffic_source"] = (
                     f"profiles/ca_op_2x16x2048x64_hbm_traffic.md (commit {tr.get('commit')})")
+    if not args.no_extra_shapes and not args.shape:
+        # BASELINE config 5 (the long-context stress inputs; the backward in
+        # passes under the default 1 GiB workspace cap) and one CA-S layer's
+        # operator shape
+        out["config5"] = operator_leg(ca, dev, "config5", (1, 16, 8192, 64), steps=10, warmup=5)
+        out["ca_s_layer_op"] = operator_leg(ca, dev, "ca_s_layer", (1, 16, 2048, 64),
+                                            steps=args.steps, warmup=args.warmup)
     if not args.no_models:
         out["ca_s"] = bench_ca_s(ca, dev)
         out["ca_p"] = bench_ca_p(ca, dev)

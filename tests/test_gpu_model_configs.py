@@ -172,7 +172,7 @@ def test_config4_ca_s_step(gpu_ca):
     qb, kb = Dm.apply_rope(q.to(torch.bfloat16), k.to(torch.bfloat16), cfg.rope_theta)
     q, k = qb.float(), kb.float()
     rows = np.array([0, 1, 2, 63, 64, 511, 1024, 1535, 2046, 2047])
-    # the output is rounded to bf16: half an ulp (2^-9 relative) per element
+    # the output is rounded to bf16: half an ulp (2^-8 relative) per element
     attention_vs_oracle(q, k, v, torch.zeros(cfg.n_heads), store["y"], rows, 4e-3)
 
 

@@ -347,9 +347,11 @@ def test_fused_decoder_backward_in_passes_matches_one_pass(gpu_ca):
     """One CA-S layer ([1,2048,3*16*64], bf16, RoPE) under a 24 MiB cap: the
     token-major backward runs in sets of heads, each in passes over query
     ranges, with dK and dV summed over the passes in fp32 and rounded once.
-    Against the one-pass backward: dq is formed the same way (complete within
-    a pass) and dk, dv, dlog_gain differ only in the fp32 summation order
-    (then bf16 rounding: at most one bf16 ulp)."""
+    Against the one-pass backward: every gradient differs only in the fp32
+    summation order (dq: the dQ pass's chunking depends on the grid; dk, dv:
+    the pass sums), then bf16 rounding: at most one bf16 ulp of the element,
+    plus fp32 rounding (1e-6 of the tensor's largest value) where a sum
+    cancels to near zero."""
     say("[case] token-major backward in passes vs one pass, bf16")
     lib = gpu_ca.native.load()
     T, H, D = 2048, 16, 64
@@ -363,9 +365,11 @@ def test_fused_decoder_backward_in_passes_matches_one_pass(gpu_ca):
     b = many[0].float().view(1, T, 3, H, D)
     for i, name in enumerate(("dq", "dk", "dv")):
         d = (a[:, :, i] - b[:, :, i]).abs()
-        bound = 2.0 ** -7 * torch.maximum(a[:, :, i].abs(), b[:, :, i].abs()) + 1e-30
+        scale = a[:, :, i].abs().max().item()
+        bound = 2.0 ** -7 * torch.maximum(a[:, :, i].abs(), b[:, :, i].abs()) + 1e-6 * scale
         frac = (d > 0).float().mean().item()
-        say(f"   {name}: max |diff| {d.max().item():.3g}, {100 * frac:.2f}% of elements differ")
+        say(f"   {name}: max |diff| {d.max().item():.3g} (of max {scale:.3g}), "
+            f"{100 * frac:.2f}% of elements differ, worst excess {(d - bound).max().item():.3g}")
         assert bool((d <= bound).all()), name
     eg = (one[1] - many[1]).abs().max().item() / one[1].abs().max().item()
     say(f"   dlog_gain rel diff {eg:.2e}")
