@@ -45,6 +45,13 @@ struct Bwd {
 // wait and the other resident work groups' work.  fp32 at D = 64 runs it on
 // every grid (config 2 dK/dV 0.309 -> 0.291 ms, [1,16,2048,64] 0.162 ->
 // 0.161 ms against the double-buffered two-wave kernel on one box).
+// Direction of each item's walk over its query tiles (see the tile loop).
+#ifndef CA_DKDV_ASCENDING
+constexpr bool kDkdvDescending = true;
+#else
+constexpr bool kDkdvDescending = false;
+#endif
+
 template <int D, class E, bool SB>
 constexpr int dkdv_waves_per_simd() {
   return D > 64 ? 1 : (q_limb_planes<E>() == 1 || SB) ? 3 : 2;
@@ -187,26 +194,36 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, E, SB>())) void ca_bwd
   };
 
   // query tiles of this item: a chunk of the pass's tiles that see an owned
-  // key of the work group
+  // key of the work group, walked from the last down (kDkdvDescending): the
+  // work groups of a slice that are resident together then all start at the
+  // pass's last tile and read each query tile at about the same time, so it
+  // is fetched once into the XCD's L2 and re-read from there (walked upwards,
+  // key group wg starts at tile 1.75 wg and the resident groups read tiles
+  // up to ~40 apart)
   const int ntl = dkdv_group_tiles(wg, pass);
   const int clen = (ntl + nch - 1) / nch;
   const int qt0 = dkdv_group_first_tile(wg, pass) + ch * clen;
   const int qt_end = min(qt0 + clen, pass.qb);
+  const int ntile = qt_end > qt0 ? qt_end - qt0 : 0;
+  constexpr int kStep = kDkdvDescending ? -1 : 1;
+  const int qt_first = kDkdvDescending ? qt_end - 1 : qt0;
   // this lane's spilled dS column in tile qt: owned slots 1 .. 14 hold keys
-  // 14 kb16 .. +13; tile qt's columns start at ds_tile, advanced per tile
-  size_t ds_tile = (size_t)bh * pass.ds_slice + (ds_floats_before(qt0) - pass.ds0);
+  // 14 kb16 .. +13; tile qt's columns start at ds_tile, moved per tile
+  size_t ds_tile = (size_t)bh * pass.ds_slice + (ds_floats_before(qt_first) - pass.ds0);
   const int ds_key = kBwdKeys * kb16 + j - 1;
   const bool ds_lane = j >= 1 && j <= kBwdKeys;
   __syncthreads();          // LDS clear before the first store
-  if (qt0 < qt_end) {
-    load_tile(qt0);
+  if (ntile > 0) {
+    load_tile(qt_first);
     store_tile(0);
   }
   __syncthreads();
 
-  for (int qt = qt0; qt < qt_end; ++qt) {
-    const int buf = SB ? 0 : (qt - qt0) & 1;
-    if (!SB && qt + 1 < qt_end) load_tile(qt + 1);
+  for (int n = 0; n < ntile; ++n) {
+    const int qt = qt_first + kStep * n;
+    const bool more = n + 1 < ntile;
+    const int buf = SB ? 0 : n & 1;
+    if (!SB && more) load_tile(qt + kStep);
     const int i0 = 32 * qt;
     // the wave's block meets this tile (and exists)
     const bool work = kb16 < nkb && kBwdKeys * kb16 <= i0 + 31;
@@ -359,14 +376,19 @@ __global__ __launch_bounds__(256, (dkdv_waves_per_simd<D, E, SB>())) void ca_bwd
       }
       prio_mfma_end<!BF>();
     }
-    ds_tile += (size_t)kDsColFloats * kBwdKeys * ds_kb_count(qt);
+    if (more) {
+      if (kDkdvDescending)
+        ds_tile -= (size_t)kDsColFloats * kBwdKeys * ds_kb_count(qt - 1);
+      else
+        ds_tile += (size_t)kDsColFloats * kBwdKeys * ds_kb_count(qt);
+    }
     if (SB) {
-      if (qt + 1 < qt_end) {
-        load_tile(qt + 1);  // issued before the barrier: its latency overlaps the wait
+      if (more) {
+        load_tile(qt + kStep);  // issued before the barrier: its latency overlaps the wait
         __syncthreads();  // every wave is done with the tile
         store_tile(0);
       }
-    } else if (qt + 1 < qt_end) {
+    } else if (more) {
       store_tile(buf ^ 1);
     }
     __syncthreads();

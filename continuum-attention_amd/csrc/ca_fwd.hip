@@ -536,6 +536,459 @@ __global__ __launch_bounds__(256, (fwd_waves_per_simd<D, E, ROPE>())) void ca_fw
   }
 }
 
+// ---- the 16x16x32 forward ---------------------------------------------------
+// The same work item (a 128-query group of one slice and a split of its
+// 32-key weight tiles) on eight waves of 16 queries each, with both products
+// on v_mfma_f32_16x16x32_bf16 (16.8 cycles per instruction against 40 for
+// 32x32x16, measured: 16% less matrix time for the same flops) and about 120
+// VGPRs, so that a CU holds two work groups of eight waves: four waves per
+// SIMD instead of two, which hides more of the segment math's latency.
+//
+// Lane layout.  A wave computes S^T = K Q^T for its 16 queries and a 32-key
+// score tile as two 16x16 blocks.  Lane l holds query l%16; its lane row
+// G = l/16 holds score keys kbase .. kbase+7 (kbase = 32t+1+8G) in registers
+// sc[0..7]: the K tile is staged with key 8G + 4b + r in LDS row
+// 16b + 4G + r (k16_row), so the rows 4G..4G+3 that the MFMA returns in lane
+// row G of block b are those keys.  Segment neighbours are then in the same
+// lane, except the left neighbour of register 0 (register 7 of lane row
+// G-1, or the previous tile's for G = 0), reached by a rotation of the lane
+// rows.  In O^T += V^T W^T the k index of lane row G is 8G + e, the weight
+// keys 32t + 8G + e that the lane itself holds, so each lane feeds its own
+// weights as the B operand.
+template <int D>
+struct Fwd16 {
+  static constexpr int KS = D / 32;         // 32-wide k steps of S^T (d)
+  static constexpr int NMB = D / 16;        // 16-row d blocks of O^T
+  static constexpr int C4 = D / 4;          // float4 chunks per row
+  static constexpr int KROW = D + 16;       // bf16 row stride of a K plane (160 bytes at D = 64)
+  static constexpr int KPLANE = 32 * KROW;
+  static constexpr int VROW = 40;           // V^T row: 32 keys + 8 padding
+  static constexpr int VPLANE = D * VROW;
+  static constexpr int KCH = 32 * C4;       // K float4 chunks per tile
+  static constexpr int KLD = (KCH + 511) / 512;
+  static constexpr int VUNITS = 16 * C4;    // (key pair, float4 chunk) units of a V tile
+  static constexpr int VLD = (VUNITS + 511) / 512;
+};
+
+// LDS row of the staged K tile that holds score key k (0..31) of the tile.
+__device__ __forceinline__ int k16_row(int k) { return 16 * ((k >> 2) & 1) + 4 * (k >> 3) + (k & 3); }
+
+// Value held by lane l ^ 16 (swaps lane rows 0 <-> 1 and 2 <-> 3).
+__device__ __forceinline__ float xrow16(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return (threadIdx.x & 16) ? __uint_as_float(r[0]) : __uint_as_float(r[1]);
+}
+// Value held by the same lane of the previous lane row (row G-1; row 0
+// receives row 3's): G odd is lane l ^ 16, G even lane l ^ 48.
+__device__ __forceinline__ float rot_row(float x) {
+  const float a = xrow16(x), b = xrow16(xhalf(x));
+  return (threadIdx.x & 16) ? a : b;
+}
+
+// q . k of key `key` (RoPE applied to the key when `rope`): each lane row
+// holds 16 of the query's d values (d = 32ks + 8G + e), reduced over the rows.
+template <int D, class E>
+__device__ __forceinline__ float halo_dot16(const float (&qv)[Fwd16<D>::KS][8],
+                                            const E* __restrict__ Ks, long long rstride,
+                                            const float* __restrict__ rope, int key) {
+  const int G = (threadIdx.x >> 4) & 3;
+  const E* kp = Ks + (long long)key * rstride;
+  float acc = 0.0f;
+#pragma unroll
+  for (int ks = 0; ks < Fwd16<D>::KS; ++ks)
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+      const int d0 = 32 * ks + 8 * G + 4 * h2;
+      f32x4 kv = ld4(kp + d0);
+      if (rope) kv = rope4_in<E>(kv, rope_entry(rope, key, D, d0));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = fmaf(qv[ks][4 * h2 + e], kv[e], acc);
+    }
+  acc += xrow16(acc);
+  return acc + xhalf(acc);
+}
+
+// Waves per SIMD: two work groups of eight waves per CU at D <= 64; one at
+// D = 128 (its double-buffered tiles take 116 KB of LDS).
+template <int D, class E, bool ROPE>
+constexpr int fwd16_waves_per_simd() {
+  return D > 64 ? 2 : 4;
+}
+
+template <int D, class E, bool ROPE>
+__global__ __launch_bounds__(512, (fwd16_waves_per_simd<D, E, ROPE>())) void ca_fwd16_kernel(
+    View Qv, View Kv, View Vv, const float* __restrict__ rope, const float* __restrict__ log_gain,
+    float* __restrict__ O, View Ov, float* __restrict__ stats, float* __restrict__ part, int BH,
+    int H, int T, int C, int G, int smax) {
+  using P = Fwd16<D>;
+  constexpr bool BF = std::is_same<E, __bf16>::value;
+  constexpr int NL = BF ? 1 : 3;  // limb planes staged per K and V tile
+  __shared__ __attribute__((aligned(16))) __bf16 lds_k[2][NL][P::KPLANE];
+  __shared__ __attribute__((aligned(16))) __bf16 lds_vt[2][NL][P::VPLANE];
+
+  const int bh = blockIdx.x % BH;
+  const int item = blockIdx.x / BH;
+  int g, split, nsplit;
+  fwd_decode_item(item, G, T, C, g, split, nsplit);
+  if (g < 0) return;
+
+  const int ntiles_all = (T + 31) / 32;
+  const int nt = min(4 * g + 4, ntiles_all);
+  const int t_b = split * C;
+  const int t_e = min(nt, t_b + C);
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6;          // 0..7
+  const int lane = tid & 63;
+  const int q16 = lane & 15;
+  const int G4 = lane >> 4;        // lane row
+  const int i = 128 * g + 16 * w + q16;  // this lane's query
+  const bool qvalid = i < T;
+  const int wave_tmax = 4 * g + (w >> 1);  // diagonal weight tile of this wave
+  const bool wave_active = (128 * g + 16 * w < T) && (t_b <= wave_tmax);
+
+  const size_t slice = (size_t)bh * T * D;
+  const E* __restrict__ Qs = view_slice<const E>(Qv, bh, H);
+  const E* __restrict__ Ks = view_slice<const E>(Kv, bh, H);
+  const E* __restrict__ Vs = view_slice<const E>(Vv, bh, H);
+  const long long krs = Kv.rstride, vrs = Vv.rstride;
+  const float* __restrict__ rope_k = ROPE ? rope : nullptr;
+  const int head = bh % H;
+  const float cl2 = head_scale_log2(log_gain, head, D);
+
+  // lane (q16, G) holds Q[i][32ks + 8G + e] (rotated when `rope`)
+  float qv[P::KS][8];
+  {
+    const E* qp = Qs + (long long)(qvalid ? i : 0) * Qv.rstride;
+#pragma unroll
+    for (int ks = 0; ks < P::KS; ++ks)
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const int d0 = 32 * ks + 8 * G4 + 4 * h2;
+        f32x4 v4 = qvalid ? ld4(qp + d0) : f32x4{0.f, 0.f, 0.f, 0.f};
+        if (rope && qvalid) v4 = rope4_in<E>(v4, rope_entry(rope, i, D, d0));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) qv[ks][4 * h2 + e] = v4[e];
+      }
+  }
+
+  // ---- split-start state (as in ca_fwd_kernel) ----
+  float m_ref = 0.f, s_carry = 0.f, r_carry = 0.f, zsum = 0.f;
+  if (wave_active) {
+    if (t_b == 0) {
+      m_ref = halo_dot16<D>(qv, Ks, krs, rope_k, 0) * cl2;
+    } else {
+      const int k0 = 32 * t_b;
+      s_carry = halo_dot16<D>(qv, Ks, krs, rope_k, k0) * cl2;
+      const float s_prev = halo_dot16<D>(qv, Ks, krs, rope_k, k0 - 1) * cl2;
+      m_ref = fmaxf(s_carry, s_prev);
+      float l_unused;
+      seg_shares(s_prev, s_carry, fast_exp2(s_prev - m_ref), fast_exp2(s_carry - m_ref), l_unused,
+                 r_carry);
+      s_carry -= m_ref;
+    }
+  }
+
+  // B operand of S^T: k step ks, element e = Q[i][32ks + 8G + e]
+  Limbs qb[P::KS];
+#pragma unroll
+  for (int ks = 0; ks < P::KS; ++ks) qb[ks] = split8(qv[ks]);
+
+  f32x4 acc_o[P::NMB];
+#pragma unroll
+  for (int mb = 0; mb < P::NMB; ++mb) acc_o[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // ---- cooperative tile loads (512 threads) ----
+  // K: float4 chunk e -> score key 32t+1+row, d = 4c..4c+3, stored in LDS row
+  // k16_row(row).  V: unit u -> weight keys 32t+2pp, +1, d = 4c..4c+3,
+  // stored transposed as packed pairs (pp = u % 16 the fast index).
+  typedef typename Raw4<E>::type R4;
+  R4 pre_k[P::KLD], pre_v[P::VLD][2];
+  f32x4 pre_cs[ROPE ? P::KLD : 1];
+  constexpr unsigned kEsz = sizeof(E);
+  const __amdgpu_buffer_rsrc_t kres = buffer_rsrc(Ks, (unsigned)view_rows_bytes(T, krs, D, kEsz));
+  const __amdgpu_buffer_rsrc_t vres = buffer_rsrc(Vs, (unsigned)view_rows_bytes(T, vrs, D, kEsz));
+  const __amdgpu_buffer_rsrc_t cres =
+      buffer_rsrc(ROPE ? rope_k : log_gain, ROPE ? (unsigned)(T * D * sizeof(float)) : 0u);
+  const unsigned kstep = 32u * (unsigned)krs * kEsz, vstep = 32u * (unsigned)vrs * kEsz;
+  const unsigned vrow = (unsigned)vrs * kEsz;
+  unsigned koff[P::KLD], csoff[P::KLD], voff[P::VLD];
+#pragma unroll
+  for (int j = 0; j < P::KLD; ++j) {
+    const int e = tid + 512 * j;
+    const int row = e / P::C4, c = e % P::C4;
+    koff[j] = ((unsigned)(1 + row) * (unsigned)krs + 4 * c) * kEsz;
+    csoff[j] = ((unsigned)(1 + row) * D + 4 * c) * (unsigned)sizeof(float);
+  }
+#pragma unroll
+  for (int j = 0; j < P::VLD; ++j) {
+    const int u = tid + 512 * j;
+    const int pp = u % 16, c = u / 16;
+    voff[j] = ((unsigned)(2 * pp) * (unsigned)vrs + 4 * c) * kEsz;
+  }
+  auto load_tile = [&](int t) {
+#pragma unroll
+    for (int j = 0; j < P::KLD; ++j) {
+      const int e = tid + 512 * j;
+      if (P::KCH % 512 == 0 || e < P::KCH) {
+        pre_k[j] = buffer_ld_raw4(kres, koff[j] + t * kstep, Ks);
+        if constexpr (ROPE)
+          pre_cs[j] = __builtin_bit_cast(f32x4, buffer_ld16(cres, csoff[j] + t * (32u * D * 4u), 0));
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < P::VLD; ++j) {
+      const int u = tid + 512 * j;
+      if (P::VUNITS % 512 == 0 || u < P::VUNITS) {
+        pre_v[j][0] = buffer_ld_raw4(vres, voff[j] + t * vstep, Vs);
+        pre_v[j][1] = buffer_ld_raw4(vres, voff[j] + t * vstep + vrow, Vs);
+      }
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < P::KLD; ++j) {
+      const int e = tid + 512 * j;
+      if (P::KCH % 512 == 0 || e < P::KCH) {
+        const int row = e / P::C4, c = e % P::C4;
+        const int off = k16_row(row) * P::KROW + 4 * c;
+        if constexpr (BF && !ROPE) {
+          *reinterpret_cast<u32x2*>(&lds_k[buf][0][off]) = pre_k[j];
+        } else {
+          f32x4 kv = raw_to_f32(pre_k[j], Ks);
+          if constexpr (ROPE) kv = rope4_in<E>(kv, pre_cs[j]);
+          if constexpr (BF) {
+            *reinterpret_cast<u32x2*>(&lds_k[buf][0][off]) =
+                u32x2{cvt_pk_bf16(kv[0], kv[1]), cvt_pk_bf16(kv[2], kv[3])};
+          } else {
+            unsigned h0, m0, l0, h1, m1, l1;
+            split_pair(kv[0], kv[1], h0, m0, l0);
+            split_pair(kv[2], kv[3], h1, m1, l1);
+            *reinterpret_cast<u32x2*>(&lds_k[buf][0][off]) = u32x2{h0, h1};
+            *reinterpret_cast<u32x2*>(&lds_k[buf][1][off]) = u32x2{m0, m1};
+            *reinterpret_cast<u32x2*>(&lds_k[buf][2][off]) = u32x2{l0, l1};
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < P::VLD; ++j) {
+      const int u = tid + 512 * j;
+      if (P::VUNITS % 512 == 0 || u < P::VUNITS) {
+        const int pp = u % 16, c = u / 16;
+        if constexpr (BF) {
+#pragma unroll
+          for (int x = 0; x < 4; ++x) {
+            const unsigned wa = pre_v[j][0][x >> 1], wb = pre_v[j][1][x >> 1];
+            const unsigned pair = (x & 1) ? ((wa >> 16) | (wb & 0xffff0000u))
+                                          : ((wa & 0xffffu) | (wb << 16));
+            *reinterpret_cast<unsigned*>(&lds_vt[buf][0][(4 * c + x) * P::VROW + 2 * pp]) = pair;
+          }
+        } else {
+          const f32x4 va = raw_to_f32(pre_v[j][0], Vs), vb = raw_to_f32(pre_v[j][1], Vs);
+#pragma unroll
+          for (int x = 0; x < 4; ++x) {
+            unsigned hv, mv, lv;
+            split_pair(va[x], vb[x], hv, mv, lv);
+            const int off = (4 * c + x) * P::VROW + 2 * pp;
+            *reinterpret_cast<unsigned*>(&lds_vt[buf][0][off]) = hv;
+            *reinterpret_cast<unsigned*>(&lds_vt[buf][1][off]) = mv;
+            *reinterpret_cast<unsigned*>(&lds_vt[buf][2][off]) = lv;
+          }
+        }
+      }
+    }
+  };
+
+  load_tile(t_b);
+  store_tile(0);
+  __syncthreads();
+
+  for (int t = t_b; t < t_e; ++t) {
+    const int buf = (t - t_b) & 1;
+    if (t + 1 < t_e) load_tile(t + 1);
+
+    auto tile = [&](auto general_tag) {
+      constexpr bool kGeneral = decltype(general_tag)::value;
+      const bool diag = kGeneral && (t == wave_tmax);
+      // ---- S^T = c log2e (K Q^T) - m_ref, two 16-key blocks ----
+      f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+      prio_mfma_begin<!BF>();
+#pragma unroll
+      for (int ks = 0; ks < P::KS; ++ks) {
+        const __bf16* kr0 = &lds_k[buf][0][q16 * P::KROW + 32 * ks + 8 * G4];
+        const __bf16* kr1 = kr0 + 16 * P::KROW;
+        if constexpr (BF) {
+          sacc[0] = mfma16_bf16(*reinterpret_cast<const bf16x8*>(kr0), qb[ks].h, sacc[0]);
+          sacc[1] = mfma16_bf16(*reinterpret_cast<const bf16x8*>(kr1), qb[ks].h, sacc[1]);
+        } else {
+          Limbs ka0, ka1;
+          ka0.h = *reinterpret_cast<const bf16x8*>(kr0);
+          ka0.m = *reinterpret_cast<const bf16x8*>(kr0 + P::KPLANE);
+          ka0.l = *reinterpret_cast<const bf16x8*>(kr0 + 2 * P::KPLANE);
+          ka1.h = *reinterpret_cast<const bf16x8*>(kr1);
+          ka1.m = *reinterpret_cast<const bf16x8*>(kr1 + P::KPLANE);
+          ka1.l = *reinterpret_cast<const bf16x8*>(kr1 + 2 * P::KPLANE);
+#pragma unroll
+          for (int st = 0; st < 6; ++st) {
+            sacc[0] = mfma16_step(st, ka0, qb[ks], sacc[0]);
+            sacc[1] = mfma16_step(st, ka1, qb[ks], sacc[1]);
+          }
+        }
+      }
+      prio_mfma_end<!BF>();
+      float sc[8];
+#pragma unroll
+      for (int r = 0; r < 8; ++r) sc[r] = fmaf(sacc[r >> 2][r & 3], cl2, -m_ref);
+      const int kbase = 32 * t + 1 + 8 * G4;  // score key of sc[0]
+      // ---- row max of the tile (visible keys only), relative to m_ref ----
+      float mt = kNegBig;
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const bool vis = !diag || (kbase + r <= i);
+        mt = fmaxf(mt, vis ? sc[r] : kNegBig);
+      }
+      mt = fmaxf(mt, xrow16(mt));
+      mt = fmaxf(mt, xhalf(mt));
+      const bool grow = mt > kLazyRescale;
+      if (wave_any(grow)) {
+        const float shift = grow ? mt : 0.0f;
+        const float alpha = grow ? fast_exp2(-shift) : 1.0f;
+#pragma unroll
+        for (int mb = 0; mb < P::NMB; ++mb) acc_o[mb] *= alpha;
+        zsum *= alpha;
+        r_carry *= alpha;
+        m_ref += shift;
+        s_carry -= shift;
+#pragma unroll
+        for (int r = 0; r < 8; ++r) sc[r] -= shift;
+      }
+      if (diag) {
+#pragma unroll
+        for (int r = 0; r < 8; ++r) sc[r] = (kbase + r <= i) ? sc[r] : 0.0f;
+      }
+      // ---- left neighbour of sc[0] and carries (relative to m_ref) ----
+      const float s_rot = rot_row(sc[7]);
+      float sl = G4 == 0 ? s_carry : s_rot;
+      s_carry = s_rot;  // row 0 of the next tile: score key 32t+32
+      float pl = fast_exp2(sl);
+
+      // ---- segments: weight register r (weight key kbase-1+r) = left share
+      // of segment r + right share of segment r-1 (+ caps) ----
+      float wt[8];
+      float r_prev = 0.f, zt = 0.f;
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const float sr = sc[r];
+        const float pr = fast_exp2(sr);
+        float Lv, Rv;
+        seg_shares(sl, sr, pl, pr, Lv, Rv);
+        const bool seg_ok = !diag || (kbase + r <= i);
+        Lv = seg_ok ? Lv : 0.0f;
+        Rv = seg_ok ? Rv : 0.0f;
+        float x = Lv + r_prev;
+        const int wk = kbase - 1 + r;
+        if constexpr (kGeneral) {
+          const float cap_last = (diag && wk == i) ? 0.5f * pl : 0.0f;
+          const float cap_first = wk == 0 ? 0.5f * pl : 0.0f;
+          x += cap_last + cap_first;
+        }
+        wt[r] = x;
+        zt += x;
+        r_prev = Rv;
+        sl = sr;
+        pl = pr;
+      }
+      const float r_rot = rot_row(r_prev);
+      const float r_in = G4 == 0 ? r_carry : r_rot;
+      r_carry = r_rot;
+      wt[0] += r_in;
+      zsum += zt + r_in;
+
+      // ---- O^T += V^T W^T: k = weight key 8G + e, d blocks in pairs ----
+      const Limbs wb = split8(wt);
+      prio_mfma_begin<!BF>();
+#pragma unroll
+      for (int m2 = 0; m2 < P::NMB; m2 += 2) {
+        Limbs va[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const __bf16* vr = &lds_vt[buf][0][(16 * (m2 + u) + q16) * P::VROW + 8 * G4];
+          va[u].h = *reinterpret_cast<const bf16x8*>(vr);
+          if (BF) {
+            va[u].m = va[u].l = bf16x8{};
+          } else {
+            va[u].m = *reinterpret_cast<const bf16x8*>(vr + P::VPLANE);
+            va[u].l = *reinterpret_cast<const bf16x8*>(vr + 2 * P::VPLANE);
+          }
+        }
+#pragma unroll
+        for (int st = 0; st < 6; ++st) {
+          if (limb_step_used<BF, false>(st)) {
+            acc_o[m2] = mfma16_step(st, va[0], wb, acc_o[m2]);
+            acc_o[m2 + 1] = mfma16_step(st, va[1], wb, acc_o[m2 + 1]);
+          }
+        }
+      }
+      prio_mfma_end<!BF>();
+    };
+    if (wave_active && t <= wave_tmax) {
+      if (t == 0 || t == wave_tmax)
+        tile(std::true_type{});
+      else
+        tile(std::false_type{});
+    }
+
+    if (t + 1 < t_e) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: lane (q16, G) holds d = 16mb + 4G + r of its query ----
+  if (128 * g + 16 * w >= T) return;
+  float ztot = zsum + xrow16(zsum);
+  ztot += xhalf(ztot);
+  const bool single = (nsplit == 1);
+  float* dst;
+  float scl;
+  if (single) {
+    dst = O + slice + (size_t)i * D;
+    scl = 1.0f / ztot;
+  } else {
+    dst = part + (((size_t)bh * smax + split) * T + i) * D;
+    scl = 1.0f;
+  }
+  if (!wave_active) {
+    if (qvalid) {
+      for (int d = G4; d < D; d += 4) dst[d] = 0.f;
+      if (G4 == 0) {
+        float* mz = part + (size_t)BH * smax * T * D + (((size_t)bh * smax + split) * T + i) * 2;
+        mz[0] = -1e30f;
+        mz[1] = 0.f;
+      }
+    }
+    return;
+  }
+  if (!qvalid) return;
+  E* otok = (single && Ov.base) ? view_slice<E>(Ov, bh, H) + (long long)i * Ov.rstride : nullptr;
+#pragma unroll
+  for (int mb = 0; mb < P::NMB; ++mb) {
+    const int d0 = 16 * mb + 4 * G4;
+    const f32x4 v4 = acc_o[mb] * scl;
+    *reinterpret_cast<f32x4*>(dst + d0) = v4;
+    if (otok) st4(otok + d0, v4);
+  }
+  if (G4 == 0) {
+    if (single) {
+      stats[((size_t)bh * T + i) * 2 + 0] = m_ref;
+      stats[((size_t)bh * T + i) * 2 + 1] = scl;
+    } else {
+      float* mz = part + (size_t)BH * smax * T * D + (((size_t)bh * smax + split) * T + i) * 2;
+      mz[0] = m_ref;
+      mz[1] = ztot;
+    }
+  }
+}
+
 // Merges split partials of rows whose group spans more than one split: one
 // float4 chunk of one row per thread, splits summed in index order.
 template <int D, class E>
@@ -573,6 +1026,17 @@ __global__ __launch_bounds__(256) void ca_fwd_combine_kernel(const float* __rest
   }
 }
 
+// Head dims that run the 16x16x32 forward (the 32x32x16 kernel serves the
+// others).
+template <int D>
+constexpr bool fwd_uses_16x16() {
+#ifdef CA_FWD_32X32_ONLY
+  return false;
+#else
+  return D == 64 || D == 128;
+#endif
+}
+
 template <int D, class E>
 hipError_t launch_fwd(const FwdIO& io, float* part, int B, int H, int T, int C,
                       hipStream_t stream) {
@@ -581,14 +1045,25 @@ hipError_t launch_fwd(const FwdIO& io, float* part, int B, int H, int T, int C,
   const int smax = fwd_max_splits(T, C);
   const int items = fwd_num_items(T, C);
   timer_begin(kFwd, stream);
-  if (io.rope && !io.k_rotated)
-    hipLaunchKernelGGL((ca_fwd_kernel<D, E, true>), dim3(items * BH), dim3(256), 0, stream, io.q,
-                       io.k, io.v, io.rope, io.log_gain, io.y, io.out, io.stats, part, BH, H, T, C,
-                       G, smax);
-  else
-    hipLaunchKernelGGL((ca_fwd_kernel<D, E, false>), dim3(items * BH), dim3(256), 0, stream, io.q,
-                       io.k, io.v, io.rope, io.log_gain, io.y, io.out, io.stats, part, BH, H, T, C,
-                       G, smax);
+  if constexpr (fwd_uses_16x16<D>()) {
+    if (io.rope && !io.k_rotated)
+      hipLaunchKernelGGL((ca_fwd16_kernel<D, E, true>), dim3(items * BH), dim3(512), 0, stream,
+                         io.q, io.k, io.v, io.rope, io.log_gain, io.y, io.out, io.stats, part, BH, H,
+                         T, C, G, smax);
+    else
+      hipLaunchKernelGGL((ca_fwd16_kernel<D, E, false>), dim3(items * BH), dim3(512), 0, stream,
+                         io.q, io.k, io.v, io.rope, io.log_gain, io.y, io.out, io.stats, part, BH, H,
+                         T, C, G, smax);
+  } else {
+    if (io.rope && !io.k_rotated)
+      hipLaunchKernelGGL((ca_fwd_kernel<D, E, true>), dim3(items * BH), dim3(256), 0, stream, io.q,
+                         io.k, io.v, io.rope, io.log_gain, io.y, io.out, io.stats, part, BH, H, T,
+                         C, G, smax);
+    else
+      hipLaunchKernelGGL((ca_fwd_kernel<D, E, false>), dim3(items * BH), dim3(256), 0, stream, io.q,
+                         io.k, io.v, io.rope, io.log_gain, io.y, io.out, io.stats, part, BH, H, T,
+                         C, G, smax);
+  }
   timer_end(kFwd, stream);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
