@@ -364,8 +364,9 @@ def main():
                          "operator legs")
     ap.add_argument("--shape", default=None,
                     help="B,H,T,D of the operator leg (diagnostics; default is BASELINE config 2)")
-    ap.add_argument("--only", choices=["ca_s", "ca_p"], default=None,
-                    help="run only one model-step leg and print its JSON (for profiling)")
+    ap.add_argument("--only", choices=["ca_s", "ca_p", "config5", "ca_s_layer_op"], default=None,
+                    help="run only one leg (a model step, or one of the extra operator shapes) and "
+                         "print its JSON (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device copy (to scale rocprof FETCH/WRITE_SIZE)")
     args = ap.parse_args()
@@ -389,9 +390,15 @@ def main():
     ca = importlib.import_module("continuum-attention_amd")
     ca.native.load()
     dev = torch.device("cuda:0")
-    if args.only:
+    if args.only in ("ca_s", "ca_p"):
         leg = {"ca_s": bench_ca_s, "ca_p": bench_ca_p}[args.only]
         print(json.dumps(leg(ca, dev, steps=args.steps, warmup=args.warmup)), flush=True)
+        return
+    if args.only:
+        name, shape = {"config5": ("config5", (1, 16, 8192, 64)),
+                       "ca_s_layer_op": ("ca_s_layer", (1, 16, 2048, 64))}[args.only]
+        print(json.dumps(operator_leg(ca, dev, name, shape, steps=args.steps, warmup=args.warmup)),
+              flush=True)
         return
     torch.backends.cuda.matmul.allow_tf32 = False
 

@@ -40,6 +40,7 @@ from torch.nn import functional as F
 
 from . import _native
 from .decoder import RMSNorm as _DecoderRMSNorm
+from .decoder import token_embedding as _token_embedding
 from .decoder import rope_continuum_attention
 from .ops import SUPPORTED_HEAD_DIMS, continuum_attention
 from .cpu import _C_J0, _C_RIGHT, _SERIES_BELOW, _series
@@ -246,38 +247,6 @@ class Block(nn.Module):
         return x + self.mlp(self.norm_mlp(x))
 
 
-# Largest vocabulary whose embedding gradient is formed as a one-hot GEMM
-# (its [tokens, vocab] one-hot matrix costs O(tokens * vocab)); the byte
-# vocabulary (256) is far below it.
-ONE_HOT_MAX_VOCAB = 4096
-
-
-class _TokenEmbedding(torch.autograd.Function):
-    """The token lookup ``weight[tokens]`` with its weight gradient formed as
-    ``one_hot(tokens)^T @ grad`` (a scatter of ones into a zeroed matrix, then
-    one GEMM): deterministic, and free of the sorting path torch's embedding
-    backward takes above 3072 lookups, which records memset nodes that HIP
-    graph replays do not reliably redo.  Same values as nn.Embedding's
-    gradient up to the summation order of the rows of equal tokens, for
-    finite gradients; a non-finite gradient row reaches every vocabulary row
-    (0 * inf is NaN in the GEMM) where nn.Embedding's touches only the looked-up
-    row.  Used for vocabularies of at most ONE_HOT_MAX_VOCAB rows."""
-
-    @staticmethod
-    def forward(ctx, tokens, weight):
-        ctx.save_for_backward(tokens)
-        ctx.num = weight.shape[0]
-        return F.embedding(tokens, weight)
-
-    @staticmethod
-    def backward(ctx, grad):
-        (tokens,) = ctx.saved_tensors
-        flat = tokens.reshape(-1, 1)
-        onehot = torch.zeros(flat.shape[0], ctx.num, device=grad.device, dtype=grad.dtype)
-        onehot.scatter_(1, flat, 1.0)
-        return None, onehot.t().mm(grad.reshape(-1, grad.shape[-1]))
-
-
 class TinyLM(nn.Module):
     """Pre-norm byte LM with learned positions and a tied head
     (architecture.py:180-241).  ``layers`` defaults to the reference's six
@@ -310,9 +279,7 @@ class TinyLM(nn.Module):
         if length > self.seq_len:
             raise ValueError("Sequence exceeds model seq_len")
         pos = torch.arange(length, device=tokens.device)
-        tok = (_TokenEmbedding.apply(tokens, self.tok_embed.weight)
-               if tokens.is_cuda and self.tok_embed.num_embeddings <= ONE_HOT_MAX_VOCAB
-               else self.tok_embed(tokens))
+        tok = _token_embedding(tokens, self.tok_embed)
         x = tok + self.pos_embed(pos)[None, :, :]
         blocks = [getattr(self, f"b{i}") for i in range(self.layers)]
         if self.final_norm._fusable(x):

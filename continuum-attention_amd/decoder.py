@@ -347,6 +347,49 @@ def rope_continuum_attention(qkv, log_gain, theta, heads, query_tile=64):
                                          int(heads), int(query_tile))
 
 
+# Largest vocabulary whose embedding gradient is formed as a one-hot GEMM
+# (its [tokens, vocab] one-hot matrix costs O(tokens * vocab)); the byte
+# vocabulary (256) is far below it.
+ONE_HOT_MAX_VOCAB = 4096
+
+
+class _TokenEmbedding(torch.autograd.Function):
+    """The token lookup ``weight[tokens]`` with its weight gradient formed as
+    ``one_hot(tokens)^T @ grad`` (a scatter of ones into a zeroed matrix, then
+    one GEMM): deterministic, and free of the sorting path torch's embedding
+    backward takes above 3072 lookups, which records memset nodes that HIP
+    graph replays do not reliably redo.  Same values as nn.Embedding's
+    gradient up to the summation order of the rows of equal tokens, for
+    finite gradients; a non-finite gradient row reaches every vocabulary row
+    (0 * inf is NaN in the GEMM) where nn.Embedding's touches only the looked-up
+    row.  Used for vocabularies of at most ONE_HOT_MAX_VOCAB rows."""
+
+    @staticmethod
+    def forward(ctx, tokens, weight):
+        ctx.save_for_backward(tokens)
+        ctx.num = weight.shape[0]
+        return F.embedding(tokens, weight)
+
+    @staticmethod
+    def backward(ctx, grad):
+        (tokens,) = ctx.saved_tensors
+        flat = tokens.reshape(-1, 1)
+        onehot = torch.zeros(flat.shape[0], ctx.num, device=grad.device, dtype=grad.dtype)
+        onehot.scatter_(1, flat, 1.0)
+        return None, onehot.t().mm(grad.reshape(-1, grad.shape[-1]))
+
+
+def token_embedding(tokens, emb: nn.Embedding):
+    """``emb(tokens)``, on GPU tensors with the one-hot GEMM weight gradient of
+    _TokenEmbedding when the vocabulary is at most ONE_HOT_MAX_VOCAB rows
+    (torch's embedding backward for the CA-S decoder's 2048 byte lookups took
+    109 us per step, a [2048, 256] x [2048, 1024] GEMM a few)."""
+    if tokens.is_cuda and emb.num_embeddings <= ONE_HOT_MAX_VOCAB and emb.padding_idx is None \
+            and emb.max_norm is None and not emb.scale_grad_by_freq and not emb.sparse:
+        return _TokenEmbedding.apply(tokens, emb.weight)
+    return emb(tokens)
+
+
 class ContinuumSelfAttention(nn.Module):
     """qkv projection -> RoPE -> CA operator -> output projection
     (cuda/continuum_attention.py:838-854)."""
@@ -434,7 +477,7 @@ class ContinuumDecoderLM(nn.Module):
     def forward(self, input_ids, targets=None):
         if input_ids.dim() != 2 or input_ids.shape[1] > self.cfg.block_size:
             raise ValueError("Input must be [B,T] with T<=block_size")
-        x = self.drop(self.byte_emb(input_ids))
+        x = self.drop(token_embedding(input_ids, self.byte_emb))
         if self.blocks and not (self.cfg.grad_checkpointing and self.training) and self.norm_f._fusable(x):
             # the blocks' chain x = x + attn(norm1(x)); x = x + mlp(norm2(x)),
             # with every residual add fused into the norm that reads its sum

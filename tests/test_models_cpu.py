@@ -232,11 +232,17 @@ def test_graph_check_uses_the_loaded_hip_runtime(Dm):
 
 
 def test_token_embedding_gradient_matches_nn_embedding():
-    """TinyLM's GPU token lookup (architecture._TokenEmbedding: the weight
-    gradient as one_hot(tokens)^T @ grad) gives nn.Embedding's output and
-    weight gradient, repeated tokens included (run here on CPU tensors)."""
+    """The GPU token lookup of TinyLM and the CA-S decoder
+    (decoder._TokenEmbedding: the weight gradient as one_hot(tokens)^T @ grad)
+    gives nn.Embedding's output and weight gradient, repeated tokens included
+    (run here on CPU tensors); token_embedding takes it only for small
+    vocabularies and plain embeddings."""
     import importlib
-    A = importlib.import_module("continuum-attention_amd.architecture")
+    A = importlib.import_module("continuum-attention_amd.decoder")
+    small, big = torch.nn.Embedding(256, 8), torch.nn.Embedding(A.ONE_HOT_MAX_VOCAB + 1, 8)
+    t = torch.randint(0, 256, (2, 5))
+    assert torch.equal(A.token_embedding(t, small), small(t))  # CPU tensors: nn.Embedding
+    assert torch.equal(A.token_embedding(t, big), big(t))
     g = torch.Generator().manual_seed(5)
     w = torch.randn(256, 24, generator=g, dtype=torch.float64)
     tokens = torch.randint(0, 256, (7, 300), generator=g)
