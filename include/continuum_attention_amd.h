@@ -49,12 +49,15 @@ const char* ca_last_error(void);
  * here the workspaces are bounded instead: ca_fwd_f32 lengthens its work
  * splits until their partials fit the workspace it is given (none at all
  * needs no workspace), and ca_bwd_f32 runs in passes over ranges of
- * 128-query groups sized to the workspace it is given (dK, dV and dlog_gain
- * are summed over the passes in a fixed order).  The size functions below
- * report the full-speed size, or, when that exceeds the cap, the size of the
- * plan that fits under it.  The cap is process-wide; default 1 GiB, 0 = no
- * cap.  Results are deterministic for a given workspace size; different
- * sizes sum in different orders and may differ by rounding. */
+ * 128-query groups sized to the workspace it is given, of every slice or,
+ * when not even one group of every slice fits, of sets of consecutive heads
+ * of one batch (dK, dV and dlog_gain are summed over the passes in a fixed
+ * order).  The size functions below report the full-speed size, or, when
+ * that exceeds the cap, the size of the plan that fits under it (or, below
+ * the least any plan needs, one 128-query group of one slice, that least
+ * size).  The cap is process-wide; default 1 GiB, 0 = no cap.  Results are
+ * deterministic for a given workspace size; different sizes sum in
+ * different orders and may differ by rounding. */
 int ca_set_workspace_cap(size_t bytes);
 size_t ca_workspace_cap(void);
 
@@ -95,10 +98,12 @@ int ca_bwd_f32(const float* q, const float* k, const float* v, const float* log_
  * runs on until the process ends.  No counterpart in the reference: for
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc).  It allocates
- * nothing; a shape whose full backward workspace exceeds the array runs in
- * passes over 128-query groups sized to it, and a shape whose single group
- * needs more fails with CA_ERR_WORKSPACE before any launch.  All calls on one
- * device share its
+ * nothing.  The shape is checked first, as ca_bwd_f32 checks it; a shape
+ * whose full backward workspace exceeds the array runs in passes sized to
+ * it (over query ranges of every slice or of sets of heads), and a shape
+ * whose least plan needs more would fail with CA_ERR_WORKSPACE before any
+ * launch (none of the shapes the kernels accept does: one 128-query group of
+ * one slice needs at most 32 MiB).  All calls on one device share its
  * array, so calls that overlap in time on one device (other streams, other
  * threads) race and must be serialised by the caller. */
 int ca_bwd_f32_noalloc(const float* q, const float* k, const float* v, const float* log_gain,
@@ -161,11 +166,15 @@ int ca_fwd_qkv(const void* qkv, int dtype, const float* rope_cs, const float* lo
 
 /* Backward of ca_fwd_qkv: dout [B, T, H*D] (dtype) -> dqkv [B, T, 3, H, D]
  * (dtype; the gradients of q and k rotated back by the transposed RoPE) and
- * dlog_gain[H].  It runs in one pass (gradients in the element type are not
- * summed over passes), so its workspace is ca_bwd_qkv_workspace_bytes,
- * regardless of the cap (with RoPE it also holds the keys rotated once; a
- * workspace without that room, ca_bwd_qkv_workspace_bytes minus
- * B*H*T*D*4 bytes rounded up to 256, also works). */
+ * dlog_gain[H].  With a workspace that holds the whole backward it runs in
+ * one pass and writes the gradients in the element type (with RoPE and room
+ * for B*H*T*D*4 more bytes, rounded up to 256, the keys are also rotated
+ * once into it).  Under the cap, with less, it runs in passes over query
+ * ranges of all slices or of sets of heads, summing dK and dV over the
+ * passes in fp32 buffers at the start of the workspace and rounding them
+ * into dqkv once (dq is complete within a pass).  ca_bwd_qkv_workspace_bytes
+ * reports the one-pass size (with the rotated keys when they fit) while it
+ * fits under the cap, else the size of the plan for the cap. */
 size_t ca_bwd_qkv_workspace_bytes(int B, int H, int T, int D);
 int ca_bwd_qkv(const void* qkv, int dtype, const float* rope_cs, const float* log_gain,
                const float* y, const float* stats, const void* dout, void* dqkv,
