@@ -144,13 +144,27 @@ ca::DkdvSplit dkdv_split_for(int BH, int D, int dtype, const ca::BwdPass& p, boo
   // rounds of them (9/4 of the two-per-CU count; at [1,16,2048,64] chunks of
   // 16 tiles took 0.277 ms per fwd+bwd against 0.283 ms for 24 and 0.281 ms
   // for 12, while fp32 operands keep 24: 0.302 ms against 0.306 ms for 16).
+  // fp32 operands at D = 64 (the single-buffered kernel, three per CU):
+  // split only below 1.5 rounds of three per CU and shorten like bf16 (at
+  // [1,16,2048,64] 16-tile chunks took dK/dV 0.157 ms against 0.168 ms for
+  // 24; config 2, 37 key groups x 32 slices, stays unsplit: 24-tile chunks
+  // made dK/dV 8 us faster and their merge in the dQ launch 14 us slower).
   int res = kDqSplitBound;
+  long long want = -1;
   if (!for_sizing) {
     const int two_per_cu = dkdv_resident_groups();
-    res = D > 64 ? two_per_cu / 2 : dtype == CA_DTYPE_BF16 ? std::min(two_per_cu * 9 / 4, kDqSplitBound)
-                                                           : two_per_cu;
+    if (D > 64) {
+      res = two_per_cu / 2;
+    } else if (dtype == CA_DTYPE_BF16) {
+      res = std::min(two_per_cu * 9 / 4, kDqSplitBound);
+    } else if (dtype == CA_DTYPE_F32 && D == 64) {
+      res = std::min(two_per_cu * 9 / 4, kDqSplitBound);
+      want = res;
+    } else {
+      res = two_per_cu;
+    }
   }
-  return ca::dkdv_split(BH, p, res);
+  return ca::dkdv_split(BH, p, res, want);
 }
 
 // Workspace layout of one backward pass (every pass lays its buffers out from

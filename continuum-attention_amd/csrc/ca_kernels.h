@@ -254,8 +254,10 @@ inline DkdvSplit dkdv_split_chunk(const BwdPass& p, int chunk) {
 // a round is taken, else the last.  resident_groups: dK/dV work groups the
 // GPU holds at once (0: never split).
 constexpr int kDkdvChunkSmall[] = {16, 12, 8, 6};
-inline DkdvSplit dkdv_split(int BH, const BwdPass& p, int resident_groups) {
-  const long long want = 2LL * resident_groups;
+// want_groups: split only when the whole groups number fewer (default: two
+// rounds of resident_groups).
+inline DkdvSplit dkdv_split(int BH, const BwdPass& p, int resident_groups, long long want_groups = -1) {
+  const long long want = want_groups >= 0 ? want_groups : 2LL * resident_groups;
   if ((long long)p.kv_groups * BH >= want) return dkdv_split_chunk(p, p.qb - p.qa);
   DkdvSplit s = dkdv_split_chunk(p, kDkdvChunkTiles);
   for (int c : kDkdvChunkSmall) {
