@@ -157,14 +157,22 @@ __device__ __forceinline__ void gain_sum(const float* __restrict__ gain_part,
 // when an earlier pass already wrote this key group, added to them.  Run by
 // extra work groups of the dQ launch, which follows the dK/dV launch that
 // wrote the partials.
+// Work groups per merged group in the two merges below: one float4 of the
+// group's partial tiles per thread (the groups are few, so a work group per
+// group left most of the GPU idle: one CA-S layer's dQ merge 14 -> 5 us).
+template <int D>
+constexpr int kv_merge_slices() { return (kDkdvKeys * 2 * (D / 4) + 255) / 256; }
+template <int D>
+constexpr int dq_merge_slices() { return (kDqRows * (D / 4) + 255) / 256; }
+
 template <int D, class E>
 __device__ __forceinline__ void merge_kv_group(const float* __restrict__ kv_part,
                                                const float* __restrict__ rope, const View& dKv,
                                                const View& dVv, const BwdPass& pass, int bh,
-                                               int wg, int H, int T, int kv_chunk,
+                                               int wg, int slice, int H, int T, int kv_chunk,
                                                int kv_part_items, bool kv_f32) {
   constexpr int C4 = D / 4;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x + 256 * slice;
   int first = 0;  // item index of the group's chunk 0 (multi-chunk groups come first)
   for (int gg = 0; gg < wg; ++gg) first += dkdv_group_chunks(gg, pass, kv_chunk);
   const int nch = dkdv_group_chunks(wg, pass, kv_chunk);
@@ -172,7 +180,7 @@ __device__ __forceinline__ void merge_kv_group(const float* __restrict__ kv_part
   const f32x4* part = reinterpret_cast<const f32x4*>(
       kv_part + ((size_t)bh * kv_part_items + first) * kDkdvKeys * 2 * D);
   const int w0 = kDkdvKeys * wg;
-  for (int e = tid; e < kDkdvKeys * 2 * C4; e += 256) {
+  for (int e = tid; e < kDkdvKeys * 2 * C4; e += 256 * kv_merge_slices<D>()) {
     const int kl = e / (2 * C4), which = (e / C4) % 2, c4 = e % C4;
     const int key = w0 + kl;
     if (key >= T) break;
@@ -221,9 +229,11 @@ __global__ __launch_bounds__(256, (std::is_same<E, __bf16>::value && D <= 64 ? 4
     const int x = blockIdx.x - n_items * BH;
     if (x < H)  // the H gain work groups
       gain_sum(gain_part, dlog_gain, x, B, H, n_kv_items, pass.first);
-    else        // then one per (multi-chunk dK/dV key group, slice)
-      merge_kv_group<D, E>(kv_part, rope, dKv, dVv, pass, (x - H) % BH, (x - H) / BH, H, T,
-                           kv_chunk, kv_part_items, kv_f32);
+    else {      // then kv_merge_slices per (multi-chunk dK/dV key group, slice)
+      const int y = (x - H) / kv_merge_slices<D>(), sl = (x - H) % kv_merge_slices<D>();
+      merge_kv_group<D, E>(kv_part, rope, dKv, dVv, pass, y % BH, y / BH, sl, H, T, kv_chunk,
+                           kv_part_items, kv_f32);
+    }
     return;
   }
   __shared__ __attribute__((aligned(16))) __bf16 kst[2 * P::STAGE];
@@ -462,19 +472,21 @@ __global__ __launch_bounds__(256, (std::is_same<E, __bf16>::value && D <= 64 ? 4
   }
 }
 
-// Merge of dQ chunk partials, in chunk order: work group BH*gi + bh sums the
-// chunks of multi-chunk dQ group g1-1-gi of slice bh (rotated back when RoPE
-// is on).  (The dK/dV chunk partials are summed by extra work groups of the
-// dQ launch.)
+// Merge of dQ chunk partials, in chunk order: the dq_merge_slices work
+// groups (BH*gi + bh)*NS + slice sum the chunks of multi-chunk dQ group
+// g1-1-gi of slice bh, one float4 of its rows per thread (rotated back when
+// RoPE is on).  (The dK/dV chunk partials are summed by extra work groups of
+// the dQ launch.)
 template <int D, class E>
 __global__ __launch_bounds__(256) void ca_bwd_merge_kernel(const float* __restrict__ dq_part,
                                                            const float* __restrict__ rope,
                                                            View dQv, BwdPass pass, int B, int H,
                                                            int T, int chunk, int n_part) {
-  const int tid = threadIdx.x;
   constexpr int C4 = D / 4;
+  constexpr int NS = dq_merge_slices<D>();
+  const int tid = threadIdx.x + 256 * (blockIdx.x % NS);
   const int BH = B * H;
-  const int m = blockIdx.x;
+  const int m = blockIdx.x / NS;
   const int bh = m % BH, gi = m / BH;
   const int qg = pass.g1 - 1 - gi;
   int first = 0;  // item index of the group's chunk 0
@@ -482,7 +494,7 @@ __global__ __launch_bounds__(256) void ca_bwd_merge_kernel(const float* __restri
   const int nch = dq_group_chunks(qg, T, chunk);
   const f32x4* part = reinterpret_cast<const f32x4*>(dq_part + ((size_t)bh * n_part + first) * kDqRows * D);
   E* dQs = view_slice<E>(dQv, bh, H);
-  for (int e = tid; e < kDqRows * C4; e += 256) {
+  for (int e = tid; e < kDqRows * C4; e += 256 * NS) {
     const int row = kDqRows * qg + e / C4, c4 = e % C4;
     if (row >= T) break;
     f32x4 s = part[e];
@@ -542,7 +554,7 @@ hipError_t launch_bwd(const BwdIO& io, const BwdWork& ws, const BwdPass& pass, c
   // the dQ grid's extra work groups: H that sum the gain partials of the dK/dV
   // items, then one per (multi-chunk dK/dV key group, slice) that sums its
   // chunk partials
-  const dim3 dq_grid(sp.items * BH + H + kvs.multi_groups * BH);
+  const dim3 dq_grid(sp.items * BH + H + kvs.multi_groups * BH * kv_merge_slices<D>());
   if (io.rope && !io.k_rotated)
     hipLaunchKernelGGL((ca_bwd_dq_kernel<D, E, true>), dq_grid, dim3(256), 0, stream, ws.dsbuf,
                        io.k, io.rope, io.log_gain, io.dq, ws.dq_part, ws.gain_part, io.dlog_gain,
@@ -559,7 +571,8 @@ hipError_t launch_bwd(const BwdIO& io, const BwdWork& ws, const BwdPass& pass, c
   // dQ chunk partials (small grids only) are merged by a launch of their own
   if (sp.multi_groups == 0) return hipSuccess;
   timer_begin(kBwdGain, stream);
-  hipLaunchKernelGGL((ca_bwd_merge_kernel<D, E>), dim3(BH * sp.multi_groups), dim3(256), 0, stream,
+  hipLaunchKernelGGL((ca_bwd_merge_kernel<D, E>), dim3(BH * sp.multi_groups * dq_merge_slices<D>()),
+                     dim3(256), 0, stream,
                      ws.dq_part, io.rope, io.dq, pass, B, H, T, sp.chunk, sp.part_items);
   timer_end(kBwdGain, stream);
   return hipGetLastError();
