@@ -159,7 +159,7 @@ __device__ __forceinline__ void gain_sum(const float* __restrict__ gain_part,
 // wrote the partials.
 // Work groups per merged group in the two merges below: one float4 of the
 // group's partial tiles per thread (the groups are few, so a work group per
-// group left most of the GPU idle: one CA-S layer's dQ merge 14 -> 5 us).
+// group left most of the GPU idle: one CA-S layer's dQ merge 14 -> 8 us).
 template <int D>
 constexpr int kv_merge_slices() { return (kDkdvKeys * 2 * (D / 4) + 255) / 256; }
 template <int D>
