@@ -8,7 +8,9 @@ upstream grad ~ N(0,1), seed 0.  One "step" is one forward + backward of the
 operator with inputs already resident in HBM.
 
 Prints ONE JSON line (rank 0).  `value` is the median fwd+bwd milliseconds
-(lower is better) of uninstrumented steps.  `roofline` is for the dominant
+(lower is better) of uninstrumented steps.  Before the warm-up steps the same
+operator step runs for --clock-warmup-s seconds (default 0.25) so that the
+GPU clock has ramped up (line field `clock_warmup`).  `roofline` is for the dominant
 kernel, from HIP events recorded around each kernel launch on the launch
 stream during a second run of the same steps; `cpu_baseline` times the CPU
 port of the reference's PyTorch CPU path (oracle/ca_cpu_port.py) on the same
@@ -133,6 +135,20 @@ def _time_steps(step, steps, warmup, first=0):
     return e0.elapsed_time(e1) / steps, out
 
 
+def _clock_warmup(step, seconds):
+    """Runs step(0) (synchronising every 10 calls) for `seconds` of wall time so
+    that the GPU clock has ramped up; returns {"s": ..., "steps": ...}."""
+    import torch
+    n = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(10):
+            step(0)
+        torch.cuda.synchronize()
+        n += 10
+    return {"s": round(time.perf_counter() - t0, 3), "steps": n}
+
+
 def _ca_kernel_ms(ca, step, steps, first=0):
     """CA kernel ms per step of an instrumented run of `steps` calls (its
     per-kernel events do not load the timed steps)."""
@@ -152,11 +168,17 @@ def _timed_steps(ca, step, steps, warmup):
     return ms, _ca_kernel_ms(ca, step, steps, warmup + steps), out
 
 
-def time_operator(ca, dev, q, k, v, rho, dy, steps, warmup):
+def time_operator(ca, dev, q, k, v, rho, dy, steps, warmup, clock_warmup_s=0.0):
     """Forward + backward of the operator on resident inputs: median fwd, bwd
     and total ms of `steps` uninstrumented steps (HIP events on the current
     stream around each half), then the same steps with HIP events around every
-    kernel launch on its stream (per-kernel times)."""
+    kernel launch on its stream (per-kernel times).
+
+    `clock_warmup_s` > 0 first runs the same step for that many seconds of
+    wall time, before the `warmup` steps: the GPU clock ramps up under load
+    (medians of 20 steps of the [2,16,2048,64] step from a cold start read
+    0.630, 0.557, 0.542, then a steady 0.537 ms), so with a handful of
+    warm-up steps the timed steps would otherwise land on the ramp."""
     import torch
     q, k, v = (x.to(dev).requires_grad_(True) for x in (q, k, v))
     rho = rho.to(dev).requires_grad_(True)
@@ -168,6 +190,7 @@ def time_operator(ca, dev, q, k, v, rho, dy, steps, warmup):
         torch.autograd.grad(y, (q, k, v, rho), dy)
         return y
 
+    clock = _clock_warmup(lambda i: step(), clock_warmup_s)
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -206,7 +229,9 @@ def time_operator(ca, dev, q, k, v, rho, dy, steps, warmup):
             "bwd_tflops": round(10 * D * P / (bwd * 1e-3) / 1e12, 2),
             "tflops": round(14 * D * P / (tot * 1e-3) / 1e12, 2),
             "roofline_frac": round(14 * D * P / (tot * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
-            "wall_s": round(wall, 3), "kernels": per_kernel, "kt": kt}
+            "wall_s": round(wall, 3),
+            "clock_warmup": clock,
+            "kernels": per_kernel, "kt": kt}
 
 
 def config5_inputs(T=8192):
@@ -224,7 +249,7 @@ def config5_inputs(T=8192):
     return q, k.contiguous(), v, torch.zeros(16), dy
 
 
-def operator_leg(ca, dev, name, shape, steps, warmup):
+def operator_leg(ca, dev, name, shape, steps, warmup, clock_warmup_s=0.0):
     """One more operator shape on the same line: fwd, bwd, total ms and
     TFLOP/s (algorithmic: 4 D, 10 D, 14 D flops per causal pair)."""
     import torch
@@ -244,7 +269,7 @@ def operator_leg(ca, dev, name, shape, steps, warmup):
     ca.ops.set_workspace_cap(0)
     full_b = lib.ca_bwd_workspace_bytes(*shape)
     ca.ops.set_workspace_cap(prev)
-    op = time_operator(ca, dev, q, k, v, rho, dy, steps, warmup)
+    op = time_operator(ca, dev, q, k, v, rho, dy, steps, warmup, clock_warmup_s)
     op.pop("kt")
     op.update({"shape": list(shape), "inputs": inputs, "steps": steps, "warmup": warmup,
                "workspace_cap_bytes": prev, "fwd_workspace_bytes": ws_f,
@@ -255,7 +280,7 @@ def operator_leg(ca, dev, name, shape, steps, warmup):
     return op
 
 
-def bench_ca_s(ca, dev, steps=20, warmup=5):
+def bench_ca_s(ca, dev, steps=20, warmup=5, clock_warmup_s=0.0):
     """one CA-S decoder training step (101,205,120 params,
     T=2048, batch 1, bf16 autocast with fp32 CA scores, AdamW + clip 1.0 as
     the library's fused HIP optimizer) on uniform-random bytes, random-init
@@ -277,13 +302,16 @@ def bench_ca_s(ca, dev, steps=20, warmup=5):
                                       steps, warmup)
     # the graph holds the gradient buffers from here on (no eager step after it)
     graphed = Dm.GraphedTrainStep(model, opt, batches[0])
+    # the GPU idles while the graph is captured: ramp its clock up again
+    clock = _clock_warmup(lambda i: graphed(batches[i % 4]), clock_warmup_s)
     ms, loss = _time_steps(lambda i: graphed(batches[i % 4]), steps, warmup)
     del graphed
     tokens = cfg.block_size
     res = {"metric": "CA-S tokens/s", "tokens_per_s": round(tokens / (ms * 1e-3), 1),
            "ms_per_step": round(ms, 3), "ca_kernels_ms_per_step": round(ca_ms, 3),
            "eager_ms_per_step": round(eager_ms, 3), "step": "GraphedTrainStep",
-           "steps": steps, "warmup": warmup, "params": nparams, "loss": round(float(loss), 4),
+           "steps": steps, "warmup": warmup, "clock_warmup": clock, "params": nparams,
+           "loss": round(float(loss), 4),
            "dtype": "bf16 autocast, f32 CA scores", "data": "synthetic uniform bytes",
            "config": {"workload": "CA-S decoder train step (BASELINE config 4)", "d_model": cfg.d_model,
                       "n_layers": cfg.n_layers, "n_heads": cfg.n_heads, "T": cfg.block_size,
@@ -294,7 +322,7 @@ def bench_ca_s(ca, dev, steps=20, warmup=5):
     return res
 
 
-def bench_ca_p(ca, dev, steps=30, warmup=10):
+def bench_ca_p(ca, dev, steps=30, warmup=10, clock_warmup_s=0.0):
     """small CA-P decoder (TinyLM backbone with 4 blocks,
     d 256, 4 heads, fixed tau 0.30, T=512, batch 16), one fp32 step on
     uniform-random bytes, random-init weights.  Timed as
@@ -315,6 +343,7 @@ def bench_ca_p(ca, dev, steps=30, warmup=10):
     prev_blas = torch.backends.cuda.preferred_blas_library()
     torch.backends.cuda.preferred_blas_library("cublas")
     step_kind = "GraphedTrainStep"
+    clock = None
     try:
         eager_ms, ca_ms, loss = _timed_steps(
             ca, lambda i: A.train_step(model, opt, data[i % 4][:, :-1], data[i % 4][:, 1:]), steps,
@@ -330,6 +359,8 @@ def bench_ca_p(ca, dev, steps=30, warmup=10):
         except ValueError:
             step_kind = "eager"
         else:
+            clock = _clock_warmup(lambda i: graphed(data[i % 4][:, :-1], data[i % 4][:, 1:]),
+                                  clock_warmup_s)
             ms, loss = _time_steps(lambda i: graphed(data[i % 4][:, :-1], data[i % 4][:, 1:]),
                                    steps, warmup)
             del graphed
@@ -339,7 +370,7 @@ def bench_ca_p(ca, dev, steps=30, warmup=10):
     res = {"metric": "CA-P tokens/s", "tokens_per_s": round(tokens / (ms * 1e-3), 1),
            "ms_per_step": round(ms, 3), "ca_kernels_ms_per_step": round(ca_ms, 3),
            "eager_ms_per_step": round(eager_ms, 3), "step": step_kind,
-           "steps": steps, "warmup": warmup, "params": A.parameters(model),
+           "steps": steps, "warmup": warmup, "clock_warmup": clock, "params": A.parameters(model),
            "loss": round(float(loss), 4), "dtype": "f32", "data": "synthetic uniform bytes",
            "config": {"workload": "CA-P TinyLM train step (BASELINE config 3)", "layers": 4,
                       "width": 256, "heads": 4, "T": 512, "batch": 16, "fixed_tau": 0.30,
@@ -354,10 +385,12 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=100,
-                    help="untimed steps first: the GPU clock ramps over the first ~60 steps of "
-                         "the [2,16,2048,64] operator (medians of 20 steps from a cold start: "
-                         "0.630, 0.557, 0.542, then 0.537 ms), so the timed steps start past it")
+    ap.add_argument("--warmup", type=int, default=20, help="untimed steps before the timed ones")
+    ap.add_argument("--clock-warmup-s", type=float, default=0.25,
+                    help="seconds of operator steps run before the warm-up steps so that the GPU "
+                         "clock has ramped up (it takes ~60 steps of the [2,16,2048,64] operator "
+                         "from a cold start: medians of 20 steps 0.630, 0.557, 0.542, then "
+                         "0.537 ms); reported as `clock_warmup` on the line, 0 turns it off")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-models", action="store_true",
                     help="skip the CA-S (config 4) and CA-P (config 3) training-step legs")
@@ -394,13 +427,14 @@ def main():
     dev = torch.device("cuda:0")
     if args.only in ("ca_s", "ca_p"):
         leg = {"ca_s": bench_ca_s, "ca_p": bench_ca_p}[args.only]
-        print(json.dumps(leg(ca, dev, steps=args.steps, warmup=args.warmup)), flush=True)
+        print(json.dumps(leg(ca, dev, steps=args.steps, warmup=args.warmup,
+                             clock_warmup_s=args.clock_warmup_s)), flush=True)
         return
     if args.only:
         name, shape = {"config5": ("config5", (1, 16, 8192, 64)),
                        "ca_s_layer_op": ("ca_s_layer", (1, 16, 2048, 64))}[args.only]
-        print(json.dumps(operator_leg(ca, dev, name, shape, steps=args.steps, warmup=args.warmup)),
-              flush=True)
+        print(json.dumps(operator_leg(ca, dev, name, shape, steps=args.steps, warmup=args.warmup,
+                                      clock_warmup_s=args.clock_warmup_s)), flush=True)
         return
     torch.backends.cuda.matmul.allow_tf32 = False
 
@@ -408,7 +442,8 @@ def main():
     B, H, T, D = shape
     g = torch.Generator().manual_seed(0)
     q, k, v, dy = (torch.randn(shape, generator=g) for _ in range(4))
-    op = time_operator(ca, dev, q, k, v, torch.zeros(H), dy, args.steps, args.warmup)
+    op = time_operator(ca, dev, q, k, v, torch.zeros(H), dy, args.steps, args.warmup,
+                       args.clock_warmup_s)
     ms, kt, per_kernel = op["total_ms"], op["kt"], op["kernels"]
     P = pairs(B, H, T)
     flops_total = 14 * D * P
@@ -442,6 +477,9 @@ def main():
         "bwd_tflops": op["bwd_tflops"],
         "algorithmic_gflop": round(flops_total / 1e9, 3),
         "wall_s_timed_region": op["wall_s"],
+        "clock_warmup": dict(op["clock_warmup"], note=(
+            "operator steps run for this long before the warm-up steps, so that the timed steps "
+            "see a ramped GPU clock")),
         "kernels": per_kernel,
         # achieved = algorithmic fp32 flops of the dominant kernel / its launch
         # time, against the fp32-MFMA peak the metric names.  The products run
@@ -468,12 +506,14 @@ def main():
         # BASELINE config 5 (the long-context stress inputs; the backward in
         # passes under the default 1 GiB workspace cap) and one CA-S layer's
         # operator shape
-        out["config5"] = operator_leg(ca, dev, "config5", (1, 16, 8192, 64), steps=20, warmup=10)
+        out["config5"] = operator_leg(ca, dev, "config5", (1, 16, 8192, 64), steps=20, warmup=10,
+                                      clock_warmup_s=args.clock_warmup_s)
         out["ca_s_layer_op"] = operator_leg(ca, dev, "ca_s_layer", (1, 16, 2048, 64),
-                                            steps=args.steps, warmup=args.warmup)
+                                            steps=args.steps, warmup=args.warmup,
+                                            clock_warmup_s=args.clock_warmup_s)
     if not args.no_models:
-        out["ca_s"] = bench_ca_s(ca, dev)
-        out["ca_p"] = bench_ca_p(ca, dev)
+        out["ca_s"] = bench_ca_s(ca, dev, clock_warmup_s=args.clock_warmup_s)
+        out["ca_p"] = bench_ca_p(ca, dev, clock_warmup_s=args.clock_warmup_s)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)
