@@ -401,6 +401,7 @@ __global__ __launch_bounds__(256, (std::is_same<E, __bf16>::value && D <= 64 ? 4
         for (int e = 0; e < 8; ++e) a[rb][e] = a_next[rb][e];
       if (st_lo + it + 1 < my_end) load_a(it + 1, a_next);
       const Limbs al0 = split8(a[0]), al1 = split8(a[1]);
+      prio_mfma_begin<!BF>();
       const __bf16* kb_base = kst + buf * P::STAGE;
 #pragma unroll
       for (int nb = 0; nb < P::NB; ++nb) {
@@ -422,6 +423,7 @@ __global__ __launch_bounds__(256, (std::is_same<E, __bf16>::value && D <= 64 ? 4
           }
         }
       }
+      prio_mfma_end<!BF>();
     }
     if (it + 1 < iters) store_k(buf ^ 1);
     __syncthreads();

@@ -190,8 +190,9 @@ __device__ __forceinline__ Limbs split8(const float* x) {
 // Wave priority raised over a wave's matrix-product blocks (s_setprio), so
 // the SIMD's other waves fill the VALU while those MFMAs are issued.  ON for
 // operands that take all six limb products: fp32 config 2 dK/dV 0.2698 ->
-// 0.2677 ms, op 0.5418 -> 0.5389 ms (mean of four runs each); bf16 operands
-// (fewer products) measured 1.5% slower with it.
+// 0.2677 ms, op 0.5418 -> 0.5389 ms (mean of four runs each), dQ 0.0736 ->
+// 0.0731 ms (two runs each); bf16 operands (fewer products) measured 1.5%
+// slower with it.
 template <bool ON>
 __device__ __forceinline__ void prio_mfma_begin() { if (ON) __builtin_amdgcn_s_setprio(1); }
 template <bool ON>
@@ -207,8 +208,17 @@ __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcp
 // arithmetic; loads whose voffset lies at or past `bytes` return zeros.  The
 // range must stay below 4 GiB.  0x00020000 is the gfx9 descriptor word 3 for
 // untyped 32-bit data.
+// `base` and `bytes` must be the same in every lane (a slice's or a whole
+// tensor's); they are taken from the first active lane, so the descriptor
+// sits in scalar registers even where the compiler formed them in vector
+// registers (the slice index's division by H runs on the VALU) -- otherwise
+// every load through it is wrapped in a loop over the lanes' descriptors.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, unsigned bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+  const unsigned long long a = reinterpret_cast<unsigned long long>(base);
+  const unsigned lo = (unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)a);
+  const unsigned hi = (unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)(a >> 32));
+  void* p = reinterpret_cast<void*>(((unsigned long long)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(p, (short)0, __builtin_amdgcn_readfirstlane((int)bytes),
                                            0x00020000);
 }
 __device__ __forceinline__ u32x4 buffer_ld16(__amdgpu_buffer_rsrc_t r, unsigned voff,

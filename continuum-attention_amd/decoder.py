@@ -27,7 +27,7 @@ from torch.nn import functional as F
 
 from . import _native
 from .ops import (SUPPORTED_HEAD_DIMS, _bwd_qkv_workspace_bytes, _fwd_qkv_workspace_bytes, _mode,
-                  continuum_attention)
+                  check_mode_limits, continuum_attention)
 
 _DTYPE_CODE = {torch.float32: _native.CA_DTYPE_F32, torch.bfloat16: _native.CA_DTYPE_BF16,
                torch.float16: _native.CA_DTYPE_F16}
@@ -286,16 +286,19 @@ class _RopeContinuumAttention(torch.autograd.Function):
     def forward(ctx, qkv, log_gain, theta, heads, query_tile):
         if int(query_tile) <= 0:
             raise ValueError("query_tile must be positive")
-        _mode()
+        mode = _mode()
         if qkv.dtype not in _DTYPE_CODE:
             raise ValueError(f"unsupported qkv dtype {qkv.dtype}")
         if qkv.device.type != "cuda":
             raise RuntimeError("continuum attention (continuum-attention_amd) runs on ROCm GPU "
                                f"tensors only; got a tensor on {qkv.device}")
-        lib = _native.load()
         Bsz, T, C3 = qkv.shape
         C = C3 // 3
         D = C // heads
+        # the operator's mode limits, on the rotated q and v in the projection's
+        # dtype as the reference passes them (cuda/continuum_attention.py:853)
+        check_mode_limits(mode, True, qkv.dtype, qkv.dtype, T, D)
+        lib = _native.load()
         dev, dt = qkv.device, _DTYPE_CODE[qkv.dtype]
         x = _aligned(qkv.detach(), 16)
         cs = rope_cos_sin(T, D, theta, dev, qkv.dtype) if theta is not None else None

@@ -20,12 +20,14 @@ dims run the reference's query-tile structure, where it does bound memory.  All 
 exact fp32 path (the reference modes differ only in fp16 rounding and launch
 structure).
 
+The reference's per-mode limits hold on every device (:662-665):
+``CA_CUDA_MODE`` prefix_v5/prefix_v6 need CUDA fp16 tensors and T <= 2048,
+and 'fused' needs T <= 2048, D <= 128 and fp16/fp32 values (ValueError).
+
 GPU tensors run the HIP kernels only (a missing library raises; there is no
 fallback).  CPU tensors run ``cpu.py``, this package's own float32
 formulation of the reference's CPU branch (``ext=None``,
-cuda/continuum_attention.py:658, 688, 737-751), with the reference's CPU-side
-errors: ``CA_CUDA_MODE`` prefix_v5/prefix_v6 need CUDA fp16 tensors, and
-'fused' needs T <= 2048, D <= 128 and fp16/fp32 values (:662-665).
+cuda/continuum_attention.py:658, 688, 737-751).
 """
 from __future__ import annotations
 
@@ -46,6 +48,18 @@ def _mode() -> str:
     if mode not in _MODES:
         raise ValueError("CA_CUDA_MODE must be dense, prefix, fused, prefix_v5, or prefix_v6")
     return mode
+
+
+def check_mode_limits(mode: str, is_cuda: bool, q_dtype: torch.dtype, v_dtype: torch.dtype,
+                      T: int, D: int) -> None:
+    """The reference's per-mode limits, raised on every device as there
+    (cuda/continuum_attention.py:662-665): prefix_v5/prefix_v6 need CUDA fp16
+    Q/K/V and T <= 2048; 'fused' needs T <= 2048, D <= 128 and fp16/fp32
+    values.  Within them every mode runs the same exact fp32 kernels."""
+    if mode in ("prefix_v5", "prefix_v6") and (not is_cuda or q_dtype != torch.float16 or T > 2048):
+        raise ValueError("CA v5/v6 paths require CUDA FP16 Q/K/V and T<=2048")
+    if mode == "fused" and (T > 2048 or D > 128 or v_dtype not in (torch.float16, torch.float32)):
+        raise ValueError("CA fused forward supports T<=2048, D<=128, FP16/FP32 values")
 
 
 def _as_f32(x: torch.Tensor) -> torch.Tensor:
@@ -265,12 +279,8 @@ class _CAExactTiled(torch.autograd.Function):
         ctx.fused = q.shape[-1] in SUPPORTED_HEAD_DIMS
         ctx.empty = False
         ctx.on_cpu = q.device.type == "cpu"
+        check_mode_limits(mode, q.device.type == "cuda", q.dtype, v.dtype, q.shape[2], q.shape[3])
         if ctx.on_cpu:
-            T, D = q.shape[2], q.shape[3]
-            if mode in ("prefix_v5", "prefix_v6"):
-                raise ValueError("CA v5/v6 paths require CUDA FP16 Q/K/V and T<=2048")
-            if mode == "fused" and (T > 2048 or D > 128 or v.dtype not in (torch.float16, torch.float32)):
-                raise ValueError("CA fused forward supports T<=2048, D<=128, FP16/FP32 values")
             for t in (k, v, log_gain):
                 if t.device != q.device:
                     raise RuntimeError("continuum_attention: all tensors must be on the same device")

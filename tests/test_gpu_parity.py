@@ -500,3 +500,41 @@ def test_empty_batch(gpu_ca, shape):
     z = torch.randn(1, 1, 0, 64, device="cuda")
     with pytest.raises(RuntimeError, match="T = 0"):
         gpu_ca.continuum_attention(z, z, z, torch.zeros(1, device="cuda"))
+
+
+def test_mode_limits_on_gpu(gpu_ca, monkeypatch):
+    """The CA_CUDA_MODE limits raise on GPU tensors as in the reference
+    (cuda/continuum_attention.py:662-665), in the operator and in the
+    decoder's fused attention; within them every mode returns the default
+    mode's result bit for bit."""
+    say("[case] CA_CUDA_MODE limits on GPU tensors")
+    g = torch.Generator().manual_seed(3)
+    q, k, v = (torch.randn(1, 2, 64, 64, generator=g).cuda() for _ in range(3))
+    rho = torch.zeros(2, device="cuda")
+    one = torch.zeros(1, device="cuda")
+    monkeypatch.delenv("CA_CUDA_MODE", raising=False)
+    ref32 = gpu_ca.continuum_attention(q, k, v, rho)
+    ref16 = gpu_ca.continuum_attention(q.half(), k.half(), v.half(), rho)
+    long16 = torch.zeros(1, 1, 2049, 16, device="cuda", dtype=torch.float16)
+    for mode in ("prefix_v5", "prefix_v6"):
+        monkeypatch.setenv("CA_CUDA_MODE", mode)
+        with pytest.raises(ValueError, match="v5/v6 paths require CUDA FP16"):
+            gpu_ca.continuum_attention(q, k, v, rho)
+        with pytest.raises(ValueError, match="v5/v6 paths require CUDA FP16"):
+            gpu_ca.continuum_attention(long16, long16, long16, one)
+        assert torch.equal(gpu_ca.continuum_attention(q.half(), k.half(), v.half(), rho), ref16)
+    monkeypatch.setenv("CA_CUDA_MODE", "fused")
+    long32 = long16.float()
+    wide = torch.zeros(1, 1, 8, 160, device="cuda")
+    for t in (long32, wide, q.bfloat16()):
+        with pytest.raises(ValueError, match="fused forward supports"):
+            gpu_ca.continuum_attention(t, t, t, one if t.shape[1] == 1 else rho)
+    assert torch.equal(gpu_ca.continuum_attention(q, k, v, rho), ref32)
+    # the decoder's fused attention: bf16 values are outside 'fused'
+    qkv = torch.randn(1, 64, 3 * 128, generator=g).cuda().bfloat16()
+    with pytest.raises(ValueError, match="fused forward supports"):
+        gpu_ca.decoder.rope_continuum_attention(qkv, rho, 10000.0, 2)
+    monkeypatch.setenv("CA_CUDA_MODE", "prefix_v5")
+    with pytest.raises(ValueError, match="v5/v6 paths require CUDA FP16"):
+        gpu_ca.decoder.rope_continuum_attention(qkv, rho, 10000.0, 2)
+    gpu_ca.decoder.rope_continuum_attention(qkv.half(), rho, 10000.0, 2)
