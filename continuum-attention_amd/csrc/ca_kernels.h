@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 
+#include <cmath>
 #include <type_traits>
 
 #include "../../include/continuum_attention_amd.h"
@@ -26,15 +27,24 @@ inline int fwd_num_items(int T, int C) {
   for (int g = 0; g < G; ++g) n += (fwd_group_tiles(g, T) + C - 1) / C;
   return n;
 }
-// Split length: 12 tiles; for short rows (at most four 128-query groups) 8,
-// 6 or 4 while the grid of BH * items would not fill `resident` work groups.
-// Measured: with longer rows the shorter splits leave the forward's time
-// unchanged and only add combine traffic.
+// Split length: 12 tiles up to T = 2048; for short rows (at most four
+// 128-query groups) 8, 6 or 4 while the grid of BH * items would not fill
+// `resident` work groups; past T = 2048, 12 sqrt(T / 2048) tiles rounded to a
+// multiple of 4 (16, 24, 32, 48 at T = 4096 .. 32768), as the grid then
+// fills the device either way and each split adds combine traffic (same-box
+// fwd+bwd at [1,16,T,64] with 12 tiles against the longer split: T = 4096
+// 1.026 -> 1.017 ms, 8192 4.04 -> 4.00 ms, 16384 16.27 -> 15.81 ms; at T =
+// 2048 longer splits were no faster).
 constexpr int kFwdSplitTiles = 12;
 constexpr int kFwdSplitSmall[] = {8, 6, 4};
 constexpr int kFwdSplitShortT = 512;
+constexpr int kFwdSplitLongT = 2048;
 inline int fwd_split_tiles(int BH, int T, int resident) {
   int C = kFwdSplitTiles;
+  if (T > kFwdSplitLongT) {
+    const double c = kFwdSplitTiles * std::sqrt((double)T / kFwdSplitLongT);
+    return 4 * (int)std::lround(c / 4.0);
+  }
   if (T > kFwdSplitShortT) return C;
   for (int c : kFwdSplitSmall) {
     if ((long long)fwd_num_items(T, C) * BH >= resident) break;
