@@ -46,11 +46,7 @@ struct Bwd {
 // every grid (config 2 dK/dV 0.309 -> 0.291 ms, [1,16,2048,64] 0.162 ->
 // 0.161 ms against the double-buffered two-wave kernel on one box).
 // Direction of each item's walk over its query tiles (see the tile loop).
-#ifndef CA_DKDV_ASCENDING
 constexpr bool kDkdvDescending = true;
-#else
-constexpr bool kDkdvDescending = false;
-#endif
 
 template <int D, class E, bool SB>
 constexpr int dkdv_waves_per_simd() {
@@ -479,9 +475,7 @@ template <int D, class E>
 hipError_t launch_bwd_dkdv(const BwdIO& io, const BwdWork& ws, const BwdPass& pass,
                            const DkdvSplit& kvs, int BH, int H, int T, hipStream_t stream) {
   // the single-buffered variant wherever it is built
-  const bool sb = dkdv_has_single_buffer<D, E>();
-  auto kernel = sb ? ca_bwd_dkdv_kernel<D, E, dkdv_has_single_buffer<D, E>()>
-                   : ca_bwd_dkdv_kernel<D, E, false>;
+  auto kernel = ca_bwd_dkdv_kernel<D, E, dkdv_has_single_buffer<D, E>()>;
   hipLaunchKernelGGL(kernel, dim3(kvs.items * BH), dim3(256), 0, stream, io.k,
                      io.v, io.rope, io.k_rotated ? nullptr : io.rope, ws.limbs, ws.qstat,
                      io.log_gain, io.dk, io.dv, ws.dsbuf,

@@ -1030,11 +1030,7 @@ __global__ __launch_bounds__(256) void ca_fwd_combine_kernel(const float* __rest
 // others).
 template <int D>
 constexpr bool fwd_uses_16x16() {
-#ifdef CA_FWD_32X32_ONLY
-  return false;
-#else
   return D == 64 || D == 128;
-#endif
 }
 
 template <int D, class E>
