@@ -51,6 +51,21 @@ def test_workspace_sizes(ca):
     assert lib.ca_bwd_workspace_bytes(0, 1, 1, 64) == 0
 
 
+@pytest.mark.parametrize("T,tiles", [(2048, 12), (3000, 16), (4096, 16), (8192, 24), (16384, 32)])
+def test_forward_split_length_follows_the_row_length(ca, T, tiles):
+    """The forward's split length (seen through its partials' size: one
+    [T][D + 2] fp32 block per slice and split of the longest row) is 12 tiles
+    up to T = 2048 and 12 sqrt(T / 2048), to a multiple of 4, beyond."""
+    lib = ca.native.load()
+    prev = lib.ca_workspace_cap()
+    ca.ops.set_workspace_cap(0)
+    try:
+        splits = -(-min(4 * ((T + 127) // 128), (T + 31) // 32) // tiles)
+        assert lib.ca_fwd_workspace_bytes(1, 16, T, 64) == 16 * splits * T * 66 * 4
+    finally:
+        ca.ops.set_workspace_cap(prev)
+
+
 @pytest.mark.parametrize("shape,code", [((0, 1, 8, 64), 1), ((1, 1, 0, 64), 1),
                                         ((1, 1, 8, 256), 2), ((1, 1, 8, 24), 2)])
 def test_argument_errors_before_any_launch(ca, shape, code):

@@ -156,6 +156,16 @@ def test_every_split_length(gpu_ca, split_override, splits):
     check_full(q, k, v, rho, dy, y, grads, f"splits {splits}")
 
 
+def test_default_splits_past_t2048(gpu_ca):
+    """[1,2,3000,64] with the automatic splits, which past T = 2048 grow with
+    the row length (16-tile forward splits here, a ragged last query group
+    and key stage) in full against the oracle."""
+    say("[case] default splits [1,2,3000,64]")
+    q, k, v, rho, dy = inputs((1, 2, 3000, 64), 23, [0.1, -0.2])
+    y, grads = run_hip(gpu_ca, q, k, v, rho, dy)
+    check_full(q, k, v, rho, dy, y, grads, "T=3000 default splits")
+
+
 @pytest.mark.parametrize("D,splits", [(128, (4, 16, 6)), (32, (6, 10, 8)), (16, (1, 3, 1))])
 def test_forced_splits_other_head_dims(gpu_ca, split_override, D, splits):
     say(f"[case] forced splits {splits} [1,2,700,{D}]")
