@@ -554,8 +554,8 @@ hipError_t launch_bwd(const BwdIO& io, const BwdWork& ws, const BwdPass& pass, c
   if (e != hipSuccess) return e;
   timer_begin(kBwdDq, stream);
   // the dQ grid's extra work groups: H that sum the gain partials of the dK/dV
-  // items, then one per (multi-chunk dK/dV key group, slice) that sums its
-  // chunk partials
+  // items, then kv_merge_slices per (multi-chunk dK/dV key group, slice) that
+  // sum its chunk partials
   const dim3 dq_grid(sp.items * BH + H + kvs.multi_groups * BH * kv_merge_slices<D>());
   if (io.rope && !io.k_rotated)
     hipLaunchKernelGGL((ca_bwd_dq_kernel<D, E, true>), dq_grid, dim3(256), 0, stream, ws.dsbuf,
