@@ -143,12 +143,21 @@ ca::DkdvSplit dkdv_split_for(int BH, int D, int dtype, const ca::BwdPass& p, boo
   // bf16 operands at D <= 64: three per CU, and the split test asks for 1.5
   // rounds of them (9/4 of the two-per-CU count; at [1,16,2048,64] chunks of
   // 16 tiles took 0.277 ms per fwd+bwd against 0.283 ms for 24 and 0.281 ms
-  // for 12, while fp32 operands keep 24: 0.302 ms against 0.306 ms for 16).
-  // fp32 operands at D = 64 (the single-buffered kernel, three per CU):
-  // split only below 1.5 rounds of three per CU and shorten like bf16 (at
-  // [1,16,2048,64] 16-tile chunks took dK/dV 0.157 ms against 0.168 ms for
-  // 24; config 2, 37 key groups x 32 slices, stays unsplit: 24-tile chunks
-  // made dK/dV 8 us faster and their merge in the dQ launch 14 us slower).
+  // for 12).
+  // fp32 operands at D = 64 (the single-buffered kernel, three per CU): split
+  // only below 1.5 rounds of three per CU (config 2, 37 key groups x 32
+  // slices, stays unsplit: 24-tile chunks made dK/dV 8 us faster and the
+  // dQ launch, which merges their partials, 13 us slower), then from 16-tile
+  // chunks down until one round is filled.  Kernel time per fwd+bwd against
+  // the earlier rule (1.5 rounds, from 24 tiles): [1,32,1500,64] 356 -> 243
+  // us (16-tile chunks instead of 24), [16,4,512,64] (one CA-P layer) 138 ->
+  // 129 us (12 instead of 6), [1,16,1024,64] 132.5 -> 126 us, [2,8,1024,64]
+  // 132.6 -> 126.4 us, [4,8,700,64] 133 -> 128 us, but [2,4,2048,64] 194.5
+  // -> 200 us (12 instead of 8); config 2, config 5 and [1,16,2048,64] keep
+  // their lengths.  The workspace is
+  // sized for chunks from kDkdvChunkTiles down (for_sizing), so a shorter
+  // first chunk is taken only where its items and partials fit that size;
+  // elsewhere the earlier rule applies.
   int res = kDqSplitBound;
   long long want = -1;
   if (!for_sizing) {
@@ -160,6 +169,10 @@ ca::DkdvSplit dkdv_split_for(int BH, int D, int dtype, const ca::BwdPass& p, boo
     } else if (dtype == CA_DTYPE_F32 && D == 64) {
       res = std::min(two_per_cu * 9 / 4, kDqSplitBound);
       want = res;
+      const ca::DkdvSplit s =
+          ca::dkdv_split(BH, p, std::min(two_per_cu * 3 / 2, kDqSplitBound), want, 16);
+      const ca::DkdvSplit sized = dkdv_split_for(BH, D, dtype, p, true);
+      if (s.items <= sized.items && s.part_items <= sized.part_items) return s;
     } else {
       res = two_per_cu;
     }

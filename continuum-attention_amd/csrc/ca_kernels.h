@@ -259,18 +259,20 @@ inline DkdvSplit dkdv_split_chunk(const BwdPass& p, int chunk) {
   }
   return s;
 }
-// Shorter chunks while kDkdvChunkTiles leaves less than one round (fewer
-// would only add partials and merge work): the first length whose items fill
-// a round is taken, else the last.  resident_groups: dK/dV work groups the
-// GPU holds at once (0: never split).
+// Shorter chunks while the first length (kDkdvChunkTiles unless given)
+// leaves less than one round (fewer would only add partials and merge
+// work): the first length whose items fill a round is taken, else the last.
+// resident_groups: dK/dV work groups the GPU holds at once (0: never split).
 constexpr int kDkdvChunkSmall[] = {16, 12, 8, 6};
 // want_groups: split only when the whole groups number fewer (default: two
 // rounds of resident_groups).
-inline DkdvSplit dkdv_split(int BH, const BwdPass& p, int resident_groups, long long want_groups = -1) {
+inline DkdvSplit dkdv_split(int BH, const BwdPass& p, int resident_groups, long long want_groups = -1,
+                            int first_chunk = kDkdvChunkTiles) {
   const long long want = want_groups >= 0 ? want_groups : 2LL * resident_groups;
   if ((long long)p.kv_groups * BH >= want) return dkdv_split_chunk(p, p.qb - p.qa);
-  DkdvSplit s = dkdv_split_chunk(p, kDkdvChunkTiles);
+  DkdvSplit s = dkdv_split_chunk(p, first_chunk);
   for (int c : kDkdvChunkSmall) {
+    if (c >= first_chunk) continue;
     if ((long long)s.items * BH >= resident_groups) break;
     s = dkdv_split_chunk(p, c);
   }
