@@ -148,13 +148,14 @@ ca::DkdvSplit dkdv_split_for(int BH, int D, int dtype, const ca::BwdPass& p, boo
   // only below 1.5 rounds of three per CU (config 2, 37 key groups x 32
   // slices, stays unsplit: 24-tile chunks made dK/dV 8 us faster and the
   // dQ launch, which merges their partials, 13 us slower), then from 16-tile
-  // chunks down until one round is filled.  Kernel time per fwd+bwd against
-  // the earlier rule (1.5 rounds, from 24 tiles): [1,32,1500,64] 356 -> 243
-  // us (16-tile chunks instead of 24), [16,4,512,64] (one CA-P layer) 138 ->
-  // 129 us (12 instead of 6), [1,16,1024,64] 132.5 -> 126 us, [2,8,1024,64]
-  // 132.6 -> 126.4 us, [4,8,700,64] 133 -> 128 us, but [2,4,2048,64] 194.5
-  // -> 200 us (12 instead of 8); config 2, config 5 and [1,16,2048,64] keep
-  // their lengths.  The workspace is
+  // chunks down until one round is filled.  Kernel time per fwd+bwd
+  // (rocprof, sum of the operator's kernels) against the earlier rule (1.5
+  // rounds, from 24 tiles): [16,4,512,64] (one CA-P layer) 125.1 -> 117.4 us
+  // (12-tile chunks instead of 6), [2,8,1024,64] 118.5 -> 111.8 us,
+  // [1,16,1024,64] 118.3 -> 112.2 us, [4,8,700,64] 119.1 -> 114.4 us,
+  // [1,32,1500,64] 368.4 -> 354.2 us (16 instead of 24), but [2,4,2048,64]
+  // 176.8 -> 183.3 us (12 instead of 8); config 2, config 5 and
+  // [1,16,2048,64] keep their lengths.  The workspace is
   // sized for chunks from kDkdvChunkTiles down (for_sizing), so a shorter
   // first chunk is taken only where its items and partials fit that size;
   // elsewhere the earlier rule applies.
