@@ -166,6 +166,21 @@ def test_default_splits_past_t2048(gpu_ca):
     check_full(q, k, v, rho, dy, y, grads, "T=3000 default splits")
 
 
+def test_default_splits_dkdv_fallback_shape(gpu_ca):
+    """[1,16,3000,64] with the automatic splits: there the fp32 dK/dV rule's
+    16-tile chunks would need more partials than the workspace is sized for,
+    so the launch takes the longer chunks it was sized for.  Heads 0 and 15
+    (independent slices, each with its own dlog_gain) against the oracle."""
+    say("[case] default splits [1,16,3000,64], heads 0 and 15")
+    q, k, v, rho, dy = inputs((1, 16, 3000, 64), 24, [0.1 * (h % 5) - 0.2 for h in range(16)])
+    y, grads = run_hip(gpu_ca, q, k, v, rho, dy)
+    for h in (0, 15):
+        sl = slice(h, h + 1)
+        check_full(q[:, sl], k[:, sl], v[:, sl], rho[sl], dy[:, sl], y[:, sl],
+                   [grads[0][:, sl], grads[1][:, sl], grads[2][:, sl], grads[3][sl]],
+                   f"T=3000 H=16 head {h}")
+
+
 @pytest.mark.parametrize("D,splits", [(128, (4, 16, 6)), (32, (6, 10, 8)), (16, (1, 3, 1))])
 def test_forced_splits_other_head_dims(gpu_ca, split_override, D, splits):
     say(f"[case] forced splits {splits} [1,2,700,{D}]")
